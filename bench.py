@@ -1,0 +1,177 @@
+#!/usr/bin/env python3
+"""Benchmark of the variable-K FP8 grouped wgrad on one MI355X.
+
+Workload (BASELINE headline): gate_up_wgrad, G=32 experts, M_total=131072 tokens, LHS e4m3
+[131072, 2880], RHS e5m2 [131072, 5760], C bf16 [32, 2880, 5760], per-tensor scales, seeded
+uniform-multinomial group sizes, inputs generated directly in HBM. One step = one launch of the
+grouped wgrad (all 32 experts). FLOPs per step = 2 * M_total * OUT_M * OUT_N (reference
+bench.py:742, launcher.cpp:76).
+
+Prints ONE JSON line with ms, TFLOPS, the MFMA roofline fraction and a CPU baseline (the
+build's numpy oracle on a bounded sample of the same workload, timed on this host's cores).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+FP8_DENSE_PEAK_TFLOPS = 5000.0    # MI355X dense FP8 MFMA peak
+REF_OPT_ASM_TFLOPS = 1237.0       # reference optimized ASM, gate_up_wgrad, C launcher (README.md:60)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gate_up_wgrad.txt")
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--config", default="gate_up_wgrad",
+                    choices=["gate_up_wgrad", "down_wgrad", "gate_up_zipf", "gate_up_mx", "constant"])
+    ap.add_argument("--mfma", default="k128", choices=["k128", "k32"])
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="approximate CPU work for the cpu_baseline sample (0 disables)")
+    ap.add_argument("--extra", action="store_true", help="also time the other configs (not part of the line)")
+    return ap.parse_args()
+
+
+def read_traffic():
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE), if recorded."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def make_runner(pkg, p, dev, mfma):
+    import torch
+    if p.is_mx:
+        out = torch.empty((p.G, p.OUT_M, p.OUT_N), dtype=torch.bfloat16, device=dev)
+        return lambda: pkg.grouped_gemm_mxfp8_variable_k(p.lhs, p.rhs, p.lhs_mx, p.rhs_mx, p.group_offs, out=out)
+    sl = torch.tensor(p.lhs_scale, dtype=torch.float32, device=dev)
+    sr = torch.tensor(p.rhs_scale, dtype=torch.float32, device=dev)
+    out = torch.empty((p.G, p.OUT_M, p.OUT_N), dtype=torch.bfloat16, device=dev)
+    return lambda: pkg.grouped_gemm_fp8_tensorwise_variable_k(p.lhs, p.rhs, sl, sr, p.group_offs, out=out, mfma=mfma)
+
+
+def time_steps(run, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()          # the library launches on this stream
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def cpu_baseline(p, seconds):
+    """Numpy oracle (fp32 dequantize + BLAS sgemm + bf16 RNE) on whole groups of the workload
+    until ~`seconds` of CPU time; throughput in TFLOPS over the groups processed."""
+    import numpy as np
+    from oracle import vark_oracle as orc
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:
+        threads = os.cpu_count() or 1
+    offs = p.group_offs.cpu().numpy()
+    done_flops, t_total, groups, tokens = 0.0, 0.0, 0, 0
+    for g in range(p.G):
+        lo, hi = int(offs[g]), int(offs[g + 1])
+        if hi == lo:
+            continue
+        L = p.lhs[lo:hi].cpu().numpy()
+        R = p.rhs[lo:hi].cpu().numpy()
+        sub = np.array([0, hi - lo], dtype=np.int64)
+        t0 = time.perf_counter()
+        orc.vark_wgrad_tensorwise(L, R, p.lhs_scale, p.rhs_scale, sub)
+        t_total += time.perf_counter() - t0
+        done_flops += 2.0 * (hi - lo) * p.OUT_M * p.OUT_N
+        groups += 1
+        tokens += hi - lo
+        if t_total >= seconds:
+            break
+    return {"value": round(done_flops / t_total / 1e12, 4), "unit": "TFLOPS", "cores": int(threads),
+            "kind": "port",
+            "sample": f"{groups} of {p.G} groups ({tokens} tokens, {done_flops / 1e12:.2f} TFLOP) of {p.name}: "
+                      f"numpy fp32 dequantize + OpenBLAS sgemm + bf16 RNE, {t_total:.1f} s"}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: the grouped wgrad needs no collective and this build runs "
+              f"on a single MI355X (asked for --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from __graft_entry__ import load_package
+    pkg = load_package()
+    dev = torch.device("cuda:0")
+    if args.config == "constant":
+        p = pkg.inputs.constant_problem(device=dev)
+    else:
+        p = pkg.inputs.make_problem(args.config, seed=args.seed, device=dev)
+    torch.cuda.synchronize()
+    run = make_runner(pkg, p, dev, args.mfma)
+    ms = time_steps(run, args.steps, args.warmup)
+    tflops = p.flops / (ms * 1e-3) / 1e12
+    traffic = read_traffic() if args.config == "gate_up_wgrad" else None
+    line = {
+        "metric": "ms + TFLOPS (% FP8 peak) for gate_up_wgrad G=32 M=131072 on 1 MI355X",
+        "value": round(tflops, 2),
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(tflops / REF_OPT_ASM_TFLOPS, 4),
+        "dtype": "fp8",
+        "data": "synthetic",
+        "config": {"workload": p.name, "G": p.G, "M_total": p.M, "OUT_M": p.OUT_M, "OUT_N": p.OUT_N,
+                   "lhs": "e4m3fn", "rhs": "e5m2", "out": "bf16", "acc": "fp32",
+                   "inputs": "seeded N(0,1) / N(0,1e-3) quantized per-tensor, multinomial group sizes, in HBM",
+                   "kernel": f"hip gfx950 persistent 192x320 tiles, mfma {args.mfma}",
+                   "baseline_number": "reference optimized ASM 3.515 ms / 1237 TFLOPS (README.md:60)"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP8_DENSE_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / FP8_DENSE_PEAK_TFLOPS, 4), "traffic": traffic},
+    }
+    if args.extra:
+        extra = {}
+        for name in ("down_wgrad", "gate_up_zipf", "gate_up_mx", "constant"):
+            q = pkg.inputs.constant_problem(device=dev) if name == "constant" else \
+                pkg.inputs.make_problem(name, seed=args.seed, device=dev)
+            r = make_runner(pkg, q, dev, args.mfma)
+            t = time_steps(r, max(args.steps // 4, 10), max(args.warmup // 4, 5))
+            extra[name] = {"ms": round(t, 4), "TFLOPS": round(q.flops / (t * 1e-3) / 1e12, 2)}
+            del q, r
+        if args.mfma == "k128":
+            r = make_runner(pkg, p, dev, "k32")
+            t = time_steps(r, max(args.steps // 4, 10), max(args.warmup // 4, 5))
+            extra["gate_up_wgrad_k32_mfma"] = {"ms": round(t, 4), "TFLOPS": round(p.flops / (t * 1e-3) / 1e12, 2)}
+        line["extra"] = extra
+    if args.cpu_seconds > 0 and not p.is_mx:
+        line["cpu_baseline"] = cpu_baseline(p, args.cpu_seconds)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,87 @@
+"""ctypes binding of libggemm_vark.so (declarations in include/ggemm_vark.h)."""
+from __future__ import annotations
+
+import ctypes
+import os
+
+from . import build as _build
+
+_lib = None
+
+EXPORTS = (
+    "ggemm_vark_wgrad_fp8",
+    "ggemm_vark_wgrad_fp8_k32",
+    "ggemm_vark_wgrad_mxfp8",
+    "ggemm_vark_check_offsets",
+    "ggemm_vark_num_cus",
+    "ggemm_vark_strerror",
+    "ggemm_vark_abi_version",
+    "ggemm_vark_launch_geometry",
+)
+
+ERRORS = {
+    0: "GGEMM_OK", -1: "GGEMM_E_NULL", -2: "GGEMM_E_SHAPE", -3: "GGEMM_E_STRIDE",
+    -4: "GGEMM_E_ALIGN", -5: "GGEMM_E_OFFSETS", -6: "GGEMM_E_DEVICE", -7: "GGEMM_E_MX_ALIGN",
+}
+
+
+class GGemmError(RuntimeError):
+    def __init__(self, code: int, what: str):
+        self.code = code
+        super().__init__(f"{what} failed with {ERRORS.get(code, 'hipError')} ({code}): {strerror(code)}")
+
+
+def library_path() -> str:
+    return _build.SO_PATH
+
+
+def load():
+    """Load the in-tree library; raise if it has not been built (there is no fallback path)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = library_path()
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: run `python __graft_entry__.py build` first "
+                           "(this package has no CPU or Python fallback for the kernel)")
+    lib = ctypes.CDLL(path)
+    vp, i32, i64p = ctypes.c_void_p, ctypes.c_int32, ctypes.POINTER(ctypes.c_int64)
+    tw = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp]
+    for name in ("ggemm_vark_wgrad_fp8", "ggemm_vark_wgrad_fp8_k32"):
+        f = getattr(lib, name)
+        f.argtypes = tw
+        f.restype = ctypes.c_int
+    lib.ggemm_vark_wgrad_mxfp8.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 10 + [vp]
+    lib.ggemm_vark_wgrad_mxfp8.restype = ctypes.c_int
+    lib.ggemm_vark_check_offsets.argtypes = [i64p, i32, ctypes.c_int64, i32]
+    lib.ggemm_vark_check_offsets.restype = ctypes.c_int
+    lib.ggemm_vark_num_cus.argtypes = [i32, ctypes.POINTER(i32)]
+    lib.ggemm_vark_num_cus.restype = ctypes.c_int
+    lib.ggemm_vark_strerror.argtypes = [i32]
+    lib.ggemm_vark_strerror.restype = ctypes.c_char_p
+    lib.ggemm_vark_abi_version.argtypes = []
+    lib.ggemm_vark_abi_version.restype = i32
+    lib.ggemm_vark_launch_geometry.argtypes = [ctypes.POINTER(i32)] * 5
+    lib.ggemm_vark_launch_geometry.restype = None
+    _lib = lib
+    return lib
+
+
+def strerror(code: int) -> str:
+    try:
+        return load().ggemm_vark_strerror(int(code)).decode()
+    except Exception:  # library missing: still produce a message
+        return ERRORS.get(code, "unknown")
+
+
+def check(code: int, what: str) -> None:
+    if code != 0:
+        raise GGemmError(code, what)
+
+
+def launch_geometry() -> dict:
+    lib = load()
+    vals = [ctypes.c_int32() for _ in range(5)]
+    lib.ggemm_vark_launch_geometry(*[ctypes.byref(v) for v in vals])
+    keys = ("block_threads", "dynamic_lds", "tile_m", "tile_n", "k_step")
+    return {k: v.value for k, v in zip(keys, vals)}

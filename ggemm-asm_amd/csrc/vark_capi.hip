@@ -1,0 +1,165 @@
+// extern "C" launcher library for the variable-K FP8 grouped wgrad kernels (libggemm_vark.so).
+// Validates arguments on the host, then launches the persistent kernel with the reference's
+// geometry: grid (num_cus, 1, 1), block (512, 1, 1), 64 KiB dynamic LDS
+// (reference launcher.cpp:142-171, bench.py:388-398).
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdint>
+#include <cstring>
+
+#include "../../include/ggemm_vark.h"
+#include "vark_kernel.h"
+
+GGEMM_DEFINE_TENSORWISE_KERNEL(_grouped_variable_k_gemm_kernel, false)
+GGEMM_DEFINE_TENSORWISE_KERNEL(_grouped_variable_k_gemm_kernel_k32, true)
+GGEMM_DEFINE_MX_KERNEL(_grouped_variable_k_mxfp8_gemm_kernel)
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+// per-device cache: 0 = unknown, -1 = unusable, >0 = CU count of a gfx950 device
+std::atomic<int> g_cus[kMaxDevices];
+
+int device_cus(int* cus_out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return GGEMM_E_DEVICE;
+  int c = g_cus[dev].load(std::memory_order_relaxed);
+  if (c == 0) {
+    hipDeviceProp_t p;
+    e = hipGetDeviceProperties(&p, dev);
+    if (e != hipSuccess) return (int)e;
+    c = (std::strncmp(p.gcnArchName, "gfx950", 6) == 0 && p.multiProcessorCount > 0) ? p.multiProcessorCount : -1;
+    g_cus[dev].store(c, std::memory_order_relaxed);
+  }
+  if (c < 0) return GGEMM_E_DEVICE;
+  *cus_out = c;
+  return GGEMM_OK;
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+int validate_common(const void* lhs, const void* rhs, const void* out, const void* ls, const void* rs,
+                    const int64_t* offs, int G, int OUT_M, int OUT_N, int slm, int srm, int scg, int scm,
+                    int scn) {
+  if (!lhs || !rhs || !out || !ls || !rs || !offs) return GGEMM_E_NULL;
+  if (G <= 0 || OUT_M <= 0 || OUT_N <= 0) return GGEMM_E_SHAPE;
+  if (OUT_M % 16 || OUT_N % 16) return GGEMM_E_SHAPE;
+  if (scn != 1) return GGEMM_E_STRIDE;
+  if (slm < OUT_M || srm < OUT_N || slm % 16 || srm % 16) return GGEMM_E_STRIDE;
+  if (scm < OUT_N || scm % 4 || scg % 4) return GGEMM_E_STRIDE;
+  if ((int64_t)scg < (int64_t)(OUT_M - 1) * scm + OUT_N) return GGEMM_E_STRIDE;
+  // the kernel forms 32-bit buffer offsets of up to 128 rows of a stage
+  if ((int64_t)slm * 129 > INT32_MAX || (int64_t)srm * 129 > INT32_MAX) return GGEMM_E_SHAPE;
+  if (!aligned(lhs, 16) || !aligned(rhs, 16) || !aligned(out, 8)) return GGEMM_E_ALIGN;
+  return GGEMM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+static int launch_tensorwise(bool legacy, const void* lhs, const void* rhs, void* out, const float* lhs_scale,
+                             const float* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
+                             int32_t OUT_N, int32_t slm, int32_t srm, int32_t scg, int32_t scm, int32_t scn,
+                             void* stream) {
+  int rc = validate_common(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, slm, srm, scg, scm,
+                           scn);
+  if (rc) return rc;
+  int cus = 0;
+  rc = device_cus(&cus);
+  if (rc) return rc;
+  auto kern = legacy ? _grouped_variable_k_gemm_kernel_k32 : _grouped_variable_k_gemm_kernel;
+  hipLaunchKernelGGL(kern, dim3(cus), dim3(ggemm::kThreads), ggemm::kDynLdsBytes, (hipStream_t)stream,
+                     (const uint8_t*)lhs, (const uint8_t*)rhs, (uint16_t*)out, lhs_scale, rhs_scale, group_offs, G,
+                     OUT_M, OUT_N, slm, srm, scg, scm, scn, (void*)nullptr, (void*)nullptr);
+  return (int)hipGetLastError();
+}
+
+int ggemm_vark_wgrad_fp8(const void* lhs, const void* rhs, void* out, const float* lhs_scale, const float* rhs_scale,
+                         const int64_t* group_offs, int32_t G, int32_t OUT_M, int32_t OUT_N, int32_t stride_lhs_m,
+                         int32_t stride_rhs_m, int32_t stride_cg, int32_t stride_cm, int32_t stride_cn,
+                         void* stream) {
+  return launch_tensorwise(false, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
+                           stride_rhs_m, stride_cg, stride_cm, stride_cn, stream);
+}
+
+int ggemm_vark_wgrad_fp8_k32(const void* lhs, const void* rhs, void* out, const float* lhs_scale,
+                             const float* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
+                             int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
+                             int32_t stride_cm, int32_t stride_cn, void* stream) {
+  return launch_tensorwise(true, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
+                           stride_rhs_m, stride_cg, stride_cm, stride_cn, stream);
+}
+
+int ggemm_vark_wgrad_mxfp8(const void* lhs, const void* rhs, void* out, const uint8_t* lhs_scale,
+                           const uint8_t* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
+                           int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
+                           int32_t stride_cm, int32_t stride_cn, int32_t stride_lhs_scale, int32_t stride_rhs_scale,
+                           void* stream) {
+  int rc = validate_common(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
+                           stride_rhs_m, stride_cg, stride_cm, stride_cn);
+  if (rc) return rc;
+  if (stride_lhs_scale < OUT_M || stride_rhs_scale < OUT_N || stride_lhs_scale % 16 || stride_rhs_scale % 16)
+    return GGEMM_E_STRIDE;
+  if (!aligned(lhs_scale, 16) || !aligned(rhs_scale, 16)) return GGEMM_E_ALIGN;
+  int cus = 0;
+  rc = device_cus(&cus);
+  if (rc) return rc;
+  hipLaunchKernelGGL(_grouped_variable_k_mxfp8_gemm_kernel, dim3(cus), dim3(ggemm::kThreads), ggemm::kDynLdsBytes,
+                     (hipStream_t)stream, (const uint8_t*)lhs, (const uint8_t*)rhs, (uint16_t*)out, lhs_scale,
+                     rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m, stride_rhs_m, stride_cg, stride_cm,
+                     stride_cn, stride_lhs_scale, stride_rhs_scale, (void*)nullptr, (void*)nullptr);
+  return (int)hipGetLastError();
+}
+
+int ggemm_vark_check_offsets(const int64_t* offs, int32_t G, int64_t M_total, int32_t mx) {
+  if (!offs || G <= 0) return GGEMM_E_OFFSETS;
+  if (offs[0] != 0) return GGEMM_E_OFFSETS;
+  for (int g = 0; g < G; ++g) {
+    if (offs[g + 1] < offs[g]) return GGEMM_E_OFFSETS;
+    if (mx && (offs[g] % 32)) return GGEMM_E_MX_ALIGN;
+  }
+  if (offs[G] > M_total) return GGEMM_E_OFFSETS;
+  return GGEMM_OK;
+}
+
+int ggemm_vark_num_cus(int32_t device, int32_t* num_cus) {
+  if (!num_cus) return GGEMM_E_NULL;
+  int v = 0;
+  hipError_t e = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device);
+  if (e != hipSuccess) return (int)e;
+  *num_cus = v;
+  return GGEMM_OK;
+}
+
+const char* ggemm_vark_strerror(int32_t code) {
+  switch (code) {
+    case GGEMM_OK: return "success";
+    case GGEMM_E_NULL: return "a required pointer is NULL";
+    case GGEMM_E_SHAPE: return "invalid shape (G, OUT_M, OUT_N must be > 0, OUT_M/OUT_N multiples of 16)";
+    case GGEMM_E_STRIDE: return "invalid strides (row strides >= width and multiples of 16, stride_cn == 1)";
+    case GGEMM_E_ALIGN: return "misaligned pointer (LHS/RHS 16-byte, C 8-byte)";
+    case GGEMM_E_OFFSETS: return "invalid group offsets (must start at 0, be non-decreasing, end <= M_total)";
+    case GGEMM_E_DEVICE: return "current device is not a usable gfx950 (MI355X) GPU";
+    case GGEMM_E_MX_ALIGN: return "MXFP8 groups must start on 32-token block boundaries";
+    default: break;
+  }
+  if (code > 0) return hipGetErrorString((hipError_t)code);
+  return "unknown error";
+}
+
+int32_t ggemm_vark_abi_version(void) { return GGEMM_VARK_ABI_VERSION; }
+
+void ggemm_vark_launch_geometry(int32_t* block_threads, int32_t* dynamic_lds, int32_t* tile_m, int32_t* tile_n,
+                                int32_t* k_step) {
+  if (block_threads) *block_threads = ggemm::kThreads;
+  if (dynamic_lds) *dynamic_lds = ggemm::kDynLdsBytes;
+  if (tile_m) *tile_m = ggemm::kTileM;
+  if (tile_n) *tile_n = ggemm::kTileN;
+  if (k_step) *k_step = ggemm::kKStep;
+}
+
+}  // extern "C"

@@ -1,0 +1,182 @@
+"""Code-object launch harness: drives ``variable_k_wgrad.co`` the way the reference drives its `.co`.
+
+Mirrors the reference's HIP module path (reference bench.py:43-143 ``load_kernel`` /
+``_detect_kernel_name`` / ``unload_kernel``; bench.py:288-309,364-413 ``_pack_args`` /
+``prepare_variable_k_args`` / ``launch_variable_k_kernel``; launcher.cpp:16-33,123-171 the
+96-byte ``KernelArgs`` record passed with HIP_LAUNCH_PARAM_BUFFER_POINTER). It exists to show
+the build's code object is a drop-in for that launch surface; the library entry points in
+``vark.py`` are the normal way to call the kernel.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import struct
+
+import torch
+
+KERNEL_NAME = "_grouped_variable_k_gemm_kernel"
+BLOCK = 512
+SHARED_MEM = 65536
+KERNARG_SIZE = 96
+
+_hip = None
+
+
+def load_hip():
+    global _hip
+    if _hip is not None:
+        return _hip
+    lib = None
+    for name in ("libamdhip64.so", "libamdhip64.so.7", "libamdhip64.so.6"):
+        try:
+            lib = ctypes.CDLL(name)
+            break
+        except OSError:
+            continue
+    if lib is None:
+        lib = ctypes.CDLL(os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib", "libamdhip64.so"))
+    vp = ctypes.c_void_p
+    lib.hipModuleLoadData.argtypes = [ctypes.POINTER(vp), vp]
+    lib.hipModuleLoadData.restype = ctypes.c_int
+    lib.hipModuleGetFunction.argtypes = [ctypes.POINTER(vp), vp, ctypes.c_char_p]
+    lib.hipModuleGetFunction.restype = ctypes.c_int
+    lib.hipModuleLaunchKernel.argtypes = [vp, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint,
+                                          ctypes.c_uint, ctypes.c_uint, ctypes.c_uint, vp,
+                                          ctypes.POINTER(vp), ctypes.POINTER(vp)]
+    lib.hipModuleLaunchKernel.restype = ctypes.c_int
+    lib.hipModuleUnload.argtypes = [vp]
+    lib.hipModuleUnload.restype = ctypes.c_int
+    lib.hipGetErrorString.argtypes = [ctypes.c_int]
+    lib.hipGetErrorString.restype = ctypes.c_char_p
+    _hip = lib
+    return lib
+
+
+def check_hip(err: int, msg: str = "") -> None:
+    if err != 0:
+        raise RuntimeError(f"HIP error {err} ({load_hip().hipGetErrorString(err)}): {msg}")
+
+
+# ----------------------------------------------------------------------------- ELF symbols
+
+def elf_global_functions(data: bytes) -> list[str]:
+    """Names of FUNC GLOBAL symbols of an ELF64 little-endian object (what the reference reads
+    with ``llvm-readelf -s``, bench.py:118-131), parsed directly from the section headers."""
+    if data[:4] != b"\x7fELF" or data[4] != 2 or data[5] != 1:
+        raise ValueError("not an ELF64 little-endian object")
+    e_shoff = struct.unpack_from("<Q", data, 0x28)[0]
+    e_shentsize, e_shnum = struct.unpack_from("<HH", data, 0x3A)
+    names = []
+    for i in range(e_shnum):
+        sh = e_shoff + i * e_shentsize
+        sh_type = struct.unpack_from("<I", data, sh + 4)[0]
+        if sh_type not in (2, 11):  # SHT_SYMTAB, SHT_DYNSYM
+            continue
+        sh_offset, sh_size = struct.unpack_from("<QQ", data, sh + 0x18)
+        sh_link = struct.unpack_from("<I", data, sh + 0x28)[0]
+        sh_entsize = struct.unpack_from("<Q", data, sh + 0x38)[0] or 24
+        strtab = e_shoff + sh_link * e_shentsize
+        str_off = struct.unpack_from("<Q", data, strtab + 0x18)[0]
+        for j in range(sh_size // sh_entsize):
+            st = sh_offset + j * sh_entsize
+            st_name, st_info = struct.unpack_from("<IB", data, st)
+            if (st_info & 0xF) == 2 and (st_info >> 4) == 1:  # STT_FUNC, STB_GLOBAL
+                end = data.index(b"\0", str_off + st_name)
+                names.append(data[str_off + st_name:end].decode())
+    return names
+
+
+def detect_kernel_name(data: bytes) -> str:
+    for name in elf_global_functions(data):
+        if name.startswith("_grouped"):
+            return name
+    raise RuntimeError("no FUNC GLOBAL symbol starting with _grouped in the code object")
+
+
+# ----------------------------------------------------------------------------- module API
+
+def load_kernel(co_path: str, kernel_name: str | None = None):
+    """Load a code object; returns (module, function, kernel_name)."""
+    hip = load_hip()
+    with open(co_path, "rb") as f:
+        data = f.read()
+    module = ctypes.c_void_p()
+    check_hip(hip.hipModuleLoadData(ctypes.byref(module), data), f"loading {co_path}")
+    name = kernel_name or detect_kernel_name(data)
+    func = ctypes.c_void_p()
+    check_hip(hip.hipModuleGetFunction(ctypes.byref(func), module, name.encode()), f"getting {name}")
+    return module, func, name
+
+
+def unload_kernel(module) -> None:
+    load_hip().hipModuleUnload(module)
+
+
+def get_num_cus(device: int = 0) -> int:
+    return torch.cuda.get_device_properties(device).multi_processor_count
+
+
+def _pack_args(args):
+    """16-entry kernelParams array (reference bench.py:296-309 packs the same way)."""
+    arr = (ctypes.c_void_p * len(args))()
+    storage = []
+    for i, a in enumerate(args):
+        if isinstance(a, ctypes.c_void_p):
+            p = ctypes.c_uint64(a.value or 0)
+        elif isinstance(a, ctypes.c_int32):
+            p = ctypes.c_int32(a.value)
+        else:
+            raise TypeError(f"unexpected argument type {type(a)}")
+        storage.append(p)
+        arr[i] = ctypes.cast(ctypes.pointer(p), ctypes.c_void_p)
+    return arr, storage
+
+
+def _arg_list(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N):
+    P, I = (lambda t: ctypes.c_void_p(t.data_ptr())), (lambda v: ctypes.c_int32(int(v)))
+    return [P(lhs), P(rhs), P(out), P(lhs_scale), P(rhs_scale), P(group_offs),
+            I(G), I(OUT_M), I(OUT_N), I(lhs.stride(0)), I(rhs.stride(0)),
+            I(out.stride(0)), I(out.stride(1)), I(out.stride(2)),
+            ctypes.c_void_p(0), ctypes.c_void_p(0)]
+
+
+def prepare_variable_k_args(func, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N,
+                            num_sms, shared_mem=SHARED_MEM):
+    """Closure launching with a kernelParams array on the null stream (bench.py:364-402)."""
+    hip = load_hip()
+    packed, storage = _pack_args(_arg_list(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N))
+
+    def launch():
+        check_hip(hip.hipModuleLaunchKernel(func, num_sms, 1, 1, BLOCK, 1, 1, shared_mem, None, packed, None),
+                  "launching variable-K kernel")
+
+    return launch, storage
+
+
+def launch_variable_k_kernel(func, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, num_sms,
+                             shared_mem=SHARED_MEM):
+    launch, _keep = prepare_variable_k_args(func, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M,
+                                            OUT_N, num_sms, shared_mem)
+    launch()
+
+
+def kernarg_buffer(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N) -> bytes:
+    """The 96-byte KernelArgs record of launcher.cpp:16-33: six pointers, eight int32, two null
+    scratch pointers."""
+    return struct.pack("<6Q8i2Q", lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), lhs_scale.data_ptr(),
+                       rhs_scale.data_ptr(), group_offs.data_ptr(), G, OUT_M, OUT_N, lhs.stride(0),
+                       rhs.stride(0), out.stride(0), out.stride(1), out.stride(2), 0, 0)
+
+
+def launch_with_kernarg_buffer(func, kernarg: bytes, num_sms, shared_mem=SHARED_MEM) -> None:
+    """Launch with HIP_LAUNCH_PARAM_BUFFER_POINTER (launcher.cpp:142-147)."""
+    if len(kernarg) != KERNARG_SIZE:
+        raise ValueError("kernarg record must be 96 bytes")
+    hip = load_hip()
+    buf = ctypes.create_string_buffer(kernarg, KERNARG_SIZE)
+    size = ctypes.c_size_t(KERNARG_SIZE)
+    extra = (ctypes.c_void_p * 5)(ctypes.c_void_p(1), ctypes.cast(buf, ctypes.c_void_p), ctypes.c_void_p(2),
+                                  ctypes.cast(ctypes.pointer(size), ctypes.c_void_p), ctypes.c_void_p(3))
+    check_hip(hip.hipModuleLaunchKernel(func, num_sms, 1, 1, BLOCK, 1, 1, shared_mem, None, None, extra),
+              "launching with kernarg buffer")

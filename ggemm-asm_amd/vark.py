@@ -1,0 +1,154 @@
+"""PyTorch-facing grouped wgrad ops over the C ABI.
+
+``grouped_gemm_fp8_tensorwise_variable_k`` mirrors the reference's oracle call
+``grouped_gemm_fp8_tensorwise_variable_k_triton_kernel(lhs, rhs, lhs_scale, rhs_scale,
+group_offs)`` (reference bench.py:241-246, 262-269): same argument order and meaning, a new
+bf16 ``[G, OUT_M, OUT_N]`` tensor as the result. The launch goes through
+``ggemm_vark_wgrad_fp8`` in libggemm_vark.so on torch's current stream; there is no
+fallback: a missing library or a non-gfx950 device raises.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _lib
+
+_FP8_LHS = (torch.float8_e4m3fn, torch.uint8)
+_FP8_RHS = (torch.float8_e5m2, torch.uint8)
+
+
+def _check_inputs(lhs, rhs, group_offs, lhs_dt=_FP8_LHS, rhs_dt=_FP8_RHS):
+    if lhs.dim() != 2 or rhs.dim() != 2:
+        raise ValueError("lhs and rhs must be 2-D [M_total, OUT_M] / [M_total, OUT_N]")
+    if lhs.shape[0] != rhs.shape[0]:
+        raise ValueError(f"token counts differ: lhs {tuple(lhs.shape)} vs rhs {tuple(rhs.shape)}")
+    if lhs.dtype not in lhs_dt or rhs.dtype not in rhs_dt:
+        raise TypeError(f"lhs must be float8_e4m3fn (or its uint8 bytes), rhs float8_e5m2; "
+                        f"got {lhs.dtype}, {rhs.dtype}")
+    if lhs.stride(1) != 1 or rhs.stride(1) != 1:
+        raise ValueError("lhs/rhs must be contiguous along the feature dimension")
+    if group_offs.dtype != torch.int64 or group_offs.dim() != 1 or group_offs.numel() < 2:
+        raise ValueError("group_offs must be int64 [G+1]")
+    dev = lhs.device
+    for t in (rhs, group_offs):
+        if t.device != dev:
+            raise ValueError("all tensors must be on the same device")
+    if dev.type != "cuda":
+        raise ValueError("the variable-K wgrad runs on a gfx950 GPU only (tensors are on "
+                         f"{dev}); use the CPU oracle in tests for reference results")
+
+
+def _check_out(out, G, OUT_M, OUT_N, dev):
+    if out is None:
+        return torch.empty((G, OUT_M, OUT_N), dtype=torch.bfloat16, device=dev)
+    if out.dtype != torch.bfloat16 or out.dim() != 3 or tuple(out.shape) != (G, OUT_M, OUT_N):
+        raise ValueError(f"out must be bf16 [{G}, {OUT_M}, {OUT_N}]")
+    if out.device != dev:
+        raise ValueError("out must be on the input device")
+    return out
+
+
+def _validate_offsets(group_offs, M_total, mx):
+    offs = group_offs.detach().to("cpu", torch.int64).contiguous().numpy()
+    G = offs.size - 1
+    rc = _lib.load().ggemm_vark_check_offsets(
+        offs.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)), G, M_total, 1 if mx else 0)
+    _lib.check(rc, "ggemm_vark_check_offsets")
+
+
+def _stream(dev) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def grouped_gemm_fp8_tensorwise_variable_k(lhs: torch.Tensor, rhs: torch.Tensor, lhs_scale: torch.Tensor,
+                                           rhs_scale: torch.Tensor, group_offs: torch.Tensor,
+                                           out: torch.Tensor | None = None, *, mfma: str = "k128",
+                                           validate: bool = False) -> torch.Tensor:
+    """``out[g] = lhs_scale * rhs_scale * lhs[offs[g]:offs[g+1]]^T @ rhs[offs[g]:offs[g+1]]`` (bf16).
+
+    lhs: float8_e4m3fn [M_total, OUT_M]; rhs: float8_e5m2 [M_total, OUT_N]; scales: fp32 scalar
+    tensors on the device; group_offs: int64 [G+1]. ``mfma="k32"`` selects the kernel built on the
+    K=32 MFMA the reference uses; ``validate=True`` checks group_offs on the host first (a sync).
+    """
+    _check_inputs(lhs, rhs, group_offs)
+    for s in (lhs_scale, rhs_scale):
+        if s.dtype != torch.float32 or s.numel() != 1 or s.device != lhs.device:
+            raise ValueError("scales must be single-element fp32 tensors on the input device")
+    G = group_offs.numel() - 1
+    M_total, OUT_M = lhs.shape
+    OUT_N = rhs.shape[1]
+    out = _check_out(out, G, OUT_M, OUT_N, lhs.device)
+    if validate:
+        _validate_offsets(group_offs, M_total, mx=False)
+    lib = _lib.load()
+    fn = {"k128": lib.ggemm_vark_wgrad_fp8, "k32": lib.ggemm_vark_wgrad_fp8_k32}[mfma]
+    with torch.cuda.device(lhs.device):
+        rc = fn(lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), lhs_scale.data_ptr(), rhs_scale.data_ptr(),
+                group_offs.data_ptr(), G, OUT_M, OUT_N, lhs.stride(0), rhs.stride(0), out.stride(0),
+                out.stride(1), out.stride(2), _stream(lhs.device))
+    _lib.check(rc, "ggemm_vark_wgrad_fp8" if mfma == "k128" else "ggemm_vark_wgrad_fp8_k32")
+    return out
+
+
+def grouped_gemm_mxfp8_variable_k(lhs: torch.Tensor, rhs: torch.Tensor, lhs_scale: torch.Tensor,
+                                  rhs_scale: torch.Tensor, group_offs: torch.Tensor,
+                                  out: torch.Tensor | None = None, *, validate: bool = False) -> torch.Tensor:
+    """MXFP8 variant: ``lhs_scale``/``rhs_scale`` are e8m0 bytes [ceil(M/32), OUT_M] / [.., OUT_N]
+    (uint8 or float8_e8m0fnu); token block b of a column is scaled by 2^(scale-127). Group starts
+    must be multiples of 32 (``validate=True`` checks it on the host)."""
+    _check_inputs(lhs, rhs, group_offs)
+    M_total, OUT_M = lhs.shape
+    OUT_N = rhs.shape[1]
+    nblk = (M_total + 31) // 32
+    for s, w in ((lhs_scale, OUT_M), (rhs_scale, OUT_N)):
+        if s.dtype not in (torch.uint8, getattr(torch, "float8_e8m0fnu", torch.uint8)):
+            raise TypeError("MX scales must be e8m0 bytes (uint8 or float8_e8m0fnu)")
+        if s.dim() != 2 or s.shape[0] < nblk or s.shape[1] != w or s.stride(1) != 1:
+            raise ValueError(f"MX scales must be [{nblk}, width] with unit column stride")
+        if s.device != lhs.device:
+            raise ValueError("scales must be on the input device")
+    G = group_offs.numel() - 1
+    out = _check_out(out, G, OUT_M, OUT_N, lhs.device)
+    if validate:
+        _validate_offsets(group_offs, M_total, mx=True)
+    lib = _lib.load()
+    with torch.cuda.device(lhs.device):
+        rc = lib.ggemm_vark_wgrad_mxfp8(
+            lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), lhs_scale.data_ptr(), rhs_scale.data_ptr(),
+            group_offs.data_ptr(), G, OUT_M, OUT_N, lhs.stride(0), rhs.stride(0), out.stride(0), out.stride(1),
+            out.stride(2), lhs_scale.stride(0), rhs_scale.stride(0), _stream(lhs.device))
+    _lib.check(rc, "ggemm_vark_wgrad_mxfp8")
+    return out
+
+
+# --------------------------------------------------------------------------- torch.library op
+
+def _register_custom_op():
+    """``torch.ops.ggemm.variable_k_wgrad_fp8`` for callers that dispatch through torch."""
+    try:
+        lib_def = torch.library.Library("ggemm", "DEF")
+    except Exception:  # already defined in this process
+        return
+    lib_def.define("variable_k_wgrad_fp8(Tensor lhs, Tensor rhs, Tensor lhs_scale, Tensor rhs_scale, "
+                   "Tensor group_offs) -> Tensor")
+
+    def _impl(lhs, rhs, lhs_scale, rhs_scale, group_offs):
+        return grouped_gemm_fp8_tensorwise_variable_k(lhs, rhs, lhs_scale, rhs_scale, group_offs)
+
+    def _meta(lhs, rhs, lhs_scale, rhs_scale, group_offs):
+        return lhs.new_empty((group_offs.shape[0] - 1, lhs.shape[1], rhs.shape[1]), dtype=torch.bfloat16)
+
+    lib_def.impl("variable_k_wgrad_fp8", _impl, "CUDA")
+    lib_def.impl("variable_k_wgrad_fp8", _meta, "Meta")
+    _register_custom_op.lib = lib_def  # keep the registration alive
+
+
+_register_custom_op()
+
+
+def as_bf16_bits(t: torch.Tensor) -> np.ndarray:
+    """bf16 tensor -> numpy uint16 bit patterns (host copy)."""
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)

@@ -1,0 +1,93 @@
+/* C ABI of the MI355X variable-K FP8 grouped weight-gradient library (libggemm_vark.so).
+ *
+ *   C[g] = s_lhs * s_rhs * LHS[offs[g]:offs[g+1], :]^T @ RHS[offs[g]:offs[g+1], :]
+ *
+ * All pointers are device pointers except where stated; sizes and strides are in elements.
+ * Every entry point returns 0 on success, a positive hipError_t value when the HIP runtime
+ * failed, or a negative GGEMM_E_* code when argument validation failed (nothing is launched
+ * then). Launches are asynchronous on `stream` (a hipStream_t; NULL = the null stream).
+ * No entry point allocates device memory, keeps state between calls, or synchronizes.
+ */
+#ifndef GGEMM_VARK_H
+#define GGEMM_VARK_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GGEMM_VARK_ABI_VERSION 1
+
+enum {
+  GGEMM_OK = 0,
+  GGEMM_E_NULL = -1,        /* a required pointer is NULL */
+  GGEMM_E_SHAPE = -2,       /* G, OUT_M or OUT_N <= 0, or sizes overflow int32 strides */
+  GGEMM_E_STRIDE = -3,      /* strides too small, stride_cn != 1, or not multiples of 16 / 4 */
+  GGEMM_E_ALIGN = -4,       /* LHS/RHS not 16-byte aligned or C not 8-byte aligned */
+  GGEMM_E_OFFSETS = -5,     /* host group offsets not 0-based, non-decreasing, or past M_total */
+  GGEMM_E_DEVICE = -6,      /* no usable device / not a gfx950 device */
+  GGEMM_E_MX_ALIGN = -7     /* MX: a group does not start on a 32-token block boundary */
+};
+
+/* Tensorwise FP8 grouped wgrad. Replaces the reference's code-object launch of
+ * `_grouped_variable_k_gemm_kernel` (reference bench.py:364-413 prepare_variable_k_args /
+ * launch_variable_k_kernel, launcher.cpp:123-171) and the Triton op it stands in for
+ * (reference bench.py:268, `_triton_vark(lhs, rhs, lhs_scale, rhs_scale, group_offs)`).
+ * lhs: e4m3fn [M_total, OUT_M] (row stride stride_lhs_m); rhs: e5m2 [M_total, OUT_N]
+ * (row stride stride_rhs_m); out: bf16 [G, OUT_M, OUT_N] (strides stride_cg, stride_cm,
+ * stride_cn == 1); lhs_scale / rhs_scale: fp32 scalars; group_offs: int64 [G+1], offs[0] = 0,
+ * non-decreasing. Every element of out[0:G] is written, empty groups with zeros.
+ * Requirements: OUT_M, OUT_N, stride_lhs_m, stride_rhs_m multiples of 16; stride_cm,
+ * stride_cg multiples of 4; lhs/rhs 16-byte aligned, out 8-byte aligned. */
+int ggemm_vark_wgrad_fp8(const void* lhs, const void* rhs, void* out, const float* lhs_scale,
+                         const float* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
+                         int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
+                         int32_t stride_cm, int32_t stride_cn, void* stream);
+
+/* Same as ggemm_vark_wgrad_fp8 but with the K=32 MFMA (v_mfma_f32_16x16x32_bf8_fp8) the
+ * reference kernel is built on (reference README.md:5). Kept to measure the instruction choice;
+ * same contract and results within fp32 accumulation order. */
+int ggemm_vark_wgrad_fp8_k32(const void* lhs, const void* rhs, void* out, const float* lhs_scale,
+                             const float* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
+                             int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
+                             int32_t stride_cm, int32_t stride_cn, void* stream);
+
+/* MXFP8 block-scaled grouped wgrad (no reference counterpart: the reference imports only the
+ * tensorwise kernels, reference bench.py:241-246). lhs_scale: e8m0 bytes [ceil(M_total/32), OUT_M]
+ * with row stride stride_lhs_scale; rhs_scale: e8m0 [ceil(M_total/32), OUT_N], row stride
+ * stride_rhs_scale. Token block b (tokens 32b..32b+31) of a column is multiplied by
+ * 2^(scale[b][col]-127). Every group must start at a multiple of 32 tokens (checked when
+ * host_group_offs is given, otherwise the caller's responsibility). */
+int ggemm_vark_wgrad_mxfp8(const void* lhs, const void* rhs, void* out, const uint8_t* lhs_scale,
+                           const uint8_t* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
+                           int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
+                           int32_t stride_cm, int32_t stride_cn, int32_t stride_lhs_scale,
+                           int32_t stride_rhs_scale, void* stream);
+
+/* Host-side check of a group-offset array (host memory, G+1 entries) against M_total; MX also
+ * checks 32-token alignment of group starts. Mirrors the invariants the reference generator
+ * asserts (reference bench.py:211,215-218). Returns GGEMM_OK, GGEMM_E_OFFSETS or
+ * GGEMM_E_MX_ALIGN. Touches no device. */
+int ggemm_vark_check_offsets(const int64_t* host_group_offs, int32_t G, int64_t M_total, int32_t mx);
+
+/* Number of compute units of `device` (the persistent grid size; reference launcher.cpp:78-81,
+ * bench.py:226-228). */
+int ggemm_vark_num_cus(int32_t device, int32_t* num_cus);
+
+/* Static human-readable text for a return code of this library (HIP codes included). */
+const char* ggemm_vark_strerror(int32_t code);
+
+/* GGEMM_VARK_ABI_VERSION of the loaded library. */
+int32_t ggemm_vark_abi_version(void);
+
+/* Launch geometry the library uses (and the drop-in code object expects): block threads,
+ * dynamic LDS bytes, output tile (OUT_M x OUT_N) and token stage. */
+void ggemm_vark_launch_geometry(int32_t* block_threads, int32_t* dynamic_lds, int32_t* tile_m,
+                                int32_t* tile_n, int32_t* k_step);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GGEMM_VARK_H */

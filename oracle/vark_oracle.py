@@ -1,0 +1,254 @@
+"""CPU oracle for the variable-K FP8 grouped weight-gradient GEMM.
+
+TEST INFRASTRUCTURE ONLY. This module is the checker: only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it, and never as the thing measured or shipped. The product path lives
+in the HIP library and fails loudly when that library is missing.
+
+What it restates
+----------------
+The reference kernel ``_grouped_variable_k_gemm_kernel`` (launch surface at
+reference launcher.cpp:16-33 and README.md:88-97; semantics "dW = x^T @ dy"
+at reference bench.py:182-193, oracle call shape at bench.py:262-269) computes,
+for every expert ``g``::
+
+    C[g] = s_lhs * s_rhs * LHS[offs[g]:offs[g+1], :]^T @ RHS[offs[g]:offs[g+1], :]
+
+with LHS float8 e4m3fn ``[M_total, OUT_M]``, RHS float8 e5m2
+``[M_total, OUT_N]``, fp32 accumulation and a bfloat16 output
+``[G, OUT_M, OUT_N]``. The arithmetic itself lives in third-party code that is
+not part of the reference tree (Primus-Turbo v26.2,
+``grouped_gemm_fp8_tensorwise_variable_k_triton_kernel``, imported at
+reference bench.py:241-246), so this file restates the published algorithm
+(fp32 dequantize, per-group matmul, round-to-nearest-even to bf16) as the
+build's CPU reference. The MXFP8 block-scaled variant has no reference
+counterpart; it follows the OCP MX definition (e8m0 shared exponent per
+32-element block along the token axis).
+
+Pinning (tests/test_oracle.py): fp8/e8m0/bf16 codecs against torch's
+independent implementations and textbook values; the GEMM against exact
+rational brute force on tiny ragged shapes; the launcher.cpp constant-fill
+closed form (C == 20.5); permutation / split / scale-linearity invariants;
+the reference input generator against the survey's recorded seed-42 lengths.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+E4M3_MAX = 448.0
+E5M2_MAX = 57344.0
+
+
+# --------------------------------------------------------------------------- codecs
+
+def _e4m3fn_table() -> np.ndarray:
+    """float8 e4m3fn byte -> float32 (OCP FP8: bias 7, no inf, S.1111.111 = NaN)."""
+    t = np.empty(256, dtype=np.float32)
+    for b in range(256):
+        s = -1.0 if b & 0x80 else 1.0
+        e = (b >> 3) & 0xF
+        m = b & 0x7
+        if e == 0xF and m == 0x7:
+            t[b] = np.nan
+        elif e == 0:
+            t[b] = s * (m / 8.0) * 2.0 ** -6
+        else:
+            t[b] = s * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+    return t
+
+
+def _e5m2_table() -> np.ndarray:
+    """float8 e5m2 byte -> float32 (IEEE-like: bias 15, e=31 is inf/NaN)."""
+    t = np.empty(256, dtype=np.float32)
+    for b in range(256):
+        s = -1.0 if b & 0x80 else 1.0
+        e = (b >> 2) & 0x1F
+        m = b & 0x3
+        if e == 0x1F:
+            t[b] = s * np.inf if m == 0 else np.nan
+        elif e == 0:
+            t[b] = s * (m / 4.0) * 2.0 ** -14
+        else:
+            t[b] = s * (1.0 + m / 4.0) * 2.0 ** (e - 15)
+    return t
+
+
+E4M3_TABLE = _e4m3fn_table()
+E5M2_TABLE = _e5m2_table()
+
+
+def decode_e4m3(b: np.ndarray) -> np.ndarray:
+    return E4M3_TABLE[np.asarray(b, dtype=np.uint8)]
+
+
+def decode_e5m2(b: np.ndarray) -> np.ndarray:
+    return E5M2_TABLE[np.asarray(b, dtype=np.uint8)]
+
+
+def decode_e8m0(b: np.ndarray) -> np.ndarray:
+    """OCP e8m0 shared exponent -> float32: 2**(b-127); 0xFF is NaN."""
+    b = np.asarray(b, dtype=np.uint8)
+    with np.errstate(over="ignore"):
+        out = np.ldexp(np.float32(1.0), b.astype(np.int32) - 127).astype(np.float32)
+    out[b == 0xFF] = np.nan
+    return out
+
+
+def bf16_bits_rne(x: np.ndarray) -> np.ndarray:
+    """float32 -> bfloat16 bit patterns (uint16), round to nearest even; NaN -> 0x7FC0."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    r = r.astype(np.uint16)
+    r[np.isnan(x)] = 0x7FC0
+    return r
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# --------------------------------------------------------------------------- GEMMs
+
+def _check_offs(group_offs: np.ndarray, m_total: int) -> np.ndarray:
+    offs = np.asarray(group_offs, dtype=np.int64)
+    if offs.ndim != 1 or offs.size < 1:
+        raise ValueError("group_offs must be 1-D with G+1 entries")
+    if offs[0] != 0 or np.any(np.diff(offs) < 0) or offs[-1] > m_total:
+        raise ValueError("group_offs must start at 0, be non-decreasing and end <= M_total")
+    return offs
+
+
+def vark_wgrad_tensorwise_f32(lhs: np.ndarray, rhs: np.ndarray, lhs_scale: float, rhs_scale: float,
+                              group_offs: np.ndarray, acc_dtype=np.float32) -> np.ndarray:
+    """Per-group ``(sL*LHS_g)^T @ (sR*RHS_g)`` before output rounding.
+
+    lhs: uint8 [M, OUT_M] holding e4m3fn bytes; rhs: uint8 [M, OUT_N] holding e5m2 bytes.
+    Dequantize in float32 (BASELINE CPU reference: "PyTorch fp32 dequantize + per-group
+    matmul"), contract in ``acc_dtype`` (float32 BLAS by default, float64 for tight checks).
+    Follows the semantics of reference bench.py:186-193 / 262-269.
+    """
+    lhs = np.asarray(lhs, dtype=np.uint8)
+    rhs = np.asarray(rhs, dtype=np.uint8)
+    offs = _check_offs(group_offs, lhs.shape[0])
+    G = offs.size - 1
+    out = np.zeros((G, lhs.shape[1], rhs.shape[1]), dtype=acc_dtype)
+    sl = np.float32(lhs_scale)
+    sr = np.float32(rhs_scale)
+    for g in range(G):
+        lo, hi = int(offs[g]), int(offs[g + 1])
+        if hi == lo:
+            continue
+        a = (decode_e4m3(lhs[lo:hi]) * sl).astype(acc_dtype)
+        b = (decode_e5m2(rhs[lo:hi]) * sr).astype(acc_dtype)
+        out[g] = a.T @ b
+    return out
+
+
+def vark_wgrad_tensorwise(lhs, rhs, lhs_scale, rhs_scale, group_offs) -> np.ndarray:
+    """bf16 bit patterns [G, OUT_M, OUT_N] (uint16) of the tensorwise grouped wgrad."""
+    return bf16_bits_rne(vark_wgrad_tensorwise_f32(lhs, rhs, lhs_scale, rhs_scale, group_offs))
+
+
+def vark_wgrad_mxfp8_f32(lhs: np.ndarray, rhs: np.ndarray, lhs_sc: np.ndarray, rhs_sc: np.ndarray,
+                         group_offs: np.ndarray, acc_dtype=np.float32) -> np.ndarray:
+    """MX block-scaled variant before rounding.
+
+    lhs_sc: uint8 e8m0 [ceil(M/32), OUT_M]; rhs_sc: uint8 e8m0 [ceil(M/32), OUT_N]; token block
+    ``k // 32`` scales rows ``32*(k//32) .. +31``. Every group must start on a multiple of 32 so a
+    block never straddles two experts (BASELINE config 5 pads groups to multiples of 32).
+    ``C[g] = sum_k (2^XL * L)[k,:]^T (2^XR * R)[k,:]`` over the group's tokens.
+    """
+    lhs = np.asarray(lhs, dtype=np.uint8)
+    rhs = np.asarray(rhs, dtype=np.uint8)
+    offs = _check_offs(group_offs, lhs.shape[0])
+    if np.any(offs[:-1] % 32):
+        raise ValueError("MX groups must start on 32-token block boundaries")
+    G = offs.size - 1
+    out = np.zeros((G, lhs.shape[1], rhs.shape[1]), dtype=acc_dtype)
+    for g in range(G):
+        lo, hi = int(offs[g]), int(offs[g + 1])
+        if hi == lo:
+            continue
+        blk = np.arange(lo, hi) // 32
+        a = (decode_e4m3(lhs[lo:hi]) * decode_e8m0(lhs_sc[blk])).astype(acc_dtype)
+        b = (decode_e5m2(rhs[lo:hi]) * decode_e8m0(rhs_sc[blk])).astype(acc_dtype)
+        out[g] = a.T @ b
+    return out
+
+
+def vark_wgrad_mxfp8(lhs, rhs, lhs_sc, rhs_sc, group_offs) -> np.ndarray:
+    return bf16_bits_rne(vark_wgrad_mxfp8_f32(lhs, rhs, lhs_sc, rhs_sc, group_offs))
+
+
+# --------------------------------------------------------------------------- brute force
+
+def vark_wgrad_bruteforce_exact(lhs, rhs, lhs_scale, rhs_scale, group_offs):
+    """Pure-Python exact rational triple loop (tiny shapes only).
+
+    Returns ``(value, abs_sum)`` nested lists ``[G][OUT_M][OUT_N]`` of Fractions: the exact
+    ``sL*sR*sum_k L[k,m] R[k,n]`` and the exact ``|sL*sR| * sum_k |L[k,m] R[k,n]|`` (the scale of
+    the rounding-error bound of any floating-point evaluation). Every fp8 value and the fp32
+    scales are dyadic rationals, so ``fractions.Fraction`` is exact.
+    """
+    from fractions import Fraction
+    lhs = np.asarray(lhs, dtype=np.uint8)
+    rhs = np.asarray(rhs, dtype=np.uint8)
+    offs = [int(v) for v in group_offs]
+    sl = Fraction(float(np.float32(lhs_scale)))
+    sr = Fraction(float(np.float32(rhs_scale)))
+    # non-finite codes have no rational value; inputs for this check must not use them
+    dl = [Fraction(float(v)) if np.isfinite(v) else None for v in E4M3_TABLE]
+    dr = [Fraction(float(v)) if np.isfinite(v) else None for v in E5M2_TABLE]
+    val, mag = [], []
+    for g in range(len(offs) - 1):
+        vb, mb = [], []
+        for m in range(lhs.shape[1]):
+            vr, mr = [], []
+            for n in range(rhs.shape[1]):
+                acc = Fraction(0)
+                aab = Fraction(0)
+                for k in range(offs[g], offs[g + 1]):
+                    t = dl[lhs[k, m]] * dr[rhs[k, n]]
+                    acc += t
+                    aab += abs(t)
+                vr.append(acc * sl * sr)
+                mr.append(aab * abs(sl * sr))
+            vb.append(vr)
+            mb.append(mr)
+        val.append(vb)
+        mag.append(mb)
+    return val, mag
+
+
+# --------------------------------------------------------------------------- comparison
+
+def compare(out_bits: np.ndarray, ref_bits: np.ndarray, group_offs=None) -> dict:
+    """Parity metrics used throughout the tests (bounds from the north-star statement).
+
+    cosine >= 0.99999; max relative error <= 2e-2 over |ref| > 1e-3 * max|ref|;
+    empty groups exactly zero (bit pattern 0x0000 or 0x8000).
+    """
+    a = bf16_bits_to_f32(out_bits).astype(np.float64).ravel()
+    b = bf16_bits_to_f32(ref_bits).astype(np.float64).ravel()
+    denom = np.linalg.norm(a) * np.linalg.norm(b)
+    cos = float(a @ b / denom) if denom > 0 else (1.0 if np.array_equal(a, b) else 0.0)
+    amax = np.abs(b).max() if b.size else 0.0
+    mask = np.abs(b) > 1e-3 * amax
+    rel = float(np.max(np.abs(a[mask] - b[mask]) / np.abs(b[mask]))) if mask.any() else 0.0
+    res = {"cos": cos, "max_rel": rel, "exact_frac": float(np.mean(a == b)) if a.size else 1.0,
+           "nonfinite": int(np.count_nonzero(~np.isfinite(a)))}
+    if group_offs is not None:
+        offs = np.asarray(group_offs, dtype=np.int64)
+        empty = [g for g in range(offs.size - 1) if offs[g + 1] == offs[g]]
+        bits = np.asarray(out_bits, dtype=np.uint16)
+        res["empty_groups"] = empty
+        res["empty_zero"] = bool(all(np.all((bits[g] & 0x7FFF) == 0) for g in empty))
+    return res
+
+
+def parity_ok(metrics: dict) -> bool:
+    ok = metrics["cos"] >= 0.99999 and metrics["max_rel"] <= 2e-2 and metrics["nonfinite"] == 0
+    if "empty_zero" in metrics:
+        ok = ok and metrics["empty_zero"]
+    return ok

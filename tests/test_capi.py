@@ -1,0 +1,158 @@
+"""CPU checks of the C-ABI library and the drop-in code object (no kernel launches).
+
+Argument validation runs before any HIP call, so invalid-argument paths are exercised here with
+fake (never dereferenced) pointers.
+"""
+import ctypes
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+import torch
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "ggemm_vark.h")
+
+
+def _header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w]+\s*\*?\s*(ggemm_vark_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_header_symbol(pkg):
+    lib = pkg.load_library()
+    names = _header_functions()
+    assert len(names) >= 8
+    for n in names:
+        assert hasattr(lib, n), n
+    from ggemm_asm_amd import _lib
+    assert set(names) == set(_lib.EXPORTS)
+
+
+def test_abi_version_and_geometry(pkg):
+    lib = pkg.load_library()
+    ver = int(re.search(r"#define GGEMM_VARK_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
+    assert lib.ggemm_vark_abi_version() == ver
+    assert pkg.launch_geometry() == {"block_threads": 512, "dynamic_lds": 65536, "tile_m": 192,
+                                     "tile_n": 320, "k_step": 128}
+
+
+def _offs(vals):
+    a = (ctypes.c_int64 * len(vals))(*vals)
+    return a
+
+
+@pytest.mark.parametrize("vals,M,mx,rc", [
+    ([0, 96, 256, 256, 512], 512, 0, 0),
+    ([0, 96, 256, 256, 512], 511, 0, -5),     # past M_total
+    ([1, 96, 256], 512, 0, -5),               # not 0-based
+    ([0, 96, 90, 512], 512, 0, -5),           # decreasing
+    ([0, 64, 64, 160, 205], 205, 1, 0),       # MX: starts aligned, ragged last group allowed
+    ([0, 96, 100, 512], 512, 1, -7),          # MX: group 2 starts at 100
+])
+def test_check_offsets(pkg, vals, M, mx, rc):
+    lib = pkg.load_library()
+    assert lib.ggemm_vark_check_offsets(_offs(vals), len(vals) - 1, M, mx) == rc
+
+
+def test_strerror(pkg):
+    lib = pkg.load_library()
+    for code in range(-7, 1):
+        s = lib.ggemm_vark_strerror(code).decode()
+        assert s and s != "unknown error"
+
+
+FAKE = 0x100000  # 16-byte aligned, never dereferenced: validation fails before any HIP call
+
+
+def _call(lib, **kw):
+    a = dict(lhs=FAKE, rhs=FAKE, out=FAKE, ls=FAKE, rs=FAKE, offs=FAKE, G=32, OUT_M=2880, OUT_N=5760,
+             slm=2880, srm=5760, scg=2880 * 5760, scm=5760, scn=1)
+    a.update(kw)
+    return lib.ggemm_vark_wgrad_fp8(a["lhs"], a["rhs"], a["out"], a["ls"], a["rs"], a["offs"], a["G"], a["OUT_M"],
+                                    a["OUT_N"], a["slm"], a["srm"], a["scg"], a["scm"], a["scn"], None)
+
+
+@pytest.mark.parametrize("kw,rc", [
+    (dict(lhs=0), -1), (dict(offs=0), -1), (dict(G=0), -2), (dict(OUT_M=100, slm=100), -2),
+    (dict(OUT_N=-16), -2), (dict(scn=2), -3), (dict(slm=2800), -3), (dict(srm=5768), -3),
+    (dict(scm=5762), -3), (dict(scg=100), -3), (dict(lhs=FAKE + 8), -4), (dict(out=FAKE + 2), -4),
+])
+def test_validation_rejects(pkg, kw, rc):
+    assert _call(pkg.load_library(), **kw) == rc
+
+
+def test_mx_validation_rejects(pkg):
+    lib = pkg.load_library()
+    args = [FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 64, 128, 64, 128, 64 * 128, 128, 1]
+    assert lib.ggemm_vark_wgrad_mxfp8(*args, 60, 128, None) == -3      # scale stride < OUT_M
+    assert lib.ggemm_vark_wgrad_mxfp8(*args[:3], FAKE + 4, *args[4:], 64, 128, None) == -4
+
+
+def test_python_op_refuses_cpu_tensors(pkg):
+    lhs = torch.zeros(64, 64, dtype=torch.uint8)
+    rhs = torch.zeros(64, 128, dtype=torch.uint8)
+    s = torch.tensor(1.0)
+    offs = torch.tensor([0, 64], dtype=torch.int64)
+    with pytest.raises(ValueError, match="gfx950 GPU only"):
+        pkg.grouped_gemm_fp8_tensorwise_variable_k(lhs, rhs, s, s, offs)
+
+
+def test_torch_op_meta_shape(pkg):
+    lhs = torch.empty(512, 64, dtype=torch.uint8, device="meta")
+    rhs = torch.empty(512, 128, dtype=torch.uint8, device="meta")
+    s = torch.empty((), dtype=torch.float32, device="meta")
+    offs = torch.empty(5, dtype=torch.int64, device="meta")
+    out = torch.ops.ggemm.variable_k_wgrad_fp8(lhs, rhs, s, s, offs)
+    assert out.shape == (4, 64, 128) and out.dtype == torch.bfloat16
+
+
+# ----------------------------------------------------------------------------- code object
+
+def _readelf():
+    for c in ("/opt/rocm/llvm/bin/llvm-readelf", shutil.which("llvm-readelf")):
+        if c and os.path.exists(c):
+            return c
+    pytest.skip("llvm-readelf not available")
+
+
+def test_code_object_symbol_and_kernarg_layout(pkg):
+    from ggemm_asm_amd import harness
+    data = open(pkg.CODE_OBJECT_PATH, "rb").read()
+    assert data[:4] == b"\x7fELF"
+    assert set(harness.elf_global_functions(data)) == {"_grouped_variable_k_gemm_kernel"}
+    assert harness.detect_kernel_name(data) == "_grouped_variable_k_gemm_kernel"
+    notes = subprocess.run([_readelf(), "--notes", pkg.CODE_OBJECT_PATH], capture_output=True, text=True,
+                           timeout=30).stdout
+    assert re.search(r"\.kernarg_segment_size:\s+96\b", notes)
+    assert re.search(r"\.max_flat_workgroup_size:\s+512\b", notes)
+    offs = [int(x) for x in re.findall(r"\.offset:\s+(\d+)", notes)]
+    sizes = [int(x) for x in re.findall(r"\.size:\s+(\d+)", notes)]
+    kinds = re.findall(r"\.value_kind:\s+(\w+)", notes)
+    # reference launcher.cpp:16-33: 6 pointers, 8 int32 at 48..76, 2 pointers at 80/88
+    assert offs == [0, 8, 16, 24, 32, 40, 48, 52, 56, 60, 64, 68, 72, 76, 80, 88]
+    assert sizes == [8] * 6 + [4] * 8 + [8, 8]
+    assert kinds == ["global_buffer"] * 6 + ["by_value"] * 8 + ["global_buffer"] * 2
+    lds = int(re.search(r"\.group_segment_fixed_size:\s+(\d+)", notes).group(1))
+    assert lds + 65536 <= 160 * 1024   # static LDS + the launch's 64 KiB dynamic fit gfx950's 160 KiB
+
+
+def test_m0_only_feeds_lds_dma(pkg):
+    """The LDS-DMA loads set m0 from inline asm; nothing else in the kernels may use m0."""
+    objdump = "/opt/rocm/llvm/bin/llvm-objdump"
+    if not os.path.exists(objdump):
+        pytest.skip("llvm-objdump not available")
+    txt = subprocess.run([objdump, "-d", "--mcpu=gfx950", pkg.CODE_OBJECT_PATH], capture_output=True,
+                         text=True, timeout=60).stdout
+    ins = [l.split("//")[0].strip() for l in txt.splitlines() if l.startswith("\t") or l.startswith("  ")]
+    ins = [i for i in ins if i]
+    n_dma = 0
+    for k, i in enumerate(ins):
+        if re.search(r"\bm0\b", i):
+            assert i.startswith("s_mov_b32 m0,"), i
+            assert ins[k + 1].startswith("buffer_load_dwordx4") and ins[k + 1].rstrip().endswith("lds"), ins[k + 1]
+            n_dma += 1
+    assert n_dma >= 8
