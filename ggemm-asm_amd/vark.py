@@ -59,6 +59,14 @@ def _validate_offsets(group_offs, M_total, mx):
     _lib.check(rc, "ggemm_vark_check_offsets")
 
 
+def _nonempty(t: torch.Tensor) -> torch.Tensor:
+    """A zero-token operand has a null data pointer; the kernel reads no row of it (every group is
+    empty), so hand the library a one-row placeholder with the same width instead."""
+    if t.shape[0] > 0:
+        return t
+    return torch.zeros((1, t.shape[1]), dtype=t.dtype, device=t.device)
+
+
 def _stream(dev) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
@@ -83,6 +91,7 @@ def grouped_gemm_fp8_tensorwise_variable_k(lhs: torch.Tensor, rhs: torch.Tensor,
     out = _check_out(out, G, OUT_M, OUT_N, lhs.device)
     if validate:
         _validate_offsets(group_offs, M_total, mx=False)
+    lhs, rhs = _nonempty(lhs), _nonempty(rhs)
     lib = _lib.load()
     fn = {"k128": lib.ggemm_vark_wgrad_fp8, "k32": lib.ggemm_vark_wgrad_fp8_k32}[mfma]
     with torch.cuda.device(lhs.device):
@@ -114,6 +123,8 @@ def grouped_gemm_mxfp8_variable_k(lhs: torch.Tensor, rhs: torch.Tensor, lhs_scal
     out = _check_out(out, G, OUT_M, OUT_N, lhs.device)
     if validate:
         _validate_offsets(group_offs, M_total, mx=True)
+    lhs, rhs = _nonempty(lhs), _nonempty(rhs)
+    lhs_scale, rhs_scale = _nonempty(lhs_scale), _nonempty(rhs_scale)
     lib = _lib.load()
     with torch.cuda.device(lhs.device):
         rc = lib.ggemm_vark_wgrad_mxfp8(
