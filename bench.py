@@ -38,7 +38,21 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU work for the cpu_baseline sample (0 disables)")
     ap.add_argument("--extra", action="store_true", help="also time the other configs (not part of the line)")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="only run a plain device-to-device copy of this many MiB (steps times): the "
+                         "known-size reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     return ap.parse_args()
+
+
+def copy_calibration(mib, steps):
+    import torch
+    src = torch.empty(mib << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_per_launch": mib << 20, "launches": steps}), flush=True)
 
 
 def read_traffic():
@@ -118,6 +132,9 @@ def main():
         print(f"bench.py measures one GPU only: the grouped wgrad needs no collective and this build runs "
               f"on a single MI355X (asked for --gpus {args.gpus}).", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration_mb:
+        copy_calibration(args.copy_calibration_mb, args.steps)
+        return
     import torch
     from __graft_entry__ import load_package
     pkg = load_package()

@@ -12,19 +12,22 @@
 //    shapes have no ragged tiles. 8 waves in a 2 x 4 grid, 96 x 80 per wave (6 x 5 MFMA blocks).
 //  * The token (K) axis is walked in stages of 128 tokens. A stage holds 128 x 192 LHS bytes and
 //    128 x 320 RHS bytes = 64 KiB; two stages (one in the launch's 64 KiB dynamic LDS, one static)
-//    double-buffer the global -> LDS traffic.
-//  * Global -> LDS uses buffer loads that write LDS directly (16 B per lane). The buffer resource
-//    is rebased at the stage's first token with num_records = valid rows * row stride, so tokens
-//    past the group end read as zero: ragged K tails and tiny groups need no other masking.
-//  * LDS layout per operand: [64-byte panel][128 tokens][4 x 16-byte chunks], the chunk index
-//    XOR-swizzled with (token >> 2) & 3, so the transposed reads below are bank-conflict free.
+//    double-buffer the global -> LDS traffic with one workgroup barrier per stage.
+//  * Global -> LDS uses buffer loads that write LDS directly (16 B per lane). Each such load
+//    covers consecutive token rows of the tile (3.2 rows of 320 B or 5.3 rows of 192 B), so a
+//    wave-instruction touches few cache lines. The buffer resource is rebased at the stage's
+//    first token and the tile's first column with num_records ending at the last valid token,
+//    so tokens past the group end read as zero: ragged K tails and tiny groups need no masking.
+//  * LDS layout per operand: row-major [token][W] with the 16-byte chunk index XOR-swizzled by
+//    (token >> 2) & 3, so the transposed reads below are bank-conflict free.
 //  * MFMA operands come from ds_read_b64_tr_b8: one read gives each lane 8 consecutive tokens of
 //    one column. The MFMA is v_mfma_scale_f32_16x16x128_f8f6f4 (e8m0 scale 127 == 1.0 for the
 //    per-tensor path, real block scales for MXFP8); the A operand is the RHS tile (rows of the
 //    16x16 result are OUT_N columns) so each lane ends with 4 consecutive bf16 of one C row.
 //  * Static persistent schedule (no workspace exists in the launch contract): groups are visited
 //    in descending token count, tiles within a group with the M-tile fastest, and workgroup ids
-//    are remapped so the 32 CUs of one XCD work on 32 consecutive tiles (shared L2 panels).
+//    are remapped so the 32 CUs of one XCD work on 32 consecutive tiles (shared L2 panels). The
+//    first stage of a workgroup's next tile is loaded while it finishes the current one.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -44,11 +47,12 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kTileM = 192;
 constexpr int kTileN = 320;
 constexpr int kKStep = 128;
-constexpr int kPanel = 64;                                  // bytes per LDS panel row
-constexpr int kPanelsM = kTileM / kPanel;                   // 3
-constexpr int kPanelsN = kTileN / kPanel;                   // 5
-constexpr int kPanelBytes = kKStep * kPanel;                // 8192
-constexpr int kStageBytes = (kPanelsM + kPanelsN) * kPanelBytes;  // 65536
+constexpr int kLhsBytes = kKStep * kTileM;                  // 24 KiB of LHS per stage
+constexpr int kRhsBytes = kKStep * kTileN;                  // 40 KiB of RHS per stage
+constexpr int kStageBytes = kLhsBytes + kRhsBytes;          // 64 KiB
+constexpr int kDmaPerStage = kStageBytes / 1024;            // 1 KiB per wave-instruction
+constexpr int kDmaPerWave = kDmaPerStage / kWaves;          // 8
+constexpr int kDmaLhs = kLhsBytes / 1024;                   // first 24 instructions carry LHS
 constexpr int kWaveM = 96;
 constexpr int kWaveN = 80;
 constexpr int kMB = kWaveM / 16;                            // 6 MFMA blocks along OUT_M
@@ -59,7 +63,8 @@ constexpr int kMxScaleStage = 4 * kTileM + 4 * kTileN;      // 2048 B of e8m0 pe
 constexpr uint32_t kRsrcWord3 = 0x00020000u;                // raw buffer, 32-bit data format
 
 static_assert(kStageBytes == kDynLdsBytes, "one stage must fill the dynamic LDS window");
-static_assert((kPanelsM + kPanelsN) * (kKStep / 16) == 8 * kWaves, "8 LDS-DMA loads per wave per stage");
+static_assert(kDmaPerWave * kWaves == kDmaPerStage && kDmaLhs % kWaves == 0, "uniform LDS-DMA split");
+static_assert(kTileM % 64 == 0 && kTileN % 64 == 0, "rows are whole groups of four 16-byte chunks");
 
 // ----------------------------------------------------------------------------------- helpers
 
@@ -73,8 +78,8 @@ __device__ __forceinline__ const hsa_kernel_dispatch_packet_t* dispatch_packet()
   return (const hsa_kernel_dispatch_packet_t*)__builtin_amdgcn_dispatch_ptr();
 }
 
-// Wait until at most N vector-memory loads of this wave are outstanding (gfx9 s_waitcnt layout:
-// vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14, expcnt bits 6:4, lgkmcnt bits 11:8).
+// Wait until at most N vector-memory operations of this wave are outstanding (gfx9 s_waitcnt
+// layout: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14, expcnt bits 6:4, lgkmcnt bits 11:8).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -82,15 +87,13 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // Workgroup barrier that orders this wave's LDS traffic but does not drain outstanding global
-// loads (the next stage's prefetch stays in flight across it).
+// loads (a prefetch issued before it stays in flight).
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Byte offset of (panel, token row, logical 16-byte chunk) inside a stage.
-__device__ __forceinline__ int lds_off(int panel, int row, int chunk) {
-  return panel * kPanelBytes + row * kPanel + 16 * (chunk ^ ((row >> 2) & 3));
-}
+// 16-byte chunk swizzle of an LDS row: chunk c of token t sits at chunk c ^ ((t >> 2) & 3).
+__device__ __forceinline__ int swizzle(int token) { return (token >> 2) & 3; }
 
 // ----------------------------------------------------------------------------------- loads
 
@@ -120,33 +123,52 @@ __device__ __forceinline__ uint32_t lds_u32(const GG_LDS void* p) {
   return (uint32_t)reinterpret_cast<uintptr_t>(p);
 }
 
-// Issue this wave's 8 LDS-DMA loads for one stage: wave w moves token rows [16w, 16w+16) of every
-// panel. Lane l covers row 16w + l/4, physical chunk l%4, i.e. logical chunk (l%4) ^ swizzle(row);
-// the 64 lanes write 1 KiB of LDS contiguously, the layout lds_off() describes.
-__device__ __forceinline__ void issue_stage(GG_LDS uint8_t* stage, const uint8_t* lhs, const uint8_t* rhs,
-                                            int64_t row0, int rows_valid, int stride_l, int stride_r,
-                                            int m0, int n0, int wave, int lane) {
-  const v4i rl = make_rsrc(lhs + row0 * (int64_t)stride_l, rows_valid * stride_l);
-  const v4i rr = make_rsrc(rhs + row0 * (int64_t)stride_r, rows_valid * stride_r);
-  const int row = wave * 16 + (lane >> 2);
-  const int chunk = (lane & 3) ^ ((row >> 2) & 3);
-  const int voff_l = row * stride_l + m0 + chunk * 16;
-  const int voff_r = row * stride_r + n0 + chunk * 16;
-  const uint32_t dst = lds_u32(stage) + wave * 16 * kPanel;
+// Stage loads: 64 wave-instructions of 1 KiB fill the stage LDS linearly (instructions 0-23 the
+// LHS rows of 192 B, 24-63 the RHS rows of 320 B). Wave w issues instructions w, w+8, ..., w+56.
+// Lane l of instruction i writes physical chunk q = 64*i' + l of its operand (i' = index within
+// the operand), i.e. token row q / W16 and physical chunk q % W16 (W16 = 12 or 20 chunks per row),
+// which holds logical chunk (q % W16) ^ swizzle(row). Per-lane byte offsets relative to the
+// stage's (first token, first column) do not depend on the tile or the step: computed once.
+struct DmaPlan {
+  int voff[kDmaPerWave];
+};
+
+__device__ __forceinline__ DmaPlan make_dma_plan(int wave, int lane, int stride_l, int stride_r) {
+  DmaPlan d;
 #pragma unroll
-  for (int p = 0; p < kPanelsM + kPanelsN; ++p) {
-    if (p < kPanelsM)
-      dma16(rl, dst + p * kPanelBytes, voff_l + p * kPanel);
-    else
-      dma16(rr, dst + p * kPanelBytes, voff_r + (p - kPanelsM) * kPanel);
+  for (int j = 0; j < kDmaPerWave; ++j) {
+    const int i = wave + kWaves * j;
+    if (j < kDmaLhs / kWaves) {
+      const int q = 64 * i + lane, w16 = kTileM / 16;
+      const int row = q / w16, pc = q - row * w16;
+      d.voff[j] = row * stride_l + 16 * (pc ^ swizzle(row));
+    } else {
+      const int q = 64 * (i - kDmaLhs) + lane, w16 = kTileN / 16;
+      const int row = q / w16, pc = q - row * w16;
+      d.voff[j] = row * stride_r + 16 * (pc ^ swizzle(row));
+    }
   }
+  return d;
+}
+
+// Issue this wave's loads of one stage: tokens [row0, row0 + rows_valid) of the group (the rest of
+// the 128-token stage reads as zero), columns [m0, m0 + 192) of LHS and [n0, n0 + 320) of RHS.
+// num_records ends exactly at the last valid token's row end, so no load reaches past it.
+__device__ __forceinline__ void issue_stage(uint32_t stage, const uint8_t* lhs, const uint8_t* rhs, int64_t row0,
+                                            int rows_valid, int stride_l, int stride_r, int m0, int n0,
+                                            const DmaPlan& plan, int wave) {
+  const v4i rl = make_rsrc(lhs + row0 * (int64_t)stride_l + m0, rows_valid * stride_l - m0);
+  const v4i rr = make_rsrc(rhs + row0 * (int64_t)stride_r + n0, rows_valid * stride_r - n0);
+#pragma unroll
+  for (int j = 0; j < kDmaPerWave; ++j)
+    dma16(j < kDmaLhs / kWaves ? rl : rr, stage + (wave + kWaves * j) * 1024, plan.voff[j]);
 }
 
 // MXFP8: one LDS-DMA load per wave per stage brings the stage's e8m0 rows into LDS.
 // Chunk c of the 128 x 16 B list: c < 48 -> LHS block c/12, columns m0 + 16*(c%12);
 // otherwise RHS block (c-48)/20, columns n0 + 16*((c-48)%20). Waves 0-2 carry LHS, 3-7 RHS,
 // 16 active lanes each. Blocks past the group end read as 0 (scale 2^-127 on zero data).
-__device__ __forceinline__ void issue_stage_scales(GG_LDS uint8_t* sstage, const uint8_t* lsc, const uint8_t* rsc,
+__device__ __forceinline__ void issue_stage_scales(uint32_t sstage, const uint8_t* lsc, const uint8_t* rsc,
                                                    int64_t blk0, int blocks_valid, int stride_ls, int stride_rs,
                                                    int m0, int n0, int wave, int lane) {
   const bool is_l = wave < 3;
@@ -156,23 +178,25 @@ __device__ __forceinline__ void issue_stage_scales(GG_LDS uint8_t* sstage, const
   const int c = wave * 16 + (lane & 15);
   const int voff = is_l ? (c / 12) * stride + m0 + 16 * (c % 12) : ((c - 48) / 20) * stride + n0 + 16 * ((c - 48) % 20);
   // only lanes 0-15 are active: they write 256 bytes at sstage + 256 * wave + 16 * lane
-  if (lane < 16) dma16(r, lds_u32(sstage) + wave * 256, voff);
+  if (lane < 16) dma16(r, sstage + wave * 256, voff);
 }
 
 // ----------------------------------------------------------------------------------- compute
 
-// Transposed reads of one 16-column operand block for one stage. Lane l (group q = l/16,
-// s = l%16) reads row rbase + {0,16,64,80} where rbase = 32*(q>>1) + 8*(q&1) + s/2, columns
-// 8*(s&1)..+7 of the block; the hardware returns to lane l the 8 tokens of column l%16. The four
-// reads fill bytes 0-7, 8-15, 16-23, 24-31 of the 16x16x128 operand: lane groups 0,1 x bytes
-// 0-15 hold tokens 0-31 (e8m0 block 0), groups 2,3 x bytes 0-15 tokens 32-63 (block 1),
-// groups 0,1 x bytes 16-31 tokens 64-95 (block 2), groups 2,3 x bytes 16-31 tokens 96-127
-// (block 3) -- the pairing the scaled MFMA expects for lane-group-q scale registers.
+// Transposed reads of one 16-column operand block for one stage (row pitch kRow bytes). Lane l
+// (group q = l/16, s = l%16) reads token rbase + {0,16,64,80} where rbase = 32*(q>>1) + 8*(q&1)
+// + s/2, columns 8*(s&1)..+7 of the block; the hardware returns to lane l the 8 tokens of column
+// l%16. The four reads fill bytes 0-7, 8-15, 16-23, 24-31 of the 16x16x128 operand: lane groups
+// 0,1 x bytes 0-15 hold tokens 0-31 (e8m0 block 0), groups 2,3 x bytes 0-15 tokens 32-63
+// (block 1), groups 0,1 x bytes 16-31 tokens 64-95 (block 2), groups 2,3 x bytes 16-31 tokens
+// 96-127 (block 3) -- the pairing the scaled MFMA expects for lane-group-q scale registers.
+// Tokens rbase + 16k share rbase's swizzle, so one address plus immediates covers all four.
+template <int kRow>
 __device__ __forceinline__ v8i read_operand(const GG_LDS uint8_t* p) {
   v2i r0 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((GG_LDS v2i*)(p));
-  v2i r1 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((GG_LDS v2i*)(p + 16 * kPanel));
-  v2i r2 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((GG_LDS v2i*)(p + 64 * kPanel));
-  v2i r3 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((GG_LDS v2i*)(p + 80 * kPanel));
+  v2i r1 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((GG_LDS v2i*)(p + 16 * kRow));
+  v2i r2 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((GG_LDS v2i*)(p + 64 * kRow));
+  v2i r3 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((GG_LDS v2i*)(p + 80 * kRow));
   return v8i{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
 }
 
@@ -193,6 +217,20 @@ __device__ __forceinline__ v4f mfma(const v8i& a_rhs, const v8i& b_lhs, v4f acc,
   }
 }
 
+// Instruction order of one stage's compute: all n-side reads plus m-blocks 0 and 1 first, then
+// for each m-block its five MFMAs followed by the reads of m-block i+2 into the registers block i
+// just released -- LDS latency of every m-block hides behind the previous block's MFMAs.
+template <int kFirstReads, int kMfmaPerCall>
+__device__ __forceinline__ void pin_stage_schedule() {
+  __builtin_amdgcn_sched_group_barrier(0x100, kFirstReads, 0);
+#pragma unroll
+  for (int i = 0; i < kMB - 2; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, kNB * kMfmaPerCall, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 2 * kNB * kMfmaPerCall, 0);
+}
+
 // ----------------------------------------------------------------------------------- kernel body
 
 struct VarKArgs {
@@ -206,6 +244,11 @@ struct VarKArgs {
   int stride_lhs_m, stride_rhs_m;
   int stride_cg, stride_cm, stride_cn;
   int stride_lhs_scale, stride_rhs_scale;  // MX only
+};
+
+struct Tile {
+  int g, m0, n0, nsteps;
+  int64_t kb, klen;
 };
 
 template <bool kMX, bool kLegacyK32>
@@ -256,6 +299,21 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
   const int pid = blockIdx.x;
   const int vpid = (num_wg % 8 == 0) ? (pid % 8) * (num_wg / 8) + pid / 8 : pid;
 
+  auto tile_at = [&](int64_t t) {
+    Tile T;
+    const int slot = (int)(t / tiles_per_group);
+    const int in_g = (int)(t - (int64_t)slot * tiles_per_group);
+    T.g = sorted ? s_order[slot] : slot;
+    const int tn = in_g / n_tm;
+    T.m0 = (in_g - tn * n_tm) * kTileM;
+    T.n0 = tn * kTileN;
+    T.kb = a.group_offs[T.g];
+    const int64_t ke = a.group_offs[T.g + 1];
+    T.klen = ke > T.kb ? ke - T.kb : 0;
+    T.nsteps = (int)((T.klen + kKStep - 1) / kKStep);
+    return T;
+  };
+
   float alpha = 1.0f;
   if constexpr (!kMX) alpha = *(const float*)a.lhs_scale * *(const float*)a.rhs_scale;
 
@@ -264,37 +322,44 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
   const int q = lane >> 4;
   const int s16 = lane & 15;
   const int rbase = 32 * (q >> 1) + 8 * (q & 1) + (s16 >> 1);
-  const int swz = (rbase >> 2) & 3;
+  const int swz = swizzle(rbase);
   const int colb = 8 * (s16 & 1);
 
   // per-lane LDS byte offsets (stage-relative) of each operand block's first transposed read
   int off_m[kMB], off_n[kNB];
 #pragma unroll
-  for (int i = 0; i < kMB; ++i) {
-    const int c0 = wm * kWaveM + i * 16;
-    off_m[i] = (c0 >> 6) * kPanelBytes + rbase * kPanel + 16 * (((c0 & 63) >> 4) ^ swz) + colb;
-  }
+  for (int i = 0; i < kMB; ++i) off_m[i] = rbase * kTileM + 16 * (((wm * kWaveM + i * 16) >> 4) ^ swz) + colb;
 #pragma unroll
-  for (int i = 0; i < kNB; ++i) {
-    const int c0 = wn * kWaveN + i * 16;
-    off_n[i] = (kPanelsM + (c0 >> 6)) * kPanelBytes + rbase * kPanel + 16 * (((c0 & 63) >> 4) ^ swz) + colb;
-  }
+  for (int j = 0; j < kNB; ++j)
+    off_n[j] = kLhsBytes + rbase * kTileN + 16 * (((wn * kWaveN + j * 16) >> 4) ^ swz) + colb;
 
-  GG_LDS uint8_t* stage1 = (GG_LDS uint8_t*)stage1_mem;
+  const DmaPlan plan = make_dma_plan(wave, lane, a.stride_lhs_m, a.stride_rhs_m);
+  const uint32_t slot_base[2] = {lds_u32(stage0), lds_u32((GG_LDS uint8_t*)stage1_mem)};
+  GG_LDS uint8_t* const slot_ptr[2] = {stage0, (GG_LDS uint8_t*)stage1_mem};
   GG_LDS uint8_t* scales = (GG_LDS uint8_t*)s_scales;
 
-  for (int64_t t = vpid; t < total; t += num_wg) {
-    const int slot = (int)(t / tiles_per_group);
-    const int in_g = (int)(t - (int64_t)slot * tiles_per_group);
-    const int g = sorted ? s_order[slot] : slot;
-    const int tn = in_g / n_tm;
-    const int tm = in_g - tn * n_tm;
-    const int m0 = tm * kTileM;
-    const int n0 = tn * kTileN;
-    const int64_t kb = a.group_offs[g];
-    const int64_t ke = a.group_offs[g + 1];
-    const int64_t klen = ke > kb ? ke - kb : 0;
-    const int nsteps = (int)((klen + kKStep - 1) / kKStep);
+  auto issue = [&](const Tile& T, int step, int slot) {
+    const int64_t k0 = (int64_t)step * kKStep;
+    const int64_t rem = T.klen - k0;
+    const int rv = (int)(rem < kKStep ? rem : kKStep);
+    issue_stage(slot_base[slot], a.lhs, a.rhs, T.kb + k0, rv, a.stride_lhs_m, a.stride_rhs_m, T.m0, T.n0, plan,
+                wave);
+    if constexpr (kMX)
+      issue_stage_scales(lds_u32(scales + slot * kMxScaleStage), (const uint8_t*)a.lhs_scale,
+                         (const uint8_t*)a.rhs_scale, (T.kb + k0) / 32, (rv + 31) / 32, a.stride_lhs_scale,
+                         a.stride_rhs_scale, T.m0, T.n0, wave, lane);
+  };
+
+  int cur = 0;              // LDS slot holding the next stage to compute
+  bool prefetched = false;  // stage 0 of tile t was issued during the previous tile
+  int64_t t = vpid;
+  Tile T;
+  if (t < total) T = tile_at(t);
+  while (t < total) {
+    const int64_t t_next = t + num_wg;
+    const bool has_next = t_next < total;
+    Tile N;
+    if (has_next) N = tile_at(t_next);
 
     v4f acc[kMB][kNB];
 #pragma unroll
@@ -302,74 +367,60 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
 #pragma unroll
       for (int j = 0; j < kNB; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    if (nsteps > 0) {
-      {
-        const int rv = (int)(klen < kKStep ? klen : kKStep);
-        issue_stage(stage0, a.lhs, a.rhs, kb, rv, a.stride_lhs_m, a.stride_rhs_m, m0, n0, wave, lane);
-        if constexpr (kMX)
-          issue_stage_scales(scales, (const uint8_t*)a.lhs_scale, (const uint8_t*)a.rhs_scale, kb / 32,
-                             (rv + 31) / 32, a.stride_lhs_scale, a.stride_rhs_scale, m0, n0, wave, lane);
+    if (T.nsteps > 0 && !prefetched) issue(T, 0, cur);
+    prefetched = false;
+    for (int s = 0; s < T.nsteps; ++s) {
+      // Stage s landed for this wave; after the barrier it has for all waves, and every wave is
+      // done computing stage s-1, so its slot may take the next prefetch.
+      wait_vmcnt<0>();
+      lds_barrier();
+      if (s + 1 < T.nsteps) {
+        issue(T, s + 1, cur ^ 1);
+      } else if (has_next && N.nsteps > 0) {
+        issue(N, 0, cur ^ 1);
+        prefetched = true;
       }
-      for (int s = 0; s < nsteps; ++s) {
-        GG_LDS uint8_t* cur = (s & 1) ? stage1 : stage0;
-        if (s + 1 < nsteps) {
-          const int64_t k0 = (int64_t)(s + 1) * kKStep;
-          const int64_t rem = klen - k0;
-          const int rv = (int)(rem < kKStep ? rem : kKStep);
-          GG_LDS uint8_t* nxt = (s & 1) ? stage0 : stage1;
-          issue_stage(nxt, a.lhs, a.rhs, kb + k0, rv, a.stride_lhs_m, a.stride_rhs_m, m0, n0, wave, lane);
-          if constexpr (kMX) {
-            issue_stage_scales(scales + ((s + 1) & 1) * kMxScaleStage, (const uint8_t*)a.lhs_scale,
-                               (const uint8_t*)a.rhs_scale, (kb + k0) / 32, (rv + 31) / 32,
-                               a.stride_lhs_scale, a.stride_rhs_scale, m0, n0, wave, lane);
-            wait_vmcnt<9>();
-          } else {
-            wait_vmcnt<8>();
-          }
-        } else {
-          wait_vmcnt<0>();
-        }
-        lds_barrier();
 
-        int sc_n[kNB], sc_m[kMB];
+      const GG_LDS uint8_t* st = slot_ptr[cur];
+      int sc_n[kNB], sc_m[kMB];
 #pragma unroll
-        for (int j = 0; j < kNB; ++j) sc_n[j] = 127;
+      for (int j = 0; j < kNB; ++j) sc_n[j] = 127;
 #pragma unroll
-        for (int i = 0; i < kMB; ++i) sc_m[i] = 127;
-        if constexpr (kMX) {
-          const GG_LDS uint8_t* ss = scales + (s & 1) * kMxScaleStage;
+      for (int i = 0; i < kMB; ++i) sc_m[i] = 127;
+      if constexpr (kMX) {
+        const GG_LDS uint8_t* ss = scales + cur * kMxScaleStage;
 #pragma unroll
-          for (int j = 0; j < kNB; ++j) sc_n[j] = ss[4 * kTileM + q * kTileN + wn * kWaveN + j * 16 + s16];
+        for (int j = 0; j < kNB; ++j) sc_n[j] = ss[4 * kTileM + q * kTileN + wn * kWaveN + j * 16 + s16];
 #pragma unroll
-          for (int i = 0; i < kMB; ++i) sc_m[i] = ss[q * kTileM + wm * kWaveM + i * 16 + s16];
-        }
-
-        v8i bn[kNB];
-#pragma unroll
-        for (int j = 0; j < kNB; ++j) bn[j] = read_operand(cur + off_n[j]);
-        // m-side operands double-buffered: block i+1 is read while block i feeds the MFMAs
-        v8i am[2];
-        am[0] = read_operand(cur + off_m[0]);
-#pragma unroll
-        for (int i = 0; i < kMB; ++i) {
-          if (i + 1 < kMB) am[(i + 1) & 1] = read_operand(cur + off_m[i + 1]);
-#pragma unroll
-          for (int j = 0; j < kNB; ++j) acc[i][j] = mfma<kLegacyK32>(bn[j], am[i & 1], acc[i][j], sc_n[j], sc_m[i]);
-        }
-        lds_barrier();
+        for (int i = 0; i < kMB; ++i) sc_m[i] = ss[q * kTileM + wm * kWaveM + i * 16 + s16];
       }
+
+      v8i bn[kNB], am[2];
+      bn[0] = read_operand<kTileN>(st + off_n[0]);
+      am[0] = read_operand<kTileM>(st + off_m[0]);
+#pragma unroll
+      for (int j = 1; j < kNB; ++j) bn[j] = read_operand<kTileN>(st + off_n[j]);
+      am[1] = read_operand<kTileM>(st + off_m[1]);
+#pragma unroll
+      for (int i = 0; i < kMB; ++i) {
+#pragma unroll
+        for (int j = 0; j < kNB; ++j) acc[i][j] = mfma<kLegacyK32>(bn[j], am[i & 1], acc[i][j], sc_n[j], sc_m[i]);
+        if (i + 2 < kMB) am[i & 1] = read_operand<kTileM>(st + off_m[i + 2]);
+      }
+      pin_stage_schedule<4 * (kNB + 2) + (kMX ? kNB + kMB : 0), kLegacyK32 ? 4 : 1>();
+      cur ^= 1;
     }
 
     // ---- epilogue: lane holds C[m][n..n+3] for m = m0+wm*96+i*16+s16, n = n0+wn*80+j*16+4q
-    uint16_t* cg = a.out + (int64_t)g * a.stride_cg;
+    uint16_t* cg = a.out + (int64_t)T.g * a.stride_cg;
 #pragma unroll
     for (int i = 0; i < kMB; ++i) {
-      const int m = m0 + wm * kWaveM + i * 16 + s16;
+      const int m = T.m0 + wm * kWaveM + i * 16 + s16;
       if (m >= a.OUT_M) continue;
       uint16_t* crow = cg + (int64_t)m * a.stride_cm;
 #pragma unroll
       for (int j = 0; j < kNB; ++j) {
-        const int n = n0 + wn * kWaveN + j * 16 + 4 * q;
+        const int n = T.n0 + wn * kWaveN + j * 16 + 4 * q;
         if (n >= a.OUT_N) continue;
         const v4f v = acc[i][j];
         uint2 pk;
@@ -378,6 +429,8 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
         *reinterpret_cast<uint2*>(crow + n) = pk;
       }
     }
+    t = t_next;
+    T = N;
   }
 }
 
