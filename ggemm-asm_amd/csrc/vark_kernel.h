@@ -299,13 +299,21 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
   const int pid = blockIdx.x;
   const int vpid = (num_wg % 8 == 0) ? (pid % 8) * (num_wg / 8) + pid / 8 : pid;
 
+  // Tiles of a group are visited in bands of kBandN N-tiles, M-tile by M-tile inside a band, so 32
+  // consecutive tiles (what one XCD's CUs hold at a time) form an 8 x 4 block of the group's grid:
+  // 8 * 192 B of LHS plus 4 * 320 B of RHS per token, the least L2 footprint for 32 tiles.
+  constexpr int kBandN = 4;
   auto tile_at = [&](int64_t t) {
     Tile T;
     const int slot = (int)(t / tiles_per_group);
     const int in_g = (int)(t - (int64_t)slot * tiles_per_group);
     T.g = sorted ? s_order[slot] : slot;
-    const int tn = in_g / n_tm;
-    T.m0 = (in_g - tn * n_tm) * kTileM;
+    const int band = in_g / (n_tm * kBandN);
+    const int r = in_g - band * n_tm * kBandN;
+    const int bw = min(kBandN, n_tn - band * kBandN);
+    const int tm = r / bw;
+    const int tn = band * kBandN + (r - tm * bw);
+    T.m0 = tm * kTileM;
     T.n0 = tn * kTileN;
     T.kb = a.group_offs[T.g];
     const int64_t ke = a.group_offs[T.g + 1];
