@@ -24,10 +24,11 @@
 //    one column. The MFMA is v_mfma_scale_f32_16x16x128_f8f6f4 (e8m0 scale 127 == 1.0 for the
 //    per-tensor path, real block scales for MXFP8); the A operand is the RHS tile (rows of the
 //    16x16 result are OUT_N columns) so each lane ends with 4 consecutive bf16 of one C row.
-//  * Static persistent schedule (no workspace exists in the launch contract): groups are visited
-//    in descending token count, tiles within a group with the M-tile fastest, and workgroup ids
-//    are remapped so the 32 CUs of one XCD work on 32 consecutive tiles (shared L2 panels). The
-//    first stage of a workgroup's next tile is loaded while it finishes the current one.
+//  * Static persistent schedule (no workspace exists in the launch contract): groups are sorted by
+//    descending token count, each XCD takes a contiguous slice of the tile list carrying 1/8 of
+//    the work, and its 32 CUs walk the slice round-robin in 4-wide N bands, so CUs of one XCD
+//    share L2 panels and different XCDs stream different rows. The first stage of a workgroup's
+//    next tile is loaded while it finishes the current one.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -59,6 +60,7 @@ constexpr int kMB = kWaveM / 16;                            // 6 MFMA blocks alo
 constexpr int kNB = kWaveN / 16;                            // 5 MFMA blocks along OUT_N
 constexpr int kDynLdsBytes = 65536;                         // launch contract: 64 KiB dynamic LDS
 constexpr int kMaxSortG = 1024;                             // larger G: natural group order
+constexpr int kXcds = 8;                                    // MI355X: 8 XCDs, 32 CUs each
 constexpr int kMxScaleStage = 4 * kTileM + 4 * kTileN;      // 2048 B of e8m0 per stage
 constexpr uint32_t kRsrcWord3 = 0x00020000u;                // raw buffer, 32-bit data format
 
@@ -257,6 +259,7 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
   __shared__ __attribute__((aligned(1024))) uint8_t stage1_mem[kStageBytes];
   __shared__ int s_order[kMaxSortG];
   __shared__ int s_size[kMaxSortG];
+  __shared__ int64_t s_bound[kXcds + 1];
   __shared__ __attribute__((aligned(16))) uint8_t s_scales[kMX ? 2 * kMxScaleStage : 16];
 
   const hsa_kernel_dispatch_packet_t* pkt = dispatch_packet();
@@ -295,9 +298,41 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
   const int tiles_per_group = n_tm * n_tn;
   const int64_t total = (int64_t)G * tiles_per_group;
 
-  // XCD-aware remap: hardware deals workgroup ids round-robin over the 8 XCDs.
+  // ---- XCD partition. The hardware deals workgroup ids round-robin over the 8 XCDs, each with its
+  // own L2. Every XCD takes a contiguous slice of the (size-sorted) tile list holding 1/8 of the
+  // total work (tile weight: its stage count + 1 for the epilogue), and its workgroups walk that
+  // slice round-robin. XCDs then stream different groups at any moment instead of all pulling
+  // the same rows through the same memory-side slices, and the 32 CUs of an XCD share panels.
   const int pid = blockIdx.x;
-  const int vpid = (num_wg % 8 == 0) ? (pid % 8) * (num_wg / 8) + pid / 8 : pid;
+  const int n_xcd = (num_wg % kXcds == 0) ? kXcds : 1;
+  const int xcd = pid % n_xcd;
+  const int wg_in_xcd = pid / n_xcd;
+  const int wgs_per_xcd = num_wg / n_xcd;
+  if (tid == 0) {
+    if (sorted && n_xcd > 1) {
+      int64_t total_w = 0;
+      for (int sl = 0; sl < G; ++sl) total_w += (int64_t)tiles_per_group * (((int64_t)s_size[s_order[sl]] + kKStep - 1) / kKStep + 1);
+      int64_t acc_w = 0;
+      int x = 1;
+      s_bound[0] = 0;
+      for (int sl = 0; sl < G && x < n_xcd; ++sl) {
+        const int64_t w = ((int64_t)s_size[s_order[sl]] + kKStep - 1) / kKStep + 1;
+        const int64_t slot_w = w * tiles_per_group;
+        while (x < n_xcd && acc_w + slot_w >= (total_w * x) / n_xcd) {
+          const int64_t need = (total_w * x) / n_xcd - acc_w;
+          const int64_t i = (need + w - 1) / w;
+          s_bound[x++] = (int64_t)sl * tiles_per_group + (i < tiles_per_group ? i : tiles_per_group);
+        }
+        acc_w += slot_w;
+      }
+      for (; x <= n_xcd; ++x) s_bound[x] = total;
+    } else {
+      for (int x = 0; x <= n_xcd; ++x) s_bound[x] = total * x / n_xcd;
+    }
+  }
+  __syncthreads();
+  const int64_t t_begin = s_bound[xcd] + wg_in_xcd;
+  const int64_t t_end = s_bound[xcd + 1];
 
   // Tiles of a group are visited in bands of kBandN N-tiles, M-tile by M-tile inside a band, so 32
   // consecutive tiles (what one XCD's CUs hold at a time) form an 8 x 4 block of the group's grid:
@@ -360,12 +395,12 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
 
   int cur = 0;              // LDS slot holding the next stage to compute
   bool prefetched = false;  // stage 0 of tile t was issued during the previous tile
-  int64_t t = vpid;
+  int64_t t = t_begin;
   Tile T;
-  if (t < total) T = tile_at(t);
-  while (t < total) {
-    const int64_t t_next = t + num_wg;
-    const bool has_next = t_next < total;
+  if (t < t_end) T = tile_at(t);
+  while (t < t_end) {
+    const int64_t t_next = t + wgs_per_xcd;
+    const bool has_next = t_next < t_end;
     Tile N;
     if (has_next) N = tile_at(t_next);
 
