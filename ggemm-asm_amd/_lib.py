@@ -61,7 +61,7 @@ def load():
     lib.ggemm_vark_strerror.restype = ctypes.c_char_p
     lib.ggemm_vark_abi_version.argtypes = []
     lib.ggemm_vark_abi_version.restype = i32
-    lib.ggemm_vark_launch_geometry.argtypes = [ctypes.POINTER(i32)] * 5
+    lib.ggemm_vark_launch_geometry.argtypes = [i32] + [ctypes.POINTER(i32)] * 5
     lib.ggemm_vark_launch_geometry.restype = None
     _lib = lib
     return lib
@@ -79,9 +79,9 @@ def check(code: int, what: str) -> None:
         raise GGemmError(code, what)
 
 
-def launch_geometry() -> dict:
+def launch_geometry(out_n: int = 5760) -> dict:
     lib = load()
     vals = [ctypes.c_int32() for _ in range(5)]
-    lib.ggemm_vark_launch_geometry(*[ctypes.byref(v) for v in vals])
+    lib.ggemm_vark_launch_geometry(int(out_n), *[ctypes.byref(v) for v in vals])
     keys = ("block_threads", "dynamic_lds", "tile_m", "tile_n", "k_step")
     return {k: v.value for k, v in zip(keys, vals)}

@@ -153,12 +153,12 @@ const char* ggemm_vark_strerror(int32_t code) {
 
 int32_t ggemm_vark_abi_version(void) { return GGEMM_VARK_ABI_VERSION; }
 
-void ggemm_vark_launch_geometry(int32_t* block_threads, int32_t* dynamic_lds, int32_t* tile_m, int32_t* tile_n,
-                                int32_t* k_step) {
+void ggemm_vark_launch_geometry(int32_t out_n, int32_t* block_threads, int32_t* dynamic_lds, int32_t* tile_m,
+                                int32_t* tile_n, int32_t* k_step) {
   if (block_threads) *block_threads = ggemm::kThreads;
   if (dynamic_lds) *dynamic_lds = ggemm::kDynLdsBytes;
   if (tile_m) *tile_m = ggemm::kTileM;
-  if (tile_n) *tile_n = ggemm::kTileN;
+  if (tile_n) *tile_n = (out_n > 0 && out_n % 384 == 0) ? 384 : 320;   // tensorwise kernels; MXFP8: 320
   if (k_step) *k_step = ggemm::kKStep;
 }
 

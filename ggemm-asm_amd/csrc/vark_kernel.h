@@ -8,18 +8,21 @@
 // bench.py:182-193 "dW = x^T @ dy").
 //
 // Structure (one 512-thread workgroup per CU, persistent):
-//  * Output tiles of 192 (OUT_M) x 320 (OUT_N): both divide 2880 and 5760, so the production
-//    shapes have no ragged tiles. 8 waves in a 2 x 4 grid, 96 x 80 per wave (6 x 5 MFMA blocks).
-//  * The token (K) axis is walked in stages of 128 tokens. A stage holds 128 x 192 LHS bytes and
-//    128 x 320 RHS bytes = 64 KiB; two stages (one in the launch's 64 KiB dynamic LDS, one static)
-//    double-buffer the global -> LDS traffic with one workgroup barrier per stage.
+//  * Output tiles of 192 (OUT_M) x TN (OUT_N), TN = 384 when OUT_N is a multiple of 384 (gate_up:
+//    5760 = 15 x 384) and 320 otherwise (down: 2880 = 9 x 320); 192 divides 2880. 8 waves in a
+//    2 x 4 grid, 96 x TN/4 per wave (6 x 6 or 6 x 5 MFMA blocks). RHS rows of a 5760-wide tensor
+//    are 45 whole 128-byte lines, so 384-byte windows are fetched without waste.
+//  * The token (K) axis is walked in stages of 128 tokens: 128 x 192 LHS bytes plus 128 x TN RHS
+//    bytes (64 or 72 KiB). Two stages live in the launch's 64 KiB dynamic LDS plus 96 KiB static
+//    (the full 160 KiB) and double-buffer global -> LDS with one workgroup barrier per stage.
 //  * Global -> LDS uses buffer loads that write LDS directly (16 B per lane). Each such load
 //    covers consecutive token rows of the tile (3.2 rows of 320 B or 5.3 rows of 192 B), so a
 //    wave-instruction touches few cache lines. The buffer resource is rebased at the stage's
 //    first token and the tile's first column with num_records ending at the last valid token,
 //    so tokens past the group end read as zero: ragged K tails and tiny groups need no masking.
-//  * LDS layout per operand: row-major [token][W] with the 16-byte chunk index XOR-swizzled by
-//    (token >> 2) & 3, so the transposed reads below are bank-conflict free.
+//  * LDS layout per operand: row-major [token][W] with the 16-byte chunk index XOR-swizzled by a
+//    function of the token chosen per row width, so the transposed reads below are bank-conflict
+//    free (16 consecutive tokens of one chunk column land in 16 distinct 4-bank slots).
 //  * MFMA operands come from ds_read_b64_tr_b8: one read gives each lane 8 consecutive tokens of
 //    one column. The MFMA is v_mfma_scale_f32_16x16x128_f8f6f4 (e8m0 scale 127 == 1.0 for the
 //    per-tensor path, real block scales for MXFP8); the A operand is the RHS tile (rows of the
@@ -46,27 +49,67 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
 constexpr int kTileM = 192;
-constexpr int kTileN = 320;
 constexpr int kKStep = 128;
 constexpr int kLhsBytes = kKStep * kTileM;                  // 24 KiB of LHS per stage
-constexpr int kRhsBytes = kKStep * kTileN;                  // 40 KiB of RHS per stage
-constexpr int kStageBytes = kLhsBytes + kRhsBytes;          // 64 KiB
-constexpr int kDmaPerStage = kStageBytes / 1024;            // 1 KiB per wave-instruction
-constexpr int kDmaPerWave = kDmaPerStage / kWaves;          // 8
-constexpr int kDmaLhs = kLhsBytes / 1024;                   // first 24 instructions carry LHS
+constexpr int kDmaLhs = kLhsBytes / 1024;                   // first 24 LDS-DMA instructions carry LHS
 constexpr int kWaveM = 96;
-constexpr int kWaveN = 80;
 constexpr int kMB = kWaveM / 16;                            // 6 MFMA blocks along OUT_M
-constexpr int kNB = kWaveN / 16;                            // 5 MFMA blocks along OUT_N
 constexpr int kDynLdsBytes = 65536;                         // launch contract: 64 KiB dynamic LDS
+constexpr int kStaticLdsBytes = 98304;                      // + 96 KiB static = gfx950's 160 KiB
 constexpr int kMaxSortG = 1024;                             // larger G: natural group order
 constexpr int kXcds = 8;                                    // MI355X: 8 XCDs, 32 CUs each
-constexpr int kMxScaleStage = 4 * kTileM + 4 * kTileN;      // 2048 B of e8m0 per stage
+constexpr int kMiscBytes = 16384;                           // group order, sizes, XCD bounds, e8m0
 constexpr uint32_t kRsrcWord3 = 0x00020000u;                // raw buffer, 32-bit data format
 
-static_assert(kStageBytes == kDynLdsBytes, "one stage must fill the dynamic LDS window");
-static_assert(kDmaPerWave * kWaves == kDmaPerStage && kDmaLhs % kWaves == 0, "uniform LDS-DMA split");
-static_assert(kTileM % 64 == 0 && kTileN % 64 == 0, "rows are whole groups of four 16-byte chunks");
+static_assert(kDmaLhs % kWaves == 0, "LHS LDS-DMA instructions split evenly over the waves");
+
+// Per-tile-width configuration. Bank slot of (token t, physical chunk c) is (t * W/16 + c) mod 16;
+// the XOR swizzle makes 16 consecutive tokens of one logical chunk hit 16 distinct slots:
+// W = 192, 320: c ^ ((t >> 2) & 3) (t mod 4 and (t >> 2) & 3 index the slot); W = 384:
+// c ^ ((t >> 1) & 7) (t mod 2 and (t >> 1) & 7 index it). Both keep c inside its aligned group of
+// 4 or 8 chunks, and rows hold whole groups (12, 20, 24 chunks).
+template <int kTN>
+struct Cfg {
+  static_assert(kTN == 320 || kTN == 384, "supported N tiles");
+  static constexpr int TN = kTN;
+  static constexpr int RhsBytes = kKStep * kTN;
+  static constexpr int DmaRhs = RhsBytes / 1024;
+  static constexpr int DmaPerWave = (kDmaLhs + DmaRhs) / kWaves;   // 8 or 9
+  static constexpr int WaveN = kTN / 4;
+  static constexpr int NB = WaveN / 16;                           // 5 or 6
+  static constexpr int ScaleStage = 4 * kTileM + 4 * kTN;         // e8m0 bytes per stage
+  static constexpr int ScaleChunksR = 4 * kTN / 16;               // 80 or 96
+  static constexpr int ScaleLanesR = (ScaleChunksR + 4) / 5;      // per RHS wave (waves 3-7)
+  static_assert((kDmaLhs + DmaRhs) % kWaves == 0, "uniform LDS-DMA split");
+  static_assert(ScaleLanesR * 5 >= ScaleChunksR && ScaleLanesR <= 64, "scale DMA coverage");
+  static_assert(4096 * 2 + 8 * (kXcds + 1) + 2 * ScaleStage + 512 <= kMiscBytes, "misc LDS budget");
+  __device__ static __forceinline__ int rswz(int t) { return kTN == 384 ? ((t >> 1) & 7) : ((t >> 2) & 3); }
+};
+__device__ __forceinline__ int lswz(int t) { return (t >> 2) & 3; }
+
+// LDS map. Slot s holds one stage: LHS rows at L[s], RHS rows at R[s]. TN = 320 (64 KiB stages):
+// slot 0 = the dynamic window, slot 1 = static [0, 64K), misc = static [64K, 80K). TN = 384
+// (72 KiB stages): slot 0 = LHS static [0, 24K) + RHS dynamic [0, 48K), slot 1 = static
+// [24K, 96K), misc = dynamic [48K, 64K).
+struct LdsMap {
+  GG_LDS uint8_t* L[2];
+  GG_LDS uint8_t* R[2];
+  GG_LDS uint8_t* misc;
+};
+template <int kTN>
+__device__ __forceinline__ LdsMap lds_map(GG_LDS uint8_t* dyn, GG_LDS uint8_t* st) {
+  LdsMap m;
+  if constexpr (kTN == 320) {
+    m.L[0] = dyn; m.R[0] = dyn + kLhsBytes;
+    m.L[1] = st;  m.R[1] = st + kLhsBytes;
+    m.misc = st + 65536;
+  } else {
+    m.L[0] = st;             m.R[0] = dyn;
+    m.L[1] = st + kLhsBytes; m.R[1] = st + 2 * kLhsBytes;
+    m.misc = dyn + Cfg<kTN>::RhsBytes;
+  }
+  return m;
+}
 
 // ----------------------------------------------------------------------------------- helpers
 
@@ -94,9 +137,6 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// 16-byte chunk swizzle of an LDS row: chunk c of token t sits at chunk c ^ ((t >> 2) & 3).
-__device__ __forceinline__ int swizzle(int token) { return (token >> 2) & 3; }
-
 // ----------------------------------------------------------------------------------- loads
 
 // Raw buffer resource (gfx9 layout): 48-bit base, stride 0, num_records bytes, word3 flags.
@@ -114,9 +154,14 @@ __device__ __forceinline__ v4i make_rsrc(const void* base, int num_records) {
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(v4i rsrc, uint32_t lds_addr, int voff) {
+  // the LDS address and the resource are wave-uniform by construction; readfirstlane pins them to
+  // SGPRs (m0 and the resource operand must be scalar)
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_addr);
+  const v4i r = v4i{__builtin_amdgcn_readfirstlane(rsrc[0]), __builtin_amdgcn_readfirstlane(rsrc[1]),
+                    __builtin_amdgcn_readfirstlane(rsrc[2]), __builtin_amdgcn_readfirstlane(rsrc[3])};
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
-               : "s"(lds_addr), "v"(voff), "s"(rsrc)
+               : "s"(m0v), "v"(voff), "s"(r)
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -125,62 +170,77 @@ __device__ __forceinline__ uint32_t lds_u32(const GG_LDS void* p) {
   return (uint32_t)reinterpret_cast<uintptr_t>(p);
 }
 
-// Stage loads: 64 wave-instructions of 1 KiB fill the stage LDS linearly (instructions 0-23 the
-// LHS rows of 192 B, 24-63 the RHS rows of 320 B). Wave w issues instructions w, w+8, ..., w+56.
-// Lane l of instruction i writes physical chunk q = 64*i' + l of its operand (i' = index within
-// the operand), i.e. token row q / W16 and physical chunk q % W16 (W16 = 12 or 20 chunks per row),
-// which holds logical chunk (q % W16) ^ swizzle(row). Per-lane byte offsets relative to the
-// stage's (first token, first column) do not depend on the tile or the step: computed once.
+// Stage loads: the stage's LHS (24 x 1 KiB) and RHS (TN/8 x 1 KiB) are filled by 1 KiB
+// wave-instructions; wave w issues instructions w, w+8, ... (the first 3 carry LHS). Lane l of
+// an operand's instruction i writes its physical chunk q = 64*i + l, i.e. token row q / W16 and
+// physical chunk q % W16 (W16 = 12, 20 or 24 chunks per row), which holds logical chunk
+// (q % W16) ^ swizzle(row). Per-lane byte offsets relative to the stage's (first token, first
+// column) do not depend on the tile or the step: computed once.
+template <int kTN>
 struct DmaPlan {
-  int voff[kDmaPerWave];
+  int voff[Cfg<kTN>::DmaPerWave];
 };
 
-__device__ __forceinline__ DmaPlan make_dma_plan(int wave, int lane, int stride_l, int stride_r) {
-  DmaPlan d;
+template <int kTN>
+__device__ __forceinline__ DmaPlan<kTN> make_dma_plan(int wave, int lane, int stride_l, int stride_r) {
+  DmaPlan<kTN> d;
 #pragma unroll
-  for (int j = 0; j < kDmaPerWave; ++j) {
+  for (int j = 0; j < Cfg<kTN>::DmaPerWave; ++j) {
     const int i = wave + kWaves * j;
     if (j < kDmaLhs / kWaves) {
       const int q = 64 * i + lane, w16 = kTileM / 16;
       const int row = q / w16, pc = q - row * w16;
-      d.voff[j] = row * stride_l + 16 * (pc ^ swizzle(row));
+      d.voff[j] = row * stride_l + 16 * (pc ^ lswz(row));
     } else {
-      const int q = 64 * (i - kDmaLhs) + lane, w16 = kTileN / 16;
+      const int q = 64 * (i - kDmaLhs) + lane, w16 = kTN / 16;
       const int row = q / w16, pc = q - row * w16;
-      d.voff[j] = row * stride_r + 16 * (pc ^ swizzle(row));
+      d.voff[j] = row * stride_r + 16 * (pc ^ Cfg<kTN>::rswz(row));
     }
   }
   return d;
 }
 
 // Issue this wave's loads of one stage: tokens [row0, row0 + rows_valid) of the group (the rest of
-// the 128-token stage reads as zero), columns [m0, m0 + 192) of LHS and [n0, n0 + 320) of RHS.
+// the 128-token stage reads as zero), columns [m0, m0 + 192) of LHS and [n0, n0 + TN) of RHS.
 // num_records ends exactly at the last valid token's row end, so no load reaches past it.
-__device__ __forceinline__ void issue_stage(uint32_t stage, const uint8_t* lhs, const uint8_t* rhs, int64_t row0,
-                                            int rows_valid, int stride_l, int stride_r, int m0, int n0,
-                                            const DmaPlan& plan, int wave) {
+template <int kTN>
+__device__ __forceinline__ void issue_stage(uint32_t lbase, uint32_t rbase_lds, const uint8_t* lhs,
+                                            const uint8_t* rhs, int64_t row0, int rows_valid, int stride_l,
+                                            int stride_r, int m0, int n0, const DmaPlan<kTN>& plan, int wave) {
   const v4i rl = make_rsrc(lhs + row0 * (int64_t)stride_l + m0, rows_valid * stride_l - m0);
   const v4i rr = make_rsrc(rhs + row0 * (int64_t)stride_r + n0, rows_valid * stride_r - n0);
 #pragma unroll
-  for (int j = 0; j < kDmaPerWave; ++j)
-    dma16(j < kDmaLhs / kWaves ? rl : rr, stage + (wave + kWaves * j) * 1024, plan.voff[j]);
+  for (int j = 0; j < Cfg<kTN>::DmaPerWave; ++j) {
+    const int i = wave + kWaves * j;
+    if (j < kDmaLhs / kWaves)
+      dma16(rl, lbase + i * 1024, plan.voff[j]);
+    else
+      dma16(rr, rbase_lds + (i - kDmaLhs) * 1024, plan.voff[j]);
+  }
 }
 
-// MXFP8: one LDS-DMA load per wave per stage brings the stage's e8m0 rows into LDS.
-// Chunk c of the 128 x 16 B list: c < 48 -> LHS block c/12, columns m0 + 16*(c%12);
-// otherwise RHS block (c-48)/20, columns n0 + 16*((c-48)%20). Waves 0-2 carry LHS, 3-7 RHS,
-// 16 active lanes each. Blocks past the group end read as 0 (scale 2^-127 on zero data).
+// MXFP8: the stage's e8m0 rows (4 token blocks x 192 LHS columns, then 4 x TN RHS columns) are
+// loaded into LDS as 16-byte chunks: waves 0-2 carry the 48 LHS chunks (16 lanes each), waves 3-7
+// the RHS chunks (ScaleLanesR lanes each). Blocks past the group end read as 0 (scale 2^-127 on
+// zero data).
+template <int kTN>
 __device__ __forceinline__ void issue_stage_scales(uint32_t sstage, const uint8_t* lsc, const uint8_t* rsc,
                                                    int64_t blk0, int blocks_valid, int stride_ls, int stride_rs,
                                                    int m0, int n0, int wave, int lane) {
-  const bool is_l = wave < 3;
-  const uint8_t* base = is_l ? lsc + blk0 * (int64_t)stride_ls : rsc + blk0 * (int64_t)stride_rs;
-  const int stride = is_l ? stride_ls : stride_rs;
-  const v4i r = make_rsrc(base, blocks_valid * stride);
-  const int c = wave * 16 + (lane & 15);
-  const int voff = is_l ? (c / 12) * stride + m0 + 16 * (c % 12) : ((c - 48) / 20) * stride + n0 + 16 * ((c - 48) % 20);
-  // only lanes 0-15 are active: they write 256 bytes at sstage + 256 * wave + 16 * lane
-  if (lane < 16) dma16(r, sstage + wave * 256, voff);
+  using C = Cfg<kTN>;
+  if (wave < 3) {
+    const v4i r = make_rsrc(lsc + blk0 * (int64_t)stride_ls, blocks_valid * stride_ls);
+    const int c = wave * 16 + (lane & 15);
+    const int voff = (c / 12) * stride_ls + m0 + 16 * (c % 12);
+    if (lane < 16) dma16(r, sstage + wave * 256, voff);
+  } else {
+    const v4i r = make_rsrc(rsc + blk0 * (int64_t)stride_rs, blocks_valid * stride_rs);
+    const int c = (wave - 3) * C::ScaleLanesR + lane;
+    const int cc = c < C::ScaleChunksR ? c : 0;
+    const int voff = (cc / (kTN / 16)) * stride_rs + n0 + 16 * (cc % (kTN / 16));
+    if (lane < C::ScaleLanesR && c < C::ScaleChunksR)
+      dma16(r, sstage + 4 * kTileM + (wave - 3) * C::ScaleLanesR * 16, voff);
+  }
 }
 
 // ----------------------------------------------------------------------------------- compute
@@ -220,17 +280,17 @@ __device__ __forceinline__ v4f mfma(const v8i& a_rhs, const v8i& b_lhs, v4f acc,
 }
 
 // Instruction order of one stage's compute: all n-side reads plus m-blocks 0 and 1 first, then
-// for each m-block its five MFMAs followed by the reads of m-block i+2 into the registers block i
+// for each m-block its MFMAs followed by the reads of m-block i+2 into the registers block i
 // just released -- LDS latency of every m-block hides behind the previous block's MFMAs.
-template <int kFirstReads, int kMfmaPerCall>
+template <int kFirstReads, int kMfmaPerBlock>
 __device__ __forceinline__ void pin_stage_schedule() {
   __builtin_amdgcn_sched_group_barrier(0x100, kFirstReads, 0);
 #pragma unroll
   for (int i = 0; i < kMB - 2; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, kNB * kMfmaPerCall, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, kMfmaPerBlock, 0);
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
   }
-  __builtin_amdgcn_sched_group_barrier(0x008, 2 * kNB * kMfmaPerCall, 0);
+  __builtin_amdgcn_sched_group_barrier(0x008, 2 * kMfmaPerBlock, 0);
 }
 
 // ----------------------------------------------------------------------------------- kernel body
@@ -253,25 +313,24 @@ struct Tile {
   int64_t kb, klen;
 };
 
-template <bool kMX, bool kLegacyK32>
-__device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* stage0) {
+template <bool kMX, bool kLegacyK32, int kTN>
+__device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* dyn, GG_LDS uint8_t* st) {
   static_assert(!(kMX && kLegacyK32), "block scales need the scaled MFMA");
-  __shared__ __attribute__((aligned(1024))) uint8_t stage1_mem[kStageBytes];
-  __shared__ int s_order[kMaxSortG];
-  __shared__ int s_size[kMaxSortG];
-  __shared__ int64_t s_bound[kXcds + 1];
-  __shared__ __attribute__((aligned(16))) uint8_t s_scales[kMX ? 2 * kMxScaleStage : 16];
+  using C = Cfg<kTN>;
+  constexpr int NB = C::NB;
+  const LdsMap lm = lds_map<kTN>(dyn, st);
+  GG_LDS int* s_order = (GG_LDS int*)lm.misc;
+  GG_LDS int* s_size = (GG_LDS int*)(lm.misc + 4096);
+  GG_LDS int64_t* s_bound = (GG_LDS int64_t*)(lm.misc + 8192);
+  GG_LDS uint8_t* scales = lm.misc + 8192 + 8 * (kXcds + 1) + 56;   // 16-byte aligned
 
   const hsa_kernel_dispatch_packet_t* pkt = dispatch_packet();
-  // The launch must provide the contracted dynamic LDS; otherwise do nothing (host validates).
-  if (pkt->group_segment_size < __builtin_amdgcn_groupstaticsize() + (uint32_t)kDynLdsBytes) return;
   const int num_wg = (int)((pkt->grid_size_x + pkt->workgroup_size_x - 1) / pkt->workgroup_size_x);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = a.G;
-  if (G <= 0) return;
 
   // ---- group order: descending token count (stable), so expensive tiles are dealt first
   const bool sorted = G <= kMaxSortG;
@@ -294,7 +353,7 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
   }
 
   const int n_tm = (a.OUT_M + kTileM - 1) / kTileM;
-  const int n_tn = (a.OUT_N + kTileN - 1) / kTileN;
+  const int n_tn = (a.OUT_N + kTN - 1) / kTN;
   const int tiles_per_group = n_tm * n_tn;
   const int64_t total = (int64_t)G * tiles_per_group;
 
@@ -311,7 +370,8 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
   if (tid == 0) {
     if (sorted && n_xcd > 1) {
       int64_t total_w = 0;
-      for (int sl = 0; sl < G; ++sl) total_w += (int64_t)tiles_per_group * (((int64_t)s_size[s_order[sl]] + kKStep - 1) / kKStep + 1);
+      for (int sl = 0; sl < G; ++sl)
+        total_w += (int64_t)tiles_per_group * (((int64_t)s_size[s_order[sl]] + kKStep - 1) / kKStep + 1);
       int64_t acc_w = 0;
       int x = 1;
       s_bound[0] = 0;
@@ -335,8 +395,7 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
   const int64_t t_end = s_bound[xcd + 1];
 
   // Tiles of a group are visited in bands of kBandN N-tiles, M-tile by M-tile inside a band, so 32
-  // consecutive tiles (what one XCD's CUs hold at a time) form an 8 x 4 block of the group's grid:
-  // 8 * 192 B of LHS plus 4 * 320 B of RHS per token, the least L2 footprint for 32 tiles.
+  // consecutive tiles (what one XCD's CUs hold at a time) form an 8 x 4 block of the group's grid.
   constexpr int kBandN = 4;
   auto tile_at = [&](int64_t t) {
     Tile T;
@@ -349,7 +408,7 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
     const int tm = r / bw;
     const int tn = band * kBandN + (r - tm * bw);
     T.m0 = tm * kTileM;
-    T.n0 = tn * kTileN;
+    T.n0 = tn * kTN;
     T.kb = a.group_offs[T.g];
     const int64_t ke = a.group_offs[T.g + 1];
     T.klen = ke > T.kb ? ke - T.kb : 0;
@@ -365,32 +424,28 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
   const int q = lane >> 4;
   const int s16 = lane & 15;
   const int rbase = 32 * (q >> 1) + 8 * (q & 1) + (s16 >> 1);
-  const int swz = swizzle(rbase);
   const int colb = 8 * (s16 & 1);
 
-  // per-lane LDS byte offsets (stage-relative) of each operand block's first transposed read
-  int off_m[kMB], off_n[kNB];
+  // per-lane LDS byte offsets (operand-region relative) of each block's first transposed read
+  int off_m[kMB], off_n[NB];
 #pragma unroll
-  for (int i = 0; i < kMB; ++i) off_m[i] = rbase * kTileM + 16 * (((wm * kWaveM + i * 16) >> 4) ^ swz) + colb;
+  for (int i = 0; i < kMB; ++i) off_m[i] = rbase * kTileM + 16 * (((wm * kWaveM + i * 16) >> 4) ^ lswz(rbase)) + colb;
 #pragma unroll
-  for (int j = 0; j < kNB; ++j)
-    off_n[j] = kLhsBytes + rbase * kTileN + 16 * (((wn * kWaveN + j * 16) >> 4) ^ swz) + colb;
+  for (int j = 0; j < NB; ++j)
+    off_n[j] = rbase * kTN + 16 * (((wn * C::WaveN + j * 16) >> 4) ^ C::rswz(rbase)) + colb;
 
-  const DmaPlan plan = make_dma_plan(wave, lane, a.stride_lhs_m, a.stride_rhs_m);
-  const uint32_t slot_base[2] = {lds_u32(stage0), lds_u32((GG_LDS uint8_t*)stage1_mem)};
-  GG_LDS uint8_t* const slot_ptr[2] = {stage0, (GG_LDS uint8_t*)stage1_mem};
-  GG_LDS uint8_t* scales = (GG_LDS uint8_t*)s_scales;
+  const DmaPlan<kTN> plan = make_dma_plan<kTN>(wave, lane, a.stride_lhs_m, a.stride_rhs_m);
 
   auto issue = [&](const Tile& T, int step, int slot) {
     const int64_t k0 = (int64_t)step * kKStep;
     const int64_t rem = T.klen - k0;
     const int rv = (int)(rem < kKStep ? rem : kKStep);
-    issue_stage(slot_base[slot], a.lhs, a.rhs, T.kb + k0, rv, a.stride_lhs_m, a.stride_rhs_m, T.m0, T.n0, plan,
-                wave);
+    issue_stage<kTN>(lds_u32(slot ? lm.L[1] : lm.L[0]), lds_u32(slot ? lm.R[1] : lm.R[0]), a.lhs, a.rhs, T.kb + k0, rv, a.stride_lhs_m,
+                     a.stride_rhs_m, T.m0, T.n0, plan, wave);
     if constexpr (kMX)
-      issue_stage_scales(lds_u32(scales + slot * kMxScaleStage), (const uint8_t*)a.lhs_scale,
-                         (const uint8_t*)a.rhs_scale, (T.kb + k0) / 32, (rv + 31) / 32, a.stride_lhs_scale,
-                         a.stride_rhs_scale, T.m0, T.n0, wave, lane);
+      issue_stage_scales<kTN>(lds_u32(scales + slot * C::ScaleStage), (const uint8_t*)a.lhs_scale,
+                              (const uint8_t*)a.rhs_scale, (T.kb + k0) / 32, (rv + 31) / 32, a.stride_lhs_scale,
+                              a.stride_rhs_scale, T.m0, T.n0, wave, lane);
   };
 
   int cur = 0;              // LDS slot holding the next stage to compute
@@ -404,11 +459,11 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
     Tile N;
     if (has_next) N = tile_at(t_next);
 
-    v4f acc[kMB][kNB];
+    v4f acc[kMB][NB];
 #pragma unroll
     for (int i = 0; i < kMB; ++i)
 #pragma unroll
-      for (int j = 0; j < kNB; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < NB; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
     if (T.nsteps > 0 && !prefetched) issue(T, 0, cur);
     prefetched = false;
@@ -424,37 +479,38 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
         prefetched = true;
       }
 
-      const GG_LDS uint8_t* st = slot_ptr[cur];
-      int sc_n[kNB], sc_m[kMB];
+      const GG_LDS uint8_t* sl = cur ? lm.L[1] : lm.L[0];
+      const GG_LDS uint8_t* sr = cur ? lm.R[1] : lm.R[0];
+      int sc_n[NB], sc_m[kMB];
 #pragma unroll
-      for (int j = 0; j < kNB; ++j) sc_n[j] = 127;
+      for (int j = 0; j < NB; ++j) sc_n[j] = 127;
 #pragma unroll
       for (int i = 0; i < kMB; ++i) sc_m[i] = 127;
       if constexpr (kMX) {
-        const GG_LDS uint8_t* ss = scales + cur * kMxScaleStage;
+        const GG_LDS uint8_t* ss = scales + cur * C::ScaleStage;
 #pragma unroll
-        for (int j = 0; j < kNB; ++j) sc_n[j] = ss[4 * kTileM + q * kTileN + wn * kWaveN + j * 16 + s16];
+        for (int j = 0; j < NB; ++j) sc_n[j] = ss[4 * kTileM + q * kTN + wn * C::WaveN + j * 16 + s16];
 #pragma unroll
         for (int i = 0; i < kMB; ++i) sc_m[i] = ss[q * kTileM + wm * kWaveM + i * 16 + s16];
       }
 
-      v8i bn[kNB], am[2];
-      bn[0] = read_operand<kTileN>(st + off_n[0]);
-      am[0] = read_operand<kTileM>(st + off_m[0]);
+      v8i bn[NB], am[2];
+      bn[0] = read_operand<kTN>(sr + off_n[0]);
+      am[0] = read_operand<kTileM>(sl + off_m[0]);
 #pragma unroll
-      for (int j = 1; j < kNB; ++j) bn[j] = read_operand<kTileN>(st + off_n[j]);
-      am[1] = read_operand<kTileM>(st + off_m[1]);
+      for (int j = 1; j < NB; ++j) bn[j] = read_operand<kTN>(sr + off_n[j]);
+      am[1] = read_operand<kTileM>(sl + off_m[1]);
 #pragma unroll
       for (int i = 0; i < kMB; ++i) {
 #pragma unroll
-        for (int j = 0; j < kNB; ++j) acc[i][j] = mfma<kLegacyK32>(bn[j], am[i & 1], acc[i][j], sc_n[j], sc_m[i]);
-        if (i + 2 < kMB) am[i & 1] = read_operand<kTileM>(st + off_m[i + 2]);
+        for (int j = 0; j < NB; ++j) acc[i][j] = mfma<kLegacyK32>(bn[j], am[i & 1], acc[i][j], sc_n[j], sc_m[i]);
+        if (i + 2 < kMB) am[i & 1] = read_operand<kTileM>(sl + off_m[i + 2]);
       }
-      pin_stage_schedule<4 * (kNB + 2) + (kMX ? kNB + kMB : 0), kLegacyK32 ? 4 : 1>();
+      pin_stage_schedule<4 * (NB + 2) + (kMX ? NB + kMB : 0), NB * (kLegacyK32 ? 4 : 1)>();
       cur ^= 1;
     }
 
-    // ---- epilogue: lane holds C[m][n..n+3] for m = m0+wm*96+i*16+s16, n = n0+wn*80+j*16+4q
+    // ---- epilogue: lane holds C[m][n..n+3] for m = m0+wm*96+i*16+s16, n = n0+wn*TN/4+j*16+4q
     uint16_t* cg = a.out + (int64_t)T.g * a.stride_cg;
 #pragma unroll
     for (int i = 0; i < kMB; ++i) {
@@ -462,8 +518,8 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
       if (m >= a.OUT_M) continue;
       uint16_t* crow = cg + (int64_t)m * a.stride_cm;
 #pragma unroll
-      for (int j = 0; j < kNB; ++j) {
-        const int n = T.n0 + wn * kWaveN + j * 16 + 4 * q;
+      for (int j = 0; j < NB; ++j) {
+        const int n = T.n0 + wn * C::WaveN + j * 16 + 4 * q;
         if (n >= a.OUT_N) continue;
         const v4f v = acc[i][j];
         uint2 pk;
@@ -475,6 +531,24 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
     t = t_next;
     T = N;
   }
+}
+
+// Entry body shared by all kernels: checks the launch's LDS, then runs the 384-wide tile
+// configuration when OUT_N is a multiple of 384 (tensorwise kernels) and the 320-wide one
+// otherwise.
+template <bool kMX, bool kLegacyK32>
+__device__ __forceinline__ void vark_entry(const VarKArgs& a, GG_LDS uint8_t* dyn) {
+  __shared__ __attribute__((aligned(1024))) uint8_t static_lds[kStaticLdsBytes];
+  const hsa_kernel_dispatch_packet_t* pkt = dispatch_packet();
+  // The launch must provide the contracted dynamic LDS; otherwise do nothing (host validates).
+  if (pkt->group_segment_size < __builtin_amdgcn_groupstaticsize() + (uint32_t)kDynLdsBytes) return;
+  if (a.G <= 0) return;
+  GG_LDS uint8_t* st = (GG_LDS uint8_t*)static_lds;
+  // MXFP8 keeps the 320-wide tiles: its per-block scale registers do not fit next to 6 x 6 blocks.
+  if (!kMX && a.OUT_N % 384 == 0)
+    vark_body<kMX, kLegacyK32, 384>(a, dyn, st);
+  else
+    vark_body<kMX, kLegacyK32, 320>(a, dyn, st);
 }
 
 }  // namespace ggemm
@@ -493,7 +567,7 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
     ggemm::VarKArgs a{lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N,                  \
                       stride_lhs_m, stride_rhs_m, stride_cg, stride_cm, stride_cn, 0, 0};                \
     (void)global_scratch; (void)profile_scratch;                                                        \
-    ggemm::vark_body<false, LEGACY>(a, (GG_LDS uint8_t*)ggemm_dyn_lds);                                  \
+    ggemm::vark_entry<false, LEGACY>(a, (GG_LDS uint8_t*)ggemm_dyn_lds);                                  \
   }
 
 #define GGEMM_DEFINE_MX_KERNEL(NAME)                                                                    \
@@ -507,5 +581,5 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* sta
                       stride_lhs_m, stride_rhs_m, stride_cg, stride_cm, stride_cn,                      \
                       stride_lhs_scale, stride_rhs_scale};                                              \
     (void)global_scratch; (void)profile_scratch;                                                        \
-    ggemm::vark_body<true, false>(a, (GG_LDS uint8_t*)ggemm_dyn_lds);                                    \
+    ggemm::vark_entry<true, false>(a, (GG_LDS uint8_t*)ggemm_dyn_lds);                                    \
   }

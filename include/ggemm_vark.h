@@ -81,9 +81,10 @@ const char* ggemm_vark_strerror(int32_t code);
 /* GGEMM_VARK_ABI_VERSION of the loaded library. */
 int32_t ggemm_vark_abi_version(void);
 
-/* Launch geometry the library uses (and the drop-in code object expects): block threads,
- * dynamic LDS bytes, output tile (OUT_M x OUT_N) and token stage. */
-void ggemm_vark_launch_geometry(int32_t* block_threads, int32_t* dynamic_lds, int32_t* tile_m,
+/* Launch geometry the library uses (and the drop-in code object expects) for a problem of width
+ * OUT_N = out_n: block threads, dynamic LDS bytes, output tile (OUT_M x OUT_N; the N tile is 384
+ * when out_n is a multiple of 384, else 320) and tokens per pipeline stage. */
+void ggemm_vark_launch_geometry(int32_t out_n, int32_t* block_threads, int32_t* dynamic_lds, int32_t* tile_m,
                                 int32_t* tile_n, int32_t* k_step);
 
 #ifdef __cplusplus

@@ -36,8 +36,9 @@ def test_abi_version_and_geometry(pkg):
     lib = pkg.load_library()
     ver = int(re.search(r"#define GGEMM_VARK_ABI_VERSION (\d+)", open(HEADER).read()).group(1))
     assert lib.ggemm_vark_abi_version() == ver
-    assert pkg.launch_geometry() == {"block_threads": 512, "dynamic_lds": 65536, "tile_m": 192,
-                                     "tile_n": 320, "k_step": 128}
+    assert pkg.launch_geometry(5760) == {"block_threads": 512, "dynamic_lds": 65536, "tile_m": 192,
+                                         "tile_n": 384, "k_step": 128}
+    assert pkg.launch_geometry(2880)["tile_n"] == 320
 
 
 def _offs(vals):

@@ -121,6 +121,12 @@ RAGGED = [
     ([1000, 24], 2880 // 5, 5760 // 9),
     ([0], 64, 64),
     ([4096 + 77], 384, 640),
+    # OUT_N multiples of 384 take the 192 x 384 tile configuration
+    ([1, 2, 3, 5, 8, 13, 21, 31], 64, 384),
+    ([127, 128, 129, 0, 256, 257], 208, 768),
+    ([300, 0, 645], 400, 1152),
+    ([31] * 4 + [0] * 2, 16, 384),
+    ([2000, 96], 576, 768),
 ]
 
 
@@ -215,13 +221,14 @@ def test_mxfp8_vs_oracle(pkg, orc, cuda, lens, om, on):
 
 # ----------------------------------------------------------------------------- drop-in code object
 
-def test_code_object_kernelparams_and_kernarg_buffer(pkg, cuda):
+@pytest.mark.parametrize("out_n", [640, 768])
+def test_code_object_kernelparams_and_kernarg_buffer(pkg, cuda, out_n):
     """Our .co launched like reference bench.py (16-entry kernelParams) and like launcher.cpp
-    (96-byte buffer) gives the library's result bit for bit."""
+    (96-byte buffer) gives the library's result bit for bit (both N-tile configurations)."""
     from ggemm_asm_amd import harness
-    _say("code object via hipModuleLaunchKernel")
+    _say(f"code object via hipModuleLaunchKernel OUT_N={out_n}")
     lens = [96, 160, 0, 256, 33]
-    lhs, rhs, offs, _, _ = _rand_bytes_problem(lens, 384, 640, seed=21)
+    lhs, rhs, offs, _, _ = _rand_bytes_problem(lens, 384, out_n, seed=21)
     dl, dr, do = lhs.to(cuda), rhs.to(cuda), offs.to(cuda)
     s1, s2 = torch.tensor(0.1, device=cuda), torch.tensor(0.1, device=cuda)
     ref = pkg.grouped_gemm_fp8_tensorwise_variable_k(dl, dr, s1, s2, do)
@@ -231,16 +238,16 @@ def test_code_object_kernelparams_and_kernarg_buffer(pkg, cuda):
         n_cus = harness.get_num_cus(0)
         out1 = torch.zeros_like(ref)
         torch.cuda.synchronize()
-        harness.launch_variable_k_kernel(func, dl, dr, out1, s1, s2, do, len(lens), 384, 640, n_cus)
+        harness.launch_variable_k_kernel(func, dl, dr, out1, s1, s2, do, len(lens), 384, out_n, n_cus)
         out2 = torch.full_like(ref, 7.0)
-        harness.launch_with_kernarg_buffer(func, harness.kernarg_buffer(dl, dr, out2, s1, s2, do, len(lens), 384, 640),
+        harness.launch_with_kernarg_buffer(func, harness.kernarg_buffer(dl, dr, out2, s1, s2, do, len(lens), 384, out_n),
                                            n_cus)
         torch.cuda.synchronize()
         assert torch.equal(out1.view(torch.int16), ref.view(torch.int16))
         assert torch.equal(out2.view(torch.int16), ref.view(torch.int16))
         # fewer workgroups than CUs (any grid size must be correct)
         out3 = torch.zeros_like(ref)
-        harness.launch_variable_k_kernel(func, dl, dr, out3, s1, s2, do, len(lens), 384, 640, 24)
+        harness.launch_variable_k_kernel(func, dl, dr, out3, s1, s2, do, len(lens), 384, out_n, 24)
         torch.cuda.synchronize()
         assert torch.equal(out3.view(torch.int16), ref.view(torch.int16))
     finally:
