@@ -164,7 +164,8 @@ def main():
         "config": {"workload": p.name, "G": p.G, "M_total": p.M, "OUT_M": p.OUT_M, "OUT_N": p.OUT_N,
                    "lhs": "e4m3fn", "rhs": "e5m2", "out": "bf16", "acc": "fp32",
                    "inputs": "seeded N(0,1) / N(0,1e-3) quantized per-tensor, multinomial group sizes, in HBM",
-                   "kernel": f"hip gfx950 persistent 192x320 tiles, mfma {args.mfma}",
+                   "kernel": "hip gfx950 persistent {tile_m}x{tile_n} tiles, mfma {mfma}".format(
+                       mfma=args.mfma, **pkg.launch_geometry(p.OUT_N)),
                    "baseline_number": "reference optimized ASM 3.515 ms / 1237 TFLOPS (README.md:60)"},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP8_DENSE_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / FP8_DENSE_PEAK_TFLOPS, 4), "traffic": traffic},

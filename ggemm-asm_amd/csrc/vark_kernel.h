@@ -14,7 +14,8 @@
 //    are 45 whole 128-byte lines, so 384-byte windows are fetched without waste.
 //  * The token (K) axis is walked in stages of 128 tokens: 128 x 192 LHS bytes plus 128 x TN RHS
 //    bytes (64 or 72 KiB). Two stages live in the launch's 64 KiB dynamic LDS plus 96 KiB static
-//    (the full 160 KiB) and double-buffer global -> LDS with one workgroup barrier per stage.
+//    (the full 160 KiB, one flat space) and double-buffer global -> LDS with one workgroup
+//    barrier per stage. The epilogue stages C through the slot the last stage has freed.
 //  * Global -> LDS uses buffer loads that write LDS directly (16 B per lane). Each such load
 //    covers consecutive token rows of the tile (3.2 rows of 320 B or 5.3 rows of 192 B), so a
 //    wave-instruction touches few cache lines. The buffer resource is rebased at the stage's
@@ -84,30 +85,38 @@ struct Cfg {
   static_assert(ScaleLanesR * 5 >= ScaleChunksR && ScaleLanesR <= 64, "scale DMA coverage");
   static_assert(4096 * 2 + 8 * (kXcds + 1) + 2 * ScaleStage + 512 <= kMiscBytes, "misc LDS budget");
   __device__ static __forceinline__ int rswz(int t) { return kTN == 384 ? ((t >> 1) & 7) : ((t >> 2) & 3); }
+  // Epilogue staging: per wave 48 rows of WaveN bf16 (EpiChunks 16-byte chunks per row), read back
+  // in EpiReads 64-lane passes. Rows of 12 chunks XOR the chunk with (row >> 2) & 3 so that the
+  // 16 rows of one 8-byte write land in distinct bank slots; rows of 10 chunks need no swizzle
+  // (their starts already cover the 16 slots twice).
+  static constexpr int EpiRow = 2 * WaveN;                        // 192 or 160 bytes
+  static constexpr int EpiChunks = EpiRow / 16;                   // 12 or 10
+  static constexpr int EpiRegion = 48 * EpiRow;                   // 9216 or 7680 bytes per wave
+  static constexpr int EpiReads = (48 * EpiChunks + 63) / 64;     // 9 or 8
+  static constexpr int EpiStores = 2 * EpiReads;                  // per wave and full tile
+  static_assert(kWaves * EpiRegion <= kLhsBytes + RhsBytes, "epilogue staging fits a slot");
+  __device__ static __forceinline__ int eswz(int r) { return kTN == 384 ? ((r >> 2) & 3) : 0; }
 };
 __device__ __forceinline__ int lswz(int t) { return (t >> 2) & 3; }
 
-// LDS map. Slot s holds one stage: LHS rows at L[s], RHS rows at R[s]. TN = 320 (64 KiB stages):
-// slot 0 = the dynamic window, slot 1 = static [0, 64K), misc = static [64K, 80K). TN = 384
-// (72 KiB stages): slot 0 = LHS static [0, 24K) + RHS dynamic [0, 48K), slot 1 = static
-// [24K, 96K), misc = dynamic [48K, 64K).
+// LDS map. The launch's dynamic window starts right after the 96 KiB static array (the kernel
+// checks this), so the workgroup sees one flat 160 KiB space. Slot s (one stage: LHS rows, then
+// RHS rows) starts at s * (24 KiB + RHS bytes): 64 KiB slots for TN = 320, 72 KiB for TN = 384;
+// the group order, XCD bounds and MXFP8 scales follow the two slots. After a tile's last stage its
+// slot is free and stages the tile's C in the epilogue.
 struct LdsMap {
   GG_LDS uint8_t* L[2];
   GG_LDS uint8_t* R[2];
   GG_LDS uint8_t* misc;
 };
 template <int kTN>
-__device__ __forceinline__ LdsMap lds_map(GG_LDS uint8_t* dyn, GG_LDS uint8_t* st) {
+__device__ __forceinline__ LdsMap lds_map(GG_LDS uint8_t* base) {
+  constexpr int kSlot = kLhsBytes + Cfg<kTN>::RhsBytes;
+  static_assert(2 * kSlot + kMiscBytes <= kStaticLdsBytes + kDynLdsBytes, "LDS budget");
   LdsMap m;
-  if constexpr (kTN == 320) {
-    m.L[0] = dyn; m.R[0] = dyn + kLhsBytes;
-    m.L[1] = st;  m.R[1] = st + kLhsBytes;
-    m.misc = st + 65536;
-  } else {
-    m.L[0] = st;             m.R[0] = dyn;
-    m.L[1] = st + kLhsBytes; m.R[1] = st + 2 * kLhsBytes;
-    m.misc = dyn + Cfg<kTN>::RhsBytes;
-  }
+  m.L[0] = base;         m.R[0] = base + kLhsBytes;
+  m.L[1] = base + kSlot; m.R[1] = base + kSlot + kLhsBytes;
+  m.misc = base + 2 * kSlot;
   return m;
 }
 
@@ -166,12 +175,11 @@ __device__ __forceinline__ void dma16(v4i rsrc, uint32_t lds_addr, int voff) {
 }
 #pragma clang diagnostic pop
 
-// One 8-byte store of C, written as a single instruction from inline asm so that a full tile's
-// epilogue issues exactly kMB * NB stores per wave (the next tile's first wait counts on it).
-// (A non-temporal hint measured 11% slower: the partial-line stores then bypass L2 combining.)
-__device__ __forceinline__ void store_c8(uint16_t* p, uint2 v) {
-  asm volatile("global_store_dwordx2 %0, %1, off" : : "v"(p), "v"(v) : "memory");
-}
+// One 16-byte store of C (one global_store_dwordx4, so a full tile's epilogue issues exactly
+// Cfg::EpiStores stores per wave; the next tile's first wait counts on it). Left to the compiler
+// rather than inline asm: a VALU write to the data registers of a store wider than 8 bytes must
+// trail it by two wait states on gfx950, which the compiler inserts only for stores it emits.
+__device__ __forceinline__ void store_c16(uint16_t* p, v4i v) { *(v4i*)p = v; }
 
 __device__ __forceinline__ uint32_t lds_u32(const GG_LDS void* p) {
   return (uint32_t)reinterpret_cast<uintptr_t>(p);
@@ -321,11 +329,11 @@ struct Tile {
 };
 
 template <bool kMX, bool kLegacyK32, int kTN>
-__device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* dyn, GG_LDS uint8_t* st) {
+__device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds) {
   static_assert(!(kMX && kLegacyK32), "block scales need the scaled MFMA");
   using C = Cfg<kTN>;
   constexpr int NB = C::NB;
-  const LdsMap lm = lds_map<kTN>(dyn, st);
+  const LdsMap lm = lds_map<kTN>(lds);
   GG_LDS int* s_order = (GG_LDS int*)lm.misc;
   GG_LDS int* s_size = (GG_LDS int*)(lm.misc + 4096);
   GG_LDS int64_t* s_bound = (GG_LDS int64_t*)(lm.misc + 8192);
@@ -457,7 +465,7 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* dyn
 
   int cur = 0;              // LDS slot holding the next stage to compute
   bool prefetched = false;  // stage 0 of tile t was issued during the previous tile
-  bool full_prev = false;   // the previous epilogue issued all kMB * NB stores in every wave
+  bool full_prev = false;   // the previous epilogue issued all EpiStores stores in every wave
   int64_t t = t_begin;
   Tile T;
   if (t < t_end) T = tile_at(t);
@@ -482,7 +490,7 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* dyn
       // Stage s landed for this wave; after the barrier it has for all waves, and every wave is
       // done computing stage s-1, so its slot may take the next prefetch.
       if (s == 0 && stores_after_stage0)
-        wait_vmcnt<kMB * NB>();
+        wait_vmcnt<C::EpiStores>();
       else
         wait_vmcnt<0>();
       lds_barrier();
@@ -524,22 +532,42 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* dyn
       cur ^= 1;
     }
 
-    // ---- epilogue: lane holds C[m][n..n+3] for m = m0+wm*96+i*16+s16, n = n0+wn*TN/4+j*16+4q
+    // ---- epilogue. Lane holds C[m][n..n+3] for m = m0+wm*96+i*16+s16, n = n0+wn*TN/4+j*16+4q.
+    // The values go through a private region of the free slot (the last stage's) so that each
+    // store instruction writes 16 bytes per lane along whole row segments of C: per pass of three
+    // m-blocks a wave stages 48 rows x TN/4 columns of bf16, reads them back as 16-byte chunks in
+    // row order and stores them. One barrier first: every wave must be done with the last stage.
+    lds_barrier();
+    GG_LDS uint8_t* stg = (cur ? lm.L[0] : lm.L[1]) + wave * C::EpiRegion;
+    // Opaque copy of the lane id: keeps the compiler from hoisting the epilogue's per-lane address
+    // arithmetic out of the tile loop, where it would hold registers through the stages.
+    int el = lane;
+    asm volatile("" : "+v"(el));
     uint16_t* cg = a.out + (int64_t)T.g * a.stride_cg;
 #pragma unroll
-    for (int i = 0; i < kMB; ++i) {
-      const int m = T.m0 + wm * kWaveM + i * 16 + s16;
-      if (m >= a.OUT_M) continue;
-      uint16_t* crow = cg + (int64_t)m * a.stride_cm;
+    for (int p = 0; p < 2; ++p) {
 #pragma unroll
-      for (int j = 0; j < NB; ++j) {
-        const int n = T.n0 + wn * C::WaveN + j * 16 + 4 * q;
-        if (n >= a.OUT_N) continue;
-        const v4f v = acc[i][j];
-        uint2 pk;
-        pk.x = f32_to_bf16_rne(v[0] * alpha) | (f32_to_bf16_rne(v[1] * alpha) << 16);
-        pk.y = f32_to_bf16_rne(v[2] * alpha) | (f32_to_bf16_rne(v[3] * alpha) << 16);
-        store_c8(crow + n, pk);
+      for (int ii = 0; ii < 3; ++ii) {
+        const int r = ii * 16 + s16;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          const v4f v = acc[3 * p + ii][j];
+          const v2i pk = v2i{(int)(f32_to_bf16_rne(v[0] * alpha) | (f32_to_bf16_rne(v[1] * alpha) << 16)),
+                             (int)(f32_to_bf16_rne(v[2] * alpha) | (f32_to_bf16_rne(v[3] * alpha) << 16))};
+          const int c = 2 * j + (q >> 1);
+          *(GG_LDS v2i*)(stg + r * C::EpiRow + 16 * (c ^ C::eswz(r)) + 8 * (q & 1)) = pk;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < C::EpiReads; ++k) {
+        const int f = k * 64 + el;
+        const int r = f / C::EpiChunks;
+        const int c = f - r * C::EpiChunks;
+        const v4i v = *(const GG_LDS v4i*)(stg + r * C::EpiRow + 16 * (c ^ C::eswz(r)));
+        const int m = T.m0 + wm * kWaveM + 48 * p + r;
+        const int n = T.n0 + wn * C::WaveN + 8 * c;
+        if ((C::EpiReads * 64 == 48 * C::EpiChunks || f < 48 * C::EpiChunks) && m < a.OUT_M && n < a.OUT_N)
+          store_c16(cg + (int64_t)m * a.stride_cm + n, v);
       }
     }
     full_prev = T.m0 + kTileM <= a.OUT_M && T.n0 + kTN <= a.OUT_N;
@@ -559,11 +587,13 @@ __device__ __forceinline__ void vark_entry(const VarKArgs& a, GG_LDS uint8_t* dy
   if (pkt->group_segment_size < __builtin_amdgcn_groupstaticsize() + (uint32_t)kDynLdsBytes) return;
   if (a.G <= 0) return;
   GG_LDS uint8_t* st = (GG_LDS uint8_t*)static_lds;
+  // The stage slots span both arrays: the dynamic window must follow the static one directly.
+  if (lds_u32(dyn) != lds_u32(st) + (uint32_t)kStaticLdsBytes) return;
   // MXFP8 keeps the 320-wide tiles: its per-block scale registers do not fit next to 6 x 6 blocks.
   if (!kMX && a.OUT_N % 384 == 0)
-    vark_body<kMX, kLegacyK32, 384>(a, dyn, st);
+    vark_body<kMX, kLegacyK32, 384>(a, st);
   else
-    vark_body<kMX, kLegacyK32, 320>(a, dyn, st);
+    vark_body<kMX, kLegacyK32, 320>(a, st);
 }
 
 }  // namespace ggemm

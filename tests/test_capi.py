@@ -141,6 +141,48 @@ def test_code_object_symbol_and_kernarg_layout(pkg):
     assert lds + 65536 <= 160 * 1024   # static LDS + the launch's 64 KiB dynamic fit gfx950's 160 KiB
 
 
+def _vgpr_set(op):
+    m = re.fullmatch(r"v\[(\d+):(\d+)\]", op) or re.fullmatch(r"v(\d+)", op)
+    if not m:
+        return set()
+    lo = int(m.group(1))
+    hi = int(m.group(2)) if m.lastindex == 2 else lo
+    return set(range(lo, hi + 1))
+
+
+def test_wide_store_data_hazard(pkg):
+    """gfx950: a VALU may not write the data VGPRs of a preceding VMEM store wider than 8 bytes
+    within two wait states. The compiler pads the stores it emits; this guards against a wide
+    store slipping in from inline asm (it corrupted the first dword of stored chunks)."""
+    objdump = "/opt/rocm/llvm/bin/llvm-objdump"
+    if not os.path.exists(objdump):
+        pytest.skip("llvm-objdump not available")
+    txt = subprocess.run([objdump, "-d", "--mcpu=gfx950", pkg.CODE_OBJECT_PATH], capture_output=True,
+                         text=True, timeout=60).stdout
+    ins = [l.split("//")[0].strip() for l in txt.splitlines() if l.startswith("\t") or l.startswith("  ")]
+    ins = [i for i in ins if i]
+    n_wide = 0
+    for k, i in enumerate(ins):
+        m = re.match(r"(global|buffer|flat)_store_dword(x3|x4)\s+(\S+),\s*(\S+)", i)
+        if not m:
+            continue
+        n_wide += 1
+        data = _vgpr_set(m.group(4).rstrip(",") if m.group(1) == "global" else m.group(3).rstrip(","))
+        states = 0
+        for nxt in ins[k + 1:k + 4]:
+            if states >= 2:
+                break
+            nop = re.match(r"s_nop\s+(\d+)", nxt)
+            if nop:
+                states += int(nop.group(1)) + 1
+                continue
+            if nxt.startswith("v_"):
+                dst = nxt.split()[1].rstrip(",") if len(nxt.split()) > 1 else ""
+                assert not (_vgpr_set(dst) & data), f"store-data hazard: {i!r} then {nxt!r}"
+            states += 1
+    assert n_wide >= 1
+
+
 def test_m0_only_feeds_lds_dma(pkg):
     """The LDS-DMA loads set m0 from inline asm; nothing else in the kernels may use m0."""
     objdump = "/opt/rocm/llvm/bin/llvm-objdump"
