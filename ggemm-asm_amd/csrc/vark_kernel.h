@@ -39,12 +39,16 @@
 #include <hsa/hsa.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 namespace ggemm {
 
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 #define GG_LDS __attribute__((address_space(3)))
 
 constexpr int kThreads = 512;
@@ -279,6 +283,19 @@ __device__ __forceinline__ v8i read_operand(const GG_LDS uint8_t* p) {
   return v8i{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
 }
 
+// Compile-time loop: f(std::integral_constant<int, 0>) ... f(std::integral_constant<int, N-1>).
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// e8m0 scale registers of the 64-token pipeline hold one block scale per byte (op_sel picks it).
+constexpr int kUnitScales = 0x7f7f7f7f;   // 2^0 in every byte
+
 template <bool kLegacyK32>
 __device__ __forceinline__ v4f mfma(const v8i& a_rhs, const v8i& b_lhs, v4f acc, int sc_a, int sc_b) {
   if constexpr (kLegacyK32) {
@@ -330,28 +347,35 @@ struct Tile {
   int64_t kb, klen;
 };
 
-template <bool kMX, bool kLegacyK32, int kTN>
-__device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds) {
-  static_assert(!(kMX && kLegacyK32), "block scales need the scaled MFMA");
-  using C = Cfg<kTN>;
-  constexpr int NB = C::NB;
-  const LdsMap lm = lds_map<kTN>(lds);
-  GG_LDS int* s_order = (GG_LDS int*)lm.misc;
-  GG_LDS int* s_size = (GG_LDS int*)(lm.misc + 4096);
-  GG_LDS int64_t* s_bound = (GG_LDS int64_t*)(lm.misc + 8192);
-  GG_LDS uint8_t* scales = lm.misc + 8192 + 8 * (kXcds + 1) + 56;   // 16-byte aligned
+// ----------------------------------------------------------------------------------- schedule
 
+// Persistent static schedule (no workspace exists in the launch contract). Groups are ranked by
+// descending token count (stable), so expensive tiles are dealt first. The hardware deals
+// workgroup ids round-robin over the 8 XCDs, each with its own L2: every XCD takes a contiguous
+// slice of the size-sorted tile list holding 1/8 of the total work (tile weight: its stage count
+// + 1 for the epilogue), and its workgroups walk that slice round-robin. XCDs then stream
+// different groups at any moment instead of all pulling the same rows through the same
+// memory-side slices, and the 32 CUs of an XCD share panels. Tiles of a group are visited in
+// bands of kBandN N-tiles, M-tile by M-tile inside a band, so 32 consecutive tiles (what one
+// XCD's CUs hold at a time) form an 8 x 4 block of the group's grid.
+struct Sched {
+  int t_begin, t_end, step;   // this workgroup's tiles: t_begin, t_begin + step, ... below t_end
+  int n_tm, n_tn, tiles_per_group;
+  bool sorted;
+  bool valid;                 // false: more tiles than 32-bit indices cover (C would need > 512 GiB)
+};
+
+template <int kTN, int kK>
+__device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_order, GG_LDS int* s_size,
+                                            GG_LDS int64_t* s_bound) {
+  Sched S;
   const hsa_kernel_dispatch_packet_t* pkt = dispatch_packet();
   const int num_wg = (int)((pkt->grid_size_x + pkt->workgroup_size_x - 1) / pkt->workgroup_size_x);
-
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = a.G;
 
-  // ---- group order: descending token count (stable), so expensive tiles are dealt first
-  const bool sorted = G <= kMaxSortG;
-  if (sorted) {
+  S.sorted = G <= kMaxSortG;
+  if (S.sorted) {
     for (int g = tid; g < G; g += kThreads) {
       int64_t sz = a.group_offs[g + 1] - a.group_offs[g];
       s_size[g] = (int)(sz > 0x7fffffff ? 0x7fffffff : (sz < 0 ? 0 : sz));
@@ -369,36 +393,32 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
     __syncthreads();
   }
 
-  const int n_tm = (a.OUT_M + kTileM - 1) / kTileM;
-  const int n_tn = (a.OUT_N + kTN - 1) / kTN;
-  const int tiles_per_group = n_tm * n_tn;
-  const int64_t total = (int64_t)G * tiles_per_group;
+  S.n_tm = (a.OUT_M + kTileM - 1) / kTileM;
+  S.n_tn = (a.OUT_N + kTN - 1) / kTN;
+  S.tiles_per_group = S.n_tm * S.n_tn;
+  const int64_t total = (int64_t)G * S.tiles_per_group;
+  S.valid = total <= (1 << 30);
+  S.t_begin = S.t_end = S.step = 0;
+  if (!S.valid) return S;
 
-  // ---- XCD partition. The hardware deals workgroup ids round-robin over the 8 XCDs, each with its
-  // own L2. Every XCD takes a contiguous slice of the (size-sorted) tile list holding 1/8 of the
-  // total work (tile weight: its stage count + 1 for the epilogue), and its workgroups walk that
-  // slice round-robin. XCDs then stream different groups at any moment instead of all pulling
-  // the same rows through the same memory-side slices, and the 32 CUs of an XCD share panels.
   const int pid = blockIdx.x;
   const int n_xcd = (num_wg % kXcds == 0) ? kXcds : 1;
   const int xcd = pid % n_xcd;
-  const int wg_in_xcd = pid / n_xcd;
-  const int wgs_per_xcd = num_wg / n_xcd;
+  const int tpg = S.tiles_per_group;
   if (tid == 0) {
-    if (sorted && n_xcd > 1) {
+    if (S.sorted && n_xcd > 1) {
       int64_t total_w = 0;
-      for (int sl = 0; sl < G; ++sl)
-        total_w += (int64_t)tiles_per_group * (((int64_t)s_size[s_order[sl]] + kKStep - 1) / kKStep + 1);
+      for (int sl = 0; sl < G; ++sl) total_w += (int64_t)tpg * (((int64_t)s_size[s_order[sl]] + kK - 1) / kK + 1);
       int64_t acc_w = 0;
       int x = 1;
       s_bound[0] = 0;
       for (int sl = 0; sl < G && x < n_xcd; ++sl) {
-        const int64_t w = ((int64_t)s_size[s_order[sl]] + kKStep - 1) / kKStep + 1;
-        const int64_t slot_w = w * tiles_per_group;
+        const int64_t w = ((int64_t)s_size[s_order[sl]] + kK - 1) / kK + 1;
+        const int64_t slot_w = w * tpg;
         while (x < n_xcd && acc_w + slot_w >= (total_w * x) / n_xcd) {
           const int64_t need = (total_w * x) / n_xcd - acc_w;
           const int64_t i = (need + w - 1) / w;
-          s_bound[x++] = (int64_t)sl * tiles_per_group + (i < tiles_per_group ? i : tiles_per_group);
+          s_bound[x++] = (int64_t)sl * tpg + (i < tpg ? i : tpg);
         }
         acc_w += slot_w;
       }
@@ -408,30 +428,52 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
     }
   }
   __syncthreads();
-  const int64_t t_begin = s_bound[xcd] + wg_in_xcd;
-  const int64_t t_end = s_bound[xcd + 1];
+  S.t_begin = (int)s_bound[xcd] + pid / n_xcd;
+  S.t_end = (int)s_bound[xcd + 1];
+  S.step = num_wg / n_xcd;
+  return S;
+}
 
-  // Tiles of a group are visited in bands of kBandN N-tiles, M-tile by M-tile inside a band, so 32
-  // consecutive tiles (what one XCD's CUs hold at a time) form an 8 x 4 block of the group's grid.
+template <int kTN, int kK>
+__device__ __forceinline__ Tile tile_at(const Sched& S, const VarKArgs& a, const GG_LDS int* s_order, int t) {
   constexpr int kBandN = 4;
-  auto tile_at = [&](int64_t t) {
-    Tile T;
-    const int slot = (int)(t / tiles_per_group);
-    const int in_g = (int)(t - (int64_t)slot * tiles_per_group);
-    T.g = sorted ? s_order[slot] : slot;
-    const int band = in_g / (n_tm * kBandN);
-    const int r = in_g - band * n_tm * kBandN;
-    const int bw = min(kBandN, n_tn - band * kBandN);
-    const int tm = r / bw;
-    const int tn = band * kBandN + (r - tm * bw);
-    T.m0 = tm * kTileM;
-    T.n0 = tn * kTN;
-    T.kb = a.group_offs[T.g];
-    const int64_t ke = a.group_offs[T.g + 1];
-    T.klen = ke > T.kb ? ke - T.kb : 0;
-    T.nsteps = (int)((T.klen + kKStep - 1) / kKStep);
-    return T;
-  };
+  Tile T;
+  const int slot = t / S.tiles_per_group;
+  const int in_g = t - slot * S.tiles_per_group;
+  T.g = S.sorted ? s_order[slot] : slot;
+  const int band = in_g / (S.n_tm * kBandN);
+  const int r = in_g - band * S.n_tm * kBandN;
+  const int bw = min(kBandN, S.n_tn - band * kBandN);
+  const int tm = r / bw;
+  const int tn = band * kBandN + (r - tm * bw);
+  T.m0 = tm * kTileM;
+  T.n0 = tn * kTN;
+  T.kb = a.group_offs[T.g];
+  const int64_t ke = a.group_offs[T.g + 1];
+  T.klen = ke > T.kb ? ke - T.kb : 0;
+  T.nsteps = (int)((T.klen + kK - 1) / kK);
+  return T;
+}
+
+template <bool kMX, bool kLegacyK32, int kTN>
+__device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds) {
+  static_assert(!(kMX && kLegacyK32), "block scales need the scaled MFMA");
+  using C = Cfg<kTN>;
+  constexpr int NB = C::NB;
+  const LdsMap lm = lds_map<kTN>(lds);
+  GG_LDS int* s_order = (GG_LDS int*)lm.misc;
+  GG_LDS int* s_size = (GG_LDS int*)(lm.misc + 4096);
+  GG_LDS int64_t* s_bound = (GG_LDS int64_t*)(lm.misc + 8192);
+  GG_LDS uint8_t* scales = lm.misc + 8192 + 8 * (kXcds + 1) + 56;   // 16-byte aligned
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  const Sched S = make_sched<kTN, kKStep>(a, s_order, s_size, s_bound);
+  if (!S.valid) return;
+  const int t_begin = S.t_begin, t_end = S.t_end, wgs_per_xcd = S.step;
+  auto tile_at_ = [&](int t) { return tile_at<kTN, kKStep>(S, a, s_order, t); };
 
   float alpha = 1.0f;
   if constexpr (!kMX) alpha = *(const float*)a.lhs_scale * *(const float*)a.rhs_scale;
@@ -468,14 +510,14 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
   int cur = 0;              // LDS slot holding the next stage to compute
   bool prefetched = false;  // stage 0 of tile t was issued during the previous tile
   bool full_prev = false;   // the previous epilogue issued all EpiStores stores in every wave
-  int64_t t = t_begin;
+  int t = t_begin;
   Tile T;
-  if (t < t_end) T = tile_at(t);
+  if (t < t_end) T = tile_at_(t);
   while (t < t_end) {
-    const int64_t t_next = t + wgs_per_xcd;
+    const int t_next = t + wgs_per_xcd;
     const bool has_next = t_next < t_end;
     Tile N;
-    if (has_next) N = tile_at(t_next);
+    if (has_next) N = tile_at_(t_next);
 
     v4f acc[kMB][NB];
 #pragma unroll
@@ -578,6 +620,238 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
   }
 }
 
+// ----------------------------------------------------------------------------------- 32x32x64 body
+
+// MXFP8 kernel when OUT_N is a multiple of 384: 192 x 384 tiles computed with
+// v_mfma_scale_f32_32x32x64_f8f6f4, two per 32 x 32 block and 128-token stage, on the same stage
+// pipeline as the 16x16x128 body (two 72 KiB slots, one barrier per stage, the next tile's first
+// stage issued during the last one, C staged through the freed slot). The 16x16x128 body cannot
+// hold 6 x 6 blocks next to their per-block scale registers at this width (it spills); 3 x 3
+// blocks of 32 x 32 need 48 operand VGPRs instead of 64, and one packed scale register per side.
+// (For the per-tensor kernel this body measured 2% slower than the 16x16x128 one: it takes 3%
+// fewer cycles per launch but draws more power, and the kernel runs power-limited, ~2.0-2.1 GHz
+// with loads and MFMAs both busy against ~2.4 GHz with either alone.)
+//
+//  * 8 waves in a 2 x 4 grid, 96 x 96 per wave = 3 x 3 blocks of 32 x 32 (16 accumulators each,
+//    144 in all); per half-stage 3 n-blocks + 3 m-blocks of 8 operand VGPRs.
+//  * 32x32x64 operand layout (measured): lane l feeds row l % 32 of its operand; bytes 0-15 hold
+//    16 tokens of K-block 0 (the half-stage's tokens 0-31), bytes 16-31 16 tokens of K-block 1
+//    (32-63), lane half h = l / 32 taking tokens 16h.. of each block; the e8m0 scale of K-block b
+//    for row i comes from lane i + 32b. Here bytes 0-15 = tokens 16h + 0..15 and bytes 16-31 =
+//    tokens 32 + 16h + 0..15: four ds_read_b64_tr_b8 at tokens +0, +8, +32, +40 of a lane base.
+//  * Accumulator r of lane l is C row (the A = RHS side) 8 (r / 4) + 4 (l / 32) + r % 4, column
+//    (the B = LHS side) l % 32: four consecutive OUT_N values of one OUT_M row per group of four.
+//  * LDS rows [token][W] with the 16-byte chunk XOR-swizzled by ((t >> 2) & 1) << 1 (W = 192) or
+//    ((t >> 1) & 3) << 1 (W = 384): the 8 tokens x 2 chunks a 32-lane half of a transposed read
+//    touches land in 32 distinct 8-byte bank pairs, and tokens +8, +32, +40, +64 keep the base's
+//    swizzle, so every read of a block is one address plus immediates.
+namespace x32 {
+constexpr int kTN = 384;
+constexpr int kRhsBytes = kKStep * kTN;                   // 48 KiB
+constexpr int kSlot = kLhsBytes + kRhsBytes;              // 72 KiB
+constexpr int kDmaRhs = kRhsBytes / 1024;                 // 48
+constexpr int kPerWave = (kDmaLhs + kDmaRhs) / kWaves;    // 9: 3 LHS + 6 RHS
+constexpr int kLhsPerWave = kDmaLhs / kWaves;             // 3
+constexpr int kMisc = 2 * kSlot;                          // 144 KiB: group order, XCD bounds, scales
+constexpr int kScaleStage = 4 * kTileM + 4 * kTN;         // e8m0 bytes per stage
+constexpr int kScaleOff = 8192 + 128;
+constexpr int kEpiRows = 32;                              // one 32 x 32 block row per pass
+constexpr int kEpiRegion = kEpiRows * 192;                // 6 KiB per wave
+constexpr int kEpiReads = kEpiRows * 12 / 64;             // 6 chunk reads per pass
+constexpr int kEpiStores = 3 * kEpiReads;                 // per wave and full tile
+static_assert((kDmaLhs + kDmaRhs) % kWaves == 0 && kDmaLhs % kWaves == 0, "uniform LDS-DMA split");
+static_assert(kMisc + kMiscBytes <= kStaticLdsBytes + kDynLdsBytes, "LDS budget");
+static_assert(kScaleOff + 2 * kScaleStage <= kMiscBytes, "misc budget");
+static_assert(kWaves * kEpiRegion <= kSlot, "epilogue staging fits a slot");
+__device__ __forceinline__ int swz_l(int t) { return ((t >> 2) & 1) << 1; }
+__device__ __forceinline__ int swz_r(int t) { return ((t >> 1) & 3) << 1; }
+__device__ __forceinline__ int swz_e(int r) { return (r >> 2) & 3; }   // epilogue rows of 12 chunks
+
+// Per-lane byte offsets of this wave's nine LDS-DMA instructions (relative to the stage's first
+// token and the tile's first column). Instruction i = wave + 8 j fills LDS bytes [1024 i, +1024)
+// of the slot: chunks q = 64 i + lane of the LHS rows (i < 24, 12 chunks per row), then of the
+// RHS rows (24 chunks per row); physical chunk pc of row t holds logical chunk pc ^ swizzle(t).
+struct Plan {
+  int voff[kPerWave];
+};
+__device__ __forceinline__ Plan make_plan(int wave, int lane, int stride_l, int stride_r) {
+  Plan d;
+#pragma unroll
+  for (int j = 0; j < kPerWave; ++j) {
+    const int i = wave + kWaves * j;
+    if (j < kLhsPerWave) {
+      const int q = 64 * i + lane, row = q / 12, pc = q - row * 12;
+      d.voff[j] = row * stride_l + 16 * (pc ^ swz_l(row));
+    } else {
+      const int q = 64 * (i - kDmaLhs) + lane, row = q / 24, pc = q - row * 24;
+      d.voff[j] = row * stride_r + 16 * (pc ^ swz_r(row));
+    }
+  }
+  return d;
+}
+
+// Four transposed reads of one 32-column operand block (row pitch kRow bytes) at a lane's base.
+template <int kRow>
+__device__ __forceinline__ v8i read32(const GG_LDS uint8_t* p) {
+  v2i r0 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((GG_LDS v2i*)(p));
+  v2i r1 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((GG_LDS v2i*)(p + 8 * kRow));
+  v2i r2 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((GG_LDS v2i*)(p + 32 * kRow));
+  v2i r3 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((GG_LDS v2i*)(p + 40 * kRow));
+  return v8i{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+}
+}  // namespace x32
+
+__device__ __forceinline__ void vark_body32(const VarKArgs& a, GG_LDS uint8_t* lds) {
+  using namespace x32;
+  GG_LDS uint8_t* misc = lds + kMisc;
+  GG_LDS int* s_order = (GG_LDS int*)misc;
+  GG_LDS int* s_size = (GG_LDS int*)(misc + 4096);
+  GG_LDS int64_t* s_bound = (GG_LDS int64_t*)(misc + 8192);
+  GG_LDS uint8_t* scales = misc + kScaleOff;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  const Sched S = make_sched<kTN, kKStep>(a, s_order, s_size, s_bound);
+  if (!S.valid) return;
+
+  const int wm = wave & 1;   // wave row (OUT_M) in the 2 x 4 wave grid
+  const int wn = wave >> 1;  // wave column (OUT_N)
+  const int g16 = lane >> 4, t16 = lane & 15;
+  const int cb = g16 & 1, hh = g16 >> 1;
+  const int tb0 = 16 * hh + (t16 >> 1);
+  const int rowi = lane & 31;
+  int off_m[3], off_n[3];   // slot-relative byte offsets of each block's first transposed read
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    off_m[i] = tb0 * kTileM + 16 * ((wm * 6 + 2 * i + cb) ^ swz_l(tb0)) + 8 * (t16 & 1);
+    off_n[i] = kLhsBytes + tb0 * kTN + 16 * ((wn * 6 + 2 * i + cb) ^ swz_r(tb0)) + 8 * (t16 & 1);
+  }
+  const Plan plan = make_plan(wave, lane, a.stride_lhs_m, a.stride_rhs_m);
+
+  auto issue = [&](const Tile& T, int step, int slot) {
+    const int64_t k0 = (int64_t)step * kKStep;
+    const int64_t rem = T.klen - k0;
+    const int rv = (int)(rem < kKStep ? rem : kKStep);
+    const uint32_t base = lds_u32(lds + slot * kSlot);
+    const v4i rl = make_rsrc(a.lhs + (T.kb + k0) * (int64_t)a.stride_lhs_m + T.m0, rv * a.stride_lhs_m - T.m0);
+    const v4i rr = make_rsrc(a.rhs + (T.kb + k0) * (int64_t)a.stride_rhs_m + T.n0, rv * a.stride_rhs_m - T.n0);
+#pragma unroll
+    for (int j = 0; j < kPerWave; ++j)
+      dma16(j < kLhsPerWave ? rl : rr, base + 1024 * (wave + kWaves * j), plan.voff[j]);
+    issue_stage_scales<kTN>(lds_u32(scales + slot * kScaleStage), (const uint8_t*)a.lhs_scale,
+                            (const uint8_t*)a.rhs_scale, (T.kb + k0) / 32, (rv + 31) / 32, a.stride_lhs_scale,
+                            a.stride_rhs_scale, T.m0, T.n0, wave, lane);
+  };
+
+  int cur = 0;              // LDS slot holding the next stage to compute
+  bool prefetched = false;  // stage 0 of tile t was issued during the previous tile
+  bool full_prev = false;   // the previous epilogue issued all kEpiStores stores in every wave
+  int t = S.t_begin;
+  Tile T;
+  if (t < S.t_end) T = tile_at<kTN, kKStep>(S, a, s_order, t);
+  while (t < S.t_end) {
+    const int t_next = t + S.step;
+    const bool has_next = t_next < S.t_end;
+    Tile N;
+    if (has_next) N = tile_at<kTN, kKStep>(S, a, s_order, t_next);
+
+    v16f acc[3][3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+      for (int j = 0; j < 3; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    if (T.nsteps > 0 && !prefetched) issue(T, 0, cur);
+    // Stage 0 issued before the previous tile's stores: those stores are the youngest vector
+    // memory operations, so waiting down to their count retires exactly the older loads.
+    const bool stores_after_stage0 = prefetched && full_prev;
+    prefetched = false;
+    for (int s = 0; s < T.nsteps; ++s) {
+      // Stage s landed for this wave; after the barrier it has for all waves, and every wave is
+      // done computing stage s-1, so its slot may take the next prefetch.
+      if (s == 0 && stores_after_stage0)
+        wait_vmcnt<kEpiStores>();
+      else
+        wait_vmcnt<0>();
+      lds_barrier();
+      if (s + 1 < T.nsteps) {
+        issue(T, s + 1, cur ^ 1);
+      } else if (has_next && N.nsteps > 0) {
+        issue(N, 0, cur ^ 1);
+        prefetched = true;
+      }
+
+      const GG_LDS uint8_t* sb = lds + cur * kSlot;
+      static_for<2>([&](auto HF) {
+        constexpr int hf = decltype(HF)::value;   // tokens 64 hf .. 64 hf + 63 of the stage
+        // e8m0 scales of this lane's block 2 hf + hh: n-block j in byte j of scn, m-block i in
+        // byte i of scm (the MFMA's op_sel picks the byte)
+        const GG_LDS uint8_t* ss = scales + cur * kScaleStage;
+        const GG_LDS uint8_t* sn = ss + 4 * kTileM + (2 * hf + hh) * kTN + wn * 96 + rowi;
+        const GG_LDS uint8_t* sm = ss + (2 * hf + hh) * kTileM + wm * 96 + rowi;
+        const int scn = (int)sn[0] | ((int)sn[32] << 8) | ((int)sn[64] << 16);
+        const int scm = (int)sm[0] | ((int)sm[32] << 8) | ((int)sm[64] << 16);
+        v8i bn[3], am[3];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) bn[j] = read32<kTN>(sb + off_n[j] + 64 * hf * kTN);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) am[i] = read32<kTileM>(sb + off_m[i] + 64 * hf * kTileM);
+        static_for<3>([&](auto I) {
+          constexpr int i = decltype(I)::value;
+          static_for<3>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            // A (RHS) is e5m2 -> format 1 (bf8); B (LHS) is e4m3 -> format 0 (fp8)
+            acc[i][j] =
+                __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bn[j], am[i], acc[i][j], 1, 0, j, scn, i, scm);
+          });
+        });
+      });
+      cur ^= 1;
+    }
+
+    // ---- epilogue. Lane holds C[m][n..n+3] for m = m0 + 96 wm + 32 i + l % 32 and
+    // n = n0 + 96 wn + 32 j + 8 g + 4 (l / 32), g = 0..3. After one barrier the slot of the last
+    // stage is free; each wave stages one 32-row block row per pass through a private 6 KiB
+    // region of it, reads the rows back as 16-byte chunks and stores them non-temporally.
+    lds_barrier();
+    GG_LDS uint8_t* stg = lds + (cur ^ 1) * kSlot + wave * kEpiRegion;
+    // Opaque copy of the lane id: keeps the per-lane address arithmetic below out of the stage loop.
+    int el = lane;
+    asm volatile("" : "+v"(el));
+    const int hl = el >> 5, rl = el & 31;
+    uint16_t* cg = a.out + (int64_t)T.g * a.stride_cg;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+#pragma unroll
+      for (int j = 0; j < 3; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const v2i pk = v2i{(int)(f32_to_bf16_rne(acc[i][j][4 * g]) | (f32_to_bf16_rne(acc[i][j][4 * g + 1]) << 16)),
+                             (int)(f32_to_bf16_rne(acc[i][j][4 * g + 2]) | (f32_to_bf16_rne(acc[i][j][4 * g + 3]) << 16))};
+          const int c = 4 * j + g;   // 16-byte chunk of columns 32 j + 8 g .. + 7; half hl
+          *(GG_LDS v2i*)(stg + rl * 192 + 16 * (c ^ swz_e(rl)) + 8 * hl) = pk;
+        }
+#pragma unroll
+      for (int k = 0; k < kEpiReads; ++k) {
+        const int f = 64 * k + el;
+        const int r = f / 12;
+        const int c = f - 12 * r;
+        const v4i v = *(const GG_LDS v4i*)(stg + r * 192 + 16 * (c ^ swz_e(r)));
+        const int m = T.m0 + 96 * wm + 32 * i + r;
+        const int n = T.n0 + 96 * wn + 8 * c;
+        if (m < a.OUT_M && n < a.OUT_N) store_c16(cg + (int64_t)m * a.stride_cm + n, v);
+      }
+    }
+    full_prev = T.m0 + kTileM <= a.OUT_M && T.n0 + kTN <= a.OUT_N;
+    t = t_next;
+    T = N;
+  }
+}
+
 // Entry body shared by all kernels: checks the launch's LDS, then runs the 384-wide tile
 // configuration when OUT_N is a multiple of 384 (tensorwise kernels) and the 320-wide one
 // otherwise.
@@ -591,11 +865,14 @@ __device__ __forceinline__ void vark_entry(const VarKArgs& a, GG_LDS uint8_t* dy
   GG_LDS uint8_t* st = (GG_LDS uint8_t*)static_lds;
   // The stage slots span both arrays: the dynamic window must follow the static one directly.
   if (lds_u32(dyn) != lds_u32(st) + (uint32_t)kStaticLdsBytes) return;
-  // MXFP8 keeps the 320-wide tiles: its per-block scale registers do not fit next to 6 x 6 blocks.
-  if (!kMX && a.OUT_N % 384 == 0)
-    vark_body<kMX, kLegacyK32, 384>(a, st);
-  else
+  if (a.OUT_N % 384 == 0) {
+    if constexpr (kMX)
+      vark_body32(a, st);
+    else
+      vark_body<false, kLegacyK32, 384>(a, st);
+  } else {
     vark_body<kMX, kLegacyK32, 320>(a, st);
+  }
 }
 
 }  // namespace ggemm

@@ -152,11 +152,13 @@ def test_all_fp8_codes_error_bound(pkg, orc, cuda, mfma):
     _error_bound_ok(orc, pkg.as_bf16_bits(out), lhs, rhs, offs, sl, sr, f"codes/{mfma}")
 
 
-def test_mxfp8_all_codes_random_scales(pkg, orc, cuda):
-    """MX path with random codes and random e8m0 scales, against the same rigorous bound."""
-    _say("mxfp8 all-codes random scales")
-    lens = [64, 0, 96, 45]
-    lhs, rhs, offs, (sl, sr), _ = _rand_bytes_problem(lens, 64, 128, seed=8, mx=True, dist="codes")
+@pytest.mark.parametrize("on", [128, 384, 768])
+def test_mxfp8_all_codes_random_scales(pkg, orc, cuda, on):
+    """MX path with random codes and random e8m0 scales (every scale byte position of both tile
+    widths), against the same rigorous bound."""
+    _say(f"mxfp8 all-codes random scales OUT_N={on}")
+    lens = [64, 0, 96, 32, 213]
+    lhs, rhs, offs, (sl, sr), _ = _rand_bytes_problem(lens, 208, on, seed=8, mx=True, dist="codes")
     out = pkg.grouped_gemm_mxfp8_variable_k(lhs.to(cuda), rhs.to(cuda), sl.to(cuda), sr.to(cuda), offs.to(cuda))
     torch.cuda.synchronize()
     _error_bound_ok(orc, pkg.as_bf16_bits(out), lhs, rhs, offs, 1.0, 1.0, "mx codes", lsc=sl, rsc=sr)
@@ -205,7 +207,9 @@ def test_many_groups_natural_order(pkg, orc, cuda):
     _assert_parity(orc, pkg.as_bf16_bits(out), ref, offs.numpy(), "G=1100")
 
 
-MX_CASES = [([64, 0, 96, 45], 64, 128), ([32] * 5 + [0, 128, 256], 192, 320), ([512, 0, 64], 208, 336)]
+MX_CASES = [([64, 0, 96, 45], 64, 128), ([32] * 5 + [0, 128, 256], 192, 320), ([512, 0, 64], 208, 336),
+            # OUT_N multiples of 384 take the 192 x 384 tile configuration
+            ([64, 0, 96, 45], 64, 384), ([32] * 5 + [0, 128, 256], 400, 768), ([1024, 32], 192, 1152)]
 
 
 @pytest.mark.parametrize("lens,om,on", MX_CASES, ids=[f"mx{i}" for i in range(len(MX_CASES))])
