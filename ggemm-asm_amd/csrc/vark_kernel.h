@@ -33,6 +33,9 @@
 //    the work, and its 32 CUs walk the slice round-robin in 4-wide N bands, so CUs of one XCD
 //    share L2 panels and different XCDs stream different rows. The first stage of a workgroup's
 //    next tile is loaded while it finishes the current one.
+//  * The MXFP8 kernel at OUT_N multiples of 384 runs a second body on the same pipeline with the
+//    32x32x64 scaled MFMA (vark_body32 below): 6 x 6 blocks of 16 x 16 do not fit next to their
+//    per-block scale registers.
 #pragma once
 
 #include <hip/hip_runtime.h>
