@@ -66,6 +66,7 @@ constexpr int kDynLdsBytes = 65536;                         // launch contract: 
 constexpr int kStaticLdsBytes = 98304;                      // + 96 KiB static = gfx950's 160 KiB
 constexpr int kMaxSortG = 1024;                             // larger G: natural group order
 constexpr int kXcds = 8;                                    // MI355X: 8 XCDs, 32 CUs each
+constexpr int kXcdPairs = kXcds / 2;                        // schedule slices, two XCDs each
 constexpr int kMiscBytes = 16384;                           // group order, sizes, XCD bounds, e8m0
 constexpr uint32_t kRsrcWord3 = 0x00020000u;                // raw buffer, 32-bit data format
 
@@ -354,13 +355,15 @@ struct Tile {
 
 // Persistent static schedule (no workspace exists in the launch contract). Groups are ranked by
 // descending token count (stable), so expensive tiles are dealt first. The hardware deals
-// workgroup ids round-robin over the 8 XCDs, each with its own L2: every XCD takes a contiguous
-// slice of the size-sorted tile list holding 1/8 of the total work (tile weight: its stage count
-// + 1 for the epilogue), and its workgroups walk that slice round-robin. XCDs then stream
-// different groups at any moment instead of all pulling the same rows through the same
-// memory-side slices, and the 32 CUs of an XCD share panels. Tiles of a group are visited in
-// bands of kBandN N-tiles, M-tile by M-tile inside a band, so 32 consecutive tiles (what one
-// XCD's CUs hold at a time) form an 8 x 4 block of the group's grid.
+// workgroup ids round-robin over the 8 XCDs, each with its own L2. The size-sorted tile list is
+// cut into kXcdPairs contiguous slices of equal work (tile weight: its stage count + 1 for the
+// epilogue); the two XCDs x and x + kXcdPairs share slice x and take alternate rounds of 32
+// consecutive tiles, their 32 workgroups one tile each. The 32 CUs of an XCD then share L2
+// panels, and only four groups stream at a time, so their rows stay in the memory-side cache
+// (256 MB) for the partner XCD (one XCD per slice keeps eight groups, ~280 MB, in flight and
+// measured 1.5% slower). Tiles of a group are visited in bands of kBandN N-tiles, M-tile by
+// M-tile inside a band, so 32 consecutive tiles (one XCD's round) form an 8 x 4 block of the
+// group's grid.
 struct Sched {
   int t_begin, t_end, step;   // this workgroup's tiles: t_begin, t_begin + step, ... below t_end
   int n_tm, n_tn, tiles_per_group;
@@ -405,8 +408,13 @@ __device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_ord
   if (!S.valid) return S;
 
   const int pid = blockIdx.x;
-  const int n_xcd = (num_wg % kXcds == 0) ? kXcds : 1;
-  const int xcd = pid % n_xcd;
+  // XCDs per slice and slices: pairs when the grid spreads evenly over the 8 XCDs
+  const bool spread = num_wg % kXcds == 0;
+  const int xcds = spread ? kXcds : 1;
+  const int n_xcd = spread ? kXcdPairs : 1;   // slices
+  const int per_slice = xcds / n_xcd;
+  const int xcd = pid % xcds;
+  const int slice = xcd % n_xcd, part = xcd / n_xcd;
   const int tpg = S.tiles_per_group;
   if (tid == 0) {
     if (S.sorted && n_xcd > 1) {
@@ -431,9 +439,10 @@ __device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_ord
     }
   }
   __syncthreads();
-  S.t_begin = (int)s_bound[xcd] + pid / n_xcd;
-  S.t_end = (int)s_bound[xcd + 1];
-  S.step = num_wg / n_xcd;
+  const int wgs_per_xcd = num_wg / xcds;
+  S.t_begin = (int)s_bound[slice] + part * wgs_per_xcd + pid / xcds;
+  S.t_end = (int)s_bound[slice + 1];
+  S.step = per_slice * wgs_per_xcd;
   return S;
 }
 
