@@ -559,11 +559,15 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
 
       const GG_LDS uint8_t* sl = cur ? lm.L[1] : lm.L[0];
       const GG_LDS uint8_t* sr = cur ? lm.R[1] : lm.R[0];
+      // Per-tensor path: constant zero scale operands. The compiler then emits the unscaled
+      // v_mfma_f32_16x16x128_f8f6f4 (one instruction instead of a scale-load prefix plus the MFMA),
+      // which computes exactly what scale 127 (2^0) does (measured bit-identical); a CPU test
+      // checks the code object holds the unscaled form.
       int sc_n[NB], sc_m[kMB];
 #pragma unroll
-      for (int j = 0; j < NB; ++j) sc_n[j] = 127;
+      for (int j = 0; j < NB; ++j) sc_n[j] = 0;
 #pragma unroll
-      for (int i = 0; i < kMB; ++i) sc_m[i] = 127;
+      for (int i = 0; i < kMB; ++i) sc_m[i] = 0;
       if constexpr (kMX) {
         const GG_LDS uint8_t* ss = scales + cur * C::ScaleStage;
 #pragma unroll

@@ -183,6 +183,19 @@ def test_wide_store_data_hazard(pkg):
     assert n_wide >= 1
 
 
+def test_tensorwise_code_object_uses_unscaled_mfma(pkg):
+    """The per-tensor kernels pass constant zero scale operands so the compiler emits the unscaled
+    v_mfma_f32_16x16x128_f8f6f4 (equal to scale 2^0, measured bit-identical on the GPU). A
+    compiler that emitted the scaled form for them would multiply C by 2^-254: catch it here."""
+    objdump = "/opt/rocm/llvm/bin/llvm-objdump"
+    if not os.path.exists(objdump):
+        pytest.skip("llvm-objdump not available")
+    txt = subprocess.run([objdump, "-d", "--mcpu=gfx950", pkg.CODE_OBJECT_PATH], capture_output=True,
+                         text=True, timeout=60).stdout
+    assert re.search(r"\bv_mfma_f32_16x16x128_f8f6f4\b", txt)
+    assert "v_mfma_scale" not in txt
+
+
 def test_m0_only_feeds_lds_dma(pkg):
     """The LDS-DMA loads set m0 from inline asm; nothing else in the kernels may use m0."""
     objdump = "/opt/rocm/llvm/bin/llvm-objdump"
