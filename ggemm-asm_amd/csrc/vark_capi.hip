@@ -53,6 +53,9 @@ int validate_common(const void* lhs, const void* rhs, const void* out, const voi
   if ((int64_t)scg < (int64_t)(OUT_M - 1) * scm + OUT_N) return GGEMM_E_STRIDE;
   // the kernel forms 32-bit buffer offsets of up to 128 rows of a stage
   if ((int64_t)slm * 129 > INT32_MAX || (int64_t)srm * 129 > INT32_MAX) return GGEMM_E_SHAPE;
+  // ... and 32-bit tile indices: at most 2^30 output tiles (counted with the narrower 320 tile)
+  const int64_t tiles = (int64_t)((OUT_M + ggemm::kTileM - 1) / ggemm::kTileM) * ((OUT_N + 319) / 320);
+  if ((int64_t)G * tiles > (int64_t(1) << 30)) return GGEMM_E_SHAPE;
   if (!aligned(lhs, 16) || !aligned(rhs, 16) || !aligned(out, 8)) return GGEMM_E_ALIGN;
   return GGEMM_OK;
 }
@@ -139,7 +142,9 @@ const char* ggemm_vark_strerror(int32_t code) {
   switch (code) {
     case GGEMM_OK: return "success";
     case GGEMM_E_NULL: return "a required pointer is NULL";
-    case GGEMM_E_SHAPE: return "invalid shape (G, OUT_M, OUT_N must be > 0, OUT_M/OUT_N multiples of 16)";
+    case GGEMM_E_SHAPE:
+      return "invalid shape (G, OUT_M, OUT_N must be > 0, OUT_M/OUT_N multiples of 16, row strides below "
+             "2^31/129, at most 2^30 output tiles)";
     case GGEMM_E_STRIDE: return "invalid strides (row strides >= width and multiples of 16, stride_cn == 1)";
     case GGEMM_E_ALIGN: return "misaligned pointer (LHS/RHS 16-byte, C 8-byte)";
     case GGEMM_E_OFFSETS: return "invalid group offsets (must start at 0, be non-decreasing, end <= M_total)";

@@ -22,7 +22,8 @@ extern "C" {
 enum {
   GGEMM_OK = 0,
   GGEMM_E_NULL = -1,        /* a required pointer is NULL */
-  GGEMM_E_SHAPE = -2,       /* G, OUT_M or OUT_N <= 0, or sizes overflow int32 strides */
+  GGEMM_E_SHAPE = -2,       /* G, OUT_M or OUT_N <= 0, OUT_M/OUT_N not multiples of 16, row strides
+                               too large for 32-bit stage offsets, or more than 2^30 output tiles */
   GGEMM_E_STRIDE = -3,      /* strides too small, stride_cn != 1, or not multiples of 16 / 4 */
   GGEMM_E_ALIGN = -4,       /* LHS/RHS not 16-byte aligned or C not 8-byte aligned */
   GGEMM_E_OFFSETS = -5,     /* host group offsets not 0-based, non-decreasing, or past M_total */

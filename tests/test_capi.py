@@ -81,6 +81,8 @@ def _call(lib, **kw):
     (dict(lhs=0), -1), (dict(offs=0), -1), (dict(G=0), -2), (dict(OUT_M=100, slm=100), -2),
     (dict(OUT_N=-16), -2), (dict(scn=2), -3), (dict(slm=2800), -3), (dict(srm=5768), -3),
     (dict(scm=5762), -3), (dict(scg=100), -3), (dict(lhs=FAKE + 8), -4), (dict(out=FAKE + 2), -4),
+    # more than 2^30 tiles of at most 192 x 320: 32-bit tile indices would overflow
+    (dict(G=(1 << 30) // 270 + 1), -2),
 ])
 def test_validation_rejects(pkg, kw, rc):
     assert _call(pkg.load_library(), **kw) == rc
