@@ -1,4 +1,5 @@
-"""ctypes binding of libggemm_vark.so (declarations in include/ggemm_vark.h)."""
+"""ctypes binding of libggemm_vark.so (declarations in include/ggemm_vark.h and
+include/ggemm_persistent.h)."""
 from __future__ import annotations
 
 import ctypes
@@ -19,9 +20,14 @@ EXPORTS = (
     "ggemm_vark_launch_geometry",
 )
 
+PERSISTENT_EXPORTS = (
+    "ggemm_persistent_fp8",
+)
+
 ERRORS = {
     0: "GGEMM_OK", -1: "GGEMM_E_NULL", -2: "GGEMM_E_SHAPE", -3: "GGEMM_E_STRIDE",
     -4: "GGEMM_E_ALIGN", -5: "GGEMM_E_OFFSETS", -6: "GGEMM_E_DEVICE", -7: "GGEMM_E_MX_ALIGN",
+    -8: "GGEMM_E_FORMAT",
 }
 
 
@@ -63,6 +69,8 @@ def load():
     lib.ggemm_vark_abi_version.restype = i32
     lib.ggemm_vark_launch_geometry.argtypes = [i32] + [ctypes.POINTER(i32)] * 5
     lib.ggemm_vark_launch_geometry.restype = None
+    lib.ggemm_persistent_fp8.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 9 + [ctypes.c_int64, vp]
+    lib.ggemm_persistent_fp8.restype = ctypes.c_int
     _lib = lib
     return lib
 

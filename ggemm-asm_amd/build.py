@@ -1,9 +1,12 @@
 """In-tree build of the HIP artefacts for gfx950.
 
-* ``lib/libggemm_vark.so`` -- the extern "C" launcher library (include/ggemm_vark.h) with the
-  tensorwise, K=32-MFMA and MXFP8 kernels.
+* ``lib/libggemm_vark.so`` -- the extern "C" launcher library: the variable-K wgrad kernels
+  (tensorwise, K=32-MFMA, MXFP8; include/ggemm_vark.h) and the persistent fwd/dgrad grouped GEMM
+  (include/ggemm_persistent.h).
 * ``lib/variable_k_wgrad.co`` -- the drop-in code object exporting only
   ``_grouped_variable_k_gemm_kernel`` with the reference kernarg layout.
+* ``lib/persistent_e4m3.co`` / ``lib/persistent_e5m2.co`` -- drop-in code objects exporting only
+  ``_grouped_fp8_persistent_gemm_kernel`` (e4m3 A for the forward sites, e5m2 A for dgrad).
 """
 from __future__ import annotations
 
@@ -16,6 +19,8 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_DIR = os.path.join(PKG_DIR, "lib")
 SO_PATH = os.path.join(LIB_DIR, "libggemm_vark.so")
 CO_PATH = os.path.join(LIB_DIR, "variable_k_wgrad.co")
+PERSISTENT_CO_PATHS = {"e4m3": os.path.join(LIB_DIR, "persistent_e4m3.co"),
+                       "e5m2": os.path.join(LIB_DIR, "persistent_e5m2.co")}
 ARCH = "gfx950"
 
 # Packed-FP32 VALU ops are disabled for all device code (they are left to no hand-written use).
@@ -43,23 +48,36 @@ def _run(cmd: list[str], verbose: bool) -> None:
 def build_so(verbose: bool = False) -> str:
     os.makedirs(LIB_DIR, exist_ok=True)
     tmp = SO_PATH + ".tmp"
-    _run([hipcc(), *DEVICE_FLAGS, "-fPIC", "-shared", os.path.join(CSRC, "vark_capi.hip"), "-o", tmp], verbose)
+    _run([hipcc(), *DEVICE_FLAGS, "-fPIC", "-shared", os.path.join(CSRC, "vark_capi.hip"),
+          os.path.join(CSRC, "persistent_capi.hip"), "-o", tmp], verbose)
     os.replace(tmp, SO_PATH)
     return SO_PATH
 
 
-def build_co(verbose: bool = False) -> str:
+def _build_raw_co(src: str, out: str, defines: list[str], verbose: bool) -> str:
     os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = CO_PATH + ".tmp"
-    # a raw AMDGPU ELF (not a clang offload bundle), like the reference's code object
-    _run([hipcc(), *DEVICE_FLAGS, "--cuda-device-only", "--no-gpu-bundle-output",
-          os.path.join(CSRC, "vark_co.hip"), "-o", tmp], verbose)
-    os.replace(tmp, CO_PATH)
-    return CO_PATH
+    tmp = out + ".tmp"
+    # a raw AMDGPU ELF (not a clang offload bundle), like the reference's code objects
+    _run([hipcc(), *DEVICE_FLAGS, *defines, "--cuda-device-only", "--no-gpu-bundle-output",
+          os.path.join(CSRC, src), "-o", tmp], verbose)
+    os.replace(tmp, out)
+    return out
+
+
+def build_co(verbose: bool = False) -> str:
+    return _build_raw_co("vark_co.hip", CO_PATH, [], verbose)
+
+
+def build_persistent_co(verbose: bool = False) -> dict:
+    for fmt, path in PERSISTENT_CO_PATHS.items():
+        _build_raw_co("persistent_co.hip", path, [f"-DGGEMM_A_E5M2={int(fmt == 'e5m2')}"], verbose)
+    return dict(PERSISTENT_CO_PATHS)
 
 
 def build_all(verbose: bool = False) -> tuple[str, str]:
-    return build_so(verbose), build_co(verbose)
+    so, co = build_so(verbose), build_co(verbose)
+    build_persistent_co(verbose)
+    return so, co
 
 
 if __name__ == "__main__":

@@ -1,0 +1,379 @@
+// Persistent grouped FP8 GEMM (forward and data-gradient sites) for gfx950 (MI355X, CDNA4).
+//
+//   C[r, :] = s_a * s_b * A[r, :] @ B[g]^T      for every row r of group g: offs[g] <= r < offs[g+1]
+//
+// A float8 [M_total, K] (e4m3fn at the forward sites, e5m2 at the data-gradient sites), K
+// contiguous; B float8 e4m3fn [G, N, K], K contiguous (the reference's trans_b = True); C bfloat16
+// [M_total, N]; fp32 accumulation. Rows past offs[G] are not written. Semantics and launch surface
+// follow the reference harness (reference bench.py:151-181 call sites, 238-247 Triton call,
+// 312-361 argument packing and launch): grid (num_cus, 1, 1), block (512, 1, 1), 64 KiB dynamic LDS.
+//
+// Structure (the variable-K kernel's stage pipeline, with K-major operands):
+//  * Output tiles of 192 rows of one group x TN columns, TN = 384 when N % 384 == 0, else 320. A
+//    group of len rows has ceil(len / 192) M-tiles; rows of its last tile past the group end are
+//    neither loaded (they read as zero) nor stored.
+//  * The K axis in stages of 128: LDS rows of 128 bytes, A's 192 rows then B's TN rows (72 or
+//    64 KiB per stage), two stages in the flat 160 KiB, one barrier per stage, the next tile's
+//    first stage issued during the current tile's last.
+//  * LDS-DMA of 16 bytes per lane, 8 rows x 128 bytes per wave-instruction; logical chunk c of row
+//    r is stored at physical chunk c ^ ((r >> 1) & 7), so the 16 rows x 16 bytes that one 16-lane
+//    group reads land in 16 distinct 4-bank slots.
+//  * K tail (K % 128 != 0, K a multiple of 16): the lanes whose chunk lies past K load from an
+//    out-of-range buffer offset, which returns zeros, so both operands hold zeros there.
+//  * MFMA: v_mfma_f32_16x16x128_f8f6f4 (unscaled; the per-tensor scales multiply in the
+//    epilogue). Its A operand is a block of 16 B rows (C columns) and its B operand a block of 16
+//    A rows (C rows), so a lane ends with 4 consecutive columns of one C row. Lane group q feeds K
+//    chunks 2q and 2q+1 of the stage (operand bytes 0-15 and 16-31): any assignment of K to
+//    operand bytes gives the same sum as long as both operands use it.
+//  * Schedule: tile counts of every group prefix-summed in LDS, each tile's group found by binary
+//    search; a group's tiles in 4-wide N bands, M-tile fastest; XCD pairs share contiguous slices
+//    of equal tile counts (every tile costs ceil(K/128) stages) and alternate rounds of 32 tiles.
+#pragma once
+
+#include "vark_kernel.h"
+
+namespace ggemm {
+namespace nt {
+
+constexpr int kMaxGroups = 2047;             // group offsets and tile prefix sums held in LDS
+constexpr uint32_t kOob = 0x7fff0000u;       // buffer offset past every num_records (host-checked)
+constexpr int kRow = 128;                    // LDS bytes per operand row and stage (= kKStep)
+constexpr int64_t kMaxRow = (int64_t(1) << 31) - 256;   // group offsets (32-bit row indices)
+constexpr int64_t kMaxTiles = int64_t(1) << 30;         // tiles of one launch (32-bit tile indices)
+
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+
+struct Args {
+  const uint8_t* a;
+  const uint8_t* b;
+  uint16_t* c;
+  const float* a_scale;
+  const float* b_scale;
+  const int64_t* group_offs;
+  int G, N, K;
+  int stride_am, stride_bg, stride_bn, stride_cm, stride_cn;
+};
+
+struct Tile {
+  int g, m0, n0;       // group, first row inside the group, first column
+  int rows;            // rows of the tile inside the group (1..192)
+  int row_base;        // offs[g]
+};
+
+template <int kTN>
+struct Cfg2 {
+  static constexpr int kLhsBytes = kTileM * kRow;                    // 24 KiB of A rows
+  static constexpr int kSlot = (kTileM + kTN) * kRow;                // 72 or 64 KiB
+  static constexpr int kInstr = kSlot / 1024;                        // 72 or 64
+  static constexpr int kPerWave = kInstr / kWaves;                   // 9 or 8
+  static constexpr int kLhsInstr = kLhsBytes / 1024;                 // 24
+  static constexpr int kMisc = 2 * kSlot;
+  static constexpr int kOffsOff = kMisc + 4 * (kMaxGroups + 1);      // group offsets after the prefix sums
+  static_assert(kInstr % kWaves == 0, "uniform LDS-DMA split");
+  static_assert(kOffsOff + 4 * (kMaxGroups + 1) <= kStaticLdsBytes + kDynLdsBytes, "LDS budget");
+  static_assert(8 * kThreads <= kSlot, "prologue scan fits slot 1");
+  static_assert(kWaves * Cfg<kTN>::EpiRegion <= kSlot, "epilogue staging fits a slot");
+};
+
+// LDS-DMA instruction i = wave + 8 j fills slot bytes [1024 i, +1024): operand rows 8 i' .. 8 i' + 7
+// with i' = wave + 8 jj (A: the 24 instructions j = jj = 0..2 of every wave; B: jj = j - 3), lane l
+// writing physical chunk l % 8 of row 8 i' + l / 8. That row's swizzle, (4 i' + l / 16) & 7,
+// is 4 (wave & 1) + l / 16 for every instruction of the wave, so each lane loads the same logical
+// chunk in all of them and its byte offset is a per-lane base plus the wave-uniform 64 jj stride.
+__device__ __forceinline__ int dma_chunk(int wave, int lane) { return (lane & 7) ^ (4 * (wave & 1) + (lane >> 4)); }
+__device__ __forceinline__ int dma_base(int wave, int lane, int stride) {
+  return (8 * wave + (lane >> 3)) * stride + 16 * dma_chunk(wave, lane);
+}
+
+// One operand block of 16 rows: the low 16 bytes at lo, the high 16 at hi (= lo ^ 16).
+__device__ __forceinline__ v8i read_nt(const GG_LDS uint8_t* lo, const GG_LDS uint8_t* hi) {
+  const v4i l = *(const GG_LDS v4i*)lo;
+  const v4i h = *(const GG_LDS v4i*)hi;
+  return v8i{l[0], l[1], l[2], l[3], h[0], h[1], h[2], h[3]};
+}
+
+template <bool kAE5M2, int kTN>
+__device__ __forceinline__ void persistent_body(const Args& a, GG_LDS uint8_t* lds) {
+  using C = Cfg<kTN>;
+  using C2 = Cfg2<kTN>;
+  constexpr int NB = C::NB;
+  GG_LDS int* s_pre = (GG_LDS int*)(lds + C2::kMisc);      // tiles of groups 0..g-1, g = 0..G
+  GG_LDS int* s_offs = (GG_LDS int*)(lds + C2::kOffsOff);  // group_offs[0..G]
+  // prologue scratch in slot 1: its first stage load is issued after the first stage's barrier
+  GG_LDS int64_t* s_scan = (GG_LDS int64_t*)(lds + C2::kSlot);
+
+  const hsa_kernel_dispatch_packet_t* pkt = dispatch_packet();
+  const int num_wg = (int)((pkt->grid_size_x + pkt->workgroup_size_x - 1) / pkt->workgroup_size_x);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = a.G;
+
+  // ---- group offsets into LDS and tiles per group prefix-summed: each thread takes kPer
+  // consecutive groups, an inclusive scan over the 512 thread totals gives every thread its first
+  // group's offset. Row and tile indices below are 32-bit: offsets outside [0, kMaxRow] or more
+  // than 2^30 tiles in all (inputs of hundreds of GB; the host rejects them from M_total) make the
+  // whole grid return.
+  const int n_tn = (a.N + kTN - 1) / kTN;
+  {
+    constexpr int kPer = (kMaxGroups + 1) / kThreads;
+    // all loads first (indices clamped to G), so they are in flight together
+    int64_t o[kPer + 1];
+#pragma unroll
+    for (int k = 0; k <= kPer; ++k) o[k] = a.group_offs[min(tid * kPer + k, G)];
+    int64_t mine[kPer];
+    int64_t sum = 0;
+    bool bad = false;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int g = tid * kPer + k;
+      int64_t tiles = 0;
+      if (g <= G) {
+        bad |= o[k] < 0 || o[k] > kMaxRow;
+        s_offs[g] = (int)o[k];
+        const int64_t len = o[k + 1] - o[k];   // 0 for g = G (both clamped to offs[G])
+        tiles = len > 0 ? (len + kTileM - 1) / kTileM * n_tn : 0;
+      }
+      mine[k] = tiles;
+      sum += tiles;
+    }
+    s_scan[tid] = bad ? kMaxTiles + 1 : sum;   // a bad group pushes the total past the limit
+    __syncthreads();
+    for (int d = 1; d < kThreads; d <<= 1) {
+      const int64_t v = tid >= d ? s_scan[tid - d] : 0;
+      __syncthreads();
+      s_scan[tid] += v;
+      __syncthreads();
+    }
+    if (s_scan[kThreads - 1] > kMaxTiles) return;   // uniform: every thread reads the same total
+    int64_t run = s_scan[tid] - sum;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int g = tid * kPer + k;
+      if (g < G) s_pre[g] = (int)run;
+      run += mine[k];
+    }
+    if (tid == kThreads - 1) s_pre[G] = (int)s_scan[tid];
+    __syncthreads();
+  }
+  const int total = s_pre[G];
+
+  // ---- XCD pairs: slices of equal tile counts, the two XCDs of a slice alternating 32-tile rounds
+  const bool spread = num_wg % kXcds == 0;
+  const int xcds = spread ? kXcds : 1;
+  const int n_slices = spread ? kXcdPairs : 1;
+  const int per_slice = xcds / n_slices;
+  const int xcd = (int)blockIdx.x % xcds;
+  const int slice = xcd % n_slices, part = xcd / n_slices;
+  const int wgs_per_xcd = num_wg / xcds;
+  const int t_begin = (int)((int64_t)total * slice / n_slices) + part * wgs_per_xcd + (int)blockIdx.x / xcds;
+  const int t_end = (int)((int64_t)total * (slice + 1) / n_slices);
+  const int t_step = per_slice * wgs_per_xcd;
+
+  auto tile_at = [&](int t) {
+    // the tile's group: the last g with s_pre[g] <= t (groups without tiles share their
+    // successor's prefix, so the search lands on the group that owns t)
+    int lo = 0, hi = G - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_pre[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    // wave-uniform by construction: scalar registers and scalar loads from here on
+    lo = __builtin_amdgcn_readfirstlane(lo);
+    Tile T;
+    T.g = lo;
+    T.row_base = __builtin_amdgcn_readfirstlane(s_offs[lo]);
+    const int len = __builtin_amdgcn_readfirstlane(s_offs[lo + 1]) - T.row_base;
+    const int n_tm = (len + kTileM - 1) / kTileM;
+    const int in_g = t - __builtin_amdgcn_readfirstlane(s_pre[lo]);
+    constexpr int kBandN = 4;
+    const int band = in_g / (n_tm * kBandN);
+    const int r = in_g - band * n_tm * kBandN;
+    const int bw = min(kBandN, n_tn - band * kBandN);
+    const int tm = r / bw;
+    const int tn = band * kBandN + (r - tm * bw);
+    T.m0 = tm * kTileM;
+    T.n0 = tn * kTN;
+    T.rows = min(kTileM, len - T.m0);
+    return T;
+  };
+
+  const float alpha = *a.a_scale * *a.b_scale;
+  const int nsteps = (a.K + kKStep - 1) / kKStep;
+
+  const int wm = wave & 1;   // wave row (C rows) in the 2 x 4 wave grid
+  const int wn = wave >> 1;  // wave column (C columns)
+  const int q = lane >> 4;
+  const int s16 = lane & 15;
+  // Slot-relative byte offsets of this lane's reads in block 0 of each operand. A block starts at
+  // a multiple of 16 rows, so a lane's row swizzle is swz(s16) in every block: block i is at +2048 i.
+  // The high half (chunk 2q+1) sits at the low half's offset XOR 16 (chunk bit 0 is address bit 4;
+  // slot and block offsets are multiples of 1024).
+  const int sw = 16 * ((2 * q) ^ swz(s16));
+  const int off_m_lo = (wm * kWaveM + s16) * kRow + sw;
+  const int off_n_lo = C2::kLhsBytes + (wn * C::WaveN + s16) * kRow + sw;
+  const int off_m_hi = off_m_lo ^ 16;
+  const int off_n_hi = off_n_lo ^ 16;
+  const int va = dma_base(wave, lane, a.stride_am);
+  const int vb = dma_base(wave, lane, a.stride_bn);
+
+  auto issue = [&](const Tile& T, int step, int slot) {
+    const int k0 = step * kKStep;
+    const int kv = min(kKStep, a.K - k0);   // valid K bytes of this stage (multiple of 16)
+    const int rows_b = min(kTN, a.N - T.n0);
+    // num_records ends at the last valid row's end: rows past the group (A) or past N (B) read 0
+    const v4i ra = make_rsrc(a.a + (int64_t)(T.row_base + T.m0) * a.stride_am + k0, T.rows * a.stride_am - k0);
+    const v4i rb = make_rsrc(a.b + (int64_t)T.g * a.stride_bg + (int64_t)T.n0 * a.stride_bn + k0,
+                             rows_b * a.stride_bn - k0);
+    const uint32_t base = lds_u32(lds + slot * C2::kSlot);
+    // K tail: a lane whose chunk lies at or past K reads from an out-of-range offset (zeros)
+    const bool dead = kv < kKStep && 16 * dma_chunk(wave, lane) >= kv;
+    // Opaque copies: the nine offsets are formed here at each issue (one add each) instead of
+    // being hoisted out of the tile loop, where they would hold nine registers (and spill).
+    int xa = va, xb = vb;
+    asm volatile("" : "+v"(xa), "+v"(xb));
+    constexpr int kLhsJ = C2::kLhsInstr / kWaves;
+#pragma unroll
+    for (int j = 0; j < C2::kPerWave; ++j) {
+      const bool lhs = j < kLhsJ;
+      const int voff = (lhs ? xa : xb) + 64 * (lhs ? j : j - kLhsJ) * (lhs ? a.stride_am : a.stride_bn);
+      dma16(lhs ? ra : rb, base + 1024 * (wave + kWaves * j), dead ? (int)kOob : voff);
+    }
+  };
+
+  int cur = 0;              // LDS slot holding the next stage to compute
+  bool prefetched = false;  // stage 0 of tile t was issued during the previous tile
+  bool full_prev = false;   // the previous epilogue issued all EpiStores stores in every wave
+  int t = t_begin;
+  Tile T;
+  if (t < t_end) T = tile_at(t);
+  while (t < t_end) {
+    const int t_next = t + t_step;
+    const bool has_next = t_next < t_end;
+    Tile N;
+    if (has_next) N = tile_at(t_next);
+
+    v4f acc[kMB][NB];
+#pragma unroll
+    for (int i = 0; i < kMB; ++i)
+#pragma unroll
+      for (int j = 0; j < NB; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    if (!prefetched) issue(T, 0, cur);
+    // Stage 0 issued before the previous tile's stores: those stores are the youngest vector
+    // memory operations, so waiting down to their count retires exactly the older loads.
+    const bool stores_after_stage0 = prefetched && full_prev;
+    prefetched = false;
+    for (int s = 0; s < nsteps; ++s) {
+      if (s == 0 && stores_after_stage0)
+        wait_vmcnt<C::EpiStores>();
+      else
+        wait_vmcnt<0>();
+      lds_barrier();
+      if (s + 1 < nsteps) {
+        issue(T, s + 1, cur ^ 1);
+      } else if (has_next) {
+        issue(N, 0, cur ^ 1);
+        prefetched = true;
+      }
+
+      const GG_LDS uint8_t* sb = lds + cur * C2::kSlot;
+      const GG_LDS uint8_t* pm_lo = sb + off_m_lo;
+      const GG_LDS uint8_t* pm_hi = sb + off_m_hi;
+      const GG_LDS uint8_t* pn_lo = sb + off_n_lo;
+      const GG_LDS uint8_t* pn_hi = sb + off_n_hi;
+      v8i bn[NB], am[2];
+      bn[0] = read_nt(pn_lo, pn_hi);
+      am[0] = read_nt(pm_lo, pm_hi);
+#pragma unroll
+      for (int j = 1; j < NB; ++j) bn[j] = read_nt(pn_lo + 2048 * j, pn_hi + 2048 * j);
+      am[1] = read_nt(pm_lo + 2048, pm_hi + 2048);
+#pragma unroll
+      for (int i = 0; i < kMB; ++i) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+          // A operand: B rows (format 0 = e4m3); B operand: A rows (e4m3 -> 0, e5m2 -> 1). Constant
+          // zero scale operands select the unscaled instruction.
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bn[j], am[i & 1], acc[i][j], 0,
+                                                                       kAE5M2 ? 1 : 0, 0, 0, 0, 0);
+        if (i + 2 < kMB) am[i & 1] = read_nt(pm_lo + 2048 * (i + 2), pm_hi + 2048 * (i + 2));
+      }
+      pin_stage_schedule<2 * (NB + 2), NB, 2>();
+      cur ^= 1;
+    }
+
+    // ---- epilogue: lane holds C[m][n..n+3] for group row m = m0 + 96 wm + 16 i + s16 and column
+    // n = n0 + wn TN/4 + 16 j + 4 q; staged through a private region of the freed slot (48 rows
+    // per pass) and stored as 16-byte row chunks, as in the variable-K kernel.
+    lds_barrier();
+    GG_LDS uint8_t* stg = lds + (cur ^ 1) * C2::kSlot + wave * C::EpiRegion;
+    // Opaque copy of the lane id: keeps the epilogue's address arithmetic out of the stage loop.
+    int el = lane;
+    asm volatile("" : "+v"(el));
+    uint16_t* cbase = a.c + (int64_t)T.row_base * a.stride_cm;
+    const int m_end = T.m0 + T.rows;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+#pragma unroll
+      for (int ii = 0; ii < 3; ++ii) {
+        const int r = ii * 16 + s16;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+          const v4f v = acc[3 * p + ii][j];
+          const v2i pk = v2i{(int)(f32_to_bf16_rne(v[0] * alpha) | (f32_to_bf16_rne(v[1] * alpha) << 16)),
+                             (int)(f32_to_bf16_rne(v[2] * alpha) | (f32_to_bf16_rne(v[3] * alpha) << 16))};
+          const int c = 2 * j + (q >> 1);
+          *(GG_LDS v2i*)(stg + r * C::EpiRow + 16 * (c ^ C::eswz(r)) + 8 * (q & 1)) = pk;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < C::EpiReads; ++k) {
+        const int f = k * 64 + el;
+        const int r = f / C::EpiChunks;
+        const int c = f - r * C::EpiChunks;
+        const v4i v = *(const GG_LDS v4i*)(stg + r * C::EpiRow + 16 * (c ^ C::eswz(r)));
+        const int m = T.m0 + wm * kWaveM + 48 * p + r;
+        const int n = T.n0 + wn * C::WaveN + 8 * c;
+        if ((C::EpiReads * 64 == 48 * C::EpiChunks || f < 48 * C::EpiChunks) && m < m_end && n < a.N)
+          store_c16(cbase + (int64_t)m * a.stride_cm + n, v);
+      }
+    }
+    full_prev = T.rows == kTileM && T.n0 + kTN <= a.N;
+    t = t_next;
+    T = N;
+  }
+}
+
+template <bool kAE5M2>
+__device__ __forceinline__ void persistent_entry(const Args& a, GG_LDS uint8_t* dyn) {
+  __shared__ __attribute__((aligned(1024))) uint8_t static_lds[kStaticLdsBytes];
+  const hsa_kernel_dispatch_packet_t* pkt = dispatch_packet();
+  // The launch must provide the contracted dynamic LDS; otherwise do nothing (the host validates).
+  if (pkt->group_segment_size < __builtin_amdgcn_groupstaticsize() + (uint32_t)kDynLdsBytes) return;
+  if (a.G <= 0 || a.G > kMaxGroups || a.K <= 0 || a.N <= 0) return;
+  GG_LDS uint8_t* st = (GG_LDS uint8_t*)static_lds;
+  // The stage slots span both arrays: the dynamic window must follow the static one directly.
+  if (lds_u32(dyn) != lds_u32(st) + (uint32_t)kStaticLdsBytes) return;
+  if (a.N % 384 == 0)
+    persistent_body<kAE5M2, 384>(a, st);
+  else
+    persistent_body<kAE5M2, 320>(a, st);
+}
+
+}  // namespace nt
+}  // namespace ggemm
+
+// Kernel entry point with the reference's 16-argument / 96-byte kernarg for the persistent kernel
+// (6 pointers; 8 x i32 G, N, K, stride_am, stride_bg, stride_bn, stride_cm, stride_cn at offsets
+// 48-76; two unused scratch pointers at 80 and 88; reference bench.py:312-337).
+#define GGEMM_DEFINE_PERSISTENT_KERNEL(NAME, AE5M2)                                                      \
+  extern "C" __global__ __launch_bounds__(ggemm::kThreads) void NAME(                                   \
+      const uint8_t* a, const uint8_t* b, uint16_t* c, const float* a_scale, const float* b_scale,     \
+      const int64_t* group_offs, int G, int N, int K, int stride_am, int stride_bg, int stride_bn,      \
+      int stride_cm, int stride_cn, void* global_scratch, void* profile_scratch) {                     \
+    extern __shared__ __attribute__((aligned(1024))) uint8_t ggemm_dyn_lds[];                           \
+    ggemm::nt::Args args{a, b, c, a_scale, b_scale, group_offs, G, N, K,                                 \
+                         stride_am, stride_bg, stride_bn, stride_cm, stride_cn};                         \
+    (void)global_scratch; (void)profile_scratch;                                                        \
+    ggemm::nt::persistent_entry<AE5M2>(args, (GG_LDS uint8_t*)ggemm_dyn_lds);                             \
+  }

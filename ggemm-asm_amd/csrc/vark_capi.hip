@@ -4,11 +4,10 @@
 // (reference launcher.cpp:142-171, bench.py:388-398).
 #include <hip/hip_runtime.h>
 
-#include <atomic>
 #include <cstdint>
-#include <cstring>
 
 #include "../../include/ggemm_vark.h"
+#include "capi_common.h"
 #include "vark_kernel.h"
 
 GGEMM_DEFINE_TENSORWISE_KERNEL(_grouped_variable_k_gemm_kernel, false)
@@ -17,29 +16,8 @@ GGEMM_DEFINE_MX_KERNEL(_grouped_variable_k_mxfp8_gemm_kernel)
 
 namespace {
 
-constexpr int kMaxDevices = 64;
-// per-device cache: 0 = unknown, -1 = unusable, >0 = CU count of a gfx950 device
-std::atomic<int> g_cus[kMaxDevices];
-
-int device_cus(int* cus_out) {
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return (int)e;
-  if (dev < 0 || dev >= kMaxDevices) return GGEMM_E_DEVICE;
-  int c = g_cus[dev].load(std::memory_order_relaxed);
-  if (c == 0) {
-    hipDeviceProp_t p;
-    e = hipGetDeviceProperties(&p, dev);
-    if (e != hipSuccess) return (int)e;
-    c = (std::strncmp(p.gcnArchName, "gfx950", 6) == 0 && p.multiProcessorCount > 0) ? p.multiProcessorCount : -1;
-    g_cus[dev].store(c, std::memory_order_relaxed);
-  }
-  if (c < 0) return GGEMM_E_DEVICE;
-  *cus_out = c;
-  return GGEMM_OK;
-}
-
-bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+using ggemm::host::aligned;
+using ggemm::host::device_cus;
 
 int validate_common(const void* lhs, const void* rhs, const void* out, const void* ls, const void* rs,
                     const int64_t* offs, int G, int OUT_M, int OUT_N, int slm, int srm, int scg, int scm,
@@ -150,6 +128,7 @@ const char* ggemm_vark_strerror(int32_t code) {
     case GGEMM_E_OFFSETS: return "invalid group offsets (must start at 0, be non-decreasing, end <= M_total)";
     case GGEMM_E_DEVICE: return "current device is not a usable gfx950 (MI355X) GPU";
     case GGEMM_E_MX_ALIGN: return "MXFP8 groups must start on 32-token block boundaries";
+    case GGEMM_E_FORMAT: return "unknown fp8 format code (A: GGEMM_FP8_E4M3 or GGEMM_FP8_E5M2)";
     default: break;
   }
   if (code > 0) return hipGetErrorString((hipError_t)code);
@@ -163,7 +142,7 @@ void ggemm_vark_launch_geometry(int32_t out_n, int32_t* block_threads, int32_t* 
   if (block_threads) *block_threads = ggemm::kThreads;
   if (dynamic_lds) *dynamic_lds = ggemm::kDynLdsBytes;
   if (tile_m) *tile_m = ggemm::kTileM;
-  if (tile_n) *tile_n = (out_n > 0 && out_n % 384 == 0) ? 384 : 320;   // tensorwise kernels; MXFP8: 320
+  if (tile_n) *tile_n = (out_n > 0 && out_n % 384 == 0) ? 384 : 320;
   if (k_step) *k_step = ggemm::kKStep;
 }
 

@@ -320,13 +320,13 @@ __device__ __forceinline__ v4f mfma(const v8i& a_rhs, const v8i& b_lhs, v4f acc,
 // Instruction order of one stage's compute: all n-side reads plus m-blocks 0 and 1 first, then
 // for each m-block its MFMAs followed by the reads of m-block i+2 into the registers block i
 // just released -- LDS latency of every m-block hides behind the previous block's MFMAs.
-template <int kFirstReads, int kMfmaPerBlock>
+template <int kFirstReads, int kMfmaPerBlock, int kReadsPerBlock = 4>
 __device__ __forceinline__ void pin_stage_schedule() {
   __builtin_amdgcn_sched_group_barrier(0x100, kFirstReads, 0);
 #pragma unroll
   for (int i = 0; i < kMB - 2; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, kMfmaPerBlock, 0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, kReadsPerBlock, 0);
   }
   __builtin_amdgcn_sched_group_barrier(0x008, 2 * kMfmaPerBlock, 0);
 }

@@ -1,11 +1,12 @@
-"""Code-object launch harness: drives ``variable_k_wgrad.co`` the way the reference drives its `.co`.
+"""Code-object launch harness: drives the build's `.co` files the way the reference drives its own.
 
 Mirrors the reference's HIP module path (reference bench.py:43-143 ``load_kernel`` /
 ``_detect_kernel_name`` / ``unload_kernel``; bench.py:288-309,364-413 ``_pack_args`` /
-``prepare_variable_k_args`` / ``launch_variable_k_kernel``; launcher.cpp:16-33,123-171 the
+``prepare_variable_k_args`` / ``launch_variable_k_kernel``; bench.py:312-361
+``prepare_persistent_args`` / ``launch_persistent_kernel``; launcher.cpp:16-33,123-171 the
 96-byte ``KernelArgs`` record passed with HIP_LAUNCH_PARAM_BUFFER_POINTER). It exists to show
-the build's code object is a drop-in for that launch surface; the library entry points in
-``vark.py`` are the normal way to call the kernel.
+the build's code objects are drop-ins for that launch surface; the library entry points in
+``vark.py`` and ``persistent.py`` are the normal way to call the kernels.
 """
 from __future__ import annotations
 
@@ -16,6 +17,7 @@ import struct
 import torch
 
 KERNEL_NAME = "_grouped_variable_k_gemm_kernel"
+PERSISTENT_KERNEL_NAME = "_grouped_fp8_persistent_gemm_kernel"
 BLOCK = 512
 SHARED_MEM = 65536
 KERNARG_SIZE = 96
@@ -158,6 +160,34 @@ def launch_variable_k_kernel(func, lhs, rhs, out, lhs_scale, rhs_scale, group_of
                              shared_mem=SHARED_MEM):
     launch, _keep = prepare_variable_k_args(func, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M,
                                             OUT_N, num_sms, shared_mem)
+    launch()
+
+
+def _persistent_arg_list(a, b, out, a_scale, b_scale, group_offs, G, N, K):
+    """Reference bench.py:317-336: strides from the tensors (b as [G, N, K], out as [M, N])."""
+    P, I = (lambda t: ctypes.c_void_p(t.data_ptr())), (lambda v: ctypes.c_int32(int(v)))
+    return [P(a), P(b), P(out), P(a_scale), P(b_scale), P(group_offs),
+            I(G), I(N), I(K), I(a.stride(0)), I(b.stride(0)), I(b.stride(1)),
+            I(out.stride(0)), I(out.stride(1)), ctypes.c_void_p(0), ctypes.c_void_p(0)]
+
+
+def prepare_persistent_args(func, a, b, out, a_scale, b_scale, group_offs, G, N, K, num_sms,
+                            shared_mem=SHARED_MEM):
+    """Closure launching the persistent fwd/dgrad kernel on the null stream (bench.py:312-351)."""
+    hip = load_hip()
+    packed, storage = _pack_args(_persistent_arg_list(a, b, out, a_scale, b_scale, group_offs, G, N, K))
+
+    def launch():
+        check_hip(hip.hipModuleLaunchKernel(func, num_sms, 1, 1, BLOCK, 1, 1, shared_mem, None, packed, None),
+                  "launching persistent kernel")
+
+    return launch, storage
+
+
+def launch_persistent_kernel(func, a, b, out, a_scale, b_scale, group_offs, G, N, K, num_sms,
+                             shared_mem=SHARED_MEM):
+    launch, _keep = prepare_persistent_args(func, a, b, out, a_scale, b_scale, group_offs, G, N, K, num_sms,
+                                            shared_mem)
     launch()
 
 

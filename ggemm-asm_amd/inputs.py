@@ -224,3 +224,73 @@ def constant_problem(G: int = 32, M: int = M_TOTAL, OUT_M: int = F_DIM, OUT_N: i
     rhs = torch.full((M, OUT_N), 0x38, dtype=torch.uint8, device=device)
     offs = torch.tensor([M * i // G for i in range(G + 1)], dtype=torch.int64, device=device)
     return VarKProblem("constant", lhs, rhs, offs, G, OUT_M, OUT_N, lhs_scale=0.1, rhs_scale=0.1)
+
+
+# ----------------------------------------------------------------------------- fwd / dgrad sites
+
+# persistent-kernel call sites (reference bench.py:153-180): K, N, A format (B is always e4m3fn,
+# stored [G, N, K] -- trans_b=True)
+FWD_SITES = {
+    "gate_up_fwd": (F_DIM, F2_DIM, "e4m3"),
+    "down_fwd": (F_DIM, F_DIM, "e4m3"),
+    "down_dgrad": (F_DIM, F_DIM, "e5m2"),
+    "gate_up_dgrad": (F2_DIM, F_DIM, "e5m2"),
+}
+
+
+@dataclass
+class FwdProblem:
+    name: str
+    a: torch.Tensor              # uint8 [M, K] in a_format
+    b: torch.Tensor              # uint8 e4m3fn [G, N, K]
+    a_format: str                # "e4m3" | "e5m2"
+    group_offs: torch.Tensor     # int64 [G+1]
+    a_scale: float = 0.1
+    b_scale: float = 0.1
+    meta: dict = field(default_factory=dict)
+
+    @property
+    def M(self) -> int:
+        return int(self.a.shape[0])
+
+    @property
+    def K(self) -> int:
+        return int(self.a.shape[1])
+
+    @property
+    def N(self) -> int:
+        return int(self.b.shape[1])
+
+    @property
+    def G(self) -> int:
+        return int(self.b.shape[0])
+
+    @property
+    def flops(self) -> float:
+        return 2.0 * self.M * self.K * self.N
+
+    @property
+    def a_dtype(self) -> torch.dtype:
+        return torch.float8_e4m3fn if self.a_format == "e4m3" else torch.float8_e5m2
+
+
+def make_fwd_problem(name: str, seed: int = 0, device: str | torch.device = "cpu",
+                     lens: torch.Tensor | None = None, K: int | None = None, N: int | None = None) -> FwdProblem:
+    """A call site of the persistent kernel with the reference's own input recipe (reference
+    bench.py:205-223,238-247): seed-42 exponential group lengths over 32 experts and 131072 rows,
+    values torch.randn in bf16 cast straight to fp8 (no scaling), scales 0.1. ``seed`` seeds the
+    values (a generator on ``device``); ``lens``/``K``/``N`` override sizes for scaled-down tests."""
+    if name not in FWD_SITES:
+        raise ValueError(f"unknown site {name!r}; choose from {tuple(FWD_SITES)}")
+    device = torch.device(device)
+    K_, N_, fmt = FWD_SITES[name]
+    K_ = K if K is not None else K_
+    N_ = N if N is not None else N_
+    lens_ = torch.as_tensor(lens, dtype=torch.long) if lens is not None else make_group_lens_reference()
+    offs = make_group_offs(lens_).to(device)
+    M_, G_ = int(lens_.sum()), len(lens_)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    adt = torch.float8_e4m3fn if fmt == "e4m3" else torch.float8_e5m2
+    a = torch.randn((M_, K_), generator=gen, device=device, dtype=torch.bfloat16).to(adt).view(torch.uint8)
+    b = torch.randn((G_, N_, K_), generator=gen, device=device, dtype=torch.bfloat16).to(torch.float8_e4m3fn)
+    return FwdProblem(name, a, b.view(torch.uint8), fmt, offs, meta={"seed": seed, "lens": lens_.tolist()})

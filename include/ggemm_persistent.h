@@ -1,0 +1,56 @@
+/* C ABI of the MI355X persistent grouped FP8 GEMM (forward and data-gradient sites), exported by
+ * libggemm_vark.so next to the variable-K entry points of ggemm_vark.h (return codes, strerror
+ * and ABI version are shared).
+ *
+ *   out[r, :] = a_scale * b_scale * A[r, :] @ B[g]^T      for offs[g] <= r < offs[g+1]
+ *
+ * All pointers are device pointers; sizes and strides are in elements. Returns 0 on success, a
+ * positive hipError_t value when the HIP runtime failed, or a negative GGEMM_E_* code when
+ * argument validation failed (nothing is launched then). Launches are asynchronous on `stream`
+ * (a hipStream_t; NULL = the null stream). No allocation, no state between calls, no sync.
+ */
+#ifndef GGEMM_PERSISTENT_H
+#define GGEMM_PERSISTENT_H
+
+#include <stdint.h>
+
+#include "ggemm_vark.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* fp8 format codes of the A operand */
+#define GGEMM_FP8_E4M3 0   /* float8_e4m3fn: forward sites (x, swiglu output) */
+#define GGEMM_FP8_E5M2 1   /* float8_e5m2: data-gradient sites (output gradients) */
+
+/* Largest G: the group offsets and per-group tile prefix sums live in on-chip memory. */
+#define GGEMM_PERSISTENT_MAX_GROUPS 2047
+
+/* Grouped FP8 GEMM with a per-group weight, trans_b layout. Replaces the reference's code-object
+ * launch of `_grouped_fp8_persistent_gemm_kernel` (reference bench.py:312-361
+ * prepare_persistent_args / launch_persistent_kernel: the same 14 data arguments in the same
+ * order) and the Triton op it stands in for (reference bench.py:238-247,
+ * `_triton_fwd(a, b, a_scale, b_scale, group_offs, trans_b=True)`), at the call sites of
+ * reference bench.py:153-180 (gate_up_fwd, down_fwd, down_dgrad, gate_up_dgrad).
+ *   a:   fp8 [M_total, K] in format a_format, row stride stride_am;
+ *   b:   float8_e4m3fn [G, N, K], strides stride_bg, stride_bn (K contiguous);
+ *   out: bf16 [M_total, N], strides stride_cm, stride_cn == 1;
+ *   a_scale / b_scale: fp32 scalars; group_offs: int64 [G+1], offs[0] = 0, non-decreasing,
+ *   offs[G] <= M_total. Rows of out outside [0, offs[G]) are not written.
+ * M_total (rows of a and out) is not part of the reference kernarg; it bounds the 32-bit row and
+ * tile indices here (M_total < 2^31 - 256, at most 2^30 output tiles of 192 x 320).
+ * Requirements: 1 <= G <= GGEMM_PERSISTENT_MAX_GROUPS; N, K > 0 and multiples of 16; row strides
+ * >= K and multiples of 16, stride_bg >= (N-1)*stride_bn + K and a multiple of 16, stride_cm >= N
+ * and a multiple of 8; 192*stride_am and 384*stride_bn below 2^31 - 2^16; a, b, out 16-byte
+ * aligned. */
+int ggemm_persistent_fp8(const void* a, const void* b, void* out, const float* a_scale, const float* b_scale,
+                         const int64_t* group_offs, int32_t G, int32_t N, int32_t K, int32_t stride_am,
+                         int32_t stride_bg, int32_t stride_bn, int32_t stride_cm, int32_t stride_cn,
+                         int32_t a_format, int64_t M_total, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GGEMM_PERSISTENT_H */

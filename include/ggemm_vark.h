@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define GGEMM_VARK_ABI_VERSION 1
+#define GGEMM_VARK_ABI_VERSION 2
 
 enum {
   GGEMM_OK = 0,
@@ -28,7 +28,8 @@ enum {
   GGEMM_E_ALIGN = -4,       /* LHS/RHS not 16-byte aligned or C not 8-byte aligned */
   GGEMM_E_OFFSETS = -5,     /* host group offsets not 0-based, non-decreasing, or past M_total */
   GGEMM_E_DEVICE = -6,      /* no usable device / not a gfx950 device */
-  GGEMM_E_MX_ALIGN = -7     /* MX: a group does not start on a 32-token block boundary */
+  GGEMM_E_MX_ALIGN = -7,    /* MX: a group does not start on a 32-token block boundary */
+  GGEMM_E_FORMAT = -8       /* unknown fp8 format code (ggemm_persistent.h) */
 };
 
 /* Tensorwise FP8 grouped wgrad. Replaces the reference's code-object launch of

@@ -1,0 +1,151 @@
+"""CPU oracle for the persistent grouped FP8 GEMM (forward and data-gradient call sites).
+
+TEST INFRASTRUCTURE ONLY. This module is the checker: only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it, and never as the thing measured or shipped. The product path lives
+in the HIP library and fails loudly when that library is missing.
+
+What it restates
+----------------
+The reference harness drives ``_grouped_fp8_persistent_gemm_kernel`` (reference
+bench.py:312-361) at four call sites (reference bench.py:153-180: gate_up_fwd,
+down_fwd with e4m3 A; down_dgrad, gate_up_dgrad with e5m2 A; B always e4m3,
+``trans_b=True``) and checks it against Primus-Turbo's
+``grouped_gemm_fp8_tensorwise_triton_kernel(a, b, a_scale, b_scale, group_offs,
+trans_b=True)`` (reference bench.py:238-247; third-party, not in the reference
+tree, named as Primus v26.2 at reference bench.py:277). The kernel's
+code object is not shipped either, so the arithmetic is restated here from the
+op's published meaning: for every group ``g`` and row ``r`` in
+``[offs[g], offs[g+1])``::
+
+    out[r, :] = a_scale * b_scale * A[r, :] @ B[g]^T
+
+with fp32 dequantize, fp32 accumulation and round-to-nearest-even to bf16
+(``[M_total, N]``). ``trans_b=False`` (B as ``[G, K, N]``) is the same product
+with B transposed.
+
+Pinning (tests/test_oracle_persistent.py): exact rational brute force on tiny
+ragged shapes for both A formats; a single group against torch's own fp8
+decode and matmul; a constant-fill closed form; row-permutation, group-split and
+power-of-two scale invariants; the codecs are those of ``vark_oracle`` (pinned
+against torch and textbook values there).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .vark_oracle import E4M3_TABLE, E5M2_TABLE, bf16_bits_rne, decode_e4m3, decode_e5m2
+
+A_FORMATS = ("e4m3", "e5m2")
+
+
+def _decode(b: np.ndarray, fmt: str) -> np.ndarray:
+    if fmt == "e4m3":
+        return decode_e4m3(b)
+    if fmt == "e5m2":
+        return decode_e5m2(b)
+    raise ValueError(f"unknown fp8 format {fmt!r}")
+
+
+def _check_offs(group_offs, m_total: int) -> np.ndarray:
+    offs = np.asarray(group_offs, dtype=np.int64)
+    if offs.ndim != 1 or offs.size < 2:
+        raise ValueError("group_offs must be 1-D with G+1 entries")
+    if offs[0] != 0 or np.any(np.diff(offs) < 0) or offs[-1] > m_total:
+        raise ValueError("group_offs must start at 0, be non-decreasing and end <= M_total")
+    return offs
+
+
+def grouped_fp8_f32(a: np.ndarray, b: np.ndarray, a_scale: float, b_scale: float, group_offs,
+                    a_format: str = "e4m3", trans_b: bool = True, acc_dtype=np.float32) -> np.ndarray:
+    """Per-group ``(s_a * A_g) @ (s_b * B[g])^T`` before output rounding, ``[M_total, N]``.
+
+    a: uint8 [M_total, K] holding ``a_format`` bytes; b: uint8 e4m3fn bytes, [G, N, K] when
+    ``trans_b`` else [G, K, N]. Rows outside every group stay 0. Follows the op of reference
+    bench.py:238-247 at the call sites of bench.py:153-180.
+    """
+    a = np.asarray(a, dtype=np.uint8)
+    b = np.asarray(b, dtype=np.uint8)
+    offs = _check_offs(group_offs, a.shape[0])
+    G = offs.size - 1
+    if b.ndim != 3 or b.shape[0] != G:
+        raise ValueError(f"b must be [G={G}, ., .]")
+    bt = b if trans_b else np.swapaxes(b, 1, 2)          # [G, N, K]
+    if bt.shape[2] != a.shape[1]:
+        raise ValueError("K of a and b differ")
+    out = np.zeros((a.shape[0], bt.shape[1]), dtype=acc_dtype)
+    sa, sb = np.float32(a_scale), np.float32(b_scale)
+    for g in range(G):
+        lo, hi = int(offs[g]), int(offs[g + 1])
+        if hi == lo:
+            continue
+        x = (_decode(a[lo:hi], a_format) * sa).astype(acc_dtype)
+        w = (decode_e4m3(bt[g]) * sb).astype(acc_dtype)
+        out[lo:hi] = x @ w.T
+    return out
+
+
+def grouped_fp8(a, b, a_scale, b_scale, group_offs, a_format="e4m3", trans_b=True) -> np.ndarray:
+    """bf16 bit patterns [M_total, N] (uint16) of the grouped GEMM; rows outside groups are 0."""
+    return bf16_bits_rne(grouped_fp8_f32(a, b, a_scale, b_scale, group_offs, a_format, trans_b))
+
+
+def grouped_fp8_bruteforce_exact(a, b, a_scale, b_scale, group_offs, a_format="e4m3"):
+    """Pure-Python exact rational triple loop (tiny shapes only; b as [G, N, K]).
+
+    Returns ``(value, abs_sum)`` nested lists ``[M_total][N]`` of Fractions: the exact
+    ``s_a*s_b*sum_k A[r,k] B[g,n,k]`` and ``|s_a*s_b| * sum_k |A[r,k] B[g,n,k]|`` (the scale of the
+    rounding-error bound of a floating-point evaluation). Rows outside groups are exact zeros.
+    fp8 values and fp32 scales are dyadic rationals, so ``fractions.Fraction`` is exact.
+    """
+    from fractions import Fraction
+    a = np.asarray(a, dtype=np.uint8)
+    b = np.asarray(b, dtype=np.uint8)
+    offs = [int(v) for v in group_offs]
+    s = Fraction(float(np.float32(a_scale))) * Fraction(float(np.float32(b_scale)))
+    ta = E4M3_TABLE if a_format == "e4m3" else E5M2_TABLE
+    da = [Fraction(float(v)) if np.isfinite(v) else None for v in ta]
+    db = [Fraction(float(v)) if np.isfinite(v) else None for v in E4M3_TABLE]
+    M, K = a.shape
+    N = b.shape[1]
+    val = [[Fraction(0)] * N for _ in range(M)]
+    mag = [[Fraction(0)] * N for _ in range(M)]
+    for g in range(len(offs) - 1):
+        for r in range(offs[g], offs[g + 1]):
+            for n in range(N):
+                acc = Fraction(0)
+                aab = Fraction(0)
+                for k in range(K):
+                    t = da[a[r, k]] * db[b[g, n, k]]
+                    acc += t
+                    aab += abs(t)
+                val[r][n] = acc * s
+                mag[r][n] = aab * abs(s)
+    return val, mag
+
+
+def fp8_mfma_error_bound_rows(a_vals: np.ndarray, b_vals: np.ndarray, group_offs, scale: float = 1.0,
+                              stage: int = 128, row_chunk: int = 64) -> np.ndarray:
+    """Worst-case |kernel - exact| for the gfx950 fp8 MFMA accumulation of this GEMM (before bf16
+    output rounding), ``[M_total, N]`` float64.
+
+    Same error model as ``vark_oracle.fp8_mfma_error_bound`` (each 32-product block is summed with
+    an error <= 2^-9 * its largest |product|; block sums accumulate in fp32), with the K axis cut in
+    the kernel's 128-wide stages: a stage holds four 32-product blocks, whatever K subsets the
+    instruction groups, so its error is <= 4 * 2^-9 * max over the stage. a_vals: dequantized
+    float64 [M_total, K]; b_vals: float64 [G, N, K].
+    """
+    offs = np.asarray(group_offs, dtype=np.int64)
+    M, K = a_vals.shape
+    out = np.zeros((M, b_vals.shape[1]), dtype=np.float64)
+    aa, ab = np.abs(a_vals), np.abs(b_vals)
+    for g in range(offs.size - 1):
+        for r0 in range(int(offs[g]), int(offs[g + 1]), row_chunk):
+            r1 = min(r0 + row_chunk, int(offs[g + 1]))
+            mag = aa[r0:r1] @ ab[g].T
+            smax = np.zeros_like(mag)
+            for k0 in range(0, K, stage):
+                k1 = min(k0 + stage, K)
+                smax += np.max(aa[r0:r1, None, k0:k1] * ab[g][None, :, k0:k1], axis=2)
+            out[r0:r1] = 4 * 2.0 ** -9 * smax + (K / 16.0 + 4) * 2.0 ** -24 * mag
+    return out * abs(scale)

@@ -28,6 +28,12 @@ def orc():
 
 
 @pytest.fixture(scope="session")
+def orp():
+    from oracle import persistent_oracle
+    return persistent_oracle
+
+
+@pytest.fixture(scope="session")
 def cuda():
     import torch
     if not torch.cuda.is_available():

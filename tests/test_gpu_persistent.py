@@ -1,0 +1,253 @@
+"""GPU parity of the persistent fwd/dgrad grouped FP8 GEMM against the CPU oracle (launches through
+the C ABI or the drop-in code objects).
+
+Bar (from the north-star statement, applied to this kernel): cosine >= 0.99999, max relative error
+<= 2e-2 over |C| > 1e-3 * max|C|, no non-finite values. Small and ragged cases are compared in full
+with the oracle; adversarial all-codes inputs against a rigorous error bound of the exact result;
+the full-size call sites with the oracle on selected groups plus the size-independent row-sum
+identity ``out[r] @ 1 = s_a s_b A[r] (B[g]^T 1)`` on every row.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def _run(pkg, a, b, fmt, offs, sa, sb, dev, **kw):
+    adt = torch.float8_e4m3fn if fmt == "e4m3" else torch.float8_e5m2
+    return pkg.grouped_gemm_fp8_tensorwise(
+        a.to(dev).view(adt), b.to(dev).view(torch.float8_e4m3fn), torch.tensor(sa, dtype=torch.float32, device=dev),
+        torch.tensor(sb, dtype=torch.float32, device=dev), offs.to(dev), **kw)
+
+
+def _parity(pkg, orc, got, ref_bits, label, rows=None):
+    g = pkg.as_bf16_bits(got)
+    if rows is not None:
+        g = g[:rows]
+        ref_bits = ref_bits[:rows]
+    m = orc.compare(g, ref_bits)
+    _say(f"{label}: {m}")
+    assert orc.parity_ok(m), (label, m)
+    return m
+
+
+RAGGED = [
+    # lens, K, N: 320-wide N tiles (N % 384 != 0) and 384-wide, partial M/N tiles, K tails
+    ([1, 2, 3, 5, 8, 13, 21, 31], 128, 128),
+    ([0, 0, 193, 0], 256, 384),
+    ([191, 192, 193, 0, 385], 2880, 336),
+    ([1000, 24], 208, 768),
+    ([7], 16, 16),
+    ([300, 0, 645], 5760, 640),
+    ([64, 0, 96, 45], 144, 1152),
+    ([383, 1], 2880, 2880),
+]
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("lens,K,N", RAGGED, ids=[f"case{i}" for i in range(len(RAGGED))])
+def test_ragged_vs_oracle(pkg, orc, orp, cuda, fmt, lens, K, N):
+    site = "down_fwd" if fmt == "e4m3" else "down_dgrad"
+    _say(f"persistent {fmt} lens={lens} K={K} N={N}")
+    p = pkg.inputs.make_fwd_problem(site, seed=len(lens) + K, lens=lens, K=K, N=N)
+    out = _run(pkg, p.a, p.b, fmt, p.group_offs, 0.1, 0.1, cuda)
+    torch.cuda.synchronize()
+    ref = orp.grouped_fp8(p.a.numpy(), p.b.numpy(), 0.1, 0.1, p.group_offs.numpy(), fmt)
+    _parity(pkg, orc, out, ref, f"{fmt} {lens} K={K} N={N}", rows=int(sum(lens)))
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_all_fp8_codes_error_bound(pkg, orc, orp, cuda, fmt):
+    """Uniformly random finite codes over the whole exponent range: |got - exact| within bf16
+    rounding plus the MFMA accumulation bound of the exact rational result."""
+    lens, K, N = [100, 0, 333, 64], 400, 336
+    g = torch.Generator().manual_seed(5)
+    M = sum(lens)
+    a = torch.randint(0, 256, (M, K), generator=g, dtype=torch.int32).to(torch.uint8)
+    b = torch.randint(0, 256, (len(lens), N, K), generator=g, dtype=torch.int32).to(torch.uint8)
+    if fmt == "e4m3":
+        a[(a & 0x7F) == 0x7F] = 0x3A
+    else:
+        a[(a & 0x7C) == 0x7C] = 0x3B
+    b[(b & 0x7F) == 0x7F] = 0x3A
+    offs = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64)
+    sa, sb = 0.0173, 2.9e-4
+    _say(f"persistent all-codes {fmt}")
+    out = _run(pkg, a, b, fmt, offs, sa, sb, cuda)
+    torch.cuda.synchronize()
+    dec = orc.decode_e4m3 if fmt == "e4m3" else orc.decode_e5m2
+    av = dec(a.numpy()).astype(np.float64)
+    bv = orc.decode_e4m3(b.numpy()).astype(np.float64)
+    exact = orp.grouped_fp8_f32(a.numpy(), b.numpy(), sa, sb, offs.numpy(), fmt, acc_dtype=np.float64)
+    scale = float(np.float32(sa)) * float(np.float32(sb))
+    bound = orp.fp8_mfma_error_bound_rows(av, bv, offs.numpy(), scale)
+    mag = np.zeros_like(exact)
+    o = offs.numpy()
+    for gi in range(len(lens)):
+        mag[o[gi]:o[gi + 1]] = np.abs(av[o[gi]:o[gi + 1]]) @ np.abs(bv[gi]).T * scale
+    got = orc.bf16_bits_to_f32(pkg.as_bf16_bits(out)).astype(np.float64)
+    lim = 2.0 ** -8 * np.abs(exact) + 1.01 * bound + 4 * 2.0 ** -24 * mag + 1e-38
+    viol = np.abs(got - exact) > lim
+    _say(f"{fmt}: violations {int(viol.sum())} of {viol.size}, worst ratio {float(np.max(np.abs(got - exact) / lim)):.3f}")
+    assert not viol.any()
+
+
+def test_rows_outside_groups_untouched_and_empty_input(pkg, orc, orp, cuda):
+    lens, K, N = [50, 0, 200], 256, 384
+    p = pkg.inputs.make_fwd_problem("gate_up_fwd", seed=3, lens=lens, K=K, N=N)
+    M = p.M + 77                                   # 77 rows past offs[G]
+    a = torch.cat([p.a, torch.full((77, K), 0x38, dtype=torch.uint8)])
+    _say("persistent rows past offs[G] keep their contents")
+    out = torch.full((M, N), -3.0, dtype=torch.bfloat16, device=cuda)
+    res = pkg.grouped_gemm_fp8_tensorwise(
+        a.to(cuda).view(torch.float8_e4m3fn), p.b.to(cuda).view(torch.float8_e4m3fn),
+        torch.tensor(0.1, device=cuda), torch.tensor(0.1, device=cuda), p.group_offs.to(cuda), out=out)
+    torch.cuda.synchronize()
+    assert res.data_ptr() == out.data_ptr()
+    assert bool((out[p.M:] == -3.0).all())
+    ref = orp.grouped_fp8(a.numpy(), p.b.numpy(), 0.1, 0.1, p.group_offs.numpy())
+    _parity(pkg, orc, out, ref, "rows past offs[G]", rows=p.M)
+    # no rows at all: nothing is launched, the empty result comes back
+    e = pkg.grouped_gemm_fp8_tensorwise(
+        torch.empty((0, K), dtype=torch.float8_e4m3fn, device=cuda), p.b.to(cuda).view(torch.float8_e4m3fn),
+        torch.tensor(0.1, device=cuda), torch.tensor(0.1, device=cuda),
+        torch.zeros(len(lens) + 1, dtype=torch.int64, device=cuda))
+    assert e.shape == (0, N)
+
+
+def test_trans_b_false_and_strided_views(pkg, orc, orp, cuda):
+    lens, K, N = [130, 70, 0, 260], 320, 400
+    p = pkg.inputs.make_fwd_problem("down_dgrad", seed=4, lens=lens, K=K, N=N)
+    ref = orp.grouped_fp8(p.a.numpy(), p.b.numpy(), 0.1, 0.1, p.group_offs.numpy(), "e5m2")
+    s = torch.tensor(0.1, device=cuda)
+    do = p.group_offs.to(cuda)
+    _say("persistent trans_b=False")
+    bt = p.b.to(cuda).view(torch.float8_e4m3fn).transpose(1, 2).contiguous()      # [G, K, N]
+    out = pkg.grouped_gemm_fp8_tensorwise(p.a.to(cuda).view(torch.float8_e5m2), bt, s, s, do, trans_b=False)
+    torch.cuda.synchronize()
+    _parity(pkg, orc, out, ref, "trans_b=False")
+    _say("persistent strided a / b / out")
+    a_wide = torch.zeros((p.M, K + 64), dtype=torch.uint8, device=cuda)
+    a_wide[:, 16:16 + K] = p.a.to(cuda)
+    b_wide = torch.zeros((len(lens), N + 3, K + 32), dtype=torch.uint8, device=cuda)
+    b_wide[:, :N, 32:] = p.b.to(cuda)
+    o_wide = torch.zeros((p.M, N + 24), dtype=torch.bfloat16, device=cuda)
+    av = a_wide[:, 16:16 + K].view(torch.float8_e5m2)
+    bv = b_wide[:, :N, 32:].view(torch.float8_e4m3fn)
+    assert av.stride(0) == K + 64 and bv.stride(1) == K + 32
+    pkg.grouped_gemm_fp8_tensorwise(av, bv, s, s, do, out=o_wide[:, 8:8 + N])
+    torch.cuda.synchronize()
+    _parity(pkg, orc, o_wide[:, 8:8 + N], ref, "strided views")
+    assert bool((o_wide[:, :8] == 0).all()) and bool((o_wide[:, 8 + N:] == 0).all())
+
+
+@pytest.mark.parametrize("G", [300, 2047])
+def test_many_groups(pkg, orc, orp, cuda, G):
+    g = torch.Generator().manual_seed(G)
+    lens = torch.randint(0, 40, (G,), generator=g)
+    lens[torch.randint(0, G, (G // 3,), generator=g)] = 0
+    lens[0] = 0
+    lens[-1] = 5
+    _say(f"persistent G={G} rows={int(lens.sum())}")
+    p = pkg.inputs.make_fwd_problem("down_fwd", seed=G, lens=lens, K=48, N=32)
+    out = _run(pkg, p.a, p.b, "e4m3", p.group_offs, 0.1, 0.1, cuda)
+    torch.cuda.synchronize()
+    ref = orp.grouped_fp8(p.a.numpy(), p.b.numpy(), 0.1, 0.1, p.group_offs.numpy())
+    _parity(pkg, orc, out, ref, f"G={G}")
+
+
+@pytest.mark.parametrize("fmt,N", [("e4m3", 768), ("e5m2", 640)])
+def test_code_object_drop_in(pkg, cuda, fmt, N):
+    """Our persistent .co launched like reference bench.py:312-361 (16-entry kernelParams, null
+    stream, any grid) gives the library's result bit for bit."""
+    from ggemm_asm_amd import harness
+    lens, K = [96, 160, 0, 256, 33], 384
+    p = pkg.inputs.make_fwd_problem("gate_up_fwd" if fmt == "e4m3" else "gate_up_dgrad", seed=21, lens=lens, K=K, N=N)
+    adt = torch.float8_e4m3fn if fmt == "e4m3" else torch.float8_e5m2
+    da, db, do = p.a.to(cuda).view(adt), p.b.to(cuda).view(torch.float8_e4m3fn), p.group_offs.to(cuda)
+    s1, s2 = torch.tensor(0.1, device=cuda), torch.tensor(0.1, device=cuda)
+    _say(f"persistent code object {fmt} N={N}")
+    ref = pkg.grouped_gemm_fp8_tensorwise(da, db, s1, s2, do)
+    module, func, name = harness.load_kernel(pkg.PERSISTENT_CODE_OBJECT_PATHS[fmt])
+    assert name == "_grouped_fp8_persistent_gemm_kernel"
+    try:
+        for grid in (harness.get_num_cus(0), 24, 20, 1):
+            out = torch.zeros_like(ref)
+            torch.cuda.synchronize()
+            harness.launch_persistent_kernel(func, da, db, out, s1, s2, do, len(lens), N, K, grid)
+            torch.cuda.synchronize()
+            assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), grid
+    finally:
+        harness.unload_kernel(module)
+
+
+# ----------------------------------------------------------------------------- full-size sites
+
+def test_constant_fill_known_answer_full_size(pkg, cuda):
+    """gate_up_fwd size, A bytes 0x38 (1.0), B bytes 0x40 (2.0), scales 0.1, K = 2880: every
+    output is 0.01 * 2880 * 2 = 57.6, which is bf16 57.5 (0x4266)."""
+    _say("persistent constant fill gate_up_fwd 131072x2880x5760")
+    lens = pkg.inputs.make_group_lens_reference()
+    offs = pkg.inputs.make_group_offs(lens).to(cuda)
+    a = torch.full((131072, 2880), 0x38, dtype=torch.uint8, device=cuda).view(torch.float8_e4m3fn)
+    b = torch.full((32, 5760, 2880), 0x40, dtype=torch.uint8, device=cuda).view(torch.float8_e4m3fn)
+    s = torch.tensor(0.1, device=cuda)
+    out = pkg.grouped_gemm_fp8_tensorwise(a, b, s, s, offs)
+    torch.cuda.synchronize()
+    assert bool((out.view(torch.int16) == 0x4266).all())
+
+
+def _rowsum_identity(p, out, dev):
+    """max over rows of |sum_n out - s_a s_b A[r] . (sum_n B[g, n, :])| / (sum_n |out| + eps)."""
+    offs = p.group_offs.cpu().tolist()
+    worst = 0.0
+    adt = p.a_dtype
+    for g in range(p.G):
+        lo, hi = offs[g], offs[g + 1]
+        if hi == lo:
+            continue
+        c = out[lo:hi].float()
+        lhs = c.sum(dim=1).double()
+        A = p.a[lo:hi].view(adt).double()
+        colsum = p.b[g].view(torch.float8_e4m3fn).double().sum(dim=0)
+        rhs = (A @ colsum) * float(np.float32(p.a_scale)) * float(np.float32(p.b_scale))
+        worst = max(worst, float(((lhs - rhs).abs() / (c.abs().sum(dim=1).double() + 1e-30)).max()))
+    return worst
+
+
+@pytest.mark.parametrize("name", ["gate_up_fwd", "down_fwd", "down_dgrad", "gate_up_dgrad"])
+def test_full_size_site(pkg, orc, orp, cuda, name):
+    _say(f"persistent full-size {name}")
+    p = pkg.inputs.make_fwd_problem(name, seed=0, device=cuda)
+    sa = torch.tensor(p.a_scale, dtype=torch.float32, device=cuda)
+    sb = torch.tensor(p.b_scale, dtype=torch.float32, device=cuda)
+    run = lambda: pkg.grouped_gemm_fp8_tensorwise(p.a.view(p.a_dtype), p.b.view(torch.float8_e4m3fn), sa, sb,
+                                                  p.group_offs)
+    out = run()
+    out2 = run()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16)), "non-deterministic output"
+    assert bool(torch.isfinite(out).all())
+    worst = _rowsum_identity(p, out, cuda)
+    _say(f"{name}: row-sum identity worst relative residual {worst:.3e}")
+    assert worst < 2 ** -6
+    # oracle on the smallest, a median and the largest group: first 400 and last 200 rows of each
+    offs = p.group_offs.cpu().numpy()
+    lens = np.diff(offs)
+    order = np.argsort(lens, kind="stable")
+    cmax = float(out.float().abs().max())
+    for g in sorted({int(order[0]), int(order[len(order) // 2]), int(order[-1])}):
+        lo, hi = int(offs[g]), int(offs[g + 1])
+        rows = np.unique(np.concatenate([np.arange(lo, min(hi, lo + 400)), np.arange(max(lo, hi - 200), hi)]))
+        a_rows = p.a[torch.from_numpy(rows).to(cuda)].cpu().numpy()
+        ref = orp.grouped_fp8(a_rows, p.b[g:g + 1].cpu().numpy(), p.a_scale, p.b_scale,
+                              np.array([0, rows.size]), p.a_format)
+        got = pkg.as_bf16_bits(out[torch.from_numpy(rows).to(cuda)])
+        m = orc.compare(got, ref, ref_absmax=cmax)
+        _say(f"{name} group {g} rows={hi - lo} (checked {rows.size}): {m}")
+        assert orc.parity_ok(m), (name, g, m)
