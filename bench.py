@@ -1,11 +1,15 @@
 #!/usr/bin/env python3
-"""Benchmark of the variable-K FP8 grouped wgrad on one MI355X.
+"""Benchmark of the FP8 grouped GEMMs on one MI355X.
 
-Workload (BASELINE headline): gate_up_wgrad, G=32 experts, M_total=131072 tokens, LHS e4m3
-[131072, 2880], RHS e5m2 [131072, 5760], C bf16 [32, 2880, 5760], per-tensor scales, seeded
-uniform-multinomial group sizes, inputs generated directly in HBM. One step = one launch of the
-grouped wgrad (all 32 experts). FLOPs per step = 2 * M_total * OUT_M * OUT_N (reference
+Workload (BASELINE headline, the default): gate_up_wgrad, G=32 experts, M_total=131072 tokens,
+LHS e4m3 [131072, 2880], RHS e5m2 [131072, 5760], C bf16 [32, 2880, 5760], per-tensor scales,
+seeded uniform-multinomial group sizes, inputs generated directly in HBM. One step = one launch of
+the grouped wgrad (all 32 experts). FLOPs per step = 2 * M_total * OUT_M * OUT_N (reference
 bench.py:742, launcher.cpp:76).
+
+``--config gate_up_fwd | down_fwd | down_dgrad | gate_up_dgrad`` measures the persistent
+forward / data-gradient grouped GEMM at the reference's other call sites instead (reference
+bench.py:153-180, inputs as in bench.py:205-223,238-247; FLOPs = 2 * M_total * K * N).
 
 Prints ONE JSON line with ms, TFLOPS, the MFMA roofline fraction and a CPU baseline (the
 build's numpy oracle on a bounded sample of the same workload, timed on this host's cores).
@@ -23,7 +27,11 @@ sys.path.insert(0, ROOT)
 
 FP8_DENSE_PEAK_TFLOPS = 5000.0    # MI355X dense FP8 MFMA peak
 REF_OPT_ASM_TFLOPS = 1237.0       # reference optimized ASM, gate_up_wgrad, C launcher (README.md:60)
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gate_up_wgrad.txt")
+FWD_SITES = ("gate_up_fwd", "down_fwd", "down_dgrad", "gate_up_dgrad")
+
+
+def traffic_file(name):
+    return os.path.join(ROOT, "profiles", f"traffic_{name}.txt")
 
 
 def parse_args():
@@ -32,7 +40,7 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="gate_up_wgrad",
-                    choices=["gate_up_wgrad", "down_wgrad", "gate_up_zipf", "gate_up_mx", "constant"])
+                    choices=["gate_up_wgrad", "down_wgrad", "gate_up_zipf", "gate_up_mx", "constant", *FWD_SITES])
     ap.add_argument("--mfma", default="k128", choices=["k128", "k32"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -55,10 +63,10 @@ def copy_calibration(mib, steps):
     print(json.dumps({"copy_calibration_bytes_per_launch": mib << 20, "launches": steps}), flush=True)
 
 
-def read_traffic():
+def read_traffic(name):
     """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE), if recorded."""
     try:
-        for line in open(TRAFFIC_FILE):
+        for line in open(traffic_file(name)):
             if line.startswith("traffic_bytes_per_launch:"):
                 return float(line.split(":", 1)[1])
     except OSError:
@@ -68,6 +76,12 @@ def read_traffic():
 
 def make_runner(pkg, p, dev, mfma):
     import torch
+    if hasattr(p, "a_format"):   # forward / data-gradient site: the persistent grouped GEMM
+        sa = torch.tensor(p.a_scale, dtype=torch.float32, device=dev)
+        sb = torch.tensor(p.b_scale, dtype=torch.float32, device=dev)
+        out = torch.empty((p.M, p.N), dtype=torch.bfloat16, device=dev)
+        a, b = p.a.view(p.a_dtype), p.b.view(torch.float8_e4m3fn)
+        return lambda: pkg.grouped_gemm_fp8_tensorwise(a, b, sa, sb, p.group_offs, out=out)
     if p.is_mx:
         out = torch.empty((p.G, p.OUT_M, p.OUT_N), dtype=torch.bfloat16, device=dev)
         return lambda: pkg.grouped_gemm_mxfp8_variable_k(p.lhs, p.rhs, p.lhs_mx, p.rhs_mx, p.group_offs, out=out)
@@ -93,16 +107,48 @@ def time_steps(run, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
+def _blas_threads():
+    try:
+        from threadpoolctl import threadpool_info
+        return max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:
+        return os.cpu_count() or 1
+
+
+def cpu_baseline_fwd(p, seconds):
+    """Numpy oracle of the persistent GEMM (fp32 dequantize + BLAS sgemm + bf16 RNE) on whole
+    groups until ~`seconds` of CPU time; throughput in TFLOPS over the groups processed."""
+    import numpy as np
+    from oracle import persistent_oracle as orp
+    threads = _blas_threads()
+    offs = p.group_offs.cpu().numpy()
+    done_flops, t_total, groups, rows = 0.0, 0.0, 0, 0
+    for g in range(p.G):
+        lo, hi = int(offs[g]), int(offs[g + 1])
+        if hi == lo:
+            continue
+        A = p.a[lo:hi].cpu().numpy()
+        B = p.b[g:g + 1].cpu().numpy()
+        t0 = time.perf_counter()
+        orp.grouped_fp8(A, B, p.a_scale, p.b_scale, np.array([0, hi - lo], dtype=np.int64), p.a_format)
+        t_total += time.perf_counter() - t0
+        done_flops += 2.0 * (hi - lo) * p.K * p.N
+        groups += 1
+        rows += hi - lo
+        if t_total >= seconds:
+            break
+    return {"value": round(done_flops / t_total / 1e12, 4), "unit": "TFLOPS", "cores": int(threads),
+            "kind": "port",
+            "sample": f"{groups} of {p.G} groups ({rows} rows, {done_flops / 1e12:.2f} TFLOP) of {p.name}: "
+                      f"numpy fp32 dequantize + OpenBLAS sgemm + bf16 RNE, {t_total:.1f} s"}
+
+
 def cpu_baseline(p, seconds):
     """Numpy oracle (fp32 dequantize + BLAS sgemm + bf16 RNE) on whole groups of the workload
     until ~`seconds` of CPU time; throughput in TFLOPS over the groups processed."""
     import numpy as np
     from oracle import vark_oracle as orc
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
-    except Exception:
-        threads = os.cpu_count() or 1
+    threads = _blas_threads()
     offs = p.group_offs.cpu().numpy()
     done_flops, t_total, groups, tokens = 0.0, 0.0, 0, 0
     for g in range(p.G):
@@ -139,17 +185,38 @@ def main():
     from __graft_entry__ import load_package
     pkg = load_package()
     dev = torch.device("cuda:0")
+    fwd = args.config in FWD_SITES
     if args.config == "constant":
         p = pkg.inputs.constant_problem(device=dev)
+    elif fwd:
+        p = pkg.inputs.make_fwd_problem(args.config, seed=args.seed, device=dev)
     else:
         p = pkg.inputs.make_problem(args.config, seed=args.seed, device=dev)
     torch.cuda.synchronize()
     run = make_runner(pkg, p, dev, args.mfma)
     ms = time_steps(run, args.steps, args.warmup)
     tflops = p.flops / (ms * 1e-3) / 1e12
-    traffic = read_traffic() if args.config == "gate_up_wgrad" else None
+    traffic = read_traffic(args.config)
+    if fwd:
+        geo = pkg.launch_geometry(p.N)
+        config = {"workload": p.name, "G": p.G, "M_total": p.M, "K": p.K, "N": p.N,
+                  "a": {"e4m3": "e4m3fn", "e5m2": "e5m2"}[p.a_format], "b": "e4m3fn [G, N, K] (trans_b)",
+                  "out": "bf16", "acc": "fp32",
+                  "inputs": "reference recipe: seed-42 exponential group sizes, randn bf16 cast to fp8, "
+                            "scales 0.1, in HBM",
+                  "kernel": "hip gfx950 persistent {tile_m}x{tile_n} tiles, 128-K stages, mfma k128".format(**geo),
+                  "baseline_number": "none published for this site"}
+        vs_baseline = None
+    else:
+        config = {"workload": p.name, "G": p.G, "M_total": p.M, "OUT_M": p.OUT_M, "OUT_N": p.OUT_N,
+                  "lhs": "e4m3fn", "rhs": "e5m2", "out": "bf16", "acc": "fp32",
+                  "inputs": "seeded N(0,1) / N(0,1e-3) quantized per-tensor, multinomial group sizes, in HBM",
+                  "kernel": "hip gfx950 persistent {tile_m}x{tile_n} tiles, mfma {mfma}".format(
+                      mfma=args.mfma, **pkg.launch_geometry(p.OUT_N)),
+                  "baseline_number": "reference optimized ASM 3.515 ms / 1237 TFLOPS (README.md:60)"}
+        vs_baseline = round(tflops / REF_OPT_ASM_TFLOPS, 4)
     line = {
-        "metric": "ms + TFLOPS (% FP8 peak) for gate_up_wgrad G=32 M=131072 on 1 MI355X",
+        "metric": f"ms + TFLOPS (% FP8 peak) for {p.name if fwd else 'gate_up_wgrad'} G=32 M=131072 on 1 MI355X",
         "value": round(tflops, 2),
         "unit": "TFLOPS",
         "n_gpus": 1,
@@ -158,33 +225,36 @@ def main():
         "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": round(tflops / REF_OPT_ASM_TFLOPS, 4),
+        "vs_baseline": vs_baseline,
         "dtype": "fp8",
         "data": "synthetic",
-        "config": {"workload": p.name, "G": p.G, "M_total": p.M, "OUT_M": p.OUT_M, "OUT_N": p.OUT_N,
-                   "lhs": "e4m3fn", "rhs": "e5m2", "out": "bf16", "acc": "fp32",
-                   "inputs": "seeded N(0,1) / N(0,1e-3) quantized per-tensor, multinomial group sizes, in HBM",
-                   "kernel": "hip gfx950 persistent {tile_m}x{tile_n} tiles, mfma {mfma}".format(
-                       mfma=args.mfma, **pkg.launch_geometry(p.OUT_N)),
-                   "baseline_number": "reference optimized ASM 3.515 ms / 1237 TFLOPS (README.md:60)"},
+        "config": config,
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP8_DENSE_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / FP8_DENSE_PEAK_TFLOPS, 4), "traffic": traffic},
     }
     if args.extra:
         extra = {}
-        for name in ("down_wgrad", "gate_up_zipf", "gate_up_mx", "constant"):
-            q = pkg.inputs.constant_problem(device=dev) if name == "constant" else \
-                pkg.inputs.make_problem(name, seed=args.seed, device=dev)
+        for name in ("down_wgrad", "gate_up_zipf", "gate_up_mx", "constant", *FWD_SITES):
+            if name == args.config:
+                continue
+            if name == "constant":
+                q = pkg.inputs.constant_problem(device=dev)
+            elif name in FWD_SITES:
+                q = pkg.inputs.make_fwd_problem(name, seed=args.seed, device=dev)
+            else:
+                q = pkg.inputs.make_problem(name, seed=args.seed, device=dev)
             r = make_runner(pkg, q, dev, args.mfma)
             t = time_steps(r, max(args.steps // 4, 10), max(args.warmup // 4, 5))
             extra[name] = {"ms": round(t, 4), "TFLOPS": round(q.flops / (t * 1e-3) / 1e12, 2)}
             del q, r
-        if args.mfma == "k128":
+        if args.mfma == "k128" and args.config == "gate_up_wgrad":
             r = make_runner(pkg, p, dev, "k32")
             t = time_steps(r, max(args.steps // 4, 10), max(args.warmup // 4, 5))
             extra["gate_up_wgrad_k32_mfma"] = {"ms": round(t, 4), "TFLOPS": round(p.flops / (t * 1e-3) / 1e12, 2)}
         line["extra"] = extra
-    if args.cpu_seconds > 0 and not p.is_mx:
+    if args.cpu_seconds > 0 and fwd:
+        line["cpu_baseline"] = cpu_baseline_fwd(p, args.cpu_seconds)
+    elif args.cpu_seconds > 0 and not p.is_mx:
         line["cpu_baseline"] = cpu_baseline(p, args.cpu_seconds)
     else:
         line["cpu_baseline"] = None
