@@ -16,8 +16,11 @@
 //    64 KiB per stage), two stages in the flat 160 KiB, one barrier per stage, the next tile's
 //    first stage issued during the current tile's last.
 //  * LDS-DMA of 16 bytes per lane, 8 rows x 128 bytes per wave-instruction; logical chunk c of row
-//    r is stored at physical chunk c ^ ((r >> 1) & 7), so the 16 rows x 16 bytes that one 16-lane
-//    group reads land in 16 distinct 4-bank slots.
+//    r is stored at physical chunk c ^ (r & 7) ^ ((r >> 3) & 1). The LDS serves a 128-bit read 8
+//    lanes (128 bytes, all 32 banks) per cycle, and 8 lanes of an operand read take 8 consecutive
+//    rows at one logical chunk: the swizzle puts them on 8 distinct chunks (measured: the row-pair
+//    swizzle (r >> 1) & 7, conflict-free only for 16-lane / 64-bank service, had every such read
+//    2-way conflicted). The (r >> 3) term also keeps 16 consecutive rows distinct in 256 bytes.
 //  * K tail (K % 128 != 0, K a multiple of 16): the lanes whose chunk lies past K load from an
 //    out-of-range buffer offset, which returns zeros, so both operands hold zeros there.
 //  * MFMA: v_mfma_f32_16x16x128_f8f6f4 (unscaled; the per-tensor scales multiply in the
@@ -41,7 +44,7 @@ constexpr int kRow = 128;                    // LDS bytes per operand row and st
 constexpr int64_t kMaxRow = (int64_t(1) << 31) - 256;   // group offsets (32-bit row indices)
 constexpr int64_t kMaxTiles = int64_t(1) << 30;         // tiles of one launch (32-bit tile indices)
 
-__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 struct Args {
   const uint8_t* a;
@@ -77,10 +80,10 @@ struct Cfg2 {
 
 // LDS-DMA instruction i = wave + 8 j fills slot bytes [1024 i, +1024): operand rows 8 i' .. 8 i' + 7
 // with i' = wave + 8 jj (A: the 24 instructions j = jj = 0..2 of every wave; B: jj = j - 3), lane l
-// writing physical chunk l % 8 of row 8 i' + l / 8. That row's swizzle, (4 i' + l / 16) & 7,
-// is 4 (wave & 1) + l / 16 for every instruction of the wave, so each lane loads the same logical
-// chunk in all of them and its byte offset is a per-lane base plus the wave-uniform 64 jj stride.
-__device__ __forceinline__ int dma_chunk(int wave, int lane) { return (lane & 7) ^ (4 * (wave & 1) + (lane >> 4)); }
+// writing physical chunk l % 8 of row 8 i' + l / 8. That row's swizzle, (l / 8) ^ (i' & 1), is
+// (l / 8) ^ (wave & 1) for every instruction of the wave, so each lane loads the same logical chunk
+// in all of them and its byte offset is a per-lane base plus the wave-uniform 64 jj stride.
+__device__ __forceinline__ int dma_chunk(int wave, int lane) { return (lane & 7) ^ (lane >> 3) ^ (wave & 1); }
 __device__ __forceinline__ int dma_base(int wave, int lane, int stride) {
   return (8 * wave + (lane >> 3)) * stride + 16 * dma_chunk(wave, lane);
 }
@@ -207,6 +210,7 @@ __device__ __forceinline__ void persistent_body(const Args& a, GG_LDS uint8_t* l
   const int s16 = lane & 15;
   // Slot-relative byte offsets of this lane's reads in block 0 of each operand. A block starts at
   // a multiple of 16 rows, so a lane's row swizzle is swz(s16) in every block: block i is at +2048 i.
+  // Lanes 8k .. 8k+7 (served together) read rows s16 = 8 (k & 1) + 0..7 at one logical chunk.
   // The high half (chunk 2q+1) sits at the low half's offset XOR 16 (chunk bit 0 is address bit 4;
   // slot and block offsets are multiples of 1024).
   const int sw = 16 * ((2 * q) ^ swz(s16));

@@ -28,7 +28,11 @@ def _tn(N):
 
 
 def _swz(r):
-    return (r >> 1) & 7
+    return (r & 7) ^ ((r >> 3) & 1)
+
+
+def _dma_chunk(wave, lane):
+    return (lane & 7) ^ (lane >> 3) ^ (wave & 1)
 
 
 # ----------------------------------------------------------------------------- schedule model
@@ -129,7 +133,7 @@ def test_dma_offsets_and_slot_coverage(TN):
                 row = 8 * ip + lane // 8
                 pc = lane % 8
                 lc = pc ^ _swz(row)
-                dma_chunk = (lane & 7) ^ (4 * (wave & 1) + (lane >> 4))
+                dma_chunk = _dma_chunk(wave, lane)
                 assert dma_chunk == lc
                 stride = stride_a if lhs else stride_b
                 voff = (8 * wave + (lane >> 3)) * stride + 16 * dma_chunk + 64 * jj * stride
@@ -169,6 +173,31 @@ def test_operand_reads_share_k_order_and_cover_stage(TN):
     assert ks == list(range(128))
 
 
+@pytest.mark.parametrize("TN", [320, 384])
+def test_operand_reads_bank_conflict_free(TN):
+    """Every 128-bit operand read is conflict-free when the LDS serves 8 lanes (128 bytes over 32
+    4-byte banks) per cycle -- the service the profile of the row-pair swizzle matched (every read
+    2-way conflicted) -- and also under 16-lane / 64-bank service."""
+    wave_n = TN // 4
+    for wave in range(8):
+        wm, wn = wave & 1, wave >> 1
+        addrs = {}
+        for lane in range(64):
+            q, s16 = lane >> 4, lane & 15
+            sw = 16 * ((2 * q) ^ _swz(s16))
+            for side, base, nblk in (("m", (wm * 96 + s16) * 128 + sw, 6),
+                                     ("n", TILE_M * 128 + (wn * wave_n + s16) * 128 + sw, wave_n // 16)):
+                for i in range(nblk):
+                    addrs.setdefault((side, i, "lo"), []).append(base + 2048 * i)
+                    addrs.setdefault((side, i, "hi"), []).append((base ^ 16) + 2048 * i)
+        for key, a in addrs.items():
+            assert len(a) == 64
+            for lanes, banks in ((8, 32), (16, 64)):
+                for g0 in range(0, 64, lanes):
+                    units = [(x // 16) % (banks // 4) for x in a[g0:g0 + lanes]]
+                    assert len(set(units)) == lanes, (TN, wave, key, lanes, g0, units)
+
+
 @pytest.mark.parametrize("TN,N", [(320, 2880), (320, 336), (384, 5760), (320, 16)])
 def test_epilogue_stores_in_bounds(TN, N):
     wave_n = TN // 4
@@ -204,7 +233,7 @@ def test_k_tail_dead_lanes():
                 jj = j if j < 3 else j - 3
                 for lane in range(64):
                     row = (j < 3, 8 * (wave + 8 * jj) + lane // 8)
-                    lc = (lane & 7) ^ (4 * (wave & 1) + (lane >> 4))
+                    lc = _dma_chunk(wave, lane)
                     if not (kv < 128 and 16 * lc >= kv):
                         rows.setdefault(row, []).append(lc)
         assert len(rows) == 192 + 384
