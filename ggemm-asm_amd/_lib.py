@@ -1,5 +1,5 @@
-"""ctypes binding of libggemm_vark.so (declarations in include/ggemm_vark.h and
-include/ggemm_persistent.h)."""
+"""ctypes binding of libggemm_vark.so (declarations in include/ggemm_vark.h,
+include/ggemm_persistent.h and include/ggemm_quant.h)."""
 from __future__ import annotations
 
 import ctypes
@@ -22,6 +22,12 @@ EXPORTS = (
 
 PERSISTENT_EXPORTS = (
     "ggemm_persistent_fp8",
+)
+
+QUANT_EXPORTS = (
+    "ggemm_quant_amax",
+    "ggemm_quant_fp8_tensorwise",
+    "ggemm_quant_mxfp8_grouped",
 )
 
 ERRORS = {
@@ -71,6 +77,13 @@ def load():
     lib.ggemm_vark_launch_geometry.restype = None
     lib.ggemm_persistent_fp8.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 9 + [ctypes.c_int64, vp]
     lib.ggemm_persistent_fp8.restype = ctypes.c_int
+    i64 = ctypes.c_int64
+    lib.ggemm_quant_amax.argtypes = [vp, i32, i64, i32, i64, vp, vp]
+    lib.ggemm_quant_amax.restype = ctypes.c_int
+    lib.ggemm_quant_fp8_tensorwise.argtypes = [vp, i32, i64, i32, i64, i32, vp, i64, vp, vp, vp]
+    lib.ggemm_quant_fp8_tensorwise.restype = ctypes.c_int
+    lib.ggemm_quant_mxfp8_grouped.argtypes = [vp, i32, i64, i32, i64, vp, i32, i32, vp, i64, i64, vp, i64, vp, vp]
+    lib.ggemm_quant_mxfp8_grouped.restype = ctypes.c_int
     _lib = lib
     return lib
 

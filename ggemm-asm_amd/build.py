@@ -1,8 +1,8 @@
 """In-tree build of the HIP artefacts for gfx950.
 
 * ``lib/libggemm_vark.so`` -- the extern "C" launcher library: the variable-K wgrad kernels
-  (tensorwise, K=32-MFMA, MXFP8; include/ggemm_vark.h) and the persistent fwd/dgrad grouped GEMM
-  (include/ggemm_persistent.h).
+  (tensorwise, K=32-MFMA, MXFP8; include/ggemm_vark.h), the persistent fwd/dgrad grouped GEMM
+  (include/ggemm_persistent.h) and the FP8 quantization producer (include/ggemm_quant.h).
 * ``lib/variable_k_wgrad.co`` -- the drop-in code object exporting only
   ``_grouped_variable_k_gemm_kernel`` with the reference kernarg layout.
 * ``lib/persistent_e4m3.co`` / ``lib/persistent_e5m2.co`` -- drop-in code objects exporting only
@@ -49,7 +49,7 @@ def build_so(verbose: bool = False) -> str:
     os.makedirs(LIB_DIR, exist_ok=True)
     tmp = SO_PATH + ".tmp"
     _run([hipcc(), *DEVICE_FLAGS, "-fPIC", "-shared", os.path.join(CSRC, "vark_capi.hip"),
-          os.path.join(CSRC, "persistent_capi.hip"), "-o", tmp], verbose)
+          os.path.join(CSRC, "persistent_capi.hip"), os.path.join(CSRC, "quant_capi.hip"), "-o", tmp], verbose)
     os.replace(tmp, SO_PATH)
     return SO_PATH
 

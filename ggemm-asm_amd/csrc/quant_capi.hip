@@ -1,0 +1,115 @@
+// extern "C" launchers of the FP8 quantization producer (include/ggemm_quant.h), part of
+// libggemm_vark.so. Arguments are validated on the host; nothing is launched on a validation error.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../include/ggemm_persistent.h"
+#include "../../include/ggemm_quant.h"
+#include "capi_common.h"
+#include "quant_kernel.h"
+
+static_assert(GGEMM_QUANT_MAX_GROUPS == ggemm::qt::kMaxGroups, "header and kernel agree");
+
+namespace {
+
+using ggemm::host::aligned;
+using ggemm::host::device_cus;
+namespace qt = ggemm::qt;
+
+int check_2d(const void* x, int in_dtype, int64_t rows, int cols, int64_t stride) {
+  if (!x) return GGEMM_E_NULL;
+  if (in_dtype != GGEMM_IN_BF16 && in_dtype != GGEMM_IN_F32) return GGEMM_E_FORMAT;
+  if (rows < 0 || cols <= 0 || cols % 8) return GGEMM_E_SHAPE;
+  if (stride < cols || stride % 8) return GGEMM_E_STRIDE;
+  if (!aligned(x, 16)) return GGEMM_E_ALIGN;
+  return GGEMM_OK;
+}
+
+int grid_for(int64_t chunks, int cus) {
+  const int64_t want = (chunks + qt::kThreads - 1) / qt::kThreads;
+  const int64_t cap = (int64_t)cus * 16;
+  return (int)(want < 1 ? 1 : (want > cap ? cap : want));
+}
+
+void launch_amax(const void* x, int in_dtype, int64_t rows, int cols, int64_t stride, float* amax, int cus,
+                 hipStream_t s) {
+  uint32_t* bits = reinterpret_cast<uint32_t*>(amax);
+  hipLaunchKernelGGL(qt::amax_init, dim3(1), dim3(64), 0, s, bits);
+  if (rows == 0) return;
+  const int grid = grid_for(rows * (cols / 8), cus);
+  if (in_dtype == GGEMM_IN_F32)
+    hipLaunchKernelGGL(qt::amax_kernel<true>, dim3(grid), dim3(qt::kThreads), 0, s, x, rows, cols, stride, bits);
+  else
+    hipLaunchKernelGGL(qt::amax_kernel<false>, dim3(grid), dim3(qt::kThreads), 0, s, x, rows, cols, stride, bits);
+}
+
+}  // namespace
+
+extern "C" {
+
+int ggemm_quant_amax(const void* x, int32_t in_dtype, int64_t rows, int32_t cols, int64_t stride, float* amax_out,
+                     void* stream) {
+  int rc = check_2d(x, in_dtype, rows, cols, stride);
+  if (rc) return rc;
+  if (!amax_out) return GGEMM_E_NULL;
+  if (!aligned(amax_out, 4)) return GGEMM_E_ALIGN;
+  int cus = 0;
+  rc = device_cus(&cus);
+  if (rc) return rc;
+  launch_amax(x, in_dtype, rows, cols, stride, amax_out, cus, (hipStream_t)stream);
+  return (int)hipGetLastError();
+}
+
+int ggemm_quant_fp8_tensorwise(const void* x, int32_t in_dtype, int64_t rows, int32_t cols, int64_t stride,
+                               int32_t out_format, void* out, int64_t out_stride, float* scale_out,
+                               float* amax_out, void* stream) {
+  int rc = check_2d(x, in_dtype, rows, cols, stride);
+  if (rc) return rc;
+  if (!out || !scale_out || !amax_out) return GGEMM_E_NULL;
+  if (out_format != GGEMM_FP8_E4M3 && out_format != GGEMM_FP8_E5M2) return GGEMM_E_FORMAT;
+  if (out_stride < cols || out_stride % 8) return GGEMM_E_STRIDE;
+  if (!aligned(out, 8) || !aligned(scale_out, 4) || !aligned(amax_out, 4)) return GGEMM_E_ALIGN;
+  int cus = 0;
+  rc = device_cus(&cus);
+  if (rc) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  launch_amax(x, in_dtype, rows, cols, stride, amax_out, cus, s);
+  const int grid = grid_for(rows * (cols / 8), cus);
+  const uint32_t* bits = reinterpret_cast<const uint32_t*>(amax_out);
+  uint8_t* o = static_cast<uint8_t*>(out);
+  const bool f32 = in_dtype == GGEMM_IN_F32, e5 = out_format == GGEMM_FP8_E5M2;
+  auto k = f32 ? (e5 ? qt::quant_tensorwise_kernel<true, true> : qt::quant_tensorwise_kernel<true, false>)
+               : (e5 ? qt::quant_tensorwise_kernel<false, true> : qt::quant_tensorwise_kernel<false, false>);
+  hipLaunchKernelGGL(k, dim3(grid), dim3(qt::kThreads), 0, s, x, rows, cols, stride, o, out_stride, bits, scale_out);
+  return (int)hipGetLastError();
+}
+
+int ggemm_quant_mxfp8_grouped(const void* x, int32_t in_dtype, int64_t rows, int32_t cols, int64_t stride,
+                              const int64_t* group_offs, int32_t G, int32_t out_format, void* out,
+                              int64_t out_stride, int64_t out_rows, uint8_t* scales, int64_t scale_stride,
+                              int64_t* padded_offs, void* stream) {
+  int rc = check_2d(x, in_dtype, rows, cols, stride);
+  if (rc) return rc;
+  if (!group_offs || !out || !scales || !padded_offs) return GGEMM_E_NULL;
+  if (out_format != GGEMM_FP8_E4M3 && out_format != GGEMM_FP8_E5M2) return GGEMM_E_FORMAT;
+  if (G <= 0 || G > qt::kMaxGroups || cols % 16) return GGEMM_E_SHAPE;
+  // 32-bit row indices inside the kernel
+  if (rows + 31 * (int64_t)G > 0x7fffffffLL) return GGEMM_E_SHAPE;
+  if (out_rows < rows + 31 * (int64_t)G) return GGEMM_E_SHAPE;
+  if (out_stride < cols || out_stride % 16 || scale_stride < cols || scale_stride % 16) return GGEMM_E_STRIDE;
+  if (!aligned(out, 16) || !aligned(scales, 16) || !aligned(padded_offs, 8) || !aligned(group_offs, 8))
+    return GGEMM_E_ALIGN;
+  int cus = 0;
+  rc = device_cus(&cus);
+  if (rc) return rc;
+  qt::MxArgs a{x, rows, stride, cols, group_offs, G, static_cast<uint8_t*>(out), out_stride, scales, scale_stride,
+               padded_offs};
+  const bool f32 = in_dtype == GGEMM_IN_F32, e5 = out_format == GGEMM_FP8_E5M2;
+  auto k = f32 ? (e5 ? qt::quant_mx_grouped_kernel<true, true> : qt::quant_mx_grouped_kernel<true, false>)
+               : (e5 ? qt::quant_mx_grouped_kernel<false, true> : qt::quant_mx_grouped_kernel<false, false>);
+  hipLaunchKernelGGL(k, dim3(cus * 4), dim3(qt::kThreads), 0, (hipStream_t)stream, a);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

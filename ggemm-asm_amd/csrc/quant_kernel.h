@@ -1,0 +1,300 @@
+// FP8 quantization producer for the grouped GEMMs, gfx950 (MI355X, CDNA4): the step before the
+// GEMMs, turning bf16 / fp32 activations, gradients and weights into their fp8 operands.
+//
+//  * amax:        amax = max |x| over a 2-D [rows, cols] tensor (NaN propagates).
+//  * tensorwise:  scale = amax / fmax (1 when amax == 0), q = fp8(clamp(x / scale, -fmax, fmax)).
+//  * MX, grouped: groups of rows (the token axis) padded to multiples of 32 rows; per 32-row block
+//                 and column, X = floor(log2(fl32(amax_blk / fmax))) clamped to [-127, 127]
+//                 (0 for an all-zero block), e8m0 byte X + 127, q = fp8(clamp(x * 2^-X, +-fmax));
+//                 padding rows are zero and the padded group offsets are written out.
+//
+// fmax = 448 (e4m3fn) or 57344 (e5m2). Rounding: x / scale is the correctly rounded fp32 quotient,
+// fp32 -> fp8 is round-to-nearest-even (subnormals included), -0 keeps its sign, NaN becomes the
+// format's NaN code (0x7F / 0xFF for e4m3fn, 0x7F / 0xFF for e5m2). These are the recipes of the
+// measured configurations (x / (amax/fmax) clamped and cast; MX block exponents from the block
+// amax), with floor(log2()) taken exactly on the fp32 quotient.
+//
+// All three are HBM-bound streaming kernels: 16-byte (bf16) or 32-byte (fp32) loads of 8 elements
+// per thread in the tensorwise path, 8-byte fp8 stores; the MX kernel keeps a 32-row x 4-column
+// block in registers so x is read once.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ggemm {
+namespace qt {
+
+constexpr int kThreads = 256;
+constexpr int kMaxGroups = 2047;     // MX: group offsets and padded offsets held in LDS
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+template <bool kE5M2>
+__device__ __forceinline__ constexpr float fmax_of() { return kE5M2 ? 57344.0f : 448.0f; }
+
+// fp32 -> fp8 byte, round to nearest even. |f| <= fmax unless NaN (callers clamp first).
+//  e4m3fn: bias 7, 3 mantissa bits, subnormals m * 2^-9; e5m2: bias 15, 2 bits, m * 2^-16.
+// Normal range: add the rounding increment to the fp32 bits below the kept mantissa (a carry
+// moves into the exponent, which is the correctly rounded result), then rebias. Subnormal range:
+// |f| * 2^(9 or 16) is exact, and rint rounds half to even.
+template <bool kE5M2>
+__device__ __forceinline__ uint32_t f32_to_fp8(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t s = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  constexpr int kMant = kE5M2 ? 2 : 3;
+  constexpr int kShift = 23 - kMant;
+  constexpr uint32_t kMinNormal = kE5M2 ? 0x38800000u : 0x3c800000u;   // 2^-14, 2^-6
+  constexpr uint32_t kRebias = (kE5M2 ? (127 - 15) : (127 - 7)) << kMant;
+  if (a > 0x7f800000u) return s | 0x7fu;                                   // NaN
+  if (a >= kMinNormal) {
+    const uint32_t r = (a + ((1u << (kShift - 1)) - 1) + ((a >> kShift) & 1u)) >> kShift;
+    return s | (r - kRebias);
+  }
+  const float m = __builtin_rintf(__uint_as_float(a) * (kE5M2 ? 65536.0f : 512.0f));
+  return s | (uint32_t)m;
+}
+
+// clamp to [-fmax, fmax]; NaN stays NaN
+template <bool kE5M2>
+__device__ __forceinline__ float clamp_fmax(float v) {
+  constexpr float m = fmax_of<kE5M2>();
+  return v != v ? v : fminf(fmaxf(v, -m), m);
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// 8 consecutive elements of row `row`, chunk `c` (elements 8c .. 8c+7), as fp32
+template <bool kF32>
+__device__ __forceinline__ void load8(const void* x, int64_t row, int64_t stride, int c, float v[8]) {
+  if constexpr (kF32) {
+    const v4f* p = (const v4f*)((const float*)x + row * stride + 8 * (int64_t)c);
+    const v4f a = __builtin_nontemporal_load(p), b = __builtin_nontemporal_load(p + 1);
+    v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3]; v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
+  } else {
+    const v4u w = __builtin_nontemporal_load((const v4u*)((const uint16_t*)x + row * stride + 8 * (int64_t)c));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[2 * k] = bf16_lo(w[k]);
+      v[2 * k + 1] = bf16_hi(w[k]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------- amax
+
+__global__ void __launch_bounds__(64) amax_init(uint32_t* amax_bits) {
+  if (threadIdx.x == 0) *amax_bits = 0u;
+}
+
+// max of |x| as fp32 bits (ordered like unsigned integers for non-negative values; any NaN is
+// larger than +inf, so NaN propagates), one atomic per workgroup
+template <bool kF32>
+__global__ void __launch_bounds__(kThreads) amax_kernel(const void* x, int64_t rows, int cols, int64_t stride,
+                                                        uint32_t* amax_bits) {
+  const int cpr = cols / 8;
+  const int64_t n = rows * cpr;
+  uint32_t m = 0;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    const int64_t row = i / cpr;
+    const int c = (int)(i - row * cpr);
+    float v[8];
+    load8<kF32>(x, row, stride, c, v);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) m = max(m, __float_as_uint(v[k]) & 0x7fffffffu);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
+  __shared__ uint32_t s_m[kThreads / 64];
+  if ((threadIdx.x & 63) == 0) s_m[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) m = max(m, s_m[w]);
+    if (m) atomicMax(amax_bits, m);
+  }
+}
+
+// ---------------------------------------------------------------------------------- tensorwise
+
+template <bool kE5M2>
+__device__ __forceinline__ float tensor_scale(uint32_t amax_bits) {
+  const float amax = __uint_as_float(amax_bits);
+  return amax > 0.0f ? amax / fmax_of<kE5M2>() : (amax == 0.0f ? 1.0f : amax);   // NaN stays NaN
+}
+
+template <bool kF32, bool kE5M2>
+__global__ void __launch_bounds__(kThreads) quant_tensorwise_kernel(const void* x, int64_t rows, int cols,
+                                                                    int64_t stride, uint8_t* out,
+                                                                    int64_t out_stride, const uint32_t* amax_bits,
+                                                                    float* scale_out) {
+  const float scale = tensor_scale<kE5M2>(*amax_bits);
+  if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
+  const int cpr = cols / 8;
+  const int64_t n = rows * cpr;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+    const int64_t row = i / cpr;
+    const int c = (int)(i - row * cpr);
+    float v[8];
+    load8<kF32>(x, row, stride, c, v);
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      w0 |= f32_to_fp8<kE5M2>(clamp_fmax<kE5M2>(v[k] / scale)) << (8 * k);
+      w1 |= f32_to_fp8<kE5M2>(clamp_fmax<kE5M2>(v[k + 4] / scale)) << (8 * k);
+    }
+    *(v2u*)(out + row * out_stride + 8 * (int64_t)c) = v2u{w0, w1};
+  }
+}
+
+// ---------------------------------------------------------------------------------- MX, grouped
+
+// e8m0 exponent of a 32-row block column: floor(log2(fl32(amax / fmax))) clamped to [-127, 127],
+// 0 for amax == 0; a NaN amax gives the e8m0 NaN code (returned as 128: byte 0xFF).
+template <bool kE5M2>
+__device__ __forceinline__ int block_exponent(float amax) {
+  if (amax != amax) return 128;
+  if (amax == 0.0f) return 0;
+  const float y = amax / fmax_of<kE5M2>();
+  if (y > 3.4028235e38f) return 127;                       // inf
+  const int e = (int)(__float_as_uint(y) >> 23) - 127;   // the exponent field; a subnormal
+  return e < -127 ? -127 : e;                              // quotient (field 0) is below 2^-126
+}
+
+struct MxArgs {
+  const void* x;
+  int64_t rows;
+  int64_t stride;
+  int cols;
+  const int64_t* group_offs;
+  int G;
+  uint8_t* out;
+  int64_t out_stride;
+  uint8_t* scales;
+  int64_t scale_stride;
+  int64_t* padded_offs;
+};
+
+// Persistent grid. Prologue: group offsets and padded offsets (prefix sums of ceil(len/32)*32) in
+// LDS; workgroup 0 writes the padded offsets. Work item = (32-row output block, 256 columns), one
+// per wave: lane l owns columns 4l .. 4l+3, loads the block's 32 source rows (zeros for padding),
+// reduces the column amax, and writes 32 rows of 4 fp8 bytes plus one row of 4 e8m0 bytes.
+template <bool kF32, bool kE5M2>
+__global__ void __launch_bounds__(kThreads) quant_mx_grouped_kernel(MxArgs a) {
+  __shared__ int s_offs[kMaxGroups + 1];
+  __shared__ int s_pad[kMaxGroups + 1];
+  __shared__ int s_part[kThreads];
+  __shared__ bool s_flag;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = a.G;
+  {
+    constexpr int kPer = (kMaxGroups + 1) / kThreads;     // 8 groups per thread
+    int o[kPer + 1];
+#pragma unroll
+    for (int k = 0; k <= kPer; ++k) {
+      const int64_t v = a.group_offs[min(tid * kPer + k, G)];
+      o[k] = v < 0 ? -1 : (v > a.rows ? (int)min(a.rows + 1, (int64_t)0x7fffffff) : (int)v);
+    }
+    int mine[kPer], sum = 0;
+    bool bad = false;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int g = tid * kPer + k;
+      const int len = g < G ? o[k + 1] - o[k] : 0;
+      bad |= len < 0 || (g <= G && (o[k] < 0 || o[k] > a.rows));
+      mine[k] = len > 0 ? (len + 31) / 32 * 32 : 0;
+      sum += mine[k];
+      if (g <= G) s_offs[g] = o[k];
+    }
+    // offsets outside [0, rows] or decreasing: nothing is read or written (the host checks the
+    // output capacity against rows + 31 G, which holds only for valid offsets)
+    s_part[tid] = bad ? -1 : sum;
+    __syncthreads();
+    if (tid == 0) {
+      bool any = false;
+      for (int t = 0; t < kThreads; ++t) any |= s_part[t] < 0;
+      s_flag = any;
+    }
+    __syncthreads();
+    if (s_flag) return;
+    s_part[tid] = sum;
+    __syncthreads();
+    for (int d = 1; d < kThreads; d <<= 1) {
+      const int v = tid >= d ? s_part[tid - d] : 0;
+      __syncthreads();
+      s_part[tid] += v;
+      __syncthreads();
+    }
+    int run = s_part[tid] - sum;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int g = tid * kPer + k;
+      if (g < G) s_pad[g] = run;
+      run += mine[k];
+    }
+    if (tid == kThreads - 1) s_pad[G] = s_part[tid];
+    __syncthreads();
+  }
+  if (blockIdx.x == 0)
+    for (int g = tid; g <= G; g += kThreads) a.padded_offs[g] = s_pad[g];
+
+  const int blocks = s_pad[G] / 32;
+  const int strips = (a.cols + 255) / 256;
+  const int64_t items = (int64_t)blocks * strips;
+  const int col = 4 * lane;
+  for (int64_t it = (int64_t)blockIdx.x * (kThreads / 64) + wave; it < items;
+       it += (int64_t)gridDim.x * (kThreads / 64)) {
+    const int b = (int)(it / strips);
+    const int c0 = (int)(it - (int64_t)b * strips) * 256 + col;
+    const int p0 = 32 * b;
+    int lo = 0, hi = G - 1;                                // group: the last g with s_pad[g] <= p0
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_pad[mid] <= p0) lo = mid; else hi = mid - 1;
+    }
+    const int src0 = s_offs[lo] + (p0 - s_pad[lo]);        // source row of padded row p0
+    const int valid = min(32, s_offs[lo + 1] - src0);      // source rows of this block (>= 1)
+    if (c0 >= a.cols) continue;                            // lanes past the last column
+    float v[32][4];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      if (i < valid) {
+        if constexpr (kF32) {
+          const v4f t = __builtin_nontemporal_load((const v4f*)((const float*)a.x + (int64_t)(src0 + i) * a.stride + c0));
+          v[i][0] = t[0]; v[i][1] = t[1]; v[i][2] = t[2]; v[i][3] = t[3];
+        } else {
+          const v2u t = __builtin_nontemporal_load((const v2u*)((const uint16_t*)a.x + (int64_t)(src0 + i) * a.stride + c0));
+          v[i][0] = bf16_lo(t[0]); v[i][1] = bf16_hi(t[0]); v[i][2] = bf16_lo(t[1]); v[i][3] = bf16_hi(t[1]);
+        }
+      } else {
+        v[i][0] = v[i][1] = v[i][2] = v[i][3] = 0.0f;
+      }
+    }
+    uint32_t sc = 0;
+    float mul[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t m = 0;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) m = max(m, __float_as_uint(v[i][j]) & 0x7fffffffu);
+      const int X = block_exponent<kE5M2>(__uint_as_float(m));
+      sc |= (uint32_t)(X + 127) << (8 * j);
+      mul[j] = X == 128 ? __uint_as_float(0x7fc00000u) : __builtin_ldexpf(1.0f, -X);   // exact 2^-X
+    }
+    *(uint32_t*)(a.scales + (int64_t)b * a.scale_stride + c0) = sc;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w |= f32_to_fp8<kE5M2>(clamp_fmax<kE5M2>(v[i][j] * mul[j])) << (8 * j);
+      *(uint32_t*)(a.out + (int64_t)(p0 + i) * a.out_stride + c0) = w;
+    }
+  }
+}
+
+}  // namespace qt
+}  // namespace ggemm

@@ -104,7 +104,7 @@ def quantize_tensorwise(x: torch.Tensor, fmt: str) -> tuple[torch.Tensor, float]
 def quantize_mx(x: torch.Tensor, fmt: str, block: int = 32) -> tuple[torch.Tensor, torch.Tensor]:
     """OCP-MX style block scaling along dim 0 (tokens).
 
-    e8m0 exponent X = floor(log2(amax_blk / fmax)) per ``block`` rows per column, clamped to
+    e8m0 exponent X = floor(log2(fl32(amax_blk / fmax))) per ``block`` rows per column, clamped to
     [-127, 127] and stored as X+127; an all-zero block stores 127. Elements are divided by 2^X and
     saturate-clamped to +-fmax before the cast (block max lands in [fmax, 2 fmax)).
     Rows must be a multiple of ``block``. Returns (uint8 data [M, N], uint8 scales [M/block, N]).
@@ -118,7 +118,8 @@ def quantize_mx(x: torch.Tensor, fmt: str, block: int = 32) -> tuple[torch.Tenso
     amax = xb.abs().amax(dim=1)
     X = torch.zeros_like(amax, dtype=torch.int32)
     nz = amax > 0
-    X[nz] = torch.floor(torch.log2(amax[nz] / fmax)).to(torch.int32)
+    # floor(log2(y)) taken exactly on the fp32 quotient y: frexp gives y = m 2^e, m in [0.5, 1)
+    X[nz] = torch.frexp(amax[nz] / fmax).exponent.to(torch.int32) - 1
     X = X.clamp_(-127, 127)
     scale = torch.pow(2.0, X.to(torch.float32))
     q = (xb / scale.unsqueeze(1)).clamp_(-fmax, fmax).to(dt).view(M, N)

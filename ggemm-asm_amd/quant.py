@@ -1,0 +1,120 @@
+"""PyTorch-facing FP8 quantization producer over the C ABI (include/ggemm_quant.h).
+
+The step before the grouped GEMMs: per-tensor quantization (amax, scale = amax / fmax, saturating
+round-to-nearest-even cast) for the tensorwise kernels, and MX quantization along the token axis
+with group-aligned padding (e8m0 exponents per 32-token block and column) for the MXFP8 wgrad.
+The reference tree holds no quantizer (its harness casts randn straight to fp8 with scales of 0.1,
+reference bench.py:220-223,260-261); the recipes are those of the measured configurations. Every
+launch goes through libggemm_vark.so on torch's current stream; there is no CPU path.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .vark import _stream
+
+GGEMM_IN_BF16 = 0
+GGEMM_IN_F32 = 1
+_IN = {torch.bfloat16: GGEMM_IN_BF16, torch.float32: GGEMM_IN_F32}
+_OUT = {"e4m3": (0, torch.float8_e4m3fn), "e5m2": (1, torch.float8_e5m2)}
+MAX_GROUPS = 2047
+
+
+def _as_2d(x: torch.Tensor) -> torch.Tensor:
+    if x.dim() < 2:
+        raise ValueError("x must have at least 2 dimensions (rows x cols)")
+    if x.dim() > 2:
+        if not x.is_contiguous():
+            raise ValueError("an N-d input must be contiguous (it is read as [prod(leading dims), last dim])")
+        x = x.reshape(-1, x.shape[-1])
+    if x.stride(1) != 1:
+        raise ValueError("x must be contiguous along its last dimension")
+    return x
+
+
+def _ptr(x2: torch.Tensor) -> int:
+    """A zero-row input has a null data pointer; the kernels read no row of it, so the library
+    gets a one-row placeholder of the same width (and rows = 0)."""
+    if x2.shape[0] > 0:
+        return x2.data_ptr()
+    _ptr.keep = torch.empty((1, x2.shape[1]), dtype=x2.dtype, device=x2.device)
+    return _ptr.keep.data_ptr()
+
+
+def _check(x: torch.Tensor, fmt: str):
+    if x.dtype not in _IN:
+        raise TypeError(f"x must be bfloat16 or float32, got {x.dtype}")
+    if fmt not in _OUT:
+        raise ValueError(f"fmt must be 'e4m3' or 'e5m2', got {fmt!r}")
+    if x.device.type != "cuda":
+        raise ValueError(f"the quantizer runs on a gfx950 GPU only (x is on {x.device}); use the CPU "
+                         "oracle in tests for reference results")
+
+
+def amax(x: torch.Tensor) -> torch.Tensor:
+    """max |x| as a single-element fp32 tensor on x's device (NaN propagates)."""
+    _check(x, "e4m3")
+    x2 = _as_2d(x)
+    out = torch.empty((), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = _lib.load().ggemm_quant_amax(_ptr(x2), _IN[x.dtype], x2.shape[0], x2.shape[1], max(x2.stride(0), x2.shape[1]),
+                                          out.data_ptr(), _stream(x.device))
+    _lib.check(rc, "ggemm_quant_amax")
+    return out
+
+
+def quantize_fp8_tensorwise(x: torch.Tensor, fmt: str = "e4m3"):
+    """Per-tensor FP8 quantization. Returns ``(q, scale, amax)``: q has x's shape and dtype
+    float8_e4m3fn / float8_e5m2, ``scale = amax / fmax`` (1 when amax == 0) and ``amax`` are
+    single-element fp32 device tensors; ``q * scale`` dequantizes. The GEMM entry points take
+    ``scale`` as their per-tensor scale."""
+    _check(x, fmt)
+    x2 = _as_2d(x)
+    code, dt = _OUT[fmt]
+    q = torch.empty(x.shape, dtype=dt, device=x.device)
+    q2 = q.view(-1, x.shape[-1])
+    scale = torch.empty((), dtype=torch.float32, device=x.device)
+    am = torch.empty((), dtype=torch.float32, device=x.device)
+    qp = q2 if q2.shape[0] > 0 else torch.empty((1, x.shape[-1]), dtype=dt, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = _lib.load().ggemm_quant_fp8_tensorwise(
+            _ptr(x2), _IN[x.dtype], x2.shape[0], x2.shape[1], max(x2.stride(0), x2.shape[1]), code, qp.data_ptr(),
+            qp.stride(0), scale.data_ptr(), am.data_ptr(), _stream(x.device))
+    _lib.check(rc, "ggemm_quant_fp8_tensorwise")
+    return q, scale, am
+
+
+def padded_rows(rows: int, G: int) -> int:
+    """Output rows that ``quantize_mxfp8_grouped`` needs: every group padded to 32 rows fits."""
+    return (rows + 31 * G + 31) // 32 * 32
+
+
+def quantize_mxfp8_grouped(x: torch.Tensor, group_offs: torch.Tensor, fmt: str = "e4m3"):
+    """MX quantization along the token axis (rows) with group-aligned padding.
+
+    x: bfloat16 / float32 [M, N] token-major; group_offs: int64 [G+1] on the device. Returns
+    ``(q, scales, padded_offs)``: q fp8 [padded_rows(M, G), N] (group g at rows padded_offs[g] ..,
+    zero rows up to the next multiple of 32; rows past padded_offs[G] are unspecified), scales
+    uint8 e8m0 [padded_rows / 32, N], padded_offs int64 [G+1]. The three are the MX wgrad's inputs
+    (with the matching tensor of the other operand, padded with the same offsets)."""
+    _check(x, fmt)
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("x must be 2-D [M, N], contiguous along N")
+    if group_offs.dtype != torch.int64 or group_offs.dim() != 1 or group_offs.numel() < 2:
+        raise ValueError("group_offs must be int64 [G+1]")
+    if group_offs.device != x.device:
+        raise ValueError("group_offs must be on x's device")
+    M, N = x.shape
+    G = group_offs.numel() - 1
+    rows_out = padded_rows(M, G)
+    code, dt = _OUT[fmt]
+    q = torch.empty((rows_out, N), dtype=dt, device=x.device)
+    scales = torch.empty((rows_out // 32, N), dtype=torch.uint8, device=x.device)
+    padded = torch.empty(G + 1, dtype=torch.int64, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = _lib.load().ggemm_quant_mxfp8_grouped(
+            _ptr(x), _IN[x.dtype], M, N, max(x.stride(0), N), group_offs.data_ptr(), G, code, q.data_ptr(),
+            q.stride(0), rows_out, scales.data_ptr(), scales.stride(0), padded.data_ptr(), _stream(x.device))
+    _lib.check(rc, "ggemm_quant_mxfp8_grouped")
+    return q, scales, padded

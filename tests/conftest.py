@@ -34,6 +34,12 @@ def orp():
 
 
 @pytest.fixture(scope="session")
+def orq():
+    from oracle import quant_oracle
+    return quant_oracle
+
+
+@pytest.fixture(scope="session")
 def cuda():
     import torch
     if not torch.cuda.is_available():

@@ -1,0 +1,190 @@
+"""GPU parity of the FP8 quantization producer against the CPU oracle (launches through the C ABI).
+
+Quantization is byte work: every fp8 byte, e8m0 byte, scale, amax and padded offset must equal
+the oracle's exactly.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+TDT = {"e4m3": torch.float8_e4m3fn, "e5m2": torch.float8_e5m2}
+
+
+def _say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def _bytes(t):
+    return t.detach().contiguous().view(torch.uint8).cpu().numpy()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_amax(pkg, orq, cuda, dtype):
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn((1000, 264), generator=g).to(dtype)
+    x[517, 3] = -7.25                                   # the max is negative
+    _say(f"amax {dtype}")
+    a = pkg.amax(x.to(cuda))
+    assert float(a) == float(orq.amax(x.float().numpy())) == 7.25
+    x[2, 2] = float("nan")
+    assert torch.isnan(pkg.amax(x.to(cuda))).item()
+    z = torch.zeros((0, 64), dtype=dtype, device=cuda)
+    assert float(pkg.amax(z)) == 0.0
+    q, scale, am = pkg.quantize_fp8_tensorwise(z, "e4m3")
+    assert q.shape == (0, 64) and float(scale) == 1.0 and float(am) == 0.0
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", [(4096, 2880), (777, 136), (3, 8)])
+def test_tensorwise_bit_exact(pkg, orq, cuda, fmt, dtype, shape):
+    g = torch.Generator().manual_seed(shape[0])
+    x = (torch.randn(shape, generator=g) * (1e-3 if fmt == "e5m2" else 1.0)).to(dtype)
+    _say(f"tensorwise {fmt} {dtype} {shape}")
+    q, scale, am = pkg.quantize_fp8_tensorwise(x.to(cuda), fmt)
+    torch.cuda.synchronize()
+    q_ref, s_ref, a_ref = orq.quantize_tensorwise(x.float().numpy(), fmt)
+    assert q.dtype == TDT[fmt] and q.shape == x.shape
+    assert float(am) == float(a_ref) and float(scale) == float(s_ref)
+    np.testing.assert_array_equal(_bytes(q), q_ref)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_tensorwise_rounding_ties_and_subnormals(pkg, orq, cuda, fmt):
+    """amax = fmax makes the scale 1, so x / scale is exact and every fp8 tie, both fp32 neighbours
+    of each tie, and fp32 subnormals reach the conversion unchanged."""
+    b = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(TDT[fmt]).float().numpy()
+    vals = np.sort(np.unique(b[np.isfinite(b) & (b >= 0)]))
+    mids = ((vals[:-1].astype(np.float64) + vals[1:]) / 2).astype(np.float32)
+    tiny = np.arange(1, 2000, dtype=np.uint32).view(np.float32)
+    v = np.concatenate([vals, mids, np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(0)), tiny])
+    v = np.concatenate([v, -v, [np.float32(orq.FMAX[fmt])], [-0.0]]).astype(np.float32)
+    v = np.concatenate([v, np.zeros((-v.size) % 64, np.float32)]).reshape(-1, 64)
+    _say(f"tensorwise ties {fmt} {v.shape}")
+    q, scale, _ = pkg.quantize_fp8_tensorwise(torch.from_numpy(v).to(cuda), fmt)
+    torch.cuda.synchronize()
+    assert float(scale) == 1.0
+    q_ref, _, _ = orq.quantize_tensorwise(v, fmt)
+    np.testing.assert_array_equal(_bytes(q), q_ref)
+
+
+def test_tensorwise_special_values(pkg, orq, cuda):
+    x = torch.zeros((16, 64), dtype=torch.bfloat16)
+    _say("tensorwise zeros / NaN")
+    q, scale, am = pkg.quantize_fp8_tensorwise(x.to(cuda), "e4m3")
+    assert float(scale) == 1.0 and float(am) == 0.0 and int(_bytes(q).max()) == 0
+    x[3, 5] = float("nan")
+    q, scale, am = pkg.quantize_fp8_tensorwise(x.to(cuda), "e4m3")
+    q_ref, s_ref, a_ref = orq.quantize_tensorwise(x.float().numpy(), "e4m3")
+    assert np.isnan(float(scale)) and np.isnan(float(am))
+    np.testing.assert_array_equal(_bytes(q), q_ref)
+
+
+def test_tensorwise_weight_3d_and_strided(pkg, orq, cuda):
+    g = torch.Generator().manual_seed(7)
+    w = torch.randn((4, 96, 160), generator=g).to(torch.bfloat16)
+    _say("tensorwise 3-D weight")
+    q, scale, _ = pkg.quantize_fp8_tensorwise(w.to(cuda), "e4m3")
+    q_ref, s_ref, _ = orq.quantize_tensorwise(w.float().numpy().reshape(-1, 160), "e4m3")
+    assert q.shape == w.shape and float(scale) == float(s_ref)
+    np.testing.assert_array_equal(_bytes(q).reshape(-1, 160), q_ref)
+    wide = torch.randn((300, 256), generator=g).to(torch.bfloat16).to(cuda)
+    view = wide[:, 64:64 + 128]
+    q, scale, _ = pkg.quantize_fp8_tensorwise(view, "e5m2")
+    q_ref, s_ref, _ = orq.quantize_tensorwise(view.float().cpu().numpy(), "e5m2")
+    np.testing.assert_array_equal(_bytes(q), q_ref)
+
+
+MX_CASES = [
+    ([5, 0, 33, 64, 1, 100], 48),
+    ([32, 32, 0, 31], 272),
+    ([1000, 24, 0, 0, 77], 2880 // 5),
+    ([0, 0, 7], 16),
+    ([4096 + 13], 512),
+]
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("lens,N", MX_CASES, ids=[f"mx{i}" for i in range(len(MX_CASES))])
+def test_mx_grouped_bit_exact(pkg, orq, cuda, fmt, dtype, lens, N):
+    g = torch.Generator().manual_seed(sum(lens) + N)
+    M = sum(lens)
+    x = (torch.randn((M, N), generator=g) * (1e-3 if fmt == "e5m2" else 1.0)).to(dtype)
+    if M > 40:
+        x[:32, : N // 2] = 0                                # all-zero blocks
+    offs = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64)
+    _say(f"mx {fmt} {dtype} lens={lens} N={N}")
+    q, sc, pad = pkg.quantize_mxfp8_grouped(x.to(cuda), offs.to(cuda), fmt)
+    torch.cuda.synchronize()
+    q_ref, sc_ref, pad_ref = orq.quantize_mx_grouped(x.float().numpy(), offs.numpy(), fmt, out_rows=q.shape[0])
+    pad = pad.cpu().numpy()
+    np.testing.assert_array_equal(pad, pad_ref)
+    P = int(pad[-1])
+    np.testing.assert_array_equal(_bytes(q)[:P], q_ref[:P])
+    np.testing.assert_array_equal(sc.cpu().numpy()[:P // 32], sc_ref[:P // 32])
+
+
+def test_mx_invalid_offsets_write_nothing(pkg, cuda):
+    """Offsets past the rows (which the host cannot see) make the kernel's own check skip all
+    writes: the outputs keep their previous contents."""
+    x = torch.randn((64, 32), dtype=torch.float32, device=cuda)
+    _say("mx invalid offsets")
+    from ggemm_asm_amd import _lib
+    q = torch.full((64 + 31 * 2 + 31, 32), 0x55, dtype=torch.uint8, device=cuda)
+    sc = torch.full((q.shape[0] // 32, 32), 0x66, dtype=torch.uint8, device=cuda)
+    pad = torch.full((3,), -9, dtype=torch.int64, device=cuda)
+    for bad in ([0, 40, 65], [0, 50, 40], [-1, 10, 20]):
+        offs = torch.tensor(bad, dtype=torch.int64, device=cuda)
+        rc = _lib.load().ggemm_quant_mxfp8_grouped(x.data_ptr(), 1, 64, 32, 32, offs.data_ptr(), 2, 0, q.data_ptr(),
+                                                   32, q.shape[0], sc.data_ptr(), 32, pad.data_ptr(),
+                                                   torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        torch.cuda.synchronize()
+        assert bool((q == 0x55).all()) and bool((sc == 0x66).all()) and bool((pad == -9).all()), bad
+
+
+def test_mx_producer_feeds_mx_wgrad(pkg, orc, orq, cuda):
+    """End to end: the producer quantizes x and dy of ragged groups (padding them to 32-token
+    blocks) and the MXFP8 wgrad consumes its output; the result matches the oracle wgrad of the
+    producer's bytes."""
+    lens = [100, 0, 257, 31, 64]
+    OUT_M, OUT_N = 192, 384
+    g = torch.Generator().manual_seed(11)
+    M = sum(lens)
+    x = torch.randn((M, OUT_M), generator=g).to(torch.bfloat16)
+    dy = (torch.randn((M, OUT_N), generator=g) * 1e-3).to(torch.bfloat16)
+    offs = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64, device=cuda)
+    _say("mx producer -> mx wgrad")
+    ql, sl, pad = pkg.quantize_mxfp8_grouped(x.to(cuda), offs, "e4m3")
+    qr, sr, pad2 = pkg.quantize_mxfp8_grouped(dy.to(cuda), offs, "e5m2")
+    assert torch.equal(pad, pad2)
+    out = pkg.grouped_gemm_mxfp8_variable_k(ql, qr, sl, sr, pad, validate=True)
+    torch.cuda.synchronize()
+    P = int(pad[-1])
+    ref = orc.vark_wgrad_mxfp8(_bytes(ql)[:P], _bytes(qr)[:P], sl.cpu().numpy()[:P // 32], sr.cpu().numpy()[:P // 32],
+                               pad.cpu().numpy())
+    m = orc.compare(pkg.as_bf16_bits(out), ref, pad.cpu().numpy())
+    _say(f"mx end to end: {m}")
+    assert orc.parity_ok(m) and m["empty_zero"]
+
+
+def test_tensorwise_producer_feeds_persistent_gemm(pkg, orc, orp, cuda):
+    """End to end: bf16 activations and weights quantized per tensor feed the forward GEMM."""
+    lens, K, N = [300, 0, 77], 256, 384
+    g = torch.Generator().manual_seed(12)
+    M = sum(lens)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16).to(cuda)
+    w = (torch.randn((len(lens), N, K), generator=g) * 0.02).to(torch.bfloat16).to(cuda)
+    offs = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64, device=cuda)
+    _say("tensorwise producer -> persistent fwd")
+    qx, sx, _ = pkg.quantize_fp8_tensorwise(x, "e4m3")
+    qw, sw, _ = pkg.quantize_fp8_tensorwise(w, "e4m3")
+    out = pkg.grouped_gemm_fp8_tensorwise(qx, qw, sx, sw, offs)
+    torch.cuda.synchronize()
+    ref = orp.grouped_fp8(_bytes(qx), _bytes(qw), float(sx), float(sw), offs.cpu().numpy())
+    m = orc.compare(pkg.as_bf16_bits(out), ref)
+    _say(f"tensorwise end to end: {m}")
+    assert orc.parity_ok(m)

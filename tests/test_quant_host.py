@@ -1,0 +1,67 @@
+"""CPU checks of the quantization producer's C ABI (no kernel launches: every call here fails
+validation, or passes it with nothing to launch, before any HIP call)."""
+import os
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT
+
+FAKE = 0x100000
+
+
+def test_quant_header_symbols_exported(pkg):
+    text = open(os.path.join(ROOT, "include", "ggemm_quant.h")).read()
+    names = sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(ggemm_quant_\w+)\s*\(", text, re.M)))
+    from ggemm_asm_amd import _lib
+    assert names == sorted(_lib.QUANT_EXPORTS)
+    lib = pkg.load_library()
+    for n in names:
+        assert hasattr(lib, n)
+
+
+def _tw(lib, **kw):
+    a = dict(x=FAKE, dt=0, rows=100, cols=64, stride=64, fmt=0, out=FAKE, ostride=64, scale=FAKE, amax=FAKE)
+    a.update(kw)
+    return lib.ggemm_quant_fp8_tensorwise(a["x"], a["dt"], a["rows"], a["cols"], a["stride"], a["fmt"], a["out"],
+                                          a["ostride"], a["scale"], a["amax"], None)
+
+
+@pytest.mark.parametrize("kw,rc", [
+    (dict(x=0), -1), (dict(out=0), -1), (dict(scale=0), -1), (dict(dt=2), -8), (dict(fmt=3), -8),
+    (dict(cols=60, stride=64), -2), (dict(rows=-1), -2), (dict(stride=56), -3), (dict(stride=68), -3),
+    (dict(ostride=60), -3), (dict(x=FAKE + 8), -4), (dict(out=FAKE + 4), -4),
+])
+def test_tensorwise_validation(pkg, kw, rc):
+    assert _tw(pkg.load_library(), **kw) == rc
+
+
+def _mx(lib, **kw):
+    a = dict(x=FAKE, dt=0, rows=100, cols=64, stride=64, offs=FAKE, G=4, fmt=1, out=FAKE, ostride=64, orows=100 + 124,
+             sc=FAKE, sstride=64, pad=FAKE)
+    a.update(kw)
+    return lib.ggemm_quant_mxfp8_grouped(a["x"], a["dt"], a["rows"], a["cols"], a["stride"], a["offs"], a["G"],
+                                         a["fmt"], a["out"], a["ostride"], a["orows"], a["sc"], a["sstride"],
+                                         a["pad"], None)
+
+
+@pytest.mark.parametrize("kw,rc", [
+    (dict(offs=0), -1), (dict(pad=0), -1), (dict(fmt=2), -8), (dict(G=0), -2), (dict(G=2048), -2),
+    (dict(cols=72, stride=72, ostride=80, sstride=80), -2), (dict(orows=100 + 123), -2),
+    (dict(rows=(1 << 31) - 100), -2), (dict(ostride=72), -3), (dict(sstride=48), -3),
+    (dict(out=FAKE + 8), -4), (dict(sc=FAKE + 8), -4), (dict(offs=FAKE + 4), -4),
+])
+def test_mx_validation(pkg, kw, rc):
+    assert _mx(pkg.load_library(), **kw) == rc
+
+
+def test_python_quant_refuses_cpu_and_bad_dtypes(pkg):
+    x = torch.zeros(8, 16)
+    with pytest.raises(ValueError, match="gfx950 GPU only"):
+        pkg.quantize_fp8_tensorwise(x)
+    with pytest.raises(TypeError):
+        pkg.quantize_fp8_tensorwise(x.half())
+    with pytest.raises(ValueError, match="e4m3"):
+        pkg.quantize_fp8_tensorwise(x, "e3m4")
+    assert pkg.padded_rows(100, 4) == 224 and pkg.padded_rows(0, 1) == 32
