@@ -11,6 +11,11 @@ bench.py:742, launcher.cpp:76).
 forward / data-gradient grouped GEMM at the reference's other call sites instead (reference
 bench.py:153-180, inputs as in bench.py:205-223,238-247; FLOPs = 2 * M_total * K * N).
 
+``--config quant_tensorwise | quant_mx`` measures the FP8 quantization producer (HBM-bound, GB/s):
+x bf16 [131072, 2880] -> per-tensor e4m3 (amax pass + quantize pass: 2 + 2 + 1 bytes per
+element), and dy bf16 [131072, 5760] -> grouped MX e5m2 with 32-token padding (2 + 1 + 1/32
+bytes per element).
+
 Prints ONE JSON line with ms, TFLOPS, the MFMA roofline fraction and a CPU baseline (the
 build's numpy oracle on a bounded sample of the same workload, timed on this host's cores).
 """
@@ -28,6 +33,8 @@ sys.path.insert(0, ROOT)
 FP8_DENSE_PEAK_TFLOPS = 5000.0    # MI355X dense FP8 MFMA peak
 REF_OPT_ASM_TFLOPS = 1237.0       # reference optimized ASM, gate_up_wgrad, C launcher (README.md:60)
 FWD_SITES = ("gate_up_fwd", "down_fwd", "down_dgrad", "gate_up_dgrad")
+QUANT_CONFIGS = ("quant_tensorwise", "quant_mx")
+HBM_PEAK_GBS = 8000.0             # MI355X HBM3E
 
 
 def traffic_file(name):
@@ -40,7 +47,8 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="gate_up_wgrad",
-                    choices=["gate_up_wgrad", "down_wgrad", "gate_up_zipf", "gate_up_mx", "constant", *FWD_SITES])
+                    choices=["gate_up_wgrad", "down_wgrad", "gate_up_zipf", "gate_up_mx", "constant", *FWD_SITES,
+                             *QUANT_CONFIGS])
     ap.add_argument("--mfma", default="k128", choices=["k128", "k32"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -172,6 +180,65 @@ def cpu_baseline(p, seconds):
                       f"numpy fp32 dequantize + OpenBLAS sgemm + bf16 RNE, {t_total:.1f} s"}
 
 
+def quant_workload(pkg, name, seed, dev):
+    """(runner, bytes per call, config dict, cpu-baseline callable) of a producer workload."""
+    import torch
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    if name == "quant_tensorwise":
+        x = torch.randn((pkg.inputs.M_TOTAL, pkg.inputs.F_DIM), generator=gen, device=dev, dtype=torch.bfloat16)
+        n = x.numel()
+        run = lambda: pkg.quantize_fp8_tensorwise(x, "e4m3")
+        cfg = {"workload": name, "x": "bf16 [131072, 2880] (randn)", "out": "e4m3fn, fp32 scale + amax",
+               "bytes_per_element": "2 (amax pass) + 2 (quantize pass) + 1 (fp8 out)"}
+        nbytes = 5 * n
+    else:
+        lens = pkg.inputs.multinomial_lens(pkg.inputs.E_EXPERTS, pkg.inputs.M_TOTAL, torch.Generator().manual_seed(seed))
+        offs = pkg.inputs.make_group_offs(lens).to(dev)
+        x = torch.randn((pkg.inputs.M_TOTAL, pkg.inputs.F2_DIM), generator=gen, device=dev,
+                        dtype=torch.bfloat16).mul_(1e-3)
+        n = x.numel()
+        run = lambda: pkg.quantize_mxfp8_grouped(x, offs, "e5m2")
+        cfg = {"workload": name, "x": "bf16 [131072, 5760] (randn * 1e-3), 32 multinomial groups",
+               "out": "e5m2 + e8m0 per 32-token block, groups padded to 32 rows",
+               "bytes_per_element": "2 (read) + 1 (fp8 out) + 1/32 (e8m0)"}
+        nbytes = n * (3 + 1 / 32)
+
+    def cpu(seconds):
+        """numpy oracle on row slices of the same tensor until ~`seconds`; GB/s of the same
+        per-element byte count."""
+        import numpy as np
+        from oracle import quant_oracle as orq
+        rows, t_total, done = 4096, 0.0, 0
+        xc = x[:rows].float().cpu().numpy()
+        while t_total < seconds:
+            t0 = time.perf_counter()
+            if name == "quant_tensorwise":
+                orq.quantize_tensorwise(xc, "e4m3")
+            else:
+                orq.quantize_mx_grouped(xc, np.array([0, rows], np.int64), "e5m2", out_rows=rows)
+            t_total += time.perf_counter() - t0
+            done += xc.size
+        return {"value": round(done * (nbytes / n) / t_total / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"{done // xc.size} x {rows} rows of {name}'s input through the numpy oracle, "
+                          f"{t_total:.1f} s"}
+
+    return run, nbytes, cfg, cpu
+
+
+def main_quant(args, pkg, dev):
+    run, nbytes, cfg, cpu = quant_workload(pkg, args.config, args.seed, dev)
+    ms = time_steps(run, args.steps, args.warmup)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    line = {"metric": f"GB/s of the FP8 quantization producer ({args.config}) on 1 MI355X", "value": round(gbs, 1),
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16->fp8",
+            "data": "synthetic", "config": cfg,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic(args.config)},
+            "cpu_baseline": cpu(args.cpu_seconds) if args.cpu_seconds > 0 else None}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -185,6 +252,9 @@ def main():
     from __graft_entry__ import load_package
     pkg = load_package()
     dev = torch.device("cuda:0")
+    if args.config in QUANT_CONFIGS:
+        main_quant(args, pkg, dev)
+        return
     fwd = args.config in FWD_SITES
     if args.config == "constant":
         p = pkg.inputs.constant_problem(device=dev)

@@ -27,7 +27,7 @@ int check_2d(const void* x, int in_dtype, int64_t rows, int cols, int64_t stride
 }
 
 int grid_for(int64_t chunks, int cus) {
-  const int64_t want = (chunks + qt::kThreads - 1) / qt::kThreads;
+  const int64_t want = (chunks + (int64_t)qt::kThreads * qt::kUnroll - 1) / ((int64_t)qt::kThreads * qt::kUnroll);
   const int64_t cap = (int64_t)cus * 16;
   return (int)(want < 1 ? 1 : (want > cap ? cap : want));
 }
@@ -108,7 +108,14 @@ int ggemm_quant_mxfp8_grouped(const void* x, int32_t in_dtype, int64_t rows, int
   const bool f32 = in_dtype == GGEMM_IN_F32, e5 = out_format == GGEMM_FP8_E5M2;
   auto k = f32 ? (e5 ? qt::quant_mx_grouped_kernel<true, true> : qt::quant_mx_grouped_kernel<true, false>)
                : (e5 ? qt::quant_mx_grouped_kernel<false, true> : qt::quant_mx_grouped_kernel<false, false>);
-  hipLaunchKernelGGL(k, dim3(cus * 4), dim3(qt::kThreads), 0, (hipStream_t)stream, a);
+  // persistent grid: exactly the workgroups that are resident together (the work is split
+  // statically, so a workgroup that waits for a free slot would run its share afterwards)
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(k), qt::kThreads, 0) !=
+          hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  hipLaunchKernelGGL(k, dim3(cus * per_cu), dim3(qt::kThreads), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
 }
 

@@ -9,8 +9,9 @@
 //                 padding rows are zero and the padded group offsets are written out.
 //
 // fmax = 448 (e4m3fn) or 57344 (e5m2). Rounding: x / scale is the correctly rounded fp32 quotient,
-// fp32 -> fp8 is round-to-nearest-even (subnormals included), -0 keeps its sign, NaN becomes the
-// format's NaN code (0x7F / 0xFF for e4m3fn, 0x7F / 0xFF for e5m2). These are the recipes of the
+// fp32 -> fp8 is round-to-nearest-even (subnormals included), -0 keeps its sign, NaN becomes a NaN
+// code of the format (0x7F or 0xFF: the sign of a NaN result is unspecified, as in IEEE
+// arithmetic, and the GPU's x / NaN differs from a CPU's there). These are the recipes of the
 // measured configurations (x / (amax/fmax) clamped and cast; MX block exponents from the block
 // amax), with floor(log2()) taken exactly on the fp32 quotient.
 //
@@ -26,6 +27,7 @@ namespace ggemm {
 namespace qt {
 
 constexpr int kThreads = 256;
+constexpr int kUnroll = 4;           // 16-byte chunks each thread has in flight in the streaming kernels
 constexpr int kMaxGroups = 2047;     // MX: group offsets and padded offsets held in LDS
 
 typedef float v4f __attribute__((ext_vector_type(4)));
@@ -35,11 +37,14 @@ typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 template <bool kE5M2>
 __device__ __forceinline__ constexpr float fmax_of() { return kE5M2 ? 57344.0f : 448.0f; }
 
-// fp32 -> fp8 byte, round to nearest even. |f| <= fmax unless NaN (callers clamp first).
+// fp32 -> fp8 byte, round to nearest even. |f| <= fmax unless NaN (callers clamp first). The
+// bit-level definition of the conversion; the kernels use the hardware instruction (pack4_fp8).
 //  e4m3fn: bias 7, 3 mantissa bits, subnormals m * 2^-9; e5m2: bias 15, 2 bits, m * 2^-16.
 // Normal range: add the rounding increment to the fp32 bits below the kept mantissa (a carry
 // moves into the exponent, which is the correctly rounded result), then rebias. Subnormal range:
-// |f| * 2^(9 or 16) is exact, and rint rounds half to even.
+// |f| * 2^(9 or 16) is exact, and rint rounds half to even. Both are computed and the result is
+// picked with bit masks: written as branches, the compiler emitted per-element exec-mask branches
+// that cost more than the arithmetic.
 template <bool kE5M2>
 __device__ __forceinline__ uint32_t f32_to_fp8(float f) {
   const uint32_t u = __float_as_uint(f);
@@ -49,13 +54,28 @@ __device__ __forceinline__ uint32_t f32_to_fp8(float f) {
   constexpr int kShift = 23 - kMant;
   constexpr uint32_t kMinNormal = kE5M2 ? 0x38800000u : 0x3c800000u;   // 2^-14, 2^-6
   constexpr uint32_t kRebias = (kE5M2 ? (127 - 15) : (127 - 7)) << kMant;
-  if (a > 0x7f800000u) return s | 0x7fu;                                   // NaN
-  if (a >= kMinNormal) {
-    const uint32_t r = (a + ((1u << (kShift - 1)) - 1) + ((a >> kShift) & 1u)) >> kShift;
-    return s | (r - kRebias);
+  const uint32_t rn = ((a + ((1u << (kShift - 1)) - 1) + ((a >> kShift) & 1u)) >> kShift) - kRebias;
+  // the subnormal candidate is only used for |f| < the smallest normal, where it is 0 .. 8 / 4
+  const uint32_t rs = (uint32_t)__builtin_rintf(__uint_as_float(a < kMinNormal ? a : 0u) * (kE5M2 ? 65536.0f : 512.0f));
+  const uint32_t normal = 0u - (uint32_t)(a >= kMinNormal);
+  const uint32_t nan = 0u - (uint32_t)(a > 0x7f800000u);
+  const uint32_t r = (rn & normal) | (rs & ~normal);
+  return s | (r & ~nan) | (0x7fu & nan);
+}
+
+// Four clamped fp32 values -> four fp8 bytes (v[0] in the low byte) with the gfx950 conversion
+// instruction, two values per instruction, rounding to nearest even. The GPU tests check it
+// byte for byte against the bit-level definition above on every tie, both neighbours of each tie
+// and fp32 subnormals.
+template <bool kE5M2>
+__device__ __forceinline__ uint32_t pack4_fp8(float a, float b, float c, float d) {
+  if constexpr (kE5M2) {
+    const int lo = __builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(c, d, lo, true);
+  } else {
+    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
   }
-  const float m = __builtin_rintf(__uint_as_float(a) * (kE5M2 ? 65536.0f : 512.0f));
-  return s | (uint32_t)m;
 }
 
 // clamp to [-fmax, fmax]; NaN stays NaN
@@ -98,14 +118,22 @@ __global__ void __launch_bounds__(kThreads) amax_kernel(const void* x, int64_t r
                                                         uint32_t* amax_bits) {
   const int cpr = cols / 8;
   const int64_t n = rows * cpr;
+  const int64_t T = (int64_t)gridDim.x * kThreads;
   uint32_t m = 0;
-  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
-    const int64_t row = i / cpr;
-    const int c = (int)(i - row * cpr);
-    float v[8];
-    load8<kF32>(x, row, stride, c, v);
+  // kUnroll chunks per thread and round: their loads are all in flight before the first is used
+  for (int64_t i0 = (int64_t)blockIdx.x * kThreads + threadIdx.x; i0 < n; i0 += kUnroll * T) {
+    float v[kUnroll][8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) m = max(m, __float_as_uint(v[k]) & 0x7fffffffu);
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = i0 + u * T;
+      const int64_t row = i / cpr;
+      if (i < n) load8<kF32>(x, row, stride, (int)(i - row * cpr), v[u]);
+      else for (int k = 0; k < 8; ++k) v[u][k] = 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) m = max(m, __float_as_uint(v[u][k]) & 0x7fffffffu);
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
@@ -136,18 +164,28 @@ __global__ void __launch_bounds__(kThreads) quant_tensorwise_kernel(const void* 
   if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
   const int cpr = cols / 8;
   const int64_t n = rows * cpr;
-  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
-    const int64_t row = i / cpr;
-    const int c = (int)(i - row * cpr);
-    float v[8];
-    load8<kF32>(x, row, stride, c, v);
-    uint32_t w0 = 0, w1 = 0;
+  const int64_t T = (int64_t)gridDim.x * kThreads;
+  for (int64_t i0 = (int64_t)blockIdx.x * kThreads + threadIdx.x; i0 < n; i0 += kUnroll * T) {
+    float v[kUnroll][8];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      w0 |= f32_to_fp8<kE5M2>(clamp_fmax<kE5M2>(v[k] / scale)) << (8 * k);
-      w1 |= f32_to_fp8<kE5M2>(clamp_fmax<kE5M2>(v[k + 4] / scale)) << (8 * k);
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = i0 + u * T;
+      const int64_t row = i / cpr;
+      if (i < n) load8<kF32>(x, row, stride, (int)(i - row * cpr), v[u]);
     }
-    *(v2u*)(out + row * out_stride + 8 * (int64_t)c) = v2u{w0, w1};
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = i0 + u * T;
+      if (i >= n) break;
+      const int64_t row = i / cpr;
+      const int c = (int)(i - row * cpr);
+      float y[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) y[k] = clamp_fmax<kE5M2>(v[u][k] / scale);
+      const uint32_t w0 = pack4_fp8<kE5M2>(y[0], y[1], y[2], y[3]);
+      const uint32_t w1 = pack4_fp8<kE5M2>(y[4], y[5], y[6], y[7]);
+      *(v2u*)(out + row * out_stride + 8 * (int64_t)c) = v2u{w0, w1};
+    }
   }
 }
 
@@ -256,42 +294,67 @@ __global__ void __launch_bounds__(kThreads) quant_mx_grouped_kernel(MxArgs a) {
       const int mid = (lo + hi + 1) >> 1;
       if (s_pad[mid] <= p0) lo = mid; else hi = mid - 1;
     }
-    const int src0 = s_offs[lo] + (p0 - s_pad[lo]);        // source row of padded row p0
-    const int valid = min(32, s_offs[lo + 1] - src0);      // source rows of this block (>= 1)
+    // wave-uniform: scalar registers, so the row guards below are scalar branches
+    lo = __builtin_amdgcn_readfirstlane(lo);
+    const int src0 = __builtin_amdgcn_readfirstlane(s_offs[lo] + (p0 - s_pad[lo]));   // row of padded p0
+    const int valid = __builtin_amdgcn_readfirstlane(min(32, s_offs[lo + 1] - src0));  // >= 1 source rows
     if (c0 >= a.cols) continue;                            // lanes past the last column
-    float v[32][4];
+    // The block's 32 rows x 4 columns stay in registers between the amax and the conversion:
+    // fp32 as loaded, bf16 as loaded (two values per register; widened when used).
+    constexpr int kW = kF32 ? 4 : 2;
+    uint32_t r[32][kW];
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
       if (i < valid) {
         if constexpr (kF32) {
-          const v4f t = __builtin_nontemporal_load((const v4f*)((const float*)a.x + (int64_t)(src0 + i) * a.stride + c0));
-          v[i][0] = t[0]; v[i][1] = t[1]; v[i][2] = t[2]; v[i][3] = t[3];
+          const v4u t = __builtin_nontemporal_load((const v4u*)((const float*)a.x + (int64_t)(src0 + i) * a.stride + c0));
+          r[i][0] = t[0]; r[i][1] = t[1]; r[i][2] = t[2]; r[i][3] = t[3];
         } else {
           const v2u t = __builtin_nontemporal_load((const v2u*)((const uint16_t*)a.x + (int64_t)(src0 + i) * a.stride + c0));
-          v[i][0] = bf16_lo(t[0]); v[i][1] = bf16_hi(t[0]); v[i][2] = bf16_lo(t[1]); v[i][3] = bf16_hi(t[1]);
+          r[i][0] = t[0]; r[i][1] = t[1];
         }
       } else {
-        v[i][0] = v[i][1] = v[i][2] = v[i][3] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kW; ++k) r[i][k] = 0u;
       }
     }
+    auto val = [&](int i, int j) -> float {
+      if constexpr (kF32) return __uint_as_float(r[i][j]);
+      else return (j & 1) ? bf16_hi(r[i][j >> 1]) : bf16_lo(r[i][j >> 1]);
+    };
     uint32_t sc = 0;
     float mul[4];
+    uint32_t am[4] = {0u, 0u, 0u, 0u};       // |x| bit patterns order like the values
+    if constexpr (kF32) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) am[j] = max(am[j], r[i][j] & 0x7fffffffu);
+    } else {
+      // bf16 pairs: the amax runs on the 16-bit patterns, so nothing is widened before use
+#pragma unroll
+      for (int i = 0; i < 32; ++i)
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          am[2 * k] = max(am[2 * k], r[i][k] & 0x7fffu);
+          am[2 * k + 1] = max(am[2 * k + 1], (r[i][k] >> 16) & 0x7fffu);
+        }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) am[j] <<= 16;
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      uint32_t m = 0;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) m = max(m, __float_as_uint(v[i][j]) & 0x7fffffffu);
-      const int X = block_exponent<kE5M2>(__uint_as_float(m));
+      const int X = block_exponent<kE5M2>(__uint_as_float(am[j]));
       sc |= (uint32_t)(X + 127) << (8 * j);
       mul[j] = X == 128 ? __uint_as_float(0x7fc00000u) : __builtin_ldexpf(1.0f, -X);   // exact 2^-X
     }
     *(uint32_t*)(a.scales + (int64_t)b * a.scale_stride + c0) = sc;
+    uint8_t* orow = a.out + (int64_t)p0 * a.out_stride + c0;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-      uint32_t w = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) w |= f32_to_fp8<kE5M2>(clamp_fmax<kE5M2>(v[i][j] * mul[j])) << (8 * j);
-      *(uint32_t*)(a.out + (int64_t)(p0 + i) * a.out_stride + c0) = w;
+      *(uint32_t*)orow = pack4_fp8<kE5M2>(clamp_fmax<kE5M2>(val(i, 0) * mul[0]), clamp_fmax<kE5M2>(val(i, 1) * mul[1]),
+                                          clamp_fmax<kE5M2>(val(i, 2) * mul[2]), clamp_fmax<kE5M2>(val(i, 3) * mul[3]));
+      orow += a.out_stride;
     }
   }
 }

@@ -11,7 +11,8 @@
  * All pointers are device pointers; sizes and strides in elements. Launches are asynchronous on
  * `stream`; no allocation, no synchronization. Rounding: x / scale is the correctly rounded fp32
  * quotient; fp32 -> fp8 rounds to nearest even, subnormals included; values are clamped to
- * +-fmax first (448 for e4m3fn, 57344 for e5m2); NaN stays NaN.
+ * +-fmax first (448 for e4m3fn, 57344 for e5m2); NaN stays NaN (a NaN code, 0x7F or 0xFF: the
+ * sign of a NaN is unspecified).
  */
 #ifndef GGEMM_QUANT_H
 #define GGEMM_QUANT_H

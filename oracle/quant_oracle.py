@@ -18,7 +18,8 @@ configurations:
   e8m0 byte ``X + 127``; ``q = fp8(clamp(x * 2^-X, -fmax, fmax))``; each group padded with zero rows
   to a multiple of 32, padded offsets the prefix sums of ``ceil(len/32) * 32``.
 
-``fp8()`` rounds to nearest even (subnormals included); NaN maps to the format's NaN code.
+``fp8()`` rounds to nearest even (subnormals included); NaN maps to a NaN code, ``0x7F | sign``
+here (the sign of a NaN result is unspecified in IEEE arithmetic, so checks compare NaN-ness).
 
 Pinning (tests/test_oracle_quant.py): the encoder against torch's own float8 casts on every fp8
 value, every midpoint between neighbours (ties), both neighbours of each midpoint and random fp32

@@ -70,6 +70,14 @@ def test_tensorwise_rounding_ties_and_subnormals(pkg, orq, cuda, fmt):
     np.testing.assert_array_equal(_bytes(q), q_ref)
 
 
+def _assert_bytes_nan_signless(got, ref):
+    """Bytes equal, except that a NaN code (0x7F / 0xFF) may carry either sign: the sign of a NaN
+    result is unspecified (the GPU's x / NaN and numpy's differ there)."""
+    nan = (ref & 0x7F) == 0x7F
+    assert np.all((got[nan] & 0x7F) == 0x7F)
+    np.testing.assert_array_equal(got[~nan], ref[~nan])
+
+
 def test_tensorwise_special_values(pkg, orq, cuda):
     x = torch.zeros((16, 64), dtype=torch.bfloat16)
     _say("tensorwise zeros / NaN")
@@ -79,6 +87,13 @@ def test_tensorwise_special_values(pkg, orq, cuda):
     q, scale, am = pkg.quantize_fp8_tensorwise(x.to(cuda), "e4m3")
     q_ref, s_ref, a_ref = orq.quantize_tensorwise(x.float().numpy(), "e4m3")
     assert np.isnan(float(scale)) and np.isnan(float(am))
+    _assert_bytes_nan_signless(_bytes(q), q_ref)
+    # a NaN element among finite ones: only that element is NaN, the rest quantize normally
+    x = torch.randn((16, 64)).to(torch.bfloat16)
+    amax_finite = float(x.float().abs().max())
+    q, scale, am = pkg.quantize_fp8_tensorwise(x.to(cuda), "e5m2")
+    q_ref, s_ref, _ = orq.quantize_tensorwise(x.float().numpy(), "e5m2")
+    assert float(am) == amax_finite and float(scale) == float(s_ref)
     np.testing.assert_array_equal(_bytes(q), q_ref)
 
 
