@@ -321,6 +321,16 @@ def main():
             r = make_runner(pkg, p, dev, "k32")
             t = time_steps(r, max(args.steps // 4, 10), max(args.warmup // 4, 5))
             extra["gate_up_wgrad_k32_mfma"] = {"ms": round(t, 4), "TFLOPS": round(p.flops / (t * 1e-3) / 1e12, 2)}
+            # fp32 epilogues: fp32 C, and fp32 main-grad accumulation (C += result)
+            sl = torch.tensor(p.lhs_scale, dtype=torch.float32, device=dev)
+            sr = torch.tensor(p.rhs_scale, dtype=torch.float32, device=dev)
+            c32 = torch.zeros((p.G, p.OUT_M, p.OUT_N), dtype=torch.float32, device=dev)
+            for name, acc in (("gate_up_wgrad_f32_out", False), ("gate_up_wgrad_f32_accum", True)):
+                r = lambda acc=acc: pkg.grouped_gemm_fp8_tensorwise_variable_k(
+                    p.lhs, p.rhs, sl, sr, p.group_offs, out=c32, out_dtype=torch.float32, accumulate=acc)
+                t = time_steps(r, max(args.steps // 4, 10), max(args.warmup // 4, 5))
+                extra[name] = {"ms": round(t, 4), "TFLOPS": round(p.flops / (t * 1e-3) / 1e12, 2)}
+            del c32
         line["extra"] = extra
     if args.cpu_seconds > 0 and fwd:
         line["cpu_baseline"] = cpu_baseline_fwd(p, args.cpu_seconds)

@@ -13,6 +13,8 @@
 GGEMM_DEFINE_TENSORWISE_KERNEL(_grouped_variable_k_gemm_kernel, false)
 GGEMM_DEFINE_TENSORWISE_KERNEL(_grouped_variable_k_gemm_kernel_k32, true)
 GGEMM_DEFINE_MX_KERNEL(_grouped_variable_k_mxfp8_gemm_kernel)
+GGEMM_DEFINE_TENSORWISE_F32_KERNEL(_grouped_variable_k_gemm_kernel_f32, ggemm::kOutF32)
+GGEMM_DEFINE_TENSORWISE_F32_KERNEL(_grouped_variable_k_gemm_kernel_f32_acc, ggemm::kOutF32Acc)
 
 namespace {
 
@@ -73,6 +75,28 @@ int ggemm_vark_wgrad_fp8_k32(const void* lhs, const void* rhs, void* out, const 
                              int32_t stride_cm, int32_t stride_cn, void* stream) {
   return launch_tensorwise(true, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
                            stride_rhs_m, stride_cg, stride_cm, stride_cn, stream);
+}
+
+int ggemm_vark_wgrad_fp8_out(const void* lhs, const void* rhs, void* out, const float* lhs_scale,
+                             const float* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
+                             int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
+                             int32_t stride_cm, int32_t stride_cn, int32_t out_mode, void* stream) {
+  if (out_mode == GGEMM_OUT_BF16)
+    return launch_tensorwise(false, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
+                             stride_rhs_m, stride_cg, stride_cm, stride_cn, stream);
+  if (out_mode != GGEMM_OUT_F32 && out_mode != GGEMM_OUT_F32_ACCUM) return GGEMM_E_FORMAT;
+  int rc = validate_common(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
+                           stride_rhs_m, stride_cg, stride_cm, stride_cn);
+  if (rc) return rc;
+  if (!aligned(out, 16)) return GGEMM_E_ALIGN;    // 16-byte fp32 row segments
+  int cus = 0;
+  rc = device_cus(&cus);
+  if (rc) return rc;
+  auto kern = out_mode == GGEMM_OUT_F32 ? _grouped_variable_k_gemm_kernel_f32 : _grouped_variable_k_gemm_kernel_f32_acc;
+  hipLaunchKernelGGL(kern, dim3(cus), dim3(ggemm::kThreads), ggemm::kDynLdsBytes, (hipStream_t)stream,
+                     (const uint8_t*)lhs, (const uint8_t*)rhs, (float*)out, lhs_scale, rhs_scale, group_offs, G, OUT_M,
+                     OUT_N, stride_lhs_m, stride_rhs_m, stride_cg, stride_cm, stride_cn, (void*)nullptr, (void*)nullptr);
+  return (int)hipGetLastError();
 }
 
 int ggemm_vark_wgrad_mxfp8(const void* lhs, const void* rhs, void* out, const uint8_t* lhs_scale,

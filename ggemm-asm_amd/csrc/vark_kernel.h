@@ -67,7 +67,12 @@ constexpr int kStaticLdsBytes = 98304;                      // + 96 KiB static =
 constexpr int kMaxSortG = 1024;                             // larger G: natural group order
 constexpr int kXcds = 8;                                    // MI355X: 8 XCDs, 32 CUs each
 constexpr int kXcdPairs = kXcds / 2;                        // schedule slices, two XCDs each
-constexpr int kMiscBytes = 16384;                           // group order, sizes, XCD bounds, e8m0
+constexpr int kMiscBytes = 16384;                           // group order, offsets, XCD bounds, e8m0
+// misc-region layout shared by both bodies: s_order int[1024] @0, s_kb int[1025] @4096 (the group
+// offsets), a flag @8196, s_bound int64[9] @8200; the MXFP8 scales follow at kScaleOffset.
+constexpr int kKbOffset = 4096, kFlagOffset = 8196, kBoundOffset = 8200, kScaleOffset = 8320;
+static_assert(kKbOffset + 4 * (kMaxSortG + 1) <= kFlagOffset && kBoundOffset + 8 * (kXcds + 1) <= kScaleOffset,
+              "misc layout");
 constexpr uint32_t kRsrcWord3 = 0x00020000u;                // raw buffer, 32-bit data format
 
 static_assert(kDmaLhs % kWaves == 0, "LHS LDS-DMA instructions split evenly over the waves");
@@ -91,7 +96,7 @@ struct Cfg {
   static constexpr int ScaleLanesR = (ScaleChunksR + 4) / 5;      // per RHS wave (waves 3-7)
   static_assert((kDmaLhs + DmaRhs) % kWaves == 0, "uniform LDS-DMA split");
   static_assert(ScaleLanesR * 5 >= ScaleChunksR && ScaleLanesR <= 64, "scale DMA coverage");
-  static_assert(4096 * 2 + 8 * (kXcds + 1) + 2 * ScaleStage + 512 <= kMiscBytes, "misc LDS budget");
+  static_assert(kScaleOffset + 2 * ScaleStage <= kMiscBytes, "misc LDS budget");
   __device__ static __forceinline__ int rswz(int t) { return kTN == 384 ? ((t >> 1) & 7) : ((t >> 2) & 3); }
   // Epilogue staging: per wave 48 rows of WaveN bf16 (EpiChunks 16-byte chunks per row), read back
   // in EpiReads 64-lane passes. Rows of 12 chunks XOR the chunk with (row >> 2) & 3 so that the
@@ -336,7 +341,7 @@ __device__ __forceinline__ void pin_stage_schedule() {
 struct VarKArgs {
   const uint8_t* lhs;
   const uint8_t* rhs;
-  uint16_t* out;
+  void* out;               // bf16 C, or fp32 C for the fp32 output modes
   const void* lhs_scale;   // fp32 scalar (tensorwise) or e8m0 [M/32, OUT_M] (MX)
   const void* rhs_scale;   // fp32 scalar (tensorwise) or e8m0 [M/32, OUT_N] (MX)
   const int64_t* group_offs;
@@ -367,13 +372,27 @@ struct Tile {
 struct Sched {
   int t_begin, t_end, step;   // this workgroup's tiles: t_begin, t_begin + step, ... below t_end
   int n_tm, n_tn, tiles_per_group;
-  bool sorted;
+  bool sorted;                // groups ranked by size, their offsets held in LDS (s_kb)
   bool valid;                 // false: more tiles than 32-bit indices cover (C would need > 512 GiB)
 };
 
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ int group_size(const GG_LDS int* s_kb, int g) {
+  const int d = s_kb[g + 1] - s_kb[g];
+  return d > 0 ? d : 0;
+}
+
+// Groups are sorted (and their offsets kept in LDS, so the tile loop reads them there instead of
+// issuing a global load whose wait would drain the prefetched stage) when G <= kMaxSortG and every
+// offset fits 31 bits; otherwise natural order with offsets read from memory.
 template <int kTN, int kK>
-__device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_order, GG_LDS int* s_size,
-                                            GG_LDS int64_t* s_bound) {
+__device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_order, GG_LDS int* s_kb,
+                                            GG_LDS int* s_flag, GG_LDS int64_t* s_bound) {
   Sched S;
   const hsa_kernel_dispatch_packet_t* pkt = dispatch_packet();
   const int num_wg = (int)((pkt->grid_size_x + pkt->workgroup_size_x - 1) / pkt->workgroup_size_x);
@@ -382,16 +401,22 @@ __device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_ord
 
   S.sorted = G <= kMaxSortG;
   if (S.sorted) {
-    for (int g = tid; g < G; g += kThreads) {
-      int64_t sz = a.group_offs[g + 1] - a.group_offs[g];
-      s_size[g] = (int)(sz > 0x7fffffff ? 0x7fffffff : (sz < 0 ? 0 : sz));
+    if (tid == 0) *s_flag = 0;
+    __syncthreads();
+    for (int g = tid; g <= G; g += kThreads) {
+      const int64_t o = a.group_offs[g];
+      if (o < 0 || o > 0x7fffffff) *s_flag = 1;
+      s_kb[g] = (int)o;
     }
     __syncthreads();
+    S.sorted = *s_flag == 0;
+  }
+  if (S.sorted) {
     for (int g = tid; g < G; g += kThreads) {
-      const int my = s_size[g];
+      const int my = group_size(s_kb, g);
       int rank = 0;
       for (int h = 0; h < G; ++h) {
-        const int o = s_size[h];
+        const int o = group_size(s_kb, h);
         rank += (o > my) || (o == my && h < g);
       }
       s_order[rank] = g;
@@ -419,12 +444,12 @@ __device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_ord
   if (tid == 0) {
     if (S.sorted && n_xcd > 1) {
       int64_t total_w = 0;
-      for (int sl = 0; sl < G; ++sl) total_w += (int64_t)tpg * (((int64_t)s_size[s_order[sl]] + kK - 1) / kK + 1);
+      for (int sl = 0; sl < G; ++sl) total_w += (int64_t)tpg * (((int64_t)group_size(s_kb, s_order[sl]) + kK - 1) / kK + 1);
       int64_t acc_w = 0;
       int x = 1;
       s_bound[0] = 0;
       for (int sl = 0; sl < G && x < n_xcd; ++sl) {
-        const int64_t w = ((int64_t)s_size[s_order[sl]] + kK - 1) / kK + 1;
+        const int64_t w = ((int64_t)group_size(s_kb, s_order[sl]) + kK - 1) / kK + 1;
         const int64_t slot_w = w * tpg;
         while (x < n_xcd && acc_w + slot_w >= (total_w * x) / n_xcd) {
           const int64_t need = (total_w * x) / n_xcd - acc_w;
@@ -447,7 +472,8 @@ __device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_ord
 }
 
 template <int kTN, int kK>
-__device__ __forceinline__ Tile tile_at(const Sched& S, const VarKArgs& a, const GG_LDS int* s_order, int t) {
+__device__ __forceinline__ Tile tile_at(const Sched& S, const VarKArgs& a, const GG_LDS int* s_order,
+                                        const GG_LDS int* s_kb, int t) {
   constexpr int kBandN = 4;
   Tile T;
   const int slot = t / S.tiles_per_group;
@@ -460,32 +486,46 @@ __device__ __forceinline__ Tile tile_at(const Sched& S, const VarKArgs& a, const
   const int tn = band * kBandN + (r - tm * bw);
   T.m0 = tm * kTileM;
   T.n0 = tn * kTN;
-  T.kb = a.group_offs[T.g];
-  const int64_t ke = a.group_offs[T.g + 1];
+  // wave-uniform values in scalar registers either way
+  T.g = __builtin_amdgcn_readfirstlane(T.g);
+  int64_t ke;
+  if (S.sorted) {
+    T.kb = __builtin_amdgcn_readfirstlane(s_kb[T.g]);
+    ke = __builtin_amdgcn_readfirstlane(s_kb[T.g + 1]);
+  } else {
+    T.kb = uniform64(a.group_offs[T.g]);
+    ke = uniform64(a.group_offs[T.g + 1]);
+  }
   T.klen = ke > T.kb ? ke - T.kb : 0;
   T.nsteps = (int)((T.klen + kK - 1) / kK);
   return T;
 }
 
-template <bool kMX, bool kLegacyK32, int kTN>
+// Output modes of the tensorwise kernel's epilogue: bf16 C (the reference contract), fp32 C, and
+// fp32 C accumulated in place (C += result: the main-grad accumulation of a training step).
+enum OutMode : int { kOutBF16 = 0, kOutF32 = 1, kOutF32Acc = 2 };
+
+template <bool kMX, bool kLegacyK32, int kTN, int kOut = kOutBF16>
 __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds) {
+  static_assert(kOut == kOutBF16 || !kMX, "fp32 output modes are built for the tensorwise kernel");
   static_assert(!(kMX && kLegacyK32), "block scales need the scaled MFMA");
   using C = Cfg<kTN>;
   constexpr int NB = C::NB;
   const LdsMap lm = lds_map<kTN>(lds);
   GG_LDS int* s_order = (GG_LDS int*)lm.misc;
-  GG_LDS int* s_size = (GG_LDS int*)(lm.misc + 4096);
-  GG_LDS int64_t* s_bound = (GG_LDS int64_t*)(lm.misc + 8192);
-  GG_LDS uint8_t* scales = lm.misc + 8192 + 8 * (kXcds + 1) + 56;   // 16-byte aligned
+  GG_LDS int* s_kb = (GG_LDS int*)(lm.misc + kKbOffset);
+  GG_LDS int* s_flag = (GG_LDS int*)(lm.misc + kFlagOffset);
+  GG_LDS int64_t* s_bound = (GG_LDS int64_t*)(lm.misc + kBoundOffset);
+  GG_LDS uint8_t* scales = lm.misc + kScaleOffset;   // 16-byte aligned
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  const Sched S = make_sched<kTN, kKStep>(a, s_order, s_size, s_bound);
+  const Sched S = make_sched<kTN, kKStep>(a, s_order, s_kb, s_flag, s_bound);
   if (!S.valid) return;
   const int t_begin = S.t_begin, t_end = S.t_end, wgs_per_xcd = S.step;
-  auto tile_at_ = [&](int t) { return tile_at<kTN, kKStep>(S, a, s_order, t); };
+  auto tile_at_ = [&](int t) { return tile_at<kTN, kKStep>(S, a, s_order, s_kb, t); };
 
   float alpha = 1.0f;
   if constexpr (!kMX) alpha = *(const float*)a.lhs_scale * *(const float*)a.rhs_scale;
@@ -521,7 +561,11 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
 
   int cur = 0;              // LDS slot holding the next stage to compute
   bool prefetched = false;  // stage 0 of tile t was issued during the previous tile
-  bool full_prev = false;   // the previous epilogue issued all EpiStores stores in every wave
+  bool full_prev = false;   // the previous epilogue issued all kEpiStores stores in every wave
+  // vector-memory operations of a full tile's epilogue per wave: the staged bf16 stores, or one
+  // 16-byte store per accumulator block in fp32 mode (accumulate mode mixes loads in and is not
+  // counted)
+  constexpr int kEpiStores = kOut == kOutBF16 ? C::EpiStores : kMB * NB;
   int t = t_begin;
   Tile T;
   if (t < t_end) T = tile_at_(t);
@@ -546,7 +590,7 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
       // Stage s landed for this wave; after the barrier it has for all waves, and every wave is
       // done computing stage s-1, so its slot may take the next prefetch.
       if (s == 0 && stores_after_stage0)
-        wait_vmcnt<C::EpiStores>();
+        wait_vmcnt<kEpiStores>();
       else
         wait_vmcnt<0>();
       lds_barrier();
@@ -592,45 +636,96 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
       cur ^= 1;
     }
 
-    // ---- epilogue. Lane holds C[m][n..n+3] for m = m0+wm*96+i*16+s16, n = n0+wn*TN/4+j*16+4q.
-    // The values go through a private region of the free slot (the last stage's) so that each
-    // store instruction writes 16 bytes per lane along whole row segments of C: per pass of three
-    // m-blocks a wave stages 48 rows x TN/4 columns of bf16, reads them back as 16-byte chunks in
-    // row order and stores them. One barrier first: every wave must be done with the last stage.
-    lds_barrier();
-    GG_LDS uint8_t* stg = (cur ? lm.L[0] : lm.L[1]) + wave * C::EpiRegion;
-    // Opaque copy of the lane id: keeps the compiler from hoisting the epilogue's per-lane address
-    // arithmetic out of the tile loop, where it would hold registers through the stages.
-    int el = lane;
-    asm volatile("" : "+v"(el));
-    uint16_t* cg = a.out + (int64_t)T.g * a.stride_cg;
+    if constexpr (kOut != kOutBF16) {
+      // ---- fp32 epilogue: a lane's 4 consecutive columns of one C row are already a 16-byte
+      // row segment, so it stores them directly (no LDS staging). Accumulate mode reads the old
+      // values one m-block ahead of their use.
+      float* cg = static_cast<float*>(a.out) + (int64_t)T.g * a.stride_cg;
+      const int mb = T.m0 + wm * kWaveM + s16;
+      const int nb = T.n0 + wn * C::WaveN + 4 * q;
+      // A full tile (every tile at the measured shapes) runs without per-element bounds checks:
+      // with them the compiler cannot count outstanding memory operations across the branches
+      // and drains them all before every store.
+      auto epilogue = [&](auto kFullTile) {
+        constexpr bool kFull = decltype(kFullTile)::value;
+        auto in = [&](int m, int n) { return kFull || (m < a.OUT_M && n < a.OUT_N); };
+        v4f old[2][NB];
+        auto load_old = [&](int i, v4f* dst) {
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
+          for (int j = 0; j < NB; ++j) {
+            const int m = mb + 16 * i, n = nb + 16 * j;
+            dst[j] = in(m, n) ? *(const v4f*)(cg + (int64_t)m * a.stride_cm + n) : v4f{0.f, 0.f, 0.f, 0.f};
+          }
+        };
+        if constexpr (kOut == kOutF32Acc) load_old(0, old[0]);
 #pragma unroll
-      for (int ii = 0; ii < 3; ++ii) {
-        const int r = ii * 16 + s16;
+        for (int i = 0; i < kMB; ++i) {
+          if constexpr (kOut == kOutF32Acc)
+            if (i + 1 < kMB) load_old(i + 1, old[(i + 1) & 1]);
 #pragma unroll
-        for (int j = 0; j < NB; ++j) {
-          const v4f v = acc[3 * p + ii][j];
-          const v2i pk = v2i{(int)(f32_to_bf16_rne(v[0] * alpha) | (f32_to_bf16_rne(v[1] * alpha) << 16)),
-                             (int)(f32_to_bf16_rne(v[2] * alpha) | (f32_to_bf16_rne(v[3] * alpha) << 16))};
-          const int c = 2 * j + (q >> 1);
-          *(GG_LDS v2i*)(stg + r * C::EpiRow + 16 * (c ^ C::eswz(r)) + 8 * (q & 1)) = pk;
+          for (int j = 0; j < NB; ++j) {
+            const int m = mb + 16 * i, n = nb + 16 * j;
+            // the scaled product is rounded to fp32 before the addition (the empty asm keeps the
+            // compiler from fusing them into an FMA), so accumulating equals adding the
+            // fp32-output result to C, bit for bit
+            v4f v = acc[i][j] * alpha;
+            if constexpr (kOut == kOutF32Acc) {
+              asm volatile("" : "+v"(v));
+              v += old[i & 1][j];
+            }
+            if (in(m, n)) __builtin_nontemporal_store(v, (v4f*)(cg + (int64_t)m * a.stride_cm + n));
+          }
+        }
+      };
+      const bool full = T.m0 + kTileM <= a.OUT_M && T.n0 + kTN <= a.OUT_N;
+      if (full)
+        epilogue(std::true_type{});
+      else
+        epilogue(std::false_type{});
+      // fp32 mode: a full tile issued exactly kMB x NB stores per wave (the counted wait applies);
+      // accumulate mode: loads and stores mixed, the next tile's first wait drains everything
+      full_prev = kOut == kOutF32 && full;
+    } else {
+      // ---- epilogue. Lane holds C[m][n..n+3] for m = m0+wm*96+i*16+s16, n = n0+wn*TN/4+j*16+4q.
+      // The values go through a private region of the free slot (the last stage's) so that each
+      // store instruction writes 16 bytes per lane along whole row segments of C: per pass of three
+      // m-blocks a wave stages 48 rows x TN/4 columns of bf16, reads them back as 16-byte chunks in
+      // row order and stores them. One barrier first: every wave must be done with the last stage.
+      lds_barrier();
+      GG_LDS uint8_t* stg = (cur ? lm.L[0] : lm.L[1]) + wave * C::EpiRegion;
+      // Opaque copy of the lane id: keeps the compiler from hoisting the epilogue's per-lane address
+      // arithmetic out of the tile loop, where it would hold registers through the stages.
+      int el = lane;
+      asm volatile("" : "+v"(el));
+      uint16_t* cg = static_cast<uint16_t*>(a.out) + (int64_t)T.g * a.stride_cg;
+  #pragma unroll
+      for (int p = 0; p < 2; ++p) {
+  #pragma unroll
+        for (int ii = 0; ii < 3; ++ii) {
+          const int r = ii * 16 + s16;
+  #pragma unroll
+          for (int j = 0; j < NB; ++j) {
+            const v4f v = acc[3 * p + ii][j];
+            const v2i pk = v2i{(int)(f32_to_bf16_rne(v[0] * alpha) | (f32_to_bf16_rne(v[1] * alpha) << 16)),
+                               (int)(f32_to_bf16_rne(v[2] * alpha) | (f32_to_bf16_rne(v[3] * alpha) << 16))};
+            const int c = 2 * j + (q >> 1);
+            *(GG_LDS v2i*)(stg + r * C::EpiRow + 16 * (c ^ C::eswz(r)) + 8 * (q & 1)) = pk;
+          }
+        }
+  #pragma unroll
+        for (int k = 0; k < C::EpiReads; ++k) {
+          const int f = k * 64 + el;
+          const int r = f / C::EpiChunks;
+          const int c = f - r * C::EpiChunks;
+          const v4i v = *(const GG_LDS v4i*)(stg + r * C::EpiRow + 16 * (c ^ C::eswz(r)));
+          const int m = T.m0 + wm * kWaveM + 48 * p + r;
+          const int n = T.n0 + wn * C::WaveN + 8 * c;
+          if ((C::EpiReads * 64 == 48 * C::EpiChunks || f < 48 * C::EpiChunks) && m < a.OUT_M && n < a.OUT_N)
+            store_c16(cg + (int64_t)m * a.stride_cm + n, v);
         }
       }
-#pragma unroll
-      for (int k = 0; k < C::EpiReads; ++k) {
-        const int f = k * 64 + el;
-        const int r = f / C::EpiChunks;
-        const int c = f - r * C::EpiChunks;
-        const v4i v = *(const GG_LDS v4i*)(stg + r * C::EpiRow + 16 * (c ^ C::eswz(r)));
-        const int m = T.m0 + wm * kWaveM + 48 * p + r;
-        const int n = T.n0 + wn * C::WaveN + 8 * c;
-        if ((C::EpiReads * 64 == 48 * C::EpiChunks || f < 48 * C::EpiChunks) && m < a.OUT_M && n < a.OUT_N)
-          store_c16(cg + (int64_t)m * a.stride_cm + n, v);
-      }
+      full_prev = T.m0 + kTileM <= a.OUT_M && T.n0 + kTN <= a.OUT_N;
     }
-    full_prev = T.m0 + kTileM <= a.OUT_M && T.n0 + kTN <= a.OUT_N;
     t = t_next;
     T = N;
   }
@@ -670,7 +765,7 @@ constexpr int kPerWave = (kDmaLhs + kDmaRhs) / kWaves;    // 9: 3 LHS + 6 RHS
 constexpr int kLhsPerWave = kDmaLhs / kWaves;             // 3
 constexpr int kMisc = 2 * kSlot;                          // 144 KiB: group order, XCD bounds, scales
 constexpr int kScaleStage = 4 * kTileM + 4 * kTN;         // e8m0 bytes per stage
-constexpr int kScaleOff = 8192 + 128;
+constexpr int kScaleOff = kScaleOffset;
 constexpr int kEpiRows = 32;                              // one 32 x 32 block row per pass
 constexpr int kEpiRegion = kEpiRows * 192;                // 6 KiB per wave
 constexpr int kEpiReads = kEpiRows * 12 / 64;             // 6 chunk reads per pass
@@ -721,15 +816,16 @@ __device__ __forceinline__ void vark_body32(const VarKArgs& a, GG_LDS uint8_t* l
   using namespace x32;
   GG_LDS uint8_t* misc = lds + kMisc;
   GG_LDS int* s_order = (GG_LDS int*)misc;
-  GG_LDS int* s_size = (GG_LDS int*)(misc + 4096);
-  GG_LDS int64_t* s_bound = (GG_LDS int64_t*)(misc + 8192);
+  GG_LDS int* s_kb = (GG_LDS int*)(misc + kKbOffset);
+  GG_LDS int* s_flag = (GG_LDS int*)(misc + kFlagOffset);
+  GG_LDS int64_t* s_bound = (GG_LDS int64_t*)(misc + kBoundOffset);
   GG_LDS uint8_t* scales = misc + kScaleOff;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  const Sched S = make_sched<kTN, kKStep>(a, s_order, s_size, s_bound);
+  const Sched S = make_sched<kTN, kKStep>(a, s_order, s_kb, s_flag, s_bound);
   if (!S.valid) return;
 
   const int wm = wave & 1;   // wave row (OUT_M) in the 2 x 4 wave grid
@@ -766,12 +862,12 @@ __device__ __forceinline__ void vark_body32(const VarKArgs& a, GG_LDS uint8_t* l
   bool full_prev = false;   // the previous epilogue issued all kEpiStores stores in every wave
   int t = S.t_begin;
   Tile T;
-  if (t < S.t_end) T = tile_at<kTN, kKStep>(S, a, s_order, t);
+  if (t < S.t_end) T = tile_at<kTN, kKStep>(S, a, s_order, s_kb, t);
   while (t < S.t_end) {
     const int t_next = t + S.step;
     const bool has_next = t_next < S.t_end;
     Tile N;
-    if (has_next) N = tile_at<kTN, kKStep>(S, a, s_order, t_next);
+    if (has_next) N = tile_at<kTN, kKStep>(S, a, s_order, s_kb, t_next);
 
     v16f acc[3][3];
 #pragma unroll
@@ -839,7 +935,7 @@ __device__ __forceinline__ void vark_body32(const VarKArgs& a, GG_LDS uint8_t* l
     int el = lane;
     asm volatile("" : "+v"(el));
     const int hl = el >> 5, rl = el & 31;
-    uint16_t* cg = a.out + (int64_t)T.g * a.stride_cg;
+    uint16_t* cg = static_cast<uint16_t*>(a.out) + (int64_t)T.g * a.stride_cg;
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
 #pragma unroll
@@ -871,7 +967,7 @@ __device__ __forceinline__ void vark_body32(const VarKArgs& a, GG_LDS uint8_t* l
 // Entry body shared by all kernels: checks the launch's LDS, then runs the 384-wide tile
 // configuration when OUT_N is a multiple of 384 (tensorwise kernels) and the 320-wide one
 // otherwise.
-template <bool kMX, bool kLegacyK32>
+template <bool kMX, bool kLegacyK32, int kOut = kOutBF16>
 __device__ __forceinline__ void vark_entry(const VarKArgs& a, GG_LDS uint8_t* dyn) {
   __shared__ __attribute__((aligned(1024))) uint8_t static_lds[kStaticLdsBytes];
   const hsa_kernel_dispatch_packet_t* pkt = dispatch_packet();
@@ -885,9 +981,9 @@ __device__ __forceinline__ void vark_entry(const VarKArgs& a, GG_LDS uint8_t* dy
     if constexpr (kMX)
       vark_body32(a, st);
     else
-      vark_body<false, kLegacyK32, 384>(a, st);
+      vark_body<false, kLegacyK32, 384, kOut>(a, st);
   } else {
-    vark_body<kMX, kLegacyK32, 320>(a, st);
+    vark_body<kMX, kLegacyK32, 320, kOut>(a, st);
   }
 }
 
@@ -908,6 +1004,20 @@ __device__ __forceinline__ void vark_entry(const VarKArgs& a, GG_LDS uint8_t* dy
                       stride_lhs_m, stride_rhs_m, stride_cg, stride_cm, stride_cn, 0, 0};                \
     (void)global_scratch; (void)profile_scratch;                                                        \
     ggemm::vark_entry<false, LEGACY>(a, (GG_LDS uint8_t*)ggemm_dyn_lds);                                  \
+  }
+
+// Tensorwise kernels with an fp32 output mode (kOutF32 / kOutF32Acc): same 16 arguments, C an fp32
+// tensor (strides in fp32 elements). Library entry points only; not part of the reference contract.
+#define GGEMM_DEFINE_TENSORWISE_F32_KERNEL(NAME, OUT)                                                   \
+  extern "C" __global__ __launch_bounds__(ggemm::kThreads) void NAME(                                   \
+      const uint8_t* lhs, const uint8_t* rhs, float* out, const float* lhs_scale, const float* rhs_scale, \
+      const int64_t* group_offs, int G, int OUT_M, int OUT_N, int stride_lhs_m, int stride_rhs_m,        \
+      int stride_cg, int stride_cm, int stride_cn, void* global_scratch, void* profile_scratch) {        \
+    extern __shared__ __attribute__((aligned(1024))) uint8_t ggemm_dyn_lds[];                           \
+    ggemm::VarKArgs a{lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N,                  \
+                      stride_lhs_m, stride_rhs_m, stride_cg, stride_cm, stride_cn, 0, 0};                \
+    (void)global_scratch; (void)profile_scratch;                                                        \
+    ggemm::vark_entry<false, false, OUT>(a, (GG_LDS uint8_t*)ggemm_dyn_lds);                              \
   }
 
 #define GGEMM_DEFINE_MX_KERNEL(NAME)                                                                    \

@@ -41,11 +41,11 @@ def _check_inputs(lhs, rhs, group_offs, lhs_dt=_FP8_LHS, rhs_dt=_FP8_RHS):
                          f"{dev}); use the CPU oracle in tests for reference results")
 
 
-def _check_out(out, G, OUT_M, OUT_N, dev):
+def _check_out(out, G, OUT_M, OUT_N, dev, dtype=torch.bfloat16):
     if out is None:
-        return torch.empty((G, OUT_M, OUT_N), dtype=torch.bfloat16, device=dev)
-    if out.dtype != torch.bfloat16 or out.dim() != 3 or tuple(out.shape) != (G, OUT_M, OUT_N):
-        raise ValueError(f"out must be bf16 [{G}, {OUT_M}, {OUT_N}]")
+        return torch.empty((G, OUT_M, OUT_N), dtype=dtype, device=dev)
+    if out.dtype != dtype or out.dim() != 3 or tuple(out.shape) != (G, OUT_M, OUT_N):
+        raise ValueError(f"out must be {dtype} [{G}, {OUT_M}, {OUT_N}]")
     if out.device != dev:
         raise ValueError("out must be on the input device")
     return out
@@ -74,12 +74,15 @@ def _stream(dev) -> int:
 def grouped_gemm_fp8_tensorwise_variable_k(lhs: torch.Tensor, rhs: torch.Tensor, lhs_scale: torch.Tensor,
                                            rhs_scale: torch.Tensor, group_offs: torch.Tensor,
                                            out: torch.Tensor | None = None, *, mfma: str = "k128",
-                                           validate: bool = False) -> torch.Tensor:
+                                           validate: bool = False, out_dtype: torch.dtype = torch.bfloat16,
+                                           accumulate: bool = False) -> torch.Tensor:
     """``out[g] = lhs_scale * rhs_scale * lhs[offs[g]:offs[g+1]]^T @ rhs[offs[g]:offs[g+1]]`` (bf16).
 
     lhs: float8_e4m3fn [M_total, OUT_M]; rhs: float8_e5m2 [M_total, OUT_N]; scales: fp32 scalar
     tensors on the device; group_offs: int64 [G+1]. ``mfma="k32"`` selects the kernel built on the
     K=32 MFMA the reference uses; ``validate=True`` checks group_offs on the host first (a sync).
+    ``out_dtype=torch.float32`` writes an fp32 C; ``accumulate=True`` adds the result into the fp32
+    ``out`` given (the main-grad accumulation, beta = 1).
     """
     _check_inputs(lhs, rhs, group_offs)
     for s in (lhs_scale, rhs_scale):
@@ -88,11 +91,28 @@ def grouped_gemm_fp8_tensorwise_variable_k(lhs: torch.Tensor, rhs: torch.Tensor,
     G = group_offs.numel() - 1
     M_total, OUT_M = lhs.shape
     OUT_N = rhs.shape[1]
-    out = _check_out(out, G, OUT_M, OUT_N, lhs.device)
+    if accumulate and out is None:
+        raise ValueError("accumulate=True adds into an existing fp32 `out`")
+    if accumulate:
+        out_dtype = torch.float32
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("out_dtype must be torch.bfloat16 or torch.float32")
+    out = _check_out(out, G, OUT_M, OUT_N, lhs.device, out_dtype)
     if validate:
         _validate_offsets(group_offs, M_total, mx=False)
     lhs, rhs = _nonempty(lhs), _nonempty(rhs)
     lib = _lib.load()
+    if out_dtype == torch.float32:
+        if mfma != "k128":
+            raise ValueError("the fp32 output modes use the K=128 MFMA kernel")
+        mode = 2 if accumulate else 1
+        with torch.cuda.device(lhs.device):
+            rc = lib.ggemm_vark_wgrad_fp8_out(
+                lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), lhs_scale.data_ptr(), rhs_scale.data_ptr(),
+                group_offs.data_ptr(), G, OUT_M, OUT_N, lhs.stride(0), rhs.stride(0), out.stride(0), out.stride(1),
+                out.stride(2), mode, _stream(lhs.device))
+        _lib.check(rc, "ggemm_vark_wgrad_fp8_out")
+        return out
     fn = {"k128": lib.ggemm_vark_wgrad_fp8, "k32": lib.ggemm_vark_wgrad_fp8_k32}[mfma]
     with torch.cuda.device(lhs.device):
         rc = fn(lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), lhs_scale.data_ptr(), rhs_scale.data_ptr(),

@@ -55,6 +55,25 @@ int ggemm_vark_wgrad_fp8_k32(const void* lhs, const void* rhs, void* out, const 
                              int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
                              int32_t stride_cm, int32_t stride_cn, void* stream);
 
+/* Output modes of ggemm_vark_wgrad_fp8_out. */
+#define GGEMM_OUT_BF16 0        /* C bf16 (ggemm_vark_wgrad_fp8) */
+#define GGEMM_OUT_F32 1         /* C fp32: C[g] = s_lhs s_rhs LHS_g^T RHS_g, no bf16 rounding */
+#define GGEMM_OUT_F32_ACCUM 2   /* C fp32, accumulated in place: C[g] += s_lhs s_rhs LHS_g^T RHS_g */
+
+/* Tensorwise FP8 grouped wgrad with a chosen output: the fp32 modes write (or, with
+ * GGEMM_OUT_F32_ACCUM, add into) an fp32 C [G, OUT_M, OUT_N] -- the main-grad accumulation of a
+ * training step (beta = 1), with the product rounded once to fp32 before the addition. No
+ * reference counterpart: the reference kernel writes bf16 only (reference launcher.cpp:16-33);
+ * the modes are the epilogue variants a training framework needs around it. Same arguments as
+ * ggemm_vark_wgrad_fp8 with strides in elements of C's type; fp32 C must be 16-byte aligned,
+ * stride_cm and stride_cg multiples of 4. Accumulate mode reads and writes every element of
+ * C[0:G] once per launch (empty groups add zero), so a launch is deterministic. GGEMM_OUT_BF16
+ * is the plain ggemm_vark_wgrad_fp8. */
+int ggemm_vark_wgrad_fp8_out(const void* lhs, const void* rhs, void* out, const float* lhs_scale,
+                             const float* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
+                             int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
+                             int32_t stride_cm, int32_t stride_cn, int32_t out_mode, void* stream);
+
 /* MXFP8 block-scaled grouped wgrad (no reference counterpart: the reference imports only the
  * tensorwise kernels, reference bench.py:241-246). lhs_scale: e8m0 bytes [ceil(M_total/32), OUT_M]
  * with row stride stride_lhs_scale; rhs_scale: e8m0 [ceil(M_total/32), OUT_N], row stride

@@ -25,7 +25,7 @@ def _header_functions():
 def test_library_exports_every_header_symbol(pkg):
     lib = pkg.load_library()
     names = _header_functions()
-    assert len(names) >= 8
+    assert len(names) >= 9
     for n in names:
         assert hasattr(lib, n), n
     from ggemm_asm_amd import _lib
@@ -86,6 +86,19 @@ def _call(lib, **kw):
 ])
 def test_validation_rejects(pkg, kw, rc):
     assert _call(pkg.load_library(), **kw) == rc
+
+
+@pytest.mark.parametrize("mode,kw,rc", [
+    (3, {}, -8), (-1, {}, -8), (1, dict(out=FAKE + 8), -4), (2, dict(out=FAKE + 8), -4), (1, dict(scn=2), -3),
+    (2, dict(scm=5762), -3), (1, dict(lhs=0), -1),
+])
+def test_fp32_out_validation_rejects(pkg, mode, kw, rc):
+    lib = pkg.load_library()
+    a = dict(lhs=FAKE, rhs=FAKE, out=FAKE, ls=FAKE, rs=FAKE, offs=FAKE, G=32, OUT_M=2880, OUT_N=5760,
+             slm=2880, srm=5760, scg=2880 * 5760, scm=5760, scn=1)
+    a.update(kw)
+    assert lib.ggemm_vark_wgrad_fp8_out(a["lhs"], a["rhs"], a["out"], a["ls"], a["rs"], a["offs"], a["G"], a["OUT_M"],
+                                        a["OUT_N"], a["slm"], a["srm"], a["scg"], a["scm"], a["scn"], mode, None) == rc
 
 
 def test_mx_validation_rejects(pkg):

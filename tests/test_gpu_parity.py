@@ -355,3 +355,71 @@ def test_full_size_config(pkg, orc, cuda, name):
     picks = {int(order[0]), int(order[len(order) // 2])}
     picks |= {int(g) for g in np.nonzero((lens > 0) & (lens < 32))[0][:4]}
     _oracle_groups(pkg, orc, p, out, sorted(picks))
+
+
+# ----------------------------------------------------------------------------- fp32 epilogues
+
+def _f32_parity(orc, got, ref, label):
+    """The bar on fp32 values: cosine >= 0.99999, max relative error <= 2e-2 over |ref| >
+    1e-3 max|ref|, all finite."""
+    a = got.astype(np.float64).ravel()
+    b = ref.astype(np.float64).ravel()
+    cos = float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b) + 1e-300))
+    mask = np.abs(b) > 1e-3 * np.abs(b).max()
+    rel = float(np.max(np.abs(a[mask] - b[mask]) / np.abs(b[mask]))) if mask.any() else 0.0
+    _say(f"{label}: cos {cos:.9f} max_rel {rel:.3e}")
+    assert cos >= 0.99999 and rel <= 2e-2 and np.isfinite(a).all(), (label, cos, rel)
+
+
+@pytest.mark.parametrize("lens,om,on", [([127, 128, 0, 255, 256, 257], 208, 336), ([300, 0, 645], 400, 1152),
+                                        ([31] * 4 + [0] * 2, 16, 384)], ids=["c320", "c384", "tiny"])
+def test_fp32_output_and_accumulate(pkg, orc, cuda, lens, om, on):
+    lhs, rhs, offs, _, (sl, sr) = _rand_bytes_problem(lens, om, on, seed=len(lens) + om)
+    G = len(lens)
+    _say(f"fp32 out lens={lens} {om}x{on}")
+    ref = orc.vark_wgrad_tensorwise_f32(lhs.numpy(), rhs.numpy(), sl, sr, offs.numpy(), acc_dtype=np.float64)
+    dl, dr, do = lhs.to(cuda), rhs.to(cuda), offs.to(cuda)
+    s1 = torch.tensor(sl, dtype=torch.float32, device=cuda)
+    s2 = torch.tensor(sr, dtype=torch.float32, device=cuda)
+    out = torch.full((G, om, on), float("nan"), dtype=torch.float32, device=cuda)
+    pkg.grouped_gemm_fp8_tensorwise_variable_k(dl, dr, s1, s2, do, out=out, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    _f32_parity(orc, got, ref, "fp32 out")
+    for g, L in enumerate(lens):
+        if L == 0:
+            assert np.all(got[g] == 0), g           # empty groups: exact zeros, NaN prefill overwritten
+    # the fp32 result agrees with the bf16 kernel to bf16 rounding
+    bf = pkg.grouped_gemm_fp8_tensorwise_variable_k(dl, dr, s1, s2, do)
+    assert torch.equal(out.to(torch.bfloat16).view(torch.int16), bf.view(torch.int16)) or \
+        float((out.to(torch.bfloat16).float() - bf.float()).abs().max()) <= float(bf.float().abs().max()) * 2 ** -7
+    # accumulate: C0 + result, twice in a row (C0 + 2 result)
+    c0 = torch.randn((G, om, on), generator=torch.Generator().manual_seed(5)).float()
+    acc = c0.to(cuda)
+    pkg.grouped_gemm_fp8_tensorwise_variable_k(dl, dr, s1, s2, do, out=acc, accumulate=True)
+    torch.cuda.synchronize()
+    got1 = acc.cpu().numpy()
+    _f32_parity(orc, got1 - c0.numpy(), ref, "accumulate once (minus C0)")
+    _f32_parity(orc, got1, c0.numpy() + ref, "accumulate once")
+    # the addition is the last rounding: C0 + fp32(result), exactly
+    np.testing.assert_array_equal(got1, (c0.numpy() + got).astype(np.float32))
+    pkg.grouped_gemm_fp8_tensorwise_variable_k(dl, dr, s1, s2, do, out=acc, accumulate=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(acc.cpu().numpy(), (got1 + got).astype(np.float32))
+
+
+def test_fp32_accumulate_full_size(pkg, orc, cuda):
+    """gate_up_wgrad with fp32 main-grad accumulation: C0 + result equals the fp32-output run plus
+    C0 exactly, on the whole 32 x 2880 x 5760 tensor."""
+    _say("fp32 accumulate full-size gate_up")
+    p = pkg.inputs.make_problem("gate_up_wgrad", seed=0, device=cuda)
+    sl = torch.tensor(p.lhs_scale, dtype=torch.float32, device=cuda)
+    sr = torch.tensor(p.rhs_scale, dtype=torch.float32, device=cuda)
+    f32 = pkg.grouped_gemm_fp8_tensorwise_variable_k(p.lhs, p.rhs, sl, sr, p.group_offs, out_dtype=torch.float32)
+    c0 = torch.randn(f32.shape, device=cuda, generator=torch.Generator(device=cuda).manual_seed(1)) * 1e-2
+    acc = c0.clone()
+    pkg.grouped_gemm_fp8_tensorwise_variable_k(p.lhs, p.rhs, sl, sr, p.group_offs, out=acc, accumulate=True)
+    bf = pkg.grouped_gemm_fp8_tensorwise_variable_k(p.lhs, p.rhs, sl, sr, p.group_offs)
+    torch.cuda.synchronize()
+    assert torch.equal(acc, c0 + f32)
+    assert torch.equal(f32.to(torch.bfloat16).view(torch.int16), bf.view(torch.int16))
