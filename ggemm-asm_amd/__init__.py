@@ -9,12 +9,14 @@ include/ggemm_persistent.h. Modules:
 * ``vark``       -- variable-K wgrad torch ops over the C ABI (mirror of the reference's oracle op)
 * ``persistent`` -- fwd/dgrad grouped GEMM torch op over the C ABI (same)
 * ``quant``      -- FP8 quantization producer (per-tensor and MX with group padding) over the C ABI
+* ``autograd``   -- the FP8 grouped linear layer (forward, dgrad, wgrad) as a torch autograd op
 * ``harness``    -- code-object launch paths mirroring the reference's hipModule harness
 * ``inputs``     -- seeded generators for the measured configurations
 * ``build``      -- in-tree hipcc build of the library and the drop-in code objects
 """
 from . import build, inputs  # noqa: F401
 from ._lib import GGemmError, launch_geometry, library_path, load as load_library  # noqa: F401
+from .autograd import GroupedLinearFP8, grouped_linear_fp8  # noqa: F401
 from .persistent import grouped_gemm_fp8_tensorwise  # noqa: F401
 from .quant import amax, padded_rows, quantize_fp8_tensorwise, quantize_mxfp8_grouped  # noqa: F401
 from .vark import (as_bf16_bits, grouped_gemm_fp8_tensorwise_variable_k,  # noqa: F401

@@ -1,0 +1,75 @@
+"""Autograd op for an FP8 grouped linear layer (MoE experts) built on the three kernels.
+
+``grouped_linear_fp8(x, w, group_offs)`` computes ``out[r] = x[r] @ w[g]^T`` for the rows ``r`` of
+group ``g`` (``offs[g] <= r < offs[g+1]``) in FP8 with per-tensor scales, and its backward. It is
+the caller the reference's kernels serve: the reference harness runs the three GEMMs of this layer
+separately (reference bench.py:153-193: gate_up_fwd / down_fwd ``x @ W^T``, down_dgrad /
+gate_up_dgrad ``dy @ W``, down_wgrad / gate_up_wgrad ``dW = x^T @ dy``), with the quantization and
+the autograd wiring left to the framework (Primus-Turbo, not vendored).
+
+* forward: x -> e4m3 and w -> e4m3 (per-tensor amax scales, the quantization producer);
+  ``out = grouped_gemm_fp8_tensorwise(qx, qw, sx, sw, offs)`` (persistent kernel), bf16.
+  Saved for backward: the fp8 tensors and their scales (1 byte per element, not the bf16 inputs).
+* backward: dy -> e5m2;
+  ``dx[r] = dy[r] @ w[g]`` — the persistent kernel with B = w ([G, N, K] read as [K_red=N, N_out=K],
+  the ``trans_b=False`` layout, via a transposed fp8 copy of qw); ``dW[g] = dy_g^T @ x_g`` — the
+  variable-K kernel computes ``x_g^T @ dy_g`` (the reference's wgrad orientation: e4m3 LHS, e5m2
+  RHS, C [G, K, N]) and the gradient is its transpose ([G, N, K], a view). With
+  ``main_grad=`` an fp32 [G, K, N] tensor, dW is accumulated into it instead (the fp32 epilogue,
+  beta = 1) and the returned weight gradient is None.
+There is no CPU path: the tensors must live on a gfx950 GPU.
+"""
+from __future__ import annotations
+
+import torch
+
+from .persistent import grouped_gemm_fp8_tensorwise
+from .quant import quantize_fp8_tensorwise
+from .vark import grouped_gemm_fp8_tensorwise_variable_k
+
+
+class GroupedLinearFP8(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w, group_offs, main_grad):
+        if x.dim() != 2 or w.dim() != 3 or x.shape[1] != w.shape[2]:
+            raise ValueError("x must be [M, K] and w [G, N, K]")
+        if w.shape[0] != group_offs.numel() - 1:
+            raise ValueError("w holds one weight per group")
+        qx, sx, _ = quantize_fp8_tensorwise(x.contiguous(), "e4m3")
+        qw, sw, _ = quantize_fp8_tensorwise(w.contiguous(), "e4m3")
+        out = grouped_gemm_fp8_tensorwise(qx, qw, sx, sw, group_offs)
+        ctx.save_for_backward(qx, sx, qw, sw, group_offs)
+        ctx.main_grad = main_grad
+        ctx.x_dtype, ctx.w_dtype = x.dtype, w.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, dy):
+        qx, sx, qw, sw, group_offs = ctx.saved_tensors
+        qdy, sdy, _ = quantize_fp8_tensorwise(dy.contiguous(), "e5m2")
+        dx = dw = None
+        if ctx.needs_input_grad[0]:
+            # dx[r] = dy[r] @ w[g]: B[g] = w[g] as [K_red = N, N_out = K]
+            dx = grouped_gemm_fp8_tensorwise(qdy, qw, sdy, sw, group_offs, trans_b=False)
+            dx = dx.to(ctx.x_dtype)
+        if ctx.needs_input_grad[1] or ctx.main_grad is not None:
+            if ctx.main_grad is not None:
+                grouped_gemm_fp8_tensorwise_variable_k(qx, qdy, sx, sdy, group_offs, out=ctx.main_grad,
+                                                       accumulate=True)
+            else:
+                dwt = grouped_gemm_fp8_tensorwise_variable_k(qx, qdy, sx, sdy, group_offs)   # [G, K, N]
+                dw = dwt.transpose(1, 2).to(ctx.w_dtype)
+        return dx, dw, None, None
+
+
+def grouped_linear_fp8(x: torch.Tensor, w: torch.Tensor, group_offs: torch.Tensor,
+                       main_grad: torch.Tensor | None = None) -> torch.Tensor:
+    """FP8 grouped linear layer: ``out[r] = x[r] @ w[g]^T`` for the rows of group g, bf16 out.
+
+    x: bf16 / fp32 [M, K] (rows grouped by expert); w: bf16 / fp32 [G, N, K]; group_offs: int64
+    [G+1] on the device. Backward gives dx [M, K] and dw [G, N, K]; with ``main_grad`` (fp32
+    [G, K, N], the wgrad kernel's orientation) the weight gradient is added into it instead."""
+    if main_grad is not None:
+        if main_grad.dtype != torch.float32 or tuple(main_grad.shape) != (w.shape[0], w.shape[2], w.shape[1]):
+            raise ValueError(f"main_grad must be fp32 [G, K, N] = {[w.shape[0], w.shape[2], w.shape[1]]}")
+    return GroupedLinearFP8.apply(x, w, group_offs, main_grad)

@@ -1,0 +1,97 @@
+"""GPU checks of the FP8 grouped linear autograd op (forward, dgrad, wgrad through the C ABI).
+
+Each output is compared with the oracle composition on the same fp8 bytes (the producer is
+deterministic, so the test re-quantizes the inputs to obtain them), to the bar's tolerance; and
+with an unquantized float64 reference of the layer, which only fp8 quantization separates from it
+(cosine >= 0.99) -- a check of the wiring (orientations, transposes, scales), not of the kernels.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def _bytes(t):
+    return t.detach().contiguous().view(torch.uint8).cpu().numpy()
+
+
+def _cos(a, b):
+    a, b = a.detach().double().ravel(), b.detach().double().ravel()
+    return float(a @ b / (a.norm() * b.norm() + 1e-300))
+
+
+@pytest.mark.parametrize("lens,K,N", [([100, 0, 257, 31, 64], 256, 384), ([600, 300], 2880 // 9, 640)])
+def test_grouped_linear_fp8_fwd_bwd(pkg, orc, orp, cuda, lens, K, N):
+    from ggemm_asm_amd.autograd import grouped_linear_fp8
+    g = torch.Generator().manual_seed(K + N)
+    G, M = len(lens), sum(lens)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16).to(cuda).requires_grad_(True)
+    w = (torch.randn((G, N, K), generator=g) * 0.05).to(torch.bfloat16).to(cuda).requires_grad_(True)
+    dy = (torch.randn((M, N), generator=g) * 1e-2).to(torch.bfloat16).to(cuda)
+    offs = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64, device=cuda)
+    _say(f"grouped linear fp8 lens={lens} K={K} N={N}")
+    out = grouped_linear_fp8(x, w, offs)
+    out.backward(dy)
+    torch.cuda.synchronize()
+    assert out.shape == (M, N) and x.grad.shape == x.shape and w.grad.shape == w.shape
+    o = offs.cpu().numpy()
+
+    # the same fp8 bytes the op used
+    qx, sx, _ = pkg.quantize_fp8_tensorwise(x.detach(), "e4m3")
+    qw, sw, _ = pkg.quantize_fp8_tensorwise(w.detach(), "e4m3")
+    qdy, sdy, _ = pkg.quantize_fp8_tensorwise(dy, "e5m2")
+    sx, sw, sdy = float(sx), float(sw), float(sdy)
+    ref_out = orp.grouped_fp8(_bytes(qx), _bytes(qw), sx, sw, o, "e4m3")
+    m = orc.compare(pkg.as_bf16_bits(out), ref_out)
+    _say(f"forward: {m}")
+    assert orc.parity_ok(m)
+    ref_dx = orp.grouped_fp8(_bytes(qdy), _bytes(qw), sdy, sw, o, "e5m2", trans_b=False)
+    m = orc.compare(pkg.as_bf16_bits(x.grad), ref_dx)
+    _say(f"dgrad: {m}")
+    assert orc.parity_ok(m)
+    ref_dwt = orc.vark_wgrad_tensorwise(_bytes(qx), _bytes(qdy), sx, sdy, o)          # [G, K, N]
+    m = orc.compare(pkg.as_bf16_bits(w.grad.transpose(1, 2)), ref_dwt, o)
+    _say(f"wgrad: {m}")
+    assert orc.parity_ok(m) and m["empty_zero"]
+
+    # wiring against the unquantized layer (float64 on the CPU)
+    xd, wd, dyd = x.detach().double().cpu(), w.detach().double().cpu(), dy.double().cpu()
+    out64 = torch.zeros((M, N), dtype=torch.float64)
+    dx64 = torch.zeros((M, K), dtype=torch.float64)
+    dw64 = torch.zeros((G, N, K), dtype=torch.float64)
+    for gi in range(G):
+        lo, hi = int(o[gi]), int(o[gi + 1])
+        out64[lo:hi] = xd[lo:hi] @ wd[gi].T
+        dx64[lo:hi] = dyd[lo:hi] @ wd[gi]
+        dw64[gi] = dyd[lo:hi].T @ xd[lo:hi]
+    c = (_cos(out.cpu(), out64), _cos(x.grad.cpu(), dx64), _cos(w.grad.cpu(), dw64))
+    _say(f"cosine to the unquantized layer (out, dx, dw): {c}")
+    assert min(c) >= 0.99
+
+
+def test_grouped_linear_fp8_main_grad(pkg, orc, cuda):
+    """With main_grad the weight gradient is accumulated into the fp32 [G, K, N] buffer."""
+    from ggemm_asm_amd.autograd import grouped_linear_fp8
+    lens, K, N = [64, 0, 200], 192, 384
+    g = torch.Generator().manual_seed(9)
+    G, M = len(lens), sum(lens)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16).to(cuda).requires_grad_(True)
+    w = (torch.randn((G, N, K), generator=g) * 0.05).to(torch.bfloat16).to(cuda).requires_grad_(True)
+    dy = (torch.randn((M, N), generator=g) * 1e-2).to(torch.bfloat16).to(cuda)
+    offs = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64, device=cuda)
+    c0 = torch.randn((G, K, N), generator=g).to(cuda)
+    mg = c0.clone()
+    _say("grouped linear fp8 main_grad")
+    grouped_linear_fp8(x, w, offs, main_grad=mg).backward(dy)
+    torch.cuda.synchronize()
+    assert w.grad is None and x.grad is not None
+    qx, sx, _ = pkg.quantize_fp8_tensorwise(x.detach(), "e4m3")
+    qdy, sdy, _ = pkg.quantize_fp8_tensorwise(dy, "e5m2")
+    f32 = pkg.grouped_gemm_fp8_tensorwise_variable_k(qx, qdy, sx, sdy, offs, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(mg, c0 + f32)

@@ -65,3 +65,13 @@ def test_python_quant_refuses_cpu_and_bad_dtypes(pkg):
     with pytest.raises(ValueError, match="e4m3"):
         pkg.quantize_fp8_tensorwise(x, "e3m4")
     assert pkg.padded_rows(100, 4) == 224 and pkg.padded_rows(0, 1) == 32
+
+
+def test_grouped_linear_refuses_cpu(pkg):
+    x = torch.zeros(8, 16, dtype=torch.bfloat16, requires_grad=True)
+    w = torch.zeros(2, 32, 16, dtype=torch.bfloat16, requires_grad=True)
+    offs = torch.tensor([0, 3, 8])
+    with pytest.raises(ValueError, match="gfx950 GPU only"):
+        pkg.grouped_linear_fp8(x, w, offs)
+    with pytest.raises(ValueError, match="main_grad"):
+        pkg.grouped_linear_fp8(x, w, offs, main_grad=torch.zeros(2, 32, 16))
