@@ -11,10 +11,16 @@ bench.py:742, launcher.cpp:76).
 forward / data-gradient grouped GEMM at the reference's other call sites instead (reference
 bench.py:153-180, inputs as in bench.py:205-223,238-247; FLOPs = 2 * M_total * K * N).
 
+``--config gate_up_layer`` measures one training step of the FP8 grouped linear layer at the
+gate_up shape (x bf16 [131072, 2880], w bf16 [32, 5760, 2880], dy bf16 [131072, 5760]): quantize
+x and w, forward GEMM, quantize dy, dgrad GEMM, wgrad GEMM accumulated into an fp32 main-grad;
+FLOPs = 3 * 2 * M * K * N.
+
 ``--config quant_tensorwise | quant_mx`` measures the FP8 quantization producer (HBM-bound, GB/s):
 x bf16 [131072, 2880] -> per-tensor e4m3 (amax pass + quantize pass: 2 + 2 + 1 bytes per
 element), and dy bf16 [131072, 5760] -> grouped MX e5m2 with 32-token padding (2 + 1 + 1/32
-bytes per element).
+bytes per element). ``--config quant_weight_transpose``: w bf16 [32, 5760, 2880] -> e4m3 q and its
+per-expert transpose q^T in one pass (2 + 2 + 1 + 1 bytes per element).
 
 Prints ONE JSON line with ms, TFLOPS, the MFMA roofline fraction and a CPU baseline (the
 build's numpy oracle on a bounded sample of the same workload, timed on this host's cores).
@@ -33,7 +39,8 @@ sys.path.insert(0, ROOT)
 FP8_DENSE_PEAK_TFLOPS = 5000.0    # MI355X dense FP8 MFMA peak
 REF_OPT_ASM_TFLOPS = 1237.0       # reference optimized ASM, gate_up_wgrad, C launcher (README.md:60)
 FWD_SITES = ("gate_up_fwd", "down_fwd", "down_dgrad", "gate_up_dgrad")
-QUANT_CONFIGS = ("quant_tensorwise", "quant_mx")
+QUANT_CONFIGS = ("quant_tensorwise", "quant_mx", "quant_weight_transpose")
+LAYER_CONFIGS = ("gate_up_layer",)
 HBM_PEAK_GBS = 8000.0             # MI355X HBM3E
 
 
@@ -48,7 +55,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="gate_up_wgrad",
                     choices=["gate_up_wgrad", "down_wgrad", "gate_up_zipf", "gate_up_mx", "constant", *FWD_SITES,
-                             *QUANT_CONFIGS])
+                             *QUANT_CONFIGS, *LAYER_CONFIGS])
     ap.add_argument("--mfma", default="k128", choices=["k128", "k32"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -191,6 +198,15 @@ def quant_workload(pkg, name, seed, dev):
         cfg = {"workload": name, "x": "bf16 [131072, 2880] (randn)", "out": "e4m3fn, fp32 scale + amax",
                "bytes_per_element": "2 (amax pass) + 2 (quantize pass) + 1 (fp8 out)"}
         nbytes = 5 * n
+    elif name == "quant_weight_transpose":
+        E, F, F2 = pkg.inputs.E_EXPERTS, pkg.inputs.F_DIM, pkg.inputs.F2_DIM
+        x = (torch.randn((E, F2, F), generator=gen, device=dev, dtype=torch.bfloat16) * 0.02)
+        n = x.numel()
+        run = lambda: pkg.quantize_fp8_tensorwise_transpose(x, "e4m3")
+        cfg = {"workload": name, "x": "bf16 weight [32, 5760, 2880] (randn * 0.02)",
+               "out": "e4m3fn q [32, 5760, 2880] + q^T [32, 2880, 5760], fp32 scale + amax",
+               "bytes_per_element": "2 (amax pass) + 2 (quantize pass) + 1 (q) + 1 (q^T)"}
+        nbytes = 6 * n
     else:
         lens = pkg.inputs.multinomial_lens(pkg.inputs.E_EXPERTS, pkg.inputs.M_TOTAL, torch.Generator().manual_seed(seed))
         offs = pkg.inputs.make_group_offs(lens).to(dev)
@@ -209,11 +225,13 @@ def quant_workload(pkg, name, seed, dev):
         import numpy as np
         from oracle import quant_oracle as orq
         rows, t_total, done = 4096, 0.0, 0
-        xc = x[:rows].float().cpu().numpy()
+        xc = x.reshape(-1, x.shape[-1])[:rows].float().cpu().numpy()
         while t_total < seconds:
             t0 = time.perf_counter()
             if name == "quant_tensorwise":
                 orq.quantize_tensorwise(xc, "e4m3")
+            elif name == "quant_weight_transpose":
+                np.ascontiguousarray(orq.quantize_tensorwise(xc, "e4m3")[0].T)
             else:
                 orq.quantize_mx_grouped(xc, np.array([0, rows], np.int64), "e5m2", out_rows=rows)
             t_total += time.perf_counter() - t0
@@ -239,6 +257,39 @@ def main_quant(args, pkg, dev):
     print(json.dumps(line), flush=True)
 
 
+def main_layer(args, pkg, dev):
+    import torch
+    from ggemm_asm_amd.autograd import grouped_linear_fp8
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    M, K, N, G = pkg.inputs.M_TOTAL, pkg.inputs.F_DIM, pkg.inputs.F2_DIM, pkg.inputs.E_EXPERTS
+    offs = pkg.inputs.make_group_offs(pkg.inputs.make_group_lens_reference()).to(dev)
+    x = torch.randn((M, K), generator=gen, device=dev, dtype=torch.bfloat16).requires_grad_(True)
+    w = (torch.randn((G, N, K), generator=gen, device=dev, dtype=torch.bfloat16) * 0.02).requires_grad_(True)
+    dy = torch.randn((M, N), generator=gen, device=dev, dtype=torch.bfloat16) * 1e-3
+    main_grad = torch.zeros((G, K, N), dtype=torch.float32, device=dev)
+
+    def step():
+        x.grad = None
+        out = grouped_linear_fp8(x, w, offs, main_grad=main_grad)
+        out.backward(dy)
+
+    ms = time_steps(step, args.steps, args.warmup)
+    flops = 3 * 2.0 * M * K * N
+    tflops = flops / (ms * 1e-3) / 1e12
+    line = {"metric": "ms + TFLOPS of one FP8 grouped linear training step (gate_up shape) on 1 MI355X",
+            "value": round(tflops, 2), "unit": "TFLOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "fp8", "data": "synthetic",
+            "config": {"workload": "gate_up_layer", "G": G, "M_total": M, "K": K, "N": N,
+                       "step": "quantize x, w (e4m3) + fwd GEMM + quantize dy (e5m2) + dgrad GEMM + wgrad GEMM "
+                               "accumulated into an fp32 main-grad",
+                       "inputs": "seed-42 exponential group sizes, randn bf16, in HBM"},
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP8_DENSE_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tflops / FP8_DENSE_PEAK_TFLOPS, 4), "traffic": None},
+            "cpu_baseline": None}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -254,6 +305,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.config in QUANT_CONFIGS:
         main_quant(args, pkg, dev)
+        return
+    if args.config in LAYER_CONFIGS:
+        main_layer(args, pkg, dev)
         return
     fwd = args.config in FWD_SITES
     if args.config == "constant":

@@ -7,12 +7,13 @@ separately (reference bench.py:153-193: gate_up_fwd / down_fwd ``x @ W^T``, down
 gate_up_dgrad ``dy @ W``, down_wgrad / gate_up_wgrad ``dW = x^T @ dy``), with the quantization and
 the autograd wiring left to the framework (Primus-Turbo, not vendored).
 
-* forward: x -> e4m3 and w -> e4m3 (per-tensor amax scales, the quantization producer);
+* forward: x -> e4m3 and w -> e4m3 (per-tensor amax scales, the quantization producer; when x
+  needs a gradient the weight pass also writes qw^T [G, K, N], the data-gradient GEMM's B);
   ``out = grouped_gemm_fp8_tensorwise(qx, qw, sx, sw, offs)`` (persistent kernel), bf16.
   Saved for backward: the fp8 tensors and their scales (1 byte per element, not the bf16 inputs).
 * backward: dy -> e5m2;
-  ``dx[r] = dy[r] @ w[g]`` — the persistent kernel with B = w ([G, N, K] read as [K_red=N, N_out=K],
-  the ``trans_b=False`` layout, via a transposed fp8 copy of qw); ``dW[g] = dy_g^T @ x_g`` — the
+  ``dx[r] = dy[r] @ w[g]`` — the persistent kernel with B = qw^T (K-major [G, N_out=K, K_red=N],
+  written by the forward's quantization pass); ``dW[g] = dy_g^T @ x_g`` — the
   variable-K kernel computes ``x_g^T @ dy_g`` (the reference's wgrad orientation: e4m3 LHS, e5m2
   RHS, C [G, K, N]) and the gradient is its transpose ([G, N, K], a view). With
   ``main_grad=`` an fp32 [G, K, N] tensor, dW is accumulated into it instead (the fp32 epilogue,
@@ -24,7 +25,7 @@ from __future__ import annotations
 import torch
 
 from .persistent import grouped_gemm_fp8_tensorwise
-from .quant import quantize_fp8_tensorwise
+from .quant import quantize_fp8_tensorwise, quantize_fp8_tensorwise_transpose
 from .vark import grouped_gemm_fp8_tensorwise_variable_k
 
 
@@ -36,21 +37,24 @@ class GroupedLinearFP8(torch.autograd.Function):
         if w.shape[0] != group_offs.numel() - 1:
             raise ValueError("w holds one weight per group")
         qx, sx, _ = quantize_fp8_tensorwise(x.contiguous(), "e4m3")
-        qw, sw, _ = quantize_fp8_tensorwise(w.contiguous(), "e4m3")
+        if ctx.needs_input_grad[0]:
+            qw, qwt, sw, _ = quantize_fp8_tensorwise_transpose(w.contiguous(), "e4m3")
+        else:
+            (qw, sw, _), qwt = quantize_fp8_tensorwise(w.contiguous(), "e4m3"), None
         out = grouped_gemm_fp8_tensorwise(qx, qw, sx, sw, group_offs)
-        ctx.save_for_backward(qx, sx, qw, sw, group_offs)
+        ctx.save_for_backward(qx, sx, qwt, sw, group_offs)
         ctx.main_grad = main_grad
         ctx.x_dtype, ctx.w_dtype = x.dtype, w.dtype
         return out
 
     @staticmethod
     def backward(ctx, dy):
-        qx, sx, qw, sw, group_offs = ctx.saved_tensors
+        qx, sx, qwt, sw, group_offs = ctx.saved_tensors
         qdy, sdy, _ = quantize_fp8_tensorwise(dy.contiguous(), "e5m2")
         dx = dw = None
         if ctx.needs_input_grad[0]:
-            # dx[r] = dy[r] @ w[g]: B[g] = w[g] as [K_red = N, N_out = K]
-            dx = grouped_gemm_fp8_tensorwise(qdy, qw, sdy, sw, group_offs, trans_b=False)
+            # dx[r] = dy[r] @ w[g]: B[g] = w[g]^T, [N_out = K, K_red = N] K-major
+            dx = grouped_gemm_fp8_tensorwise(qdy, qwt, sdy, sw, group_offs)
             dx = dx.to(ctx.x_dtype)
         if ctx.needs_input_grad[1] or ctx.main_grad is not None:
             if ctx.main_grad is not None:

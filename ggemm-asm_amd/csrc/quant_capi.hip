@@ -85,6 +85,41 @@ int ggemm_quant_fp8_tensorwise(const void* x, int32_t in_dtype, int64_t rows, in
   return (int)hipGetLastError();
 }
 
+int ggemm_quant_fp8_tensorwise_transpose(const void* x, int32_t in_dtype, int32_t batch, int32_t rows, int32_t cols,
+                                         int32_t out_format, void* out, void* out_t, float* scale_out,
+                                         float* amax_out, void* stream) {
+  if (!x || !out_t || !scale_out || !amax_out) return GGEMM_E_NULL;
+  if (in_dtype != GGEMM_IN_BF16 && in_dtype != GGEMM_IN_F32) return GGEMM_E_FORMAT;
+  if (out_format != GGEMM_FP8_E4M3 && out_format != GGEMM_FP8_E5M2) return GGEMM_E_FORMAT;
+  if (batch < 0 || rows <= 0 || cols <= 0 || rows % 16 || cols % 16) return GGEMM_E_SHAPE;
+  // tile index (batch * tiles per matrix) and per-matrix offsets fit the kernel's integer widths
+  const int64_t per = (int64_t)((rows + qt::kTT - 1) / qt::kTT) * ((cols + qt::kTT - 1) / qt::kTT);
+  if (per > 0x7fffffffLL) return GGEMM_E_SHAPE;
+  if (!aligned(x, 16) || !aligned(out_t, 16) || (out && !aligned(out, 16)) || !aligned(scale_out, 4) ||
+      !aligned(amax_out, 4))
+    return GGEMM_E_ALIGN;
+  int cus = 0;
+  int rc = device_cus(&cus);
+  if (rc) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t total_rows = (int64_t)batch * rows;
+  launch_amax(x, in_dtype, total_rows, cols, cols, amax_out, cus, s);
+  const bool f32 = in_dtype == GGEMM_IN_F32, e5 = out_format == GGEMM_FP8_E5M2;
+  auto k = f32 ? (e5 ? qt::quant_transpose_kernel<true, true> : qt::quant_transpose_kernel<true, false>)
+               : (e5 ? qt::quant_transpose_kernel<false, true> : qt::quant_transpose_kernel<false, false>);
+  const int64_t tiles = (int64_t)batch * per;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(k), qt::kThreads, 0) !=
+          hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  const int64_t cap = (int64_t)cus * per_cu;
+  const int grid = (int)(tiles < 1 ? 1 : (tiles < cap ? tiles : cap));
+  hipLaunchKernelGGL(k, dim3(grid), dim3(qt::kThreads), 0, s, x, batch, rows, cols, static_cast<uint8_t*>(out),
+                     static_cast<uint8_t*>(out_t), reinterpret_cast<const uint32_t*>(amax_out), scale_out);
+  return (int)hipGetLastError();
+}
+
 int ggemm_quant_mxfp8_grouped(const void* x, int32_t in_dtype, int64_t rows, int32_t cols, int64_t stride,
                               const int64_t* group_offs, int32_t G, int32_t out_format, void* out,
                               int64_t out_stride, int64_t out_rows, uint8_t* scales, int64_t scale_stride,

@@ -189,6 +189,60 @@ __global__ void __launch_bounds__(kThreads) quant_tensorwise_kernel(const void* 
   }
 }
 
+// ---------------------------------------------------------------------------------- tensorwise + transpose
+
+// Per-tensor quantization of a batch of [rows, cols] matrices (contiguous x [batch, rows, cols])
+// writing q^T [batch, cols, rows] and, when out != nullptr, q in x's layout: a weight [G, N, K]
+// quantized once for both the forward GEMM (B = w, K-major) and the data-gradient GEMM (B = w^T,
+// N-major). rows and cols are multiples of 16. Persistent grid over 64 x 64 tiles: thread t quantizes
+// 16 elements of tile row t / 4, writes its 16 bytes of q and deposits them in an LDS tile (row pitch
+// 68 bytes); after a barrier it gathers 16 bytes of tile column t / 4 for q^T. The 16-element
+// segments of a ragged edge tile are either wholly inside the matrix or wholly outside.
+constexpr int kTT = 64;                     // transpose tile edge (elements)
+constexpr int kTTPitch = kTT + 4;           // LDS row pitch in bytes
+
+template <bool kF32, bool kE5M2>
+__global__ void __launch_bounds__(kThreads) quant_transpose_kernel(const void* x, int batch, int rows, int cols,
+                                                                   uint8_t* out, uint8_t* out_t,
+                                                                   const uint32_t* amax_bits, float* scale_out) {
+  __shared__ uint8_t s_t[kTT * kTTPitch];
+  const float scale = tensor_scale<kE5M2>(*amax_bits);
+  if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
+  const int tid = threadIdx.x;
+  const int tr = tid >> 2, tc = 16 * (tid & 3);      // tile row (and q^T tile row) and first column
+  const int rt = (rows + kTT - 1) / kTT, ct = (cols + kTT - 1) / kTT;
+  const int per = rt * ct;
+  const int64_t tiles = (int64_t)batch * per;
+  for (int64_t it = blockIdx.x; it < tiles; it += gridDim.x) {
+    const int b = (int)(it / per);
+    const int rem = (int)(it - (int64_t)b * per);
+    const int r0 = (rem / ct) * kTT, c0 = (rem % ct) * kTT;
+    const int64_t base = (int64_t)b * rows * cols;
+    if (r0 + tr < rows && c0 + tc < cols) {
+      float v[16];
+      const int64_t row = (int64_t)b * rows + r0 + tr;
+      load8<kF32>(x, row, cols, (c0 + tc) / 8, v);
+      load8<kF32>(x, row, cols, (c0 + tc) / 8 + 1, v + 8);
+      uint32_t w[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        w[k] = pack4_fp8<kE5M2>(clamp_fmax<kE5M2>(v[4 * k] / scale), clamp_fmax<kE5M2>(v[4 * k + 1] / scale),
+                                clamp_fmax<kE5M2>(v[4 * k + 2] / scale), clamp_fmax<kE5M2>(v[4 * k + 3] / scale));
+      if (out) *(v4u*)(out + row * cols + c0 + tc) = v4u{w[0], w[1], w[2], w[3]};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) *(uint32_t*)(s_t + tr * kTTPitch + tc + 4 * k) = w[k];
+    }
+    __syncthreads();
+    if (c0 + tr < cols && r0 + tc < rows) {
+      uint32_t o[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[i >> 2] |= (uint32_t)s_t[(tc + i) * kTTPitch + tr] << (8 * (i & 3));
+      *(v4u*)(out_t + base + (int64_t)(c0 + tr) * rows + r0 + tc) = v4u{o[0], o[1], o[2], o[3]};
+    }
+    __syncthreads();
+  }
+}
+
 // ---------------------------------------------------------------------------------- MX, grouped
 
 // e8m0 exponent of a 32-row block column: floor(log2(fl32(amax / fmax))) clamped to [-127, 127],

@@ -85,6 +85,37 @@ def quantize_fp8_tensorwise(x: torch.Tensor, fmt: str = "e4m3"):
     return q, scale, am
 
 
+def quantize_fp8_tensorwise_transpose(x: torch.Tensor, fmt: str = "e4m3", keep: bool = True):
+    """Per-tensor FP8 quantization of a contiguous [B, R, C] (or [R, C]) tensor with a transposed
+    copy, in one pass. Returns ``(q, q_t, scale, amax)``: ``q`` is ``quantize_fp8_tensorwise(x)``'s
+    q (None when ``keep`` is False), ``q_t`` the contiguous [B, C, R] (or [C, R]) transpose of the
+    same bytes. For a weight [G, N, K], ``q`` is the forward GEMM's B and ``q_t`` the data-gradient
+    GEMM's (``dy @ w[g]`` reads ``w[g]^T`` K-major). R and C must be multiples of 16."""
+    _check(x, fmt)
+    if x.dim() not in (2, 3) or not x.is_contiguous():
+        raise ValueError("x must be a contiguous [B, R, C] or [R, C] tensor")
+    x3 = x if x.dim() == 3 else x.unsqueeze(0)
+    B, R, C = x3.shape
+    if R % 16 or C % 16:
+        raise ValueError(f"R and C must be multiples of 16, got {R} x {C}")
+    code, dt = _OUT[fmt]
+    q = torch.empty(x.shape, dtype=dt, device=x.device) if keep else None
+    q_t = torch.empty(x.shape[:-2] + (C, R), dtype=dt, device=x.device)
+    scale = torch.empty((), dtype=torch.float32, device=x.device)
+    am = torch.empty((), dtype=torch.float32, device=x.device)
+    if B == 0:                                   # nothing to read: a one-matrix placeholder pointer
+        xp = torch.empty((R, C), dtype=x.dtype, device=x.device).data_ptr()
+        tp = torch.empty((C, R), dtype=dt, device=x.device).data_ptr()
+        qp = tp if keep else None
+    else:
+        xp, tp, qp = x.data_ptr(), q_t.data_ptr(), (q.data_ptr() if keep else None)
+    with torch.cuda.device(x.device):
+        rc = _lib.load().ggemm_quant_fp8_tensorwise_transpose(
+            xp, _IN[x.dtype], B, R, C, code, qp, tp, scale.data_ptr(), am.data_ptr(), _stream(x.device))
+    _lib.check(rc, "ggemm_quant_fp8_tensorwise_transpose")
+    return q, q_t, scale, am
+
+
 def padded_rows(rows: int, G: int) -> int:
     """Output rows that ``quantize_mxfp8_grouped`` needs: every group padded to 32 rows fits."""
     return (rows + 31 * G + 31) // 32 * 32

@@ -50,6 +50,17 @@ int ggemm_quant_fp8_tensorwise(const void* x, int32_t in_dtype, int64_t rows, in
                                int32_t out_format, void* out, int64_t out_stride, float* scale_out,
                                float* amax_out, void* stream);
 
+/* Per-tensor quantization of a batch of matrices with a transposed copy: x is a contiguous
+ * [batch, rows, cols] (a weight [G, N, K]); amax_out and scale_out as in
+ * ggemm_quant_fp8_tensorwise over all batch*rows*cols elements; out_t[b, c, r] = q[b, r, c]
+ * (contiguous [batch, cols, rows]) and, when out is not NULL, out[b, r, c] = q[b, r, c] (contiguous
+ * [batch, rows, cols]); q's bytes are exactly ggemm_quant_fp8_tensorwise's. out_t is the data-gradient
+ * GEMM's K-major B (dx = dy @ w[g] reads w[g]^T), so one pass over the weight feeds both the forward
+ * and the data-gradient GEMM. rows and cols multiples of 16; x, out and out_t 16-byte aligned. */
+int ggemm_quant_fp8_tensorwise_transpose(const void* x, int32_t in_dtype, int32_t batch, int32_t rows, int32_t cols,
+                                         int32_t out_format, void* out, void* out_t, float* scale_out,
+                                         float* amax_out, void* stream);
+
 /* MX (OCP microscaling) quantization along the token axis with group-aligned padding, the input
  * of ggemm_vark_wgrad_mxfp8. x: [rows, cols] token-major; group_offs: int64 [G+1] (0-based,
  * non-decreasing, <= rows). Group g's rows are written to out rows padded_offs[g] ..

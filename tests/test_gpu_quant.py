@@ -112,6 +112,50 @@ def test_tensorwise_weight_3d_and_strided(pkg, orq, cuda):
     np.testing.assert_array_equal(_bytes(q), q_ref)
 
 
+TRANSPOSE_CASES = [((3, 80, 48), torch.bfloat16, "e4m3"), ((2, 64, 128), torch.float32, "e5m2"),
+                   ((1, 144, 208), torch.float32, "e4m3"), ((112, 16), torch.bfloat16, "e5m2"),
+                   ((5, 16, 1040), torch.bfloat16, "e4m3")]
+
+
+@pytest.mark.parametrize("shape,dtype,fmt", TRANSPOSE_CASES, ids=[f"t{i}" for i in range(len(TRANSPOSE_CASES))])
+def test_tensorwise_transpose_bit_exact(pkg, orq, cuda, shape, dtype, fmt):
+    """q and q^T against the oracle's bytes: ragged 64 x 64 edge tiles (80 = 64 + 16, 48 < 64,
+    1040 = 16 * 65), fp32 and bf16 input, a 2-D input, both formats."""
+    g = torch.Generator().manual_seed(sum(shape))
+    x = (torch.randn(shape, generator=g) * (1e-3 if fmt == "e5m2" else 1.0)).to(dtype)
+    _say(f"tensorwise transpose {fmt} {dtype} {shape}")
+    q, q_t, scale, am = pkg.quantize_fp8_tensorwise_transpose(x.to(cuda), fmt)
+    torch.cuda.synchronize()
+    R, C = shape[-2:]
+    q_ref, s_ref, a_ref = orq.quantize_tensorwise(x.float().numpy().reshape(-1, C), fmt)
+    q_ref = q_ref.reshape(shape)
+    assert float(am) == float(a_ref) and float(scale) == float(s_ref)
+    assert q.shape == x.shape and q_t.shape == shape[:-2] + (C, R) and q_t.dtype == TDT[fmt]
+    np.testing.assert_array_equal(_bytes(q), q_ref)
+    np.testing.assert_array_equal(_bytes(q_t), np.swapaxes(q_ref, -1, -2))
+    q2, q_t2, _, _ = pkg.quantize_fp8_tensorwise_transpose(x.to(cuda), fmt, keep=False)
+    assert q2 is None
+    np.testing.assert_array_equal(_bytes(q_t2), _bytes(q_t))
+
+
+def test_tensorwise_transpose_full_weight(pkg, cuda):
+    """The gate_up weight [32, 5760, 2880]: q equals the tensorwise kernel's bytes and q^T is
+    their transpose (byte for byte); an empty batch writes only amax and scale."""
+    g = torch.Generator(device=cuda).manual_seed(3)
+    w = (torch.randn((32, 5760, 2880), generator=g, device=cuda) * 0.02).to(torch.bfloat16)
+    _say("tensorwise transpose [32, 5760, 2880]")
+    q, q_t, scale, am = pkg.quantize_fp8_tensorwise_transpose(w, "e4m3")
+    q0, s0, a0 = pkg.quantize_fp8_tensorwise(w, "e4m3")
+    torch.cuda.synchronize()
+    assert float(am) == float(a0) and float(scale) == float(s0)
+    assert torch.equal(q.view(torch.uint8), q0.view(torch.uint8))
+    assert torch.equal(q_t.view(torch.uint8), q0.view(torch.uint8).transpose(1, 2).contiguous())
+    del w, q, q_t, q0
+    z = torch.zeros((0, 64, 32), dtype=torch.bfloat16, device=cuda)
+    q, q_t, scale, am = pkg.quantize_fp8_tensorwise_transpose(z, "e5m2")
+    assert q.shape == (0, 64, 32) and q_t.shape == (0, 32, 64) and float(scale) == 1.0 and float(am) == 0.0
+
+
 MX_CASES = [
     ([5, 0, 33, 64, 1, 100], 48),
     ([32, 32, 0, 31], 272),

@@ -56,6 +56,22 @@ def test_mx_validation(pkg, kw, rc):
     assert _mx(pkg.load_library(), **kw) == rc
 
 
+def _tt(lib, **kw):
+    a = dict(x=FAKE, dt=0, B=2, R=64, C=48, fmt=0, out=FAKE, out_t=FAKE, scale=FAKE, amax=FAKE)
+    a.update(kw)
+    return lib.ggemm_quant_fp8_tensorwise_transpose(a["x"], a["dt"], a["B"], a["R"], a["C"], a["fmt"], a["out"],
+                                                    a["out_t"], a["scale"], a["amax"], None)
+
+
+@pytest.mark.parametrize("kw,rc", [
+    (dict(x=0), -1), (dict(out_t=0), -1), (dict(scale=0), -1), (dict(amax=0), -1), (dict(dt=2), -8),
+    (dict(fmt=2), -8), (dict(B=-1), -2), (dict(R=0), -2), (dict(C=40), -2), (dict(R=72), -2),
+    (dict(x=FAKE + 8), -4), (dict(out=FAKE + 8), -4), (dict(out_t=FAKE + 8), -4), (dict(amax=FAKE + 2), -4),
+])
+def test_transpose_validation(pkg, kw, rc):
+    assert _tt(pkg.load_library(), **kw) == rc
+
+
 def test_python_quant_refuses_cpu_and_bad_dtypes(pkg):
     x = torch.zeros(8, 16)
     with pytest.raises(ValueError, match="gfx950 GPU only"):
@@ -65,6 +81,8 @@ def test_python_quant_refuses_cpu_and_bad_dtypes(pkg):
     with pytest.raises(ValueError, match="e4m3"):
         pkg.quantize_fp8_tensorwise(x, "e3m4")
     assert pkg.padded_rows(100, 4) == 224 and pkg.padded_rows(0, 1) == 32
+    with pytest.raises(ValueError, match="gfx950 GPU only"):
+        pkg.quantize_fp8_tensorwise_transpose(torch.zeros(2, 16, 32))
 
 
 def test_grouped_linear_refuses_cpu(pkg):
