@@ -69,10 +69,14 @@ constexpr int kXcds = 8;                                    // MI355X: 8 XCDs, 3
 constexpr int kXcdPairs = kXcds / 2;                        // schedule slices, two XCDs each
 constexpr int kMiscBytes = 16384;                           // group order, offsets, XCD bounds, e8m0
 // misc-region layout shared by both bodies: s_order int[1024] @0, s_kb int[1025] @4096 (the group
-// offsets), a flag @8196, s_bound int64[9] @8200; the MXFP8 scales follow at kScaleOffset.
+// offsets), a flag @8196, s_bound int64[9] @8200; the MXFP8 scales follow at kScaleOffset. The
+// schedule choice uses int[1024] tile weights @kScaleOffset and uint64[2 * 8] wave maxima after
+// them, in the prologue only (before the first stage's scales are loaded there).
 constexpr int kKbOffset = 4096, kFlagOffset = 8196, kBoundOffset = 8200, kScaleOffset = 8320;
+constexpr int kPredOffset = kScaleOffset + 4 * kMaxSortG;
 static_assert(kKbOffset + 4 * (kMaxSortG + 1) <= kFlagOffset && kBoundOffset + 8 * (kXcds + 1) <= kScaleOffset,
               "misc layout");
+static_assert(kPredOffset % 8 == 0 && kPredOffset + 8 * 2 * kWaves <= kMiscBytes, "misc layout");
 constexpr uint32_t kRsrcWord3 = 0x00020000u;                // raw buffer, 32-bit data format
 
 static_assert(kDmaLhs % kWaves == 0, "LHS LDS-DMA instructions split evenly over the waves");
@@ -359,18 +363,26 @@ struct Tile {
 // ----------------------------------------------------------------------------------- schedule
 
 // Persistent static schedule (no workspace exists in the launch contract). Groups are ranked by
-// descending token count (stable), so expensive tiles are dealt first. The hardware deals
-// workgroup ids round-robin over the 8 XCDs, each with its own L2. The size-sorted tile list is
-// cut into kXcdPairs contiguous slices of equal work (tile weight: its stage count + 1 for the
-// epilogue); the two XCDs x and x + kXcdPairs share slice x and take alternate rounds of 32
-// consecutive tiles, their 32 workgroups one tile each. The 32 CUs of an XCD then share L2
-// panels, and only four groups stream at a time, so their rows stay in the memory-side cache
-// (256 MB) for the partner XCD (one XCD per slice keeps eight groups, ~280 MB, in flight and
-// measured 1.5% slower). Tiles of a group are visited in bands of kBandN N-tiles, M-tile by
-// M-tile inside a band, so 32 consecutive tiles (one XCD's round) form an 8 x 4 block of the
-// group's grid.
+// descending token count (stable), so expensive tiles are dealt first; tile weight = its stage
+// count + kEpiW for the epilogue. The hardware deals workgroup ids round-robin over the 8 XCDs,
+// each with its own L2. Two static deals of the sorted tile list are candidates:
+//  * slices: the list is cut into kXcdPairs contiguous slices of equal work; the two XCDs x and
+//    x + kXcdPairs share slice x and take alternate rounds of 32 consecutive tiles, their 32
+//    workgroups one tile each. Only four groups stream at a time, so their rows stay in the
+//    memory-side cache (256 MB) for the partner XCD (one XCD per slice keeps eight groups, ~280 MB,
+//    in flight and measured 1.5% slower). Balanced when the groups are alike (uniform routing).
+//  * rounds: all workgroups take one tile per round of num_wg consecutive tiles (an XCD's 32
+//    workgroups a block of 32), in reverse order on odd rounds (boustrophedon), so the workgroup
+//    dealt the larger tile of one round is dealt the smaller of the next. With skewed routing the
+//    largest groups' tiles are few and heavy, and the slice holding them ends late; this deal
+//    spreads them over every workgroup.
+// Every workgroup computes each deal's heaviest per-workgroup weight (the same integers in every
+// workgroup) and takes the lighter deal, slices on a tie. Tiles of a group are visited in bands of
+// kBandN N-tiles, M-tile by M-tile inside a band, so 32 consecutive tiles (one XCD's round) form
+// an 8 x 4 block of the group's grid.
 struct Sched {
-  int t_begin, t_end, step;   // this workgroup's tiles: t_begin, t_begin + step, ... below t_end
+  int t_first, t_end;         // this workgroup's first tile, and the end of its tiles
+  int d0, d1;                 // its next tile is d0 further after an even round, d1 after an odd
   int n_tm, n_tn, tiles_per_group;
   bool sorted;                // groups ranked by size, their offsets held in LDS (s_kb)
   bool valid;                 // false: more tiles than 32-bit indices cover (C would need > 512 GiB)
@@ -387,10 +399,44 @@ __device__ __forceinline__ int group_size(const GG_LDS int* s_kb, int g) {
   return d > 0 ? d : 0;
 }
 
+// A workgroup's deal: tiles t_first, then alternately d0 and d1 further on, while below t_end.
+struct Deal {
+  int t_first, t_end, d0, d1;
+};
+
+// Total weight of a deal's tiles (weights per sorted group slot in s_w).
+__device__ __forceinline__ uint64_t deal_weight(const GG_LDS int* s_w, int tpg, const Deal& D) {
+  uint64_t sum = 0;
+  int t = D.t_first, d = D.d0, d_alt = D.d1;
+  if (t >= D.t_end) return 0;
+  int slot = t / tpg, slot_end = (slot + 1) * tpg;
+  while (t < D.t_end) {
+    while (t >= slot_end) {
+      ++slot;
+      slot_end += tpg;
+    }
+    sum += (uint64_t)s_w[slot];
+    t += d;
+    const int d_was = d;
+    d = d_alt;
+    d_alt = d_was;
+  }
+  return sum;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const uint64_t o = __shfl_xor(v, m, 64);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
 // Groups are sorted (and their offsets kept in LDS, so the tile loop reads them there instead of
 // issuing a global load whose wait would drain the prefetched stage) when G <= kMaxSortG and every
 // offset fits 31 bits; otherwise natural order with offsets read from memory.
-template <int kTN, int kK>
+template <int kTN, int kK, int kEpiW = 1>
 __device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_order, GG_LDS int* s_kb,
                                             GG_LDS int* s_flag, GG_LDS int64_t* s_bound) {
   Sched S;
@@ -429,7 +475,7 @@ __device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_ord
   S.tiles_per_group = S.n_tm * S.n_tn;
   const int64_t total = (int64_t)G * S.tiles_per_group;
   S.valid = total <= (1 << 30);
-  S.t_begin = S.t_end = S.step = 0;
+  S.t_first = S.t_end = S.d0 = S.d1 = 0;
   if (!S.valid) return S;
 
   const int pid = blockIdx.x;
@@ -438,18 +484,18 @@ __device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_ord
   const int xcds = spread ? kXcds : 1;
   const int n_xcd = spread ? kXcdPairs : 1;   // slices
   const int per_slice = xcds / n_xcd;
-  const int xcd = pid % xcds;
-  const int slice = xcd % n_xcd, part = xcd / n_xcd;
+  const int wgs_per_xcd = num_wg / xcds;
   const int tpg = S.tiles_per_group;
   if (tid == 0) {
     if (S.sorted && n_xcd > 1) {
       int64_t total_w = 0;
-      for (int sl = 0; sl < G; ++sl) total_w += (int64_t)tpg * (((int64_t)group_size(s_kb, s_order[sl]) + kK - 1) / kK + 1);
+      for (int sl = 0; sl < G; ++sl)
+        total_w += (int64_t)tpg * (((int64_t)group_size(s_kb, s_order[sl]) + kK - 1) / kK + kEpiW);
       int64_t acc_w = 0;
       int x = 1;
       s_bound[0] = 0;
       for (int sl = 0; sl < G && x < n_xcd; ++sl) {
-        const int64_t w = ((int64_t)group_size(s_kb, s_order[sl]) + kK - 1) / kK + 1;
+        const int64_t w = ((int64_t)group_size(s_kb, s_order[sl]) + kK - 1) / kK + kEpiW;
         const int64_t slot_w = w * tpg;
         while (x < n_xcd && acc_w + slot_w >= (total_w * x) / n_xcd) {
           const int64_t need = (total_w * x) / n_xcd - acc_w;
@@ -463,11 +509,58 @@ __device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_ord
       for (int x = 0; x <= n_xcd; ++x) s_bound[x] = total * x / n_xcd;
     }
   }
+  GG_LDS int* s_w = (GG_LDS int*)((GG_LDS uint8_t*)s_order + kScaleOffset);
+  GG_LDS uint64_t* s_pred = (GG_LDS uint64_t*)((GG_LDS uint8_t*)s_order + kPredOffset);
+  const bool choose = S.sorted && n_xcd > 1;
+  if (choose)
+    for (int sl = tid; sl < G; sl += kThreads) s_w[sl] = (group_size(s_kb, s_order[sl]) + kK - 1) / kK + kEpiW;
   __syncthreads();
-  const int wgs_per_xcd = num_wg / xcds;
-  S.t_begin = (int)s_bound[slice] + part * wgs_per_xcd + pid / xcds;
-  S.t_end = (int)s_bound[slice + 1];
-  S.step = per_slice * wgs_per_xcd;
+  // workgroup w's tiles under each deal; in the rounds deal, XCD x holds positions [32x, 32x + 32)
+  // of a round, and a round's position p is followed by the next round's num_wg - 1 - p
+  auto slice_deal = [&](int w) {
+    const int xcd = w % xcds, slice = xcd % n_xcd, part = xcd / n_xcd;
+    const int step = per_slice * wgs_per_xcd;
+    return Deal{(int)s_bound[slice] + part * wgs_per_xcd + w / xcds, (int)s_bound[slice + 1], step, step};
+  };
+  auto rounds_deal = [&](int w) {
+    const int p = (w % xcds) * wgs_per_xcd + w / xcds;
+    return Deal{p, (int)total, 2 * (num_wg - p) - 1, 2 * p + 1};
+  };
+  bool rounds = false;
+  if (choose) {
+    uint64_t mx[2] = {0, 0};
+    for (int w = tid; w < 2 * num_wg; w += kThreads) {
+      const int d = w >= num_wg, q = w - d * num_wg;
+      const uint64_t v = deal_weight(s_w, tpg, d ? rounds_deal(q) : slice_deal(q));
+      mx[d] = v > mx[d] ? v : mx[d];
+    }
+    const int wave = tid >> 6;
+    mx[0] = wave_max_u64(mx[0]);
+    mx[1] = wave_max_u64(mx[1]);
+    if ((tid & 63) == 0) {
+      s_pred[2 * wave] = mx[0];
+      s_pred[2 * wave + 1] = mx[1];
+    }
+    __syncthreads();
+    uint64_t m0 = 0, m1 = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      m0 = s_pred[2 * w] > m0 ? s_pred[2 * w] : m0;
+      m1 = s_pred[2 * w + 1] > m1 ? s_pred[2 * w + 1] : m1;
+    }
+    rounds = m1 < m0;
+    __syncthreads();   // s_w and s_pred alias the first stage's scale region
+  }
+  const Deal D = rounds ? rounds_deal(pid) : slice_deal(pid);
+  S.t_first = D.t_first;
+  S.t_end = D.t_end;
+  S.d0 = D.d0;
+  S.d1 = D.d1;
+  // workgroup-uniform: scalar registers in the tile loop
+  S.t_first = __builtin_amdgcn_readfirstlane(S.t_first);
+  S.t_end = __builtin_amdgcn_readfirstlane(S.t_end);
+  S.d0 = __builtin_amdgcn_readfirstlane(S.d0);
+  S.d1 = __builtin_amdgcn_readfirstlane(S.d1);
   return S;
 }
 
@@ -504,6 +597,9 @@ __device__ __forceinline__ Tile tile_at(const Sched& S, const VarKArgs& a, const
 // Output modes of the tensorwise kernel's epilogue: bf16 C (the reference contract), fp32 C, and
 // fp32 C accumulated in place (C += result: the main-grad accumulation of a training step).
 enum OutMode : int { kOutBF16 = 0, kOutF32 = 1, kOutF32Acc = 2 };
+// Schedule weight of a tile's epilogue in 128-token stages (bf16: 1): an fp32 C tile stores twice
+// the bytes, and the accumulating epilogue also waits for the old values to arrive.
+constexpr int kEpiWF32 = 2, kEpiWF32Acc = 4;
 
 template <bool kMX, bool kLegacyK32, int kTN, int kOut = kOutBF16>
 __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds) {
@@ -522,9 +618,9 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  const Sched S = make_sched<kTN, kKStep>(a, s_order, s_kb, s_flag, s_bound);
+  const Sched S = make_sched<kTN, kKStep, kOut == kOutBF16 ? 1 : kOut == kOutF32 ? kEpiWF32 : kEpiWF32Acc>(
+      a, s_order, s_kb, s_flag, s_bound);
   if (!S.valid) return;
-  const int t_begin = S.t_begin, t_end = S.t_end, wgs_per_xcd = S.step;
   auto tile_at_ = [&](int t) { return tile_at<kTN, kKStep>(S, a, s_order, s_kb, t); };
 
   float alpha = 1.0f;
@@ -566,12 +662,12 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
   // 16-byte store per accumulator block in fp32 mode (accumulate mode mixes loads in and is not
   // counted)
   constexpr int kEpiStores = kOut == kOutBF16 ? C::EpiStores : kMB * NB;
-  int t = t_begin;
+  int t = S.t_first, d = S.d0, d_alt = S.d1;   // d: distance to this workgroup's next tile
   Tile T;
-  if (t < t_end) T = tile_at_(t);
-  while (t < t_end) {
-    const int t_next = t + wgs_per_xcd;
-    const bool has_next = t_next < t_end;
+  if (t < S.t_end) T = tile_at_(t);
+  while (t < S.t_end) {
+    const int t_next = t + d;
+    const bool has_next = t_next < S.t_end;
     Tile N;
     if (has_next) N = tile_at_(t_next);
 
@@ -727,6 +823,9 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
       full_prev = T.m0 + kTileM <= a.OUT_M && T.n0 + kTN <= a.OUT_N;
     }
     t = t_next;
+    const int d_was = d;
+    d = d_alt;
+    d_alt = d_was;
     T = N;
   }
 }
@@ -860,11 +959,11 @@ __device__ __forceinline__ void vark_body32(const VarKArgs& a, GG_LDS uint8_t* l
   int cur = 0;              // LDS slot holding the next stage to compute
   bool prefetched = false;  // stage 0 of tile t was issued during the previous tile
   bool full_prev = false;   // the previous epilogue issued all kEpiStores stores in every wave
-  int t = S.t_begin;
+  int t = S.t_first, d = S.d0, d_alt = S.d1;   // d: distance to this workgroup's next tile
   Tile T;
   if (t < S.t_end) T = tile_at<kTN, kKStep>(S, a, s_order, s_kb, t);
   while (t < S.t_end) {
-    const int t_next = t + S.step;
+    const int t_next = t + d;
     const bool has_next = t_next < S.t_end;
     Tile N;
     if (has_next) N = tile_at<kTN, kKStep>(S, a, s_order, s_kb, t_next);
@@ -960,6 +1059,9 @@ __device__ __forceinline__ void vark_body32(const VarKArgs& a, GG_LDS uint8_t* l
     }
     full_prev = T.m0 + kTileM <= a.OUT_M && T.n0 + kTN <= a.OUT_N;
     t = t_next;
+    const int d_was = d;
+    d = d_alt;
+    d_alt = d_was;
     T = N;
   }
 }
