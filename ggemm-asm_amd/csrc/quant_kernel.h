@@ -194,11 +194,13 @@ __global__ void __launch_bounds__(kThreads) quant_tensorwise_kernel(const void* 
 // Per-tensor quantization of a batch of [rows, cols] matrices (contiguous x [batch, rows, cols])
 // writing q^T [batch, cols, rows] and, when out != nullptr, q in x's layout: a weight [G, N, K]
 // quantized once for both the forward GEMM (B = w, K-major) and the data-gradient GEMM (B = w^T,
-// N-major). rows and cols are multiples of 16. Persistent grid over 64 x 64 tiles: thread t quantizes
-// 16 elements of tile row t / 4, writes its 16 bytes of q and deposits them in an LDS tile (row pitch
-// 68 bytes); after a barrier it gathers 16 bytes of tile column t / 4 for q^T. The 16-element
-// segments of a ragged edge tile are either wholly inside the matrix or wholly outside.
-constexpr int kTT = 64;                     // transpose tile edge (elements)
+// N-major). rows and cols are multiples of 16. Persistent grid over 128 x 128 tiles, so every row
+// segment of q and of q^T a tile writes is one whole 128-byte line: thread t quantizes 16 elements
+// of each of the tile rows t / 8 + 32h (h = 0..3; all four loads issued before any is used), writes
+// its bytes of q and deposits them in an LDS tile (row pitch 132 bytes); after a barrier it gathers
+// 64 bytes of tile column t / 2 for q^T. The 16-element segments of a ragged edge tile are wholly
+// inside the matrix or outside.
+constexpr int kTT = 128;                    // transpose tile edge (elements)
 constexpr int kTTPitch = kTT + 4;           // LDS row pitch in bytes
 
 template <bool kF32, bool kE5M2>
@@ -209,7 +211,10 @@ __global__ void __launch_bounds__(kThreads) quant_transpose_kernel(const void* x
   const float scale = tensor_scale<kE5M2>(*amax_bits);
   if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
   const int tid = threadIdx.x;
-  const int tr = tid >> 2, tc = 16 * (tid & 3);      // tile row (and q^T tile row) and first column
+  const int tr = tid >> 3;                  // first tile row (then + 32, + 64, + 96)
+  const int tc = 16 * (tid & 7);            // first tile column of this thread's segments
+  const int qc = tid >> 1;                  // q^T: tile column (row of q^T)
+  const int qb = 64 * (tid & 1);            // q^T: first tile row of this thread's 64 bytes
   const int rt = (rows + kTT - 1) / kTT, ct = (cols + kTT - 1) / kTT;
   const int per = rt * ct;
   const int64_t tiles = (int64_t)batch * per;
@@ -217,27 +222,42 @@ __global__ void __launch_bounds__(kThreads) quant_transpose_kernel(const void* x
     const int b = (int)(it / per);
     const int rem = (int)(it - (int64_t)b * per);
     const int r0 = (rem / ct) * kTT, c0 = (rem % ct) * kTT;
-    const int64_t base = (int64_t)b * rows * cols;
-    if (r0 + tr < rows && c0 + tc < cols) {
-      float v[16];
-      const int64_t row = (int64_t)b * rows + r0 + tr;
-      load8<kF32>(x, row, cols, (c0 + tc) / 8, v);
-      load8<kF32>(x, row, cols, (c0 + tc) / 8 + 1, v + 8);
+    const bool col_in = c0 + tc < cols;
+    float v[4][16];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int64_t row = (int64_t)b * rows + r0 + tr + 32 * h;
+      if (col_in && r0 + tr + 32 * h < rows) {
+        load8<kF32>(x, row, cols, (c0 + tc) / 8, v[h]);
+        load8<kF32>(x, row, cols, (c0 + tc) / 8 + 1, v[h] + 8);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      if (!(col_in && r0 + tr + 32 * h < rows)) continue;
       uint32_t w[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        w[k] = pack4_fp8<kE5M2>(clamp_fmax<kE5M2>(v[4 * k] / scale), clamp_fmax<kE5M2>(v[4 * k + 1] / scale),
-                                clamp_fmax<kE5M2>(v[4 * k + 2] / scale), clamp_fmax<kE5M2>(v[4 * k + 3] / scale));
+        w[k] = pack4_fp8<kE5M2>(clamp_fmax<kE5M2>(v[h][4 * k] / scale), clamp_fmax<kE5M2>(v[h][4 * k + 1] / scale),
+                                clamp_fmax<kE5M2>(v[h][4 * k + 2] / scale),
+                                clamp_fmax<kE5M2>(v[h][4 * k + 3] / scale));
+      const int64_t row = (int64_t)b * rows + r0 + tr + 32 * h;
       if (out) *(v4u*)(out + row * cols + c0 + tc) = v4u{w[0], w[1], w[2], w[3]};
 #pragma unroll
-      for (int k = 0; k < 4; ++k) *(uint32_t*)(s_t + tr * kTTPitch + tc + 4 * k) = w[k];
+      for (int k = 0; k < 4; ++k) *(uint32_t*)(s_t + (tr + 32 * h) * kTTPitch + tc + 4 * k) = w[k];
     }
     __syncthreads();
-    if (c0 + tr < cols && r0 + tc < rows) {
-      uint32_t o[4] = {0u, 0u, 0u, 0u};
+    if (c0 + qc < cols) {
+      uint8_t* dst = out_t + (int64_t)b * rows * cols + (int64_t)(c0 + qc) * rows + r0 + qb;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) o[i >> 2] |= (uint32_t)s_t[(tc + i) * kTTPitch + tr] << (8 * (i & 3));
-      *(v4u*)(out_t + base + (int64_t)(c0 + tr) * rows + r0 + tc) = v4u{o[0], o[1], o[2], o[3]};
+      for (int h = 0; h < 4; ++h) {
+        if (r0 + qb + 16 * h >= rows) continue;
+        uint32_t o[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          o[i >> 2] |= (uint32_t)s_t[(qb + 16 * h + i) * kTTPitch + qc] << (8 * (i & 3));
+        *(v4u*)(dst + 16 * h) = v4u{o[0], o[1], o[2], o[3]};
+      }
     }
     __syncthreads();
   }

@@ -114,13 +114,15 @@ def test_tensorwise_weight_3d_and_strided(pkg, orq, cuda):
 
 TRANSPOSE_CASES = [((3, 80, 48), torch.bfloat16, "e4m3"), ((2, 64, 128), torch.float32, "e5m2"),
                    ((1, 144, 208), torch.float32, "e4m3"), ((112, 16), torch.bfloat16, "e5m2"),
-                   ((5, 16, 1040), torch.bfloat16, "e4m3")]
+                   ((5, 16, 1040), torch.bfloat16, "e4m3"), ((2, 272, 80), torch.bfloat16, "e5m2"),
+                   ((1, 208, 64), torch.float32, "e4m3")]
 
 
 @pytest.mark.parametrize("shape,dtype,fmt", TRANSPOSE_CASES, ids=[f"t{i}" for i in range(len(TRANSPOSE_CASES))])
 def test_tensorwise_transpose_bit_exact(pkg, orq, cuda, shape, dtype, fmt):
-    """q and q^T against the oracle's bytes: ragged 64 x 64 edge tiles (80 = 64 + 16, 48 < 64,
-    1040 = 16 * 65), fp32 and bf16 input, a 2-D input, both formats."""
+    """q and q^T against the oracle's bytes: ragged edges of the 128-row x 64-column tiles (rows
+    80, 144, 208 = 128 + 80, 272 = 2 * 128 + 16; columns 48, 80, 208, 1040 = 16 * 65), fp32 and bf16
+    input, a 2-D input, both formats."""
     g = torch.Generator().manual_seed(sum(shape))
     x = (torch.randn(shape, generator=g) * (1e-3 if fmt == "e5m2" else 1.0)).to(dtype)
     _say(f"tensorwise transpose {fmt} {dtype} {shape}")
