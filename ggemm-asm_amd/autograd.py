@@ -8,7 +8,8 @@ gate_up_dgrad ``dy @ W``, down_wgrad / gate_up_wgrad ``dW = x^T @ dy``), with th
 the autograd wiring left to the framework (Primus-Turbo, not vendored).
 
 * forward: x -> e4m3 and w -> e4m3 (per-tensor amax scales, the quantization producer; when x
-  needs a gradient the weight pass also writes qw^T [G, K, N], the data-gradient GEMM's B);
+  needs a gradient the weight pass also writes qw^T [G, K, N], the data-gradient GEMM's B); every
+  fp8 operand is written with rows starting on 128-byte lines (padded row stride);
   ``out = grouped_gemm_fp8_tensorwise(qx, qw, sx, sw, offs)`` (persistent kernel), bf16.
   Saved for backward: the fp8 tensors and their scales (1 byte per element, not the bf16 inputs).
 * backward: dy -> e5m2;
@@ -28,6 +29,8 @@ from .persistent import grouped_gemm_fp8_tensorwise
 from .quant import quantize_fp8_tensorwise, quantize_fp8_tensorwise_transpose
 from .vark import grouped_gemm_fp8_tensorwise_variable_k
 
+_LINE = 128   # bytes per cache line
+
 
 class GroupedLinearFP8(torch.autograd.Function):
     @staticmethod
@@ -36,11 +39,13 @@ class GroupedLinearFP8(torch.autograd.Function):
             raise ValueError("x must be [M, K] and w [G, N, K]")
         if w.shape[0] != group_offs.numel() - 1:
             raise ValueError("w holds one weight per group")
-        qx, sx, _ = quantize_fp8_tensorwise(x.contiguous(), "e4m3")
+        # operand rows start on 128-byte lines (padded buffers): K-major rows of K = 2880 bytes
+        # would otherwise straddle lines and cost the GEMMs 1.5 line requests per row segment
+        qx, sx, _ = quantize_fp8_tensorwise(x.contiguous(), "e4m3", row_align=_LINE)
         if ctx.needs_input_grad[0]:
-            qw, qwt, sw, _ = quantize_fp8_tensorwise_transpose(w.contiguous(), "e4m3")
+            qw, qwt, sw, _ = quantize_fp8_tensorwise_transpose(w.contiguous(), "e4m3", row_align=_LINE)
         else:
-            (qw, sw, _), qwt = quantize_fp8_tensorwise(w.contiguous(), "e4m3"), None
+            (qw, sw, _), qwt = quantize_fp8_tensorwise(w.contiguous(), "e4m3", row_align=_LINE), None
         out = grouped_gemm_fp8_tensorwise(qx, qw, sx, sw, group_offs)
         ctx.save_for_backward(qx, sx, qwt, sw, group_offs)
         ctx.main_grad = main_grad
@@ -50,7 +55,7 @@ class GroupedLinearFP8(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         qx, sx, qwt, sw, group_offs = ctx.saved_tensors
-        qdy, sdy, _ = quantize_fp8_tensorwise(dy.contiguous(), "e5m2")
+        qdy, sdy, _ = quantize_fp8_tensorwise(dy.contiguous(), "e5m2", row_align=_LINE)
         dx = dw = None
         if ctx.needs_input_grad[0]:
             # dx[r] = dy[r] @ w[g]: B[g] = w[g]^T, [N_out = K, K_red = N] K-major

@@ -86,12 +86,14 @@ int ggemm_quant_fp8_tensorwise(const void* x, int32_t in_dtype, int64_t rows, in
 }
 
 int ggemm_quant_fp8_tensorwise_transpose(const void* x, int32_t in_dtype, int32_t batch, int32_t rows, int32_t cols,
-                                         int32_t out_format, void* out, void* out_t, float* scale_out,
-                                         float* amax_out, void* stream) {
+                                         int32_t out_format, void* out, int64_t out_stride, void* out_t,
+                                         int64_t out_t_stride, float* scale_out, float* amax_out, void* stream) {
   if (!x || !out_t || !scale_out || !amax_out) return GGEMM_E_NULL;
   if (in_dtype != GGEMM_IN_BF16 && in_dtype != GGEMM_IN_F32) return GGEMM_E_FORMAT;
   if (out_format != GGEMM_FP8_E4M3 && out_format != GGEMM_FP8_E5M2) return GGEMM_E_FORMAT;
   if (batch < 0 || rows <= 0 || cols <= 0 || rows % 16 || cols % 16) return GGEMM_E_SHAPE;
+  if ((out && (out_stride < cols || out_stride % 16)) || out_t_stride < rows || out_t_stride % 16)
+    return GGEMM_E_STRIDE;
   // tile index (batch * tiles per matrix) and per-matrix offsets fit the kernel's integer widths
   const int64_t per = (int64_t)((rows + qt::kTT - 1) / qt::kTT) * ((cols + qt::kTT - 1) / qt::kTT);
   if (per > 0x7fffffffLL) return GGEMM_E_SHAPE;
@@ -116,7 +118,8 @@ int ggemm_quant_fp8_tensorwise_transpose(const void* x, int32_t in_dtype, int32_
   const int64_t cap = (int64_t)cus * per_cu;
   const int grid = (int)(tiles < 1 ? 1 : (tiles < cap ? tiles : cap));
   hipLaunchKernelGGL(k, dim3(grid), dim3(qt::kThreads), 0, s, x, batch, rows, cols, static_cast<uint8_t*>(out),
-                     static_cast<uint8_t*>(out_t), reinterpret_cast<const uint32_t*>(amax_out), scale_out);
+                     out_stride, static_cast<uint8_t*>(out_t), out_t_stride,
+                     reinterpret_cast<const uint32_t*>(amax_out), scale_out);
   return (int)hipGetLastError();
 }
 

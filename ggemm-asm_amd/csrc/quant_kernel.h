@@ -192,7 +192,8 @@ __global__ void __launch_bounds__(kThreads) quant_tensorwise_kernel(const void* 
 // ---------------------------------------------------------------------------------- tensorwise + transpose
 
 // Per-tensor quantization of a batch of [rows, cols] matrices (contiguous x [batch, rows, cols])
-// writing q^T [batch, cols, rows] and, when out != nullptr, q in x's layout: a weight [G, N, K]
+// writing q^T [batch, cols, rows] (row stride out_t_stride bytes) and, when out != nullptr, q
+// [batch, rows, cols] (row stride out_stride bytes; padded strides keep rows line-aligned): a weight [G, N, K]
 // quantized once for both the forward GEMM (B = w, K-major) and the data-gradient GEMM (B = w^T,
 // N-major). rows and cols are multiples of 16. Persistent grid over 128 x 128 tiles, so every row
 // segment of q and of q^T a tile writes is one whole 128-byte line: thread t quantizes 16 elements
@@ -205,8 +206,9 @@ constexpr int kTTPitch = kTT + 4;           // LDS row pitch in bytes
 
 template <bool kF32, bool kE5M2>
 __global__ void __launch_bounds__(kThreads) quant_transpose_kernel(const void* x, int batch, int rows, int cols,
-                                                                   uint8_t* out, uint8_t* out_t,
-                                                                   const uint32_t* amax_bits, float* scale_out) {
+                                                                   uint8_t* out, int64_t out_stride, uint8_t* out_t,
+                                                                   int64_t out_t_stride, const uint32_t* amax_bits,
+                                                                   float* scale_out) {
   __shared__ uint8_t s_t[kTT * kTTPitch];
   const float scale = tensor_scale<kE5M2>(*amax_bits);
   if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
@@ -242,13 +244,13 @@ __global__ void __launch_bounds__(kThreads) quant_transpose_kernel(const void* x
                                 clamp_fmax<kE5M2>(v[h][4 * k + 2] / scale),
                                 clamp_fmax<kE5M2>(v[h][4 * k + 3] / scale));
       const int64_t row = (int64_t)b * rows + r0 + tr + 32 * h;
-      if (out) *(v4u*)(out + row * cols + c0 + tc) = v4u{w[0], w[1], w[2], w[3]};
+      if (out) *(v4u*)(out + row * out_stride + c0 + tc) = v4u{w[0], w[1], w[2], w[3]};
 #pragma unroll
       for (int k = 0; k < 4; ++k) *(uint32_t*)(s_t + (tr + 32 * h) * kTTPitch + tc + 4 * k) = w[k];
     }
     __syncthreads();
     if (c0 + qc < cols) {
-      uint8_t* dst = out_t + (int64_t)b * rows * cols + (int64_t)(c0 + qc) * rows + r0 + qb;
+      uint8_t* dst = out_t + ((int64_t)b * cols + c0 + qc) * out_t_stride + r0 + qb;
 #pragma unroll
       for (int h = 0; h < 4; ++h) {
         if (r0 + qb + 16 * h >= rows) continue;

@@ -64,33 +64,50 @@ def amax(x: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def quantize_fp8_tensorwise(x: torch.Tensor, fmt: str = "e4m3"):
+def _padded_empty(shape, row_align, dt, device):
+    """An fp8 tensor of `shape` whose rows start on multiples of `row_align` bytes (a view of a
+    buffer with padded rows; None = contiguous)."""
+    last = shape[-1]
+    if not row_align or last % row_align == 0:
+        return torch.empty(shape, dtype=dt, device=device)
+    if row_align % 16:
+        raise ValueError("row_align must be a multiple of 16 bytes")
+    padded = (last + row_align - 1) // row_align * row_align
+    return torch.empty(tuple(shape[:-1]) + (padded,), dtype=dt, device=device)[..., :last]
+
+
+def quantize_fp8_tensorwise(x: torch.Tensor, fmt: str = "e4m3", row_align: int | None = None):
     """Per-tensor FP8 quantization. Returns ``(q, scale, amax)``: q has x's shape and dtype
     float8_e4m3fn / float8_e5m2, ``scale = amax / fmax`` (1 when amax == 0) and ``amax`` are
     single-element fp32 device tensors; ``q * scale`` dequantizes. The GEMM entry points take
-    ``scale`` as their per-tensor scale."""
+    ``scale`` as their per-tensor scale. ``row_align=128`` returns q as a view whose rows start on
+    128-byte lines (a padded buffer; the padding is not written): the persistent GEMM reads such
+    operands with one cache line per row segment instead of 1.5 (K = 2880: 6-9% faster)."""
     _check(x, fmt)
     x2 = _as_2d(x)
     code, dt = _OUT[fmt]
-    q = torch.empty(x.shape, dtype=dt, device=x.device)
-    q2 = q.view(-1, x.shape[-1])
+    q = _padded_empty(x.shape, row_align, dt, x.device)
+    # q's rows, contiguous or padded, are evenly strided over one buffer
+    q2 = q.as_strided((x2.shape[0], x.shape[-1]), (q.stride(-2), 1))
     scale = torch.empty((), dtype=torch.float32, device=x.device)
     am = torch.empty((), dtype=torch.float32, device=x.device)
     qp = q2 if q2.shape[0] > 0 else torch.empty((1, x.shape[-1]), dtype=dt, device=x.device)
     with torch.cuda.device(x.device):
         rc = _lib.load().ggemm_quant_fp8_tensorwise(
             _ptr(x2), _IN[x.dtype], x2.shape[0], x2.shape[1], max(x2.stride(0), x2.shape[1]), code, qp.data_ptr(),
-            qp.stride(0), scale.data_ptr(), am.data_ptr(), _stream(x.device))
+            max(qp.stride(0), qp.shape[1]), scale.data_ptr(), am.data_ptr(), _stream(x.device))
     _lib.check(rc, "ggemm_quant_fp8_tensorwise")
     return q, scale, am
 
 
-def quantize_fp8_tensorwise_transpose(x: torch.Tensor, fmt: str = "e4m3", keep: bool = True):
+def quantize_fp8_tensorwise_transpose(x: torch.Tensor, fmt: str = "e4m3", keep: bool = True,
+                                      row_align: int | None = None):
     """Per-tensor FP8 quantization of a contiguous [B, R, C] (or [R, C]) tensor with a transposed
     copy, in one pass. Returns ``(q, q_t, scale, amax)``: ``q`` is ``quantize_fp8_tensorwise(x)``'s
-    q (None when ``keep`` is False), ``q_t`` the contiguous [B, C, R] (or [C, R]) transpose of the
-    same bytes. For a weight [G, N, K], ``q`` is the forward GEMM's B and ``q_t`` the data-gradient
-    GEMM's (``dy @ w[g]`` reads ``w[g]^T`` K-major). R and C must be multiples of 16."""
+    q (None when ``keep`` is False), ``q_t`` the [B, C, R] (or [C, R]) transpose of the same bytes.
+    For a weight [G, N, K], ``q`` is the forward GEMM's B and ``q_t`` the data-gradient GEMM's
+    (``dy @ w[g]`` reads ``w[g]^T`` K-major). ``row_align`` as in ``quantize_fp8_tensorwise``, for
+    both outputs. R and C must be multiples of 16."""
     _check(x, fmt)
     if x.dim() not in (2, 3) or not x.is_contiguous():
         raise ValueError("x must be a contiguous [B, R, C] or [R, C] tensor")
@@ -99,19 +116,22 @@ def quantize_fp8_tensorwise_transpose(x: torch.Tensor, fmt: str = "e4m3", keep: 
     if R % 16 or C % 16:
         raise ValueError(f"R and C must be multiples of 16, got {R} x {C}")
     code, dt = _OUT[fmt]
-    q = torch.empty(x.shape, dtype=dt, device=x.device) if keep else None
-    q_t = torch.empty(x.shape[:-2] + (C, R), dtype=dt, device=x.device)
+    q = _padded_empty(x.shape, row_align, dt, x.device) if keep else None
+    q_t = _padded_empty(x.shape[:-2] + (C, R), row_align, dt, x.device)
     scale = torch.empty((), dtype=torch.float32, device=x.device)
     am = torch.empty((), dtype=torch.float32, device=x.device)
+    q_stride = q.stride(-2) if keep else C
+    t_stride = q_t.stride(-2)
     if B == 0:                                   # nothing to read: a one-matrix placeholder pointer
         xp = torch.empty((R, C), dtype=x.dtype, device=x.device).data_ptr()
-        tp = torch.empty((C, R), dtype=dt, device=x.device).data_ptr()
-        qp = tp if keep else None
+        tp = torch.empty((C, t_stride), dtype=dt, device=x.device).data_ptr()
+        qp = torch.empty((R, q_stride), dtype=dt, device=x.device).data_ptr() if keep else None
     else:
         xp, tp, qp = x.data_ptr(), q_t.data_ptr(), (q.data_ptr() if keep else None)
     with torch.cuda.device(x.device):
         rc = _lib.load().ggemm_quant_fp8_tensorwise_transpose(
-            xp, _IN[x.dtype], B, R, C, code, qp, tp, scale.data_ptr(), am.data_ptr(), _stream(x.device))
+            xp, _IN[x.dtype], B, R, C, code, qp, q_stride, tp, t_stride, scale.data_ptr(), am.data_ptr(),
+            _stream(x.device))
     _lib.check(rc, "ggemm_quant_fp8_tensorwise_transpose")
     return q, q_t, scale, am
 

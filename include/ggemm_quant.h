@@ -52,14 +52,17 @@ int ggemm_quant_fp8_tensorwise(const void* x, int32_t in_dtype, int64_t rows, in
 
 /* Per-tensor quantization of a batch of matrices with a transposed copy: x is a contiguous
  * [batch, rows, cols] (a weight [G, N, K]); amax_out and scale_out as in
- * ggemm_quant_fp8_tensorwise over all batch*rows*cols elements; out_t[b, c, r] = q[b, r, c]
- * (contiguous [batch, cols, rows]) and, when out is not NULL, out[b, r, c] = q[b, r, c] (contiguous
- * [batch, rows, cols]); q's bytes are exactly ggemm_quant_fp8_tensorwise's. out_t is the data-gradient
- * GEMM's K-major B (dx = dy @ w[g] reads w[g]^T), so one pass over the weight feeds both the forward
- * and the data-gradient GEMM. rows and cols multiples of 16; x, out and out_t 16-byte aligned. */
+ * ggemm_quant_fp8_tensorwise over all batch*rows*cols elements;
+ * out_t[(b * cols + c) * out_t_stride + r] = q[b, r, c] and, when out is not NULL,
+ * out[(b * rows + r) * out_stride + c] = q[b, r, c]; q's bytes are exactly
+ * ggemm_quant_fp8_tensorwise's. out_t is the data-gradient GEMM's K-major B (dx = dy @ w[g] reads
+ * w[g]^T), so one pass over the weight feeds both the forward and the data-gradient GEMM. Row
+ * strides (bytes) are multiples of 16, >= cols (out) and >= rows (out_t): a stride that is a
+ * multiple of 128 keeps every row on whole cache lines, which the GEMMs read faster. rows and cols
+ * multiples of 16; x, out and out_t 16-byte aligned. Padding bytes are not written. */
 int ggemm_quant_fp8_tensorwise_transpose(const void* x, int32_t in_dtype, int32_t batch, int32_t rows, int32_t cols,
-                                         int32_t out_format, void* out, void* out_t, float* scale_out,
-                                         float* amax_out, void* stream);
+                                         int32_t out_format, void* out, int64_t out_stride, void* out_t,
+                                         int64_t out_t_stride, float* scale_out, float* amax_out, void* stream);
 
 /* MX (OCP microscaling) quantization along the token axis with group-aligned padding, the input
  * of ggemm_vark_wgrad_mxfp8. x: [rows, cols] token-major; group_offs: int64 [G+1] (0-based,

@@ -140,6 +140,25 @@ def test_tensorwise_transpose_bit_exact(pkg, orq, cuda, shape, dtype, fmt):
     np.testing.assert_array_equal(_bytes(q_t2), _bytes(q_t))
 
 
+@pytest.mark.parametrize("shape", [(2, 80, 2880), (96, 160)])
+def test_row_aligned_outputs(pkg, orq, cuda, shape):
+    """row_align=128: the same bytes in views whose rows start on 128-byte lines (padded buffers),
+    for the plain and the transposing producer."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(shape, generator=g).to(torch.bfloat16)
+    _say(f"row-aligned producer {shape}")
+    q_ref, _, _ = orq.quantize_tensorwise(x.float().numpy().reshape(-1, shape[-1]), "e4m3")
+    q_ref = q_ref.reshape(shape)
+    q, scale, _ = pkg.quantize_fp8_tensorwise(x.to(cuda), "e4m3", row_align=128)
+    assert q.shape == x.shape and q.stride(-2) % 128 == 0 and q.stride(-2) >= shape[-1]
+    np.testing.assert_array_equal(_bytes(q), q_ref)
+    qa, qt, _, _ = pkg.quantize_fp8_tensorwise_transpose(x.to(cuda), "e4m3", row_align=128)
+    torch.cuda.synchronize()
+    assert qa.stride(-2) % 128 == 0 and qt.stride(-2) % 128 == 0
+    np.testing.assert_array_equal(_bytes(qa), q_ref)
+    np.testing.assert_array_equal(_bytes(qt), np.swapaxes(q_ref, -1, -2))
+
+
 def test_tensorwise_transpose_full_weight(pkg, cuda):
     """The gate_up weight [32, 5760, 2880]: q equals the tensorwise kernel's bytes and q^T is
     their transpose (byte for byte); an empty batch writes only amax and scale."""

@@ -57,16 +57,17 @@ def test_mx_validation(pkg, kw, rc):
 
 
 def _tt(lib, **kw):
-    a = dict(x=FAKE, dt=0, B=2, R=64, C=48, fmt=0, out=FAKE, out_t=FAKE, scale=FAKE, amax=FAKE)
+    a = dict(x=FAKE, dt=0, B=2, R=64, C=48, fmt=0, out=FAKE, os=48, out_t=FAKE, ts=64, scale=FAKE, amax=FAKE)
     a.update(kw)
     return lib.ggemm_quant_fp8_tensorwise_transpose(a["x"], a["dt"], a["B"], a["R"], a["C"], a["fmt"], a["out"],
-                                                    a["out_t"], a["scale"], a["amax"], None)
+                                                    a["os"], a["out_t"], a["ts"], a["scale"], a["amax"], None)
 
 
 @pytest.mark.parametrize("kw,rc", [
     (dict(x=0), -1), (dict(out_t=0), -1), (dict(scale=0), -1), (dict(amax=0), -1), (dict(dt=2), -8),
     (dict(fmt=2), -8), (dict(B=-1), -2), (dict(R=0), -2), (dict(C=40), -2), (dict(R=72), -2),
     (dict(x=FAKE + 8), -4), (dict(out=FAKE + 8), -4), (dict(out_t=FAKE + 8), -4), (dict(amax=FAKE + 2), -4),
+    (dict(os=32), -3), (dict(os=56), -3), (dict(ts=48), -3), (dict(ts=72), -3),
 ])
 def test_transpose_validation(pkg, kw, rc):
     assert _tt(pkg.load_library(), **kw) == rc
