@@ -309,7 +309,18 @@ __device__ __forceinline__ void static_for(F&& f) {
 // e8m0 scale registers of the 64-token pipeline hold one block scale per byte (op_sel picks it).
 constexpr int kUnitScales = 0x7f7f7f7f;   // 2^0 in every byte
 
-template <bool kLegacyK32>
+// Compile-time loop: f(std::integral_constant<int, i>) for i = I .. N-1.
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+// kSelA / kSelB: the byte of the 32-bit scale operand that holds this MFMA's e8m0 scale (block
+// scales are kept four to a register).
+template <bool kLegacyK32, int kSelA = 0, int kSelB = 0>
 __device__ __forceinline__ v4f mfma(const v8i& a_rhs, const v8i& b_lhs, v4f acc, int sc_a, int sc_b) {
   if constexpr (kLegacyK32) {
     // four K=32 steps; the per-lane token pairing of A and B is identical, so the sum matches
@@ -322,7 +333,7 @@ __device__ __forceinline__ v4f mfma(const v8i& a_rhs, const v8i& b_lhs, v4f acc,
     return acc;
   } else {
     // A (RHS) is e5m2 -> format 1 (bf8); B (LHS) is e4m3 -> format 0 (fp8)
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a_rhs, b_lhs, acc, 1, 0, 0, sc_a, 0, sc_b);
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a_rhs, b_lhs, acc, 1, 0, kSelA, sc_a, kSelB, sc_b);
   }
 }
 
@@ -703,17 +714,22 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
       // v_mfma_f32_16x16x128_f8f6f4 (one instruction instead of a scale-load prefix plus the MFMA),
       // which computes exactly what scale 127 (2^0) does (measured bit-identical); a CPU test
       // checks the code object holds the unscaled form.
-      int sc_n[NB], sc_m[kMB];
+      // MX: this lane's e8m0 scales of the stage, four blocks to a register (byte j % 4 of
+      // sc_n[j / 4] for n-block j, likewise for the m-blocks), which keeps the 192 x 384 tile's
+      // registers within the two-waves-per-SIMD budget.
+      int sc_n[(NB + 3) / 4], sc_m[(kMB + 3) / 4];
 #pragma unroll
-      for (int j = 0; j < NB; ++j) sc_n[j] = 0;
+      for (int k = 0; k < (NB + 3) / 4; ++k) sc_n[k] = 0;
 #pragma unroll
-      for (int i = 0; i < kMB; ++i) sc_m[i] = 0;
+      for (int k = 0; k < (kMB + 3) / 4; ++k) sc_m[k] = 0;
       if constexpr (kMX) {
         const GG_LDS uint8_t* ss = scales + cur * C::ScaleStage;
 #pragma unroll
-        for (int j = 0; j < NB; ++j) sc_n[j] = ss[4 * kTileM + q * kTN + wn * C::WaveN + j * 16 + s16];
+        for (int j = 0; j < NB; ++j)
+          sc_n[j >> 2] |= (int)ss[4 * kTileM + q * kTN + wn * C::WaveN + j * 16 + s16] << (8 * (j & 3));
 #pragma unroll
-        for (int i = 0; i < kMB; ++i) sc_m[i] = ss[q * kTileM + wm * kWaveM + i * 16 + s16];
+        for (int i = 0; i < kMB; ++i)
+          sc_m[i >> 2] |= (int)ss[q * kTileM + wm * kWaveM + i * 16 + s16] << (8 * (i & 3));
       }
 
       v8i bn[NB], am[2];
@@ -722,12 +738,15 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
 #pragma unroll
       for (int j = 1; j < NB; ++j) bn[j] = read_operand<kTN>(sr + off_n[j]);
       am[1] = read_operand<kTileM>(sl + off_m[1]);
-#pragma unroll
-      for (int i = 0; i < kMB; ++i) {
-#pragma unroll
-        for (int j = 0; j < NB; ++j) acc[i][j] = mfma<kLegacyK32>(bn[j], am[i & 1], acc[i][j], sc_n[j], sc_m[i]);
-        if (i + 2 < kMB) am[i & 1] = read_operand<kTileM>(sl + off_m[i + 2]);
-      }
+      static_for<0, kMB>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        static_for<0, NB>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          acc[i][j] = mfma<kLegacyK32, kMX ? j % 4 : 0, kMX ? i % 4 : 0>(bn[j], am[i & 1], acc[i][j], sc_n[j / 4],
+                                                                         sc_m[i / 4]);
+        });
+        if constexpr (i + 2 < kMB) am[i & 1] = read_operand<kTileM>(sl + off_m[i + 2]);
+      });
       pin_stage_schedule<4 * (NB + 2) + (kMX ? NB + kMB : 0), NB * (kLegacyK32 ? 4 : 1)>();
       cur ^= 1;
     }
