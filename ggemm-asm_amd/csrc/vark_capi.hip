@@ -166,7 +166,7 @@ void ggemm_vark_launch_geometry(int32_t out_n, int32_t* block_threads, int32_t* 
   if (block_threads) *block_threads = ggemm::kThreads;
   if (dynamic_lds) *dynamic_lds = ggemm::kDynLdsBytes;
   if (tile_m) *tile_m = ggemm::kTileM;
-  if (tile_n) *tile_n = (out_n > 0 && out_n % 384 == 0) ? 384 : 320;
+  if (tile_n) *tile_n = (out_n > 0 && ggemm::wide_tiles(out_n, false)) ? 384 : 320;
   if (k_step) *k_step = ggemm::kKStep;
 }
 

@@ -79,6 +79,15 @@ static_assert(kKbOffset + 4 * (kMaxSortG + 1) <= kFlagOffset && kBoundOffset + 8
 static_assert(kPredOffset % 8 == 0 && kPredOffset + 8 * 2 * kWaves <= kMiscBytes, "misc layout");
 constexpr uint32_t kRsrcWord3 = 0x00020000u;                // raw buffer, 32-bit data format
 
+// Tile width: 384 when OUT_N is a multiple of 384, and for the per-tensor kernel also when at least
+// four tiles fit and the last is at least half full (OUT_N = 2880: 7.5 tiles of 384). A row's
+// 384-byte RHS window is 3 cache lines, as is a 320-byte one, so the wider tile asks the L1 -> L2
+// request stream, the kernel's limiter, for 13% fewer lines per token at OUT_N = 2880 against 6.7%
+// of masked MFMA work (down_wgrad 1.029 -> 1.000 ms, same-box A/B, bit-identical output).
+__host__ __device__ constexpr bool wide_tiles(int out_n, bool mx) {
+  return out_n % 384 == 0 || (!mx && out_n >= 4 * 384 && out_n % 384 >= 192);
+}
+
 static_assert(kDmaLhs % kWaves == 0, "LHS LDS-DMA instructions split evenly over the waves");
 
 // Per-tile-width configuration. Bank slot of (token t, physical chunk c) is (t * W/16 + c) mod 16;
@@ -1098,7 +1107,7 @@ __device__ __forceinline__ void vark_entry(const VarKArgs& a, GG_LDS uint8_t* dy
   GG_LDS uint8_t* st = (GG_LDS uint8_t*)static_lds;
   // The stage slots span both arrays: the dynamic window must follow the static one directly.
   if (lds_u32(dyn) != lds_u32(st) + (uint32_t)kStaticLdsBytes) return;
-  if (a.OUT_N % 384 == 0) {
+  if (wide_tiles(a.OUT_N, kMX)) {
     if constexpr (kMX)
       vark_body32(a, st);
     else

@@ -38,7 +38,9 @@ def test_abi_version_and_geometry(pkg):
     assert lib.ggemm_vark_abi_version() == ver
     assert pkg.launch_geometry(5760) == {"block_threads": 512, "dynamic_lds": 65536, "tile_m": 192,
                                          "tile_n": 384, "k_step": 128}
-    assert pkg.launch_geometry(2880)["tile_n"] == 320
+    # 384-wide tiles also when at least four fit and the last is at least half full
+    assert pkg.launch_geometry(2880)["tile_n"] == 384
+    assert [pkg.launch_geometry(n)["tile_n"] for n in (640, 1344, 1536 + 191, 1536 + 192, 320)] == [320, 320, 320, 384, 320]
 
 
 def _offs(vals):

@@ -127,6 +127,8 @@ RAGGED = [
     ([300, 0, 645], 400, 1152),
     ([31] * 4 + [0] * 2, 16, 384),
     ([2000, 96], 576, 768),
+    # OUT_N = 4.5 x 384: 384-wide tiles with a half-full last one (as at OUT_N = 2880)
+    ([255, 0, 129, 640], 208, 1728),
 ]
 
 

@@ -16,7 +16,9 @@ TILE_M, K_STEP, XCDS, PAIRS = 192, 128, 8, 4
 
 
 def _tn(OUT_N):
-    return 384 if OUT_N % 384 == 0 else 320
+    """wide_tiles() of the per-tensor kernel: 384 for multiples of 384, and when at least four
+    tiles fit and the last is at least half full."""
+    return 384 if OUT_N % 384 == 0 or (OUT_N >= 4 * 384 and OUT_N % 384 >= 192) else 320
 
 
 def _schedule(lens, OUT_M, OUT_N, num_wg, epi_w=1):
