@@ -334,10 +334,17 @@ def _oracle_groups(pkg, orc, p, out, groups):
         assert orc.parity_ok(m), (p.name, g, m)
 
 
-@pytest.mark.parametrize("name", ["down_wgrad", "gate_up_wgrad", "gate_up_zipf", "gate_up_mx"])
+@pytest.mark.parametrize("name", ["down_wgrad", "gate_up_wgrad", "gate_up_zipf", "gate_up_mx", "gate_up_reference_lens"])
 def test_full_size_config(pkg, orc, cuda, name):
+    """Full-size configurations. gate_up_zipf and gate_up_reference_lens (the reference's seed-42
+    exponential group sizes) are skewed enough that the kernel deals its tiles in boustrophedon
+    rounds rather than XCD-pair slices (tests/test_vark_schedule_host.py models the choice)."""
     _say(f"full-size {name}")
-    p = pkg.inputs.make_problem(name, seed=0, device=cuda)
+    if name == "gate_up_reference_lens":
+        p = pkg.inputs.make_problem("gate_up_wgrad", seed=0, device=cuda,
+                                    lens=pkg.inputs.make_group_lens_reference())
+    else:
+        p = pkg.inputs.make_problem(name, seed=0, device=cuda)
     if p.is_mx:
         run = lambda: pkg.grouped_gemm_mxfp8_variable_k(p.lhs, p.rhs, p.lhs_mx, p.rhs_mx, p.group_offs)
     else:
@@ -410,11 +417,14 @@ def test_fp32_output_and_accumulate(pkg, orc, cuda, lens, om, on):
     np.testing.assert_array_equal(acc.cpu().numpy(), (got1 + got).astype(np.float32))
 
 
-def test_fp32_accumulate_full_size(pkg, orc, cuda):
+@pytest.mark.parametrize("routing", ["multinomial", "reference_lens"])
+def test_fp32_accumulate_full_size(pkg, orc, cuda, routing):
     """gate_up_wgrad with fp32 main-grad accumulation: C0 + result equals the fp32-output run plus
-    C0 exactly, on the whole 32 x 2880 x 5760 tensor."""
-    _say("fp32 accumulate full-size gate_up")
-    p = pkg.inputs.make_problem("gate_up_wgrad", seed=0, device=cuda)
+    C0 exactly, on the whole 32 x 2880 x 5760 tensor, with uniform routing (the slices deal) and
+    with the reference's exponential group sizes (the rounds deal, as in the layer step)."""
+    _say(f"fp32 accumulate full-size gate_up ({routing})")
+    lens = pkg.inputs.make_group_lens_reference() if routing == "reference_lens" else None
+    p = pkg.inputs.make_problem("gate_up_wgrad", seed=0, device=cuda, lens=lens)
     sl = torch.tensor(p.lhs_scale, dtype=torch.float32, device=cuda)
     sr = torch.tensor(p.rhs_scale, dtype=torch.float32, device=cuda)
     f32 = pkg.grouped_gemm_fp8_tensorwise_variable_k(p.lhs, p.rhs, sl, sr, p.group_offs, out_dtype=torch.float32)
