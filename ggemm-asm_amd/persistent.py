@@ -45,7 +45,8 @@ def grouped_gemm_fp8_tensorwise(a: torch.Tensor, b: torch.Tensor, a_scale: torch
 
     a: float8_e4m3fn (forward) or float8_e5m2 (data gradient) [M_total, K]; b: float8_e4m3fn
     [G, N, K] (``trans_b=True``, the layout of every reference call site) or [G, K, N]
-    (``trans_b=False``: transposed into a contiguous [G, N, K] copy first); scales: single-element
+    (``trans_b=False``: transposed into a contiguous [G, N, K] copy first -- a weight quantized with
+    ``quantize_fp8_tensorwise_transpose`` already has that layout); scales: single-element
     fp32 tensors on the device; group_offs: int64 [G+1]. Rows outside ``[0, offs[G])`` of a new
     ``out`` are left unwritten. ``validate=True`` checks group_offs on the host first (a sync).
     """
