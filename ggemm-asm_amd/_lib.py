@@ -23,6 +23,7 @@ EXPORTS = (
 
 PERSISTENT_EXPORTS = (
     "ggemm_persistent_fp8",
+    "ggemm_persistent_transpose_u8",
 )
 
 QUANT_EXPORTS = (
@@ -81,6 +82,9 @@ def load():
     lib.ggemm_vark_launch_geometry.restype = None
     lib.ggemm_persistent_fp8.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 9 + [ctypes.c_int64, vp]
     lib.ggemm_persistent_fp8.restype = ctypes.c_int
+    lib.ggemm_persistent_transpose_u8.argtypes = [vp, i32, i32, i32, ctypes.c_int64, ctypes.c_int64, vp,
+                                                  ctypes.c_int64, ctypes.c_int64, vp]
+    lib.ggemm_persistent_transpose_u8.restype = ctypes.c_int
     i64 = ctypes.c_int64
     lib.ggemm_quant_amax.argtypes = [vp, i32, i64, i32, i64, vp, vp]
     lib.ggemm_quant_amax.restype = ctypes.c_int

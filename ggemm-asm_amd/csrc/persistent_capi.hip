@@ -39,6 +39,54 @@ int validate(const void* a, const void* b, const void* out, const void* as, cons
   return GGEMM_OK;
 }
 
+// Byte transpose over 128 x 128 tiles (ggemm_persistent_transpose_u8): thread t loads 16 bytes of
+// each of the tile rows t / 8 + 32h (h = 0..3, all loads issued first) into an LDS tile (row pitch
+// 132 bytes), and after a barrier gathers 64 bytes of tile column t / 2, so four threads write one
+// whole 128-byte line of the destination row. Edge tiles hold whole 16-byte segments.
+constexpr int kXT = 128, kXPitch = kXT + 4, kXThreads = 256;
+typedef unsigned int xv4u __attribute__((ext_vector_type(4)));
+
+__global__ void __launch_bounds__(kXThreads) transpose_u8_kernel(const uint8_t* src, int batch, int rows, int cols,
+                                                                 int64_t sb, int64_t sr, uint8_t* dst, int64_t db,
+                                                                 int64_t dr) {
+  __shared__ uint8_t s_t[kXT * kXPitch];
+  const int tid = threadIdx.x;
+  const int tr = tid >> 3, tc = 16 * (tid & 7);
+  const int qc = tid >> 1, qb = 64 * (tid & 1);
+  const int rt = (rows + kXT - 1) / kXT, ct = (cols + kXT - 1) / kXT;
+  const int per = rt * ct;
+  const int64_t tiles = (int64_t)batch * per;
+  for (int64_t it = blockIdx.x; it < tiles; it += gridDim.x) {
+    const int b = (int)(it / per);
+    const int rem = (int)(it - (int64_t)b * per);
+    const int r0 = (rem / ct) * kXT, c0 = (rem % ct) * kXT;
+    xv4u v[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+      if (c0 + tc < cols && r0 + tr + 32 * h < rows)
+        v[h] = *(const xv4u*)(src + b * sb + (int64_t)(r0 + tr + 32 * h) * sr + c0 + tc);
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+      if (c0 + tc < cols && r0 + tr + 32 * h < rows) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) *(uint32_t*)(s_t + (tr + 32 * h) * kXPitch + tc + 4 * k) = v[h][k];
+      }
+    __syncthreads();
+    if (c0 + qc < cols) {
+      uint8_t* out = dst + b * db + (int64_t)(c0 + qc) * dr + r0 + qb;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        if (r0 + qb + 16 * h >= rows) continue;
+        uint32_t o[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[i >> 2] |= (uint32_t)s_t[(qb + 16 * h + i) * kXPitch + qc] << (8 * (i & 3));
+        *(xv4u*)(out + 16 * h) = xv4u{o[0], o[1], o[2], o[3]};
+      }
+    }
+    __syncthreads();
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -59,6 +107,36 @@ int ggemm_persistent_fp8(const void* a, const void* b, void* out, const float* a
   hipLaunchKernelGGL(kern, dim3(cus), dim3(ggemm::kThreads), ggemm::kDynLdsBytes, (hipStream_t)stream,
                      (const uint8_t*)a, (const uint8_t*)b, (uint16_t*)out, a_scale, b_scale, group_offs, G, N, K,
                      stride_am, stride_bg, stride_bn, stride_cm, stride_cn, (void*)nullptr, (void*)nullptr);
+  return (int)hipGetLastError();
+}
+
+int ggemm_persistent_transpose_u8(const void* src, int32_t batch, int32_t rows, int32_t cols, int64_t src_bstride,
+                                  int64_t src_rstride, void* dst, int64_t dst_bstride, int64_t dst_rstride,
+                                  void* stream) {
+  if (!src || !dst) return GGEMM_E_NULL;
+  if (batch < 0 || rows <= 0 || cols <= 0 || rows % 16 || cols % 16) return GGEMM_E_SHAPE;
+  if (src_rstride < cols || dst_rstride < rows || src_rstride % 16 || dst_rstride % 16 || src_bstride % 16 ||
+      dst_bstride % 16)
+    return GGEMM_E_STRIDE;
+  if (batch > 1 && (src_bstride < (int64_t)rows * src_rstride || dst_bstride < (int64_t)cols * dst_rstride))
+    return GGEMM_E_STRIDE;
+  const int64_t per = (int64_t)((rows + kXT - 1) / kXT) * ((cols + kXT - 1) / kXT);
+  if ((int64_t)batch * per > 0x7fffffffLL) return GGEMM_E_SHAPE;
+  if (!aligned(src, 16) || !aligned(dst, 16)) return GGEMM_E_ALIGN;
+  if (batch == 0) return GGEMM_OK;
+  int cus = 0;
+  const int rc = device_cus(&cus);
+  if (rc) return rc;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(transpose_u8_kernel),
+                                                   kXThreads, 0) != hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  const int64_t tiles = (int64_t)batch * per, cap = (int64_t)cus * per_cu;
+  const int grid = (int)(tiles < cap ? tiles : cap);
+  hipLaunchKernelGGL(transpose_u8_kernel, dim3(grid), dim3(kXThreads), 0, (hipStream_t)stream,
+                     static_cast<const uint8_t*>(src), batch, rows, cols, src_bstride, src_rstride,
+                     static_cast<uint8_t*>(dst), dst_bstride, dst_rstride);
   return (int)hipGetLastError();
 }
 

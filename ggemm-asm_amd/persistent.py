@@ -38,6 +38,24 @@ def _a_format(a: torch.Tensor, a_format: str | None) -> int:
     return _FORMATS[a.dtype]
 
 
+def transpose_b(b: torch.Tensor) -> torch.Tensor:
+    """[G, K, N] fp8 (N contiguous) -> a new contiguous [G, N, K] tensor of the same bytes, through
+    ``ggemm_persistent_transpose_u8`` (K and N multiples of 16)."""
+    if b.dim() != 3 or b.stride(2) != 1:
+        raise ValueError("b must be a 3-D [G, K, N] tensor contiguous along N")
+    G, K, N = b.shape
+    if b.device.type != "cuda":
+        raise ValueError(f"the byte transpose runs on a gfx950 GPU only (b is on {b.device})")
+    out = torch.empty((G, N, K), dtype=b.dtype, device=b.device)
+    if G == 0 or K == 0 or N == 0:
+        return out
+    with torch.cuda.device(b.device):
+        rc = _lib.load().ggemm_persistent_transpose_u8(b.data_ptr(), G, K, N, b.stride(0), b.stride(1), out.data_ptr(),
+                                                       out.stride(0), out.stride(1), _stream(b.device))
+    _lib.check(rc, "ggemm_persistent_transpose_u8")
+    return out
+
+
 def grouped_gemm_fp8_tensorwise(a: torch.Tensor, b: torch.Tensor, a_scale: torch.Tensor, b_scale: torch.Tensor,
                                 group_offs: torch.Tensor, trans_b: bool = True, out: torch.Tensor | None = None,
                                 *, a_format: str | None = None, validate: bool = False) -> torch.Tensor:
@@ -45,8 +63,9 @@ def grouped_gemm_fp8_tensorwise(a: torch.Tensor, b: torch.Tensor, a_scale: torch
 
     a: float8_e4m3fn (forward) or float8_e5m2 (data gradient) [M_total, K]; b: float8_e4m3fn
     [G, N, K] (``trans_b=True``, the layout of every reference call site) or [G, K, N]
-    (``trans_b=False``: transposed into a contiguous [G, N, K] copy first -- a weight quantized with
-    ``quantize_fp8_tensorwise_transpose`` already has that layout); scales: single-element
+    (``trans_b=False``: transposed into a contiguous [G, N, K] copy first by the library's byte
+    transpose -- a weight quantized with ``quantize_fp8_tensorwise_transpose`` already has that
+    layout); scales: single-element
     fp32 tensors on the device; group_offs: int64 [G+1]. Rows outside ``[0, offs[G])`` of a new
     ``out`` are left unwritten. ``validate=True`` checks group_offs on the host first (a sync).
     """
@@ -71,7 +90,7 @@ def grouped_gemm_fp8_tensorwise(a: torch.Tensor, b: torch.Tensor, a_scale: torch
         if s.dtype != torch.float32 or s.numel() != 1:
             raise ValueError("scales must be single-element fp32 tensors")
     if not trans_b:
-        b = b.transpose(1, 2).contiguous()
+        b = transpose_b(b)
     M_total, K = a.shape
     N = b.shape[1]
     if b.shape[2] != K:

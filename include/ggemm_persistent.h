@@ -49,6 +49,18 @@ int ggemm_persistent_fp8(const void* a, const void* b, void* out, const float* a
                          int32_t stride_bg, int32_t stride_bn, int32_t stride_cm, int32_t stride_cn,
                          int32_t a_format, int64_t M_total, void* stream);
 
+/* Byte transpose of a batch of matrices: dst[b][c][r] = src[b][r][c] for b < batch, r < rows,
+ * c < cols, element addresses src + b*src_bstride + r*src_rstride + c and dst + b*dst_bstride +
+ * c*dst_rstride + r. For a B given [G, K, N] (N contiguous; the trans_b=False layout of the
+ * Primus-Turbo API, reference bench.py:258-269) it writes the [G, N, K] operand ggemm_persistent_fp8
+ * reads. No counterpart kernel in the reference, whose call sites all pass trans_b=True. rows and
+ * cols multiples of 16; strides multiples of 16 with src_rstride >= cols, dst_rstride >= rows,
+ * src_bstride >= rows*src_rstride, dst_bstride >= cols*dst_rstride; src and dst 16-byte aligned,
+ * not overlapping. */
+int ggemm_persistent_transpose_u8(const void* src, int32_t batch, int32_t rows, int32_t cols, int64_t src_bstride,
+                                  int64_t src_rstride, void* dst, int64_t dst_bstride, int64_t dst_rstride,
+                                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -144,6 +144,24 @@ def test_rows_outside_groups_untouched_and_empty_input(pkg, orc, orp, cuda):
     assert e.shape == (0, N)
 
 
+@pytest.mark.parametrize("shape", [(3, 80, 48), (1, 144, 2880), (2, 272, 1040), (32, 2880, 5760)])
+def test_transpose_u8(pkg, cuda, shape):
+    """The byte transpose behind trans_b=False: every byte, ragged 128 x 128 edge tiles (rows 80,
+    144, 272 = 2 * 128 + 16; columns 48, 1040 = 16 * 65), a strided source view, and the full
+    gate_up weight in the [G, K, N] layout."""
+    G, K, N = shape
+    _say(f"byte transpose {shape}")
+    g = torch.Generator(device=cuda).manual_seed(K + N)
+    b = torch.randint(0, 256, (G, K, N), generator=g, device=cuda, dtype=torch.uint8)
+    got = pkg.persistent.transpose_b(b.view(torch.float8_e4m3fn))
+    assert got.shape == (G, N, K) and got.is_contiguous() and got.dtype == torch.float8_e4m3fn
+    assert torch.equal(got.view(torch.uint8), b.transpose(1, 2).contiguous())
+    if G * K * N < 1 << 24:
+        wide = torch.randint(0, 256, (G, K + 5, N + 32), generator=g, device=cuda, dtype=torch.uint8)
+        view = wide[:, 2:2 + K, 16:16 + N]
+        assert torch.equal(pkg.persistent.transpose_b(view).view(torch.uint8), view.transpose(1, 2).contiguous())
+
+
 def test_trans_b_false_and_strided_views(pkg, orc, orp, cuda):
     lens, K, N = [130, 70, 0, 260], 320, 400
     p = pkg.inputs.make_fwd_problem("down_dgrad", seed=4, lens=lens, K=K, N=N)

@@ -275,6 +275,24 @@ def test_persistent_validation_rejects(pkg, kw, rc):
         assert got == rc
 
 
+def _xt(lib, **kw):
+    a = dict(src=FAKE, B=2, R=64, C=48, sb=64 * 48, sr=48, dst=FAKE, db=48 * 64, dr=64)
+    a.update(kw)
+    return lib.ggemm_persistent_transpose_u8(a["src"], a["B"], a["R"], a["C"], a["sb"], a["sr"], a["dst"], a["db"],
+                                             a["dr"], None)
+
+
+@pytest.mark.parametrize("kw,rc", [
+    (dict(src=0), -1), (dict(dst=0), -1), (dict(B=-1), -2), (dict(R=0), -2), (dict(C=40, sr=48), -2),
+    (dict(R=72, sb=72 * 48, dr=80), -2), (dict(sr=32), -3), (dict(sr=56), -3), (dict(dr=48), -3),
+    (dict(sb=64 * 48 - 16), -3), (dict(db=48 * 64 - 16), -3), (dict(src=FAKE + 8), -4), (dict(dst=FAKE + 4), -4),
+    # an empty batch passes validation and returns before any device call
+    (dict(B=0), 0),
+])
+def test_transpose_u8_validation(pkg, kw, rc):
+    assert _xt(pkg.load_library(), **kw) == rc
+
+
 def test_persistent_header_symbols_exported(pkg):
     text = open(os.path.join(ROOT, "include", "ggemm_persistent.h")).read()
     names = sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(ggemm_persistent_\w+)\s*\(", text, re.M)))
