@@ -251,9 +251,10 @@ def test_code_object_kernelparams_and_kernarg_buffer(pkg, cuda, out_n):
         torch.cuda.synchronize()
         assert torch.equal(out1.view(torch.int16), ref.view(torch.int16))
         assert torch.equal(out2.view(torch.int16), ref.view(torch.int16))
-        # fewer workgroups than CUs (any grid size must be correct): 24 spreads over the 8 XCDs
-        # (XCD-pair slices), 20 and 1 do not (one slice)
-        for grid in (24, 20, 1):
+        # any grid size must be correct: 24 spreads over the 8 XCDs (two deals to choose from), 20
+        # and 1 do not (one slice); 1032 and 600 exceed the 512 threads that weigh the deals (each
+        # thread weighs several workgroups), 1032 spreading over the XCDs, 600 not
+        for grid in (24, 20, 1, 1032, 600):
             out3 = torch.zeros_like(ref)
             harness.launch_variable_k_kernel(func, dl, dr, out3, s1, s2, do, len(lens), 384, out_n, grid)
             torch.cuda.synchronize()
