@@ -315,18 +315,6 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// e8m0 scale registers of the 64-token pipeline hold one block scale per byte (op_sel picks it).
-constexpr int kUnitScales = 0x7f7f7f7f;   // 2^0 in every byte
-
-// Compile-time loop: f(std::integral_constant<int, i>) for i = I .. N-1.
-template <int I, int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>{});
-    static_for<I + 1, N>(f);
-  }
-}
-
 // kSelA / kSelB: the byte of the 32-bit scale operand that holds this MFMA's e8m0 scale (block
 // scales are kept four to a register).
 template <bool kLegacyK32, int kSelA = 0, int kSelB = 0>
@@ -747,9 +735,9 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
 #pragma unroll
       for (int j = 1; j < NB; ++j) bn[j] = read_operand<kTN>(sr + off_n[j]);
       am[1] = read_operand<kTileM>(sl + off_m[1]);
-      static_for<0, kMB>([&](auto ic) {
+      static_for<kMB>([&](auto ic) {
         constexpr int i = decltype(ic)::value;
-        static_for<0, NB>([&](auto jc) {
+        static_for<NB>([&](auto jc) {
           constexpr int j = decltype(jc)::value;
           acc[i][j] = mfma<kLegacyK32, kMX ? j % 4 : 0, kMX ? i % 4 : 0>(bn[j], am[i & 1], acc[i][j], sc_n[j / 4],
                                                                          sc_m[i / 4]);
