@@ -1,0 +1,93 @@
+"""HIP graph capture of the library's launches (torch.cuda.CUDAGraph over the C ABI).
+
+One training step's kernels at a small shape -- the producer (per-tensor, with the transposed weight
+copy, line-aligned rows), the persistent forward and data-gradient GEMMs, the variable-K wgrad in
+bf16 and accumulating into an fp32 main-grad -- are captured once and replayed several times, with
+eager work of the same library between replays (as a training loop would interleave it), and every
+replay is compared with the eager results bit for bit, including a replay after the inputs were
+overwritten in place (the graph reads its inputs, not copies). The launches record no memset: the
+amax result is cleared by a fill kernel.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+
+
+def _bits(t):
+    return t.view(torch.int16) if t.element_size() == 2 else t.view(torch.int32)
+
+
+def test_graph_replays_match_eager(pkg, cuda):
+    lens, K, N = [300, 0, 517, 64], 256, 384
+    G, M = len(lens), sum(lens)
+    g = torch.Generator(device=cuda).manual_seed(0)
+
+    def inputs():
+        x = torch.randn((M, K), generator=g, device=cuda).to(torch.bfloat16)
+        w = (torch.randn((G, N, K), generator=g, device=cuda) * 0.05).to(torch.bfloat16)
+        dy = (torch.randn((M, N), generator=g, device=cuda) * 1e-2).to(torch.bfloat16)
+        return x, w, dy
+
+    x, w, dy = inputs()
+    offs = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64, device=cuda)
+    main_grad = torch.zeros((G, K, N), dtype=torch.float32, device=cuda)
+
+    def step():
+        qx, sx, _ = pkg.quantize_fp8_tensorwise(x, "e4m3", row_align=128)
+        qw, qwt, sw, _ = pkg.quantize_fp8_tensorwise_transpose(w, "e4m3", row_align=128)
+        out = pkg.grouped_gemm_fp8_tensorwise(qx, qw, sx, sw, offs)
+        qdy, sdy, _ = pkg.quantize_fp8_tensorwise(dy, "e5m2", row_align=128)
+        dx = pkg.grouped_gemm_fp8_tensorwise(qdy, qwt, sdy, sw, offs)
+        dw = pkg.grouped_gemm_fp8_tensorwise_variable_k(qx, qdy, sx, sdy, offs)
+        pkg.grouped_gemm_fp8_tensorwise_variable_k(qx, qdy, sx, sdy, offs, out=main_grad, accumulate=True)
+        return out, dx, dw
+
+    _say("graph capture: eager reference")
+    ref = [t.clone() for t in step()]
+    dw32 = main_grad.clone()                     # one accumulation of the fp32 wgrad into zeros
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    _say("graph capture: capturing")
+    with torch.cuda.graph(graph):
+        static = step()
+    torch.cuda.synchronize()
+
+    for r in range(3):
+        _say(f"graph replay {r}")
+        pkg.quantize_fp8_tensorwise(dy, "e4m3")            # eager work of the library between replays
+        for t in static:
+            t.fill_(float("nan"))
+        main_grad.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("out", "dx", "dw"), static, ref):
+            assert torch.equal(_bits(a), _bits(b)), (r, name)
+        assert torch.equal(main_grad, dw32), r
+
+    _say("graph replay with new inputs")
+    x2, w2, dy2 = inputs()
+    x.copy_(x2)
+    w.copy_(w2)
+    dy.copy_(dy2)
+    main_grad.zero_()
+    want = [t.clone() for t in step()]
+    want32 = main_grad.clone()
+    main_grad.zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    for name, a, b in zip(("out", "dx", "dw"), static, want):
+        assert torch.equal(_bits(a), _bits(b)), name
+    assert torch.equal(main_grad, want32)
+    assert not torch.equal(_bits(want[2]), _bits(ref[2]))   # the inputs did change the result
