@@ -79,8 +79,9 @@ static_assert(kKbOffset + 4 * (kMaxSortG + 1) <= kFlagOffset && kBoundOffset + 8
 static_assert(kPredOffset % 8 == 0 && kPredOffset + 8 * 2 * kWaves <= kMiscBytes, "misc layout");
 constexpr uint32_t kRsrcWord3 = 0x00020000u;                // raw buffer, 32-bit data format
 
-// Tile width: 384 when OUT_N is a multiple of 384, and for the per-tensor kernel also when at least
-// four tiles fit and the last is at least half full (OUT_N = 2880: 7.5 tiles of 384). A row's
+// Tile width (this kernel's OUT_N, the persistent kernel's N): 384 when a multiple of 384, and for
+// the per-tensor kernels also when at least four tiles fit and the last is at least half full
+// (2880: 7.5 tiles of 384). A row's
 // 384-byte RHS window is 3 cache lines, as is a 320-byte one, so the wider tile asks the L1 -> L2
 // request stream, the kernel's limiter, for 13% fewer lines per token at OUT_N = 2880 against 6.7%
 // of masked MFMA work (down_wgrad 1.029 -> 1.000 ms, same-box A/B, bit-identical output).

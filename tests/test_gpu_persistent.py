@@ -73,7 +73,8 @@ def _parity_small_k(pkg, orc, orp, got, p, label):
 
 
 RAGGED = [
-    # lens, K, N: 320-wide N tiles (N % 384 != 0) and 384-wide, partial M/N tiles, K tails
+    # lens, K, N: 320-wide N tiles and 384-wide (N % 384 == 0, or N >= 1536 with the last tile at
+    # least half full: 1728, 2880), partial M/N tiles, K tails
     ([1, 2, 3, 5, 8, 13, 21, 31], 128, 128),
     ([0, 0, 193, 0], 256, 384),
     ([191, 192, 193, 0, 385], 2880, 336),
@@ -82,6 +83,7 @@ RAGGED = [
     ([300, 0, 645], 5760, 640),
     ([64, 0, 96, 45], 144, 1152),
     ([383, 1], 2880, 2880),
+    ([200, 77], 272, 1728),
 ]
 
 

@@ -24,7 +24,9 @@ TILE_M, K_STEP, XCDS = 192, 128, 8
 
 
 def _tn(N):
-    return 384 if N % 384 == 0 else 320
+    """wide_tiles(N, false): 384 for multiples of 384, and when at least four tiles fit and the last
+    is at least half full; else 320."""
+    return 384 if N % 384 == 0 or (N >= 4 * 384 and N % 384 >= 192) else 320
 
 
 def _swz(r):
