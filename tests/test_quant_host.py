@@ -1,7 +1,11 @@
-"""CPU checks of the quantization producer's C ABI (no kernel launches: every call here fails
-validation, or passes it with nothing to launch, before any HIP call)."""
+"""CPU checks of the quantization producer: its C ABI (no kernel launches: every call here fails
+validation, or passes it with nothing to launch, before any HIP call), and a model of the
+transposing kernels' tile arithmetic (bounds, coverage, padding untouched) run before any GPU
+launch of a new shape class."""
 import os
 import re
+
+import numpy as np
 
 import pytest
 import torch
@@ -94,3 +98,61 @@ def test_grouped_linear_refuses_cpu(pkg):
         pkg.grouped_linear_fp8(x, w, offs)
     with pytest.raises(ValueError, match="main_grad"):
         pkg.grouped_linear_fp8(x, w, offs, main_grad=torch.zeros(2, 32, 16))
+
+
+# ----------------------------------------------------------------------------- transpose index model
+
+def _transpose_model(B, R, C, q_stride, t_stride):
+    """Restatement of the 128 x 128 tile arithmetic of quant_transpose_kernel (and of
+    ggemm_persistent_transpose_u8, which shares it): every byte of q and of q^T written exactly
+    once from the right source element, no access outside the buffers."""
+    T, P = 128, 132
+    rt, ct = -(-R // T), -(-C // T)
+    per = rt * ct
+    x = np.arange(B * R * C, dtype=np.int64).reshape(B, R, C)
+    q = np.full(B * R * q_stride, -1, np.int64)
+    qt = np.full(B * C * t_stride, -1, np.int64)
+    for it in range(B * per):
+        b, rem = divmod(it, per)
+        r0, c0 = (rem // ct) * T, (rem % ct) * T
+        lds = np.full(T * P, -1, np.int64)
+        for tid in range(256):
+            tr, tc = tid >> 3, 16 * (tid & 7)
+            for h in range(4):
+                if c0 + tc < C and r0 + tr + 32 * h < R:
+                    row = b * R + r0 + tr + 32 * h
+                    assert c0 + tc + 16 <= C
+                    vals = x.reshape(-1)[row * C + c0 + tc: row * C + c0 + tc + 16]
+                    o = row * q_stride + c0 + tc
+                    assert o + 16 <= q.size and (q[o:o + 16] == -1).all()
+                    q[o:o + 16] = vals
+                    lo = (tr + 32 * h) * P + tc
+                    assert lo + 16 <= T * P
+                    lds[lo:lo + 16] = vals
+        for tid in range(256):
+            qc, qb = tid >> 1, 64 * (tid & 1)
+            if c0 + qc >= C:
+                continue
+            base = (b * C + c0 + qc) * t_stride + r0 + qb
+            for h in range(4):
+                if r0 + qb + 16 * h >= R:
+                    continue
+                vals = [lds[(qb + 16 * h + i) * P + qc] for i in range(16)]
+                assert min(vals) >= 0 and r0 + qb + 16 * h + 16 <= R
+                o = base + 16 * h
+                assert o + 16 <= qt.size and (qt[o:o + 16] == -1).all()
+                qt[o:o + 16] = vals
+    qv = q.reshape(B, R, q_stride)[:, :, :C]
+    tv = qt.reshape(B, C, t_stride)[:, :, :R]
+    assert np.array_equal(qv, x) and np.array_equal(tv, np.swapaxes(x, 1, 2))
+    # padding bytes are never written
+    assert (q.reshape(B, R, q_stride)[:, :, C:] == -1).all() and (qt.reshape(B, C, t_stride)[:, :, R:] == -1).all()
+
+
+@pytest.mark.parametrize("B,R,C,qs,ts", [
+    (3, 80, 48, 48, 80), (1, 144, 208, 256, 256), (2, 272, 80, 128, 384), (1, 208, 64, 64, 208),
+    (5, 16, 1040, 1040, 16), (1, 256, 384, 384, 256), (2, 16, 16, 128, 128),
+])
+def test_transpose_tile_index_model(B, R, C, qs, ts):
+    _transpose_model(B, R, C, qs, ts)
+
