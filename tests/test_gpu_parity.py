@@ -208,6 +208,33 @@ def test_strided_views(pkg, orc, cuda):
     assert torch.count_nonzero(big[:, 64:, :]) == 0 and torch.count_nonzero(big[:, :, 128:]) == 0
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_random_shapes_vs_oracle(pkg, orc, cuda, seed):
+    """Seeded random configurations: G in 1..40 with empty, tiny and long groups; OUT_M, OUT_N any
+    multiples of 16 up to 800 (partial tiles in both dimensions, both tile widths and the wide-tile
+    rule's boundary), realistic values: the bar on cosine, finiteness and exact-zero empty groups,
+    and its 2e-2 relative threshold, or, where a tiny group's heavy cancellation exceeds that, every
+    element within the rigorous MFMA error bound."""
+    rng = np.random.default_rng(1000 + seed)
+    G = int(rng.integers(1, 41))
+    kind = rng.integers(0, 4, G)
+    lens = np.where(kind == 0, 0, np.where(kind == 1, rng.integers(1, 32, G), rng.integers(32, 400, G)))
+    if seed % 3 == 0:
+        lens[rng.integers(0, G)] = int(rng.integers(1000, 2500))       # one long group (skew)
+    om = 16 * int(rng.integers(1, 26))
+    on = 16 * int(rng.choice([int(rng.integers(1, 51)), 96, 108, 120]))  # 1536, 1728, 1920 included
+    _say(f"random seed={seed} G={G} M={int(lens.sum())} OUT={om}x{on}")
+    lhs, rhs, offs, _, (sl, sr) = _rand_bytes_problem(lens.tolist(), om, on, seed=seed)
+    out = _run_tw(pkg, lhs, rhs, sl, sr, offs, cuda)
+    torch.cuda.synchronize()
+    ref = orc.vark_wgrad_tensorwise(lhs.numpy(), rhs.numpy(), sl, sr, offs.numpy())
+    bits = pkg.as_bf16_bits(out)
+    m = orc.compare(bits, ref, offs.numpy())
+    _say(f"random {seed}: {m}")
+    if not orc.parity_ok(m):
+        _assert_parity_small_k(orc, bits, ref, lhs, rhs, offs, sl, sr, f"random {seed}")
+
+
 @pytest.mark.parametrize("G,skew", [(1100, False), (1024, False), (1024, True)])
 def test_many_groups_natural_order(pkg, orc, cuda, G, skew):
     """G above the in-kernel sort limit (1024) uses natural group order; G = 1024 is the largest
