@@ -87,6 +87,33 @@ RAGGED = [
 ]
 
 
+@pytest.mark.parametrize("seed", range(10))
+def test_random_shapes_vs_oracle(pkg, orc, orp, cuda, seed):
+    """Seeded random configurations: G in 1..40 with empty, single-row, partial and multi-tile
+    groups; K any multiple of 16 up to 1024 (K tails inside a stage), N any multiple of 16 up to
+    800 or 1536 / 1728 / 1920 (both tile widths and the wide-tile rule); both A formats; the
+    reference's value recipe. The bar on every row, or, where a heavy cancellation at small K
+    exceeds its 2e-2 threshold, every element within the rigorous MFMA error bound."""
+    rng = np.random.default_rng(2000 + seed)
+    G = int(rng.integers(1, 41))
+    kind = rng.integers(0, 4, G)
+    lens = np.where(kind == 0, 0, np.where(kind == 1, rng.integers(1, 192, G), rng.integers(192, 700, G)))
+    K = 16 * int(rng.integers(1, 65))
+    N = 16 * int(rng.choice([int(rng.integers(1, 51)), 96, 108, 120]))
+    fmt = "e4m3" if seed % 2 == 0 else "e5m2"
+    site = "down_fwd" if fmt == "e4m3" else "down_dgrad"
+    _say(f"persistent random seed={seed} G={G} M={int(lens.sum())} K={K} N={N} {fmt}")
+    p = pkg.inputs.make_fwd_problem(site, seed=seed, lens=lens.tolist(), K=K, N=N)
+    out = _run(pkg, p.a, p.b, fmt, p.group_offs, 0.1, 0.1, cuda)
+    torch.cuda.synchronize()
+    ref = orp.grouped_fp8(p.a.numpy(), p.b.numpy(), 0.1, 0.1, p.group_offs.numpy(), fmt)
+    m = orc.compare(pkg.as_bf16_bits(out), ref)
+    _say(f"random {seed}: {m}")
+    if not orc.parity_ok(m):
+        # at small K a heavy cancellation can pass 2e-2 relative; the rigorous bound cannot
+        _parity_small_k(pkg, orc, orp, out, p, f"random {seed}")
+
+
 @pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
 @pytest.mark.parametrize("lens,K,N", RAGGED, ids=[f"case{i}" for i in range(len(RAGGED))])
 def test_ragged_vs_oracle(pkg, orc, orp, cuda, fmt, lens, K, N):
