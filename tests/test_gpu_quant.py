@@ -207,6 +207,45 @@ def test_mx_grouped_bit_exact(pkg, orq, cuda, fmt, dtype, lens, N):
     np.testing.assert_array_equal(sc.cpu().numpy()[:P // 32], sc_ref[:P // 32])
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_random_producer_shapes_bit_exact(pkg, orq, cuda, seed):
+    """Seeded random shapes through every producer entry point, byte for byte against the oracle:
+    per-tensor (plain and row-aligned), per-tensor with the transposed copy, grouped MX (G 1-40,
+    empty and one-row groups, any multiple of 16 columns), bf16 and fp32 inputs, both formats."""
+    rng = np.random.default_rng(3000 + seed)
+    fmt = "e4m3" if seed % 2 == 0 else "e5m2"
+    dtype = torch.bfloat16 if seed % 4 < 2 else torch.float32
+    G = int(rng.integers(1, 41))
+    lens = np.where(rng.integers(0, 4, G) == 0, 0, rng.integers(1, 300, G))
+    M, N = int(lens.sum()), 16 * int(rng.integers(1, 60))
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn((M, N), generator=g) * float(10.0 ** rng.uniform(-4, 2))).to(dtype)
+    _say(f"random producer seed={seed} {fmt} {dtype} G={G} M={M} N={N}")
+    xd = x.to(cuda)
+    q_ref, s_ref, a_ref = orq.quantize_tensorwise(x.float().numpy(), fmt)
+    for align in (None, 128):
+        q, scale, am = pkg.quantize_fp8_tensorwise(xd, fmt, row_align=align)
+        torch.cuda.synchronize()
+        assert float(am) == float(a_ref) and float(scale) == float(s_ref)
+        np.testing.assert_array_equal(_bytes(q), q_ref)
+    R = 16 * (M // 16)
+    if R:
+        q, q_t, _, _ = pkg.quantize_fp8_tensorwise_transpose(xd[:R].contiguous(), fmt, row_align=128)
+        torch.cuda.synchronize()
+        r_ref, _, _ = orq.quantize_tensorwise(x[:R].float().numpy(), fmt)
+        np.testing.assert_array_equal(_bytes(q), r_ref)
+        np.testing.assert_array_equal(_bytes(q_t), r_ref.T)
+    offs = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64)
+    q, sc, pad = pkg.quantize_mxfp8_grouped(xd, offs.to(cuda), fmt)
+    torch.cuda.synchronize()
+    mq, msc, mpad = orq.quantize_mx_grouped(x.float().numpy(), offs.numpy(), fmt, out_rows=q.shape[0])
+    pad = pad.cpu().numpy()
+    np.testing.assert_array_equal(pad, mpad)
+    P = int(pad[-1])
+    np.testing.assert_array_equal(_bytes(q)[:P], mq[:P])
+    np.testing.assert_array_equal(sc.cpu().numpy()[:P // 32], msc[:P // 32])
+
+
 def test_mx_invalid_offsets_write_nothing(pkg, cuda):
     """Offsets past the rows (which the host cannot see) make the kernel's own check skip all
     writes: the outputs keep their previous contents."""
