@@ -8,9 +8,9 @@
 // bench.py:182-193 "dW = x^T @ dy").
 //
 // Structure (one 512-thread workgroup per CU, persistent):
-//  * Output tiles of 192 (OUT_M) x TN (OUT_N), TN = 384 when OUT_N is a multiple of 384 (gate_up:
-//    5760 = 15 x 384) and 320 otherwise (down: 2880 = 9 x 320); 192 divides 2880. 8 waves in a
-//    2 x 4 grid, 96 x TN/4 per wave (6 x 6 or 6 x 5 MFMA blocks). RHS rows of a 5760-wide tensor
+//  * Output tiles of 192 (OUT_M) x TN (OUT_N), TN = 384 or 320 by wide_tiles() (gate_up: 5760 =
+//    15 x 384; down: 2880 = 7.5 x 384, the last N-tile half masked); 192 divides 2880. 8 waves in
+//    a 2 x 4 grid, 96 x TN/4 per wave (6 x 6 or 6 x 5 MFMA blocks). RHS rows of a 5760-wide tensor
 //    are 45 whole 128-byte lines, so 384-byte windows are fetched without waste.
 //  * The token (K) axis is walked in stages of 128 tokens: 128 x 192 LHS bytes plus 128 x TN RHS
 //    bytes (64 or 72 KiB). Two stages live in the launch's 64 KiB dynamic LDS plus 96 KiB static
@@ -25,17 +25,17 @@
 //    function of the token chosen per row width, so the transposed reads below are bank-conflict
 //    free (16 consecutive tokens of one chunk column land in 16 distinct 4-bank slots).
 //  * MFMA operands come from ds_read_b64_tr_b8: one read gives each lane 8 consecutive tokens of
-//    one column. The MFMA is v_mfma_scale_f32_16x16x128_f8f6f4 (e8m0 scale 127 == 1.0 for the
-//    per-tensor path, real block scales for MXFP8); the A operand is the RHS tile (rows of the
-//    16x16 result are OUT_N columns) so each lane ends with 4 consecutive bf16 of one C row.
+//    one column. The MFMA is the 16x16x128 f8f6f4 one: unscaled for the per-tensor path (constant
+//    zero scale operands select it), v_mfma_scale with e8m0 block scales for MXFP8; the A operand
+//    is the RHS tile (rows of the 16x16 result are OUT_N columns) so each lane ends with 4
+//    consecutive values of one C row.
 //  * Static persistent schedule (no workspace exists in the launch contract): groups are sorted by
-//    descending token count, each XCD takes a contiguous slice of the tile list carrying 1/8 of
-//    the work, and its 32 CUs walk the slice round-robin in 4-wide N bands, so CUs of one XCD
-//    share L2 panels and different XCDs stream different rows. The first stage of a workgroup's
-//    next tile is loaded while it finishes the current one.
+//    descending token count; the tile list is dealt either in equal-work slices to XCD pairs or in
+//    boustrophedon rounds over all workgroups, whichever leaves the heaviest workgroup lighter
+//    (make_sched); tiles of a group are walked in 4-wide N bands so the 32 CUs of one XCD share L2
+//    panels. The first stage of a workgroup's next tile is loaded while it finishes the current one.
 //  * The MXFP8 kernel at OUT_N multiples of 384 runs a second body on the same pipeline with the
-//    32x32x64 scaled MFMA (vark_body32 below): 6 x 6 blocks of 16 x 16 do not fit next to their
-//    per-block scale registers.
+//    32x32x64 scaled MFMA (vark_body32 below), measured faster there than the 16x16x128 body.
 #pragma once
 
 #include <hip/hip_runtime.h>
