@@ -11,12 +11,13 @@
 // Structure (the variable-K kernel's stage pipeline, with K-major operands):
 //  * Output tiles of 192 rows of one group x TN columns, TN = 384 when N % 384 == 0 or when at least
 //    four tiles fit and the last is at least half full (wide_tiles; N = 2880: 1-2% faster at the
-//    three N = 2880 sites than nine 320-wide tiles), else 320. A
-//    group of len rows has ceil(len / 192) M-tiles; rows of its last tile past the group end are
-//    neither loaded (they read as zero) nor stored.
+//    three N = 2880 sites than nine 320-wide tiles), else 320. A group of len rows has
+//    ceil(len / 192) M-tiles; rows of its last tile past the group end are neither loaded (they
+//    read as zero) nor stored.
 //  * The K axis in stages of 128: LDS rows of 128 bytes, A's 192 rows then B's TN rows (72 or
 //    64 KiB per stage), two stages in the flat 160 KiB, one barrier per stage, the next tile's
-//    first stage issued during the current tile's last.
+//    first stage issued during the current tile's last. A stage's A rows are requested at the
+//    barrier, its B rows after the first m-block's MFMAs.
 //  * LDS-DMA of 16 bytes per lane, 8 rows x 128 bytes per wave-instruction; logical chunk c of row
 //    r is stored at physical chunk c ^ (r & 7) ^ ((r >> 3) & 1). The LDS serves a 128-bit read 8
 //    lanes (128 bytes, all 32 banks) per cycle, and 8 lanes of an operand read take 8 consecutive

@@ -2,7 +2,8 @@
 // GEMMs, turning bf16 / fp32 activations, gradients and weights into their fp8 operands.
 //
 //  * amax:        amax = max |x| over a 2-D [rows, cols] tensor (NaN propagates).
-//  * tensorwise:  scale = amax / fmax (1 when amax == 0), q = fp8(clamp(x / scale, -fmax, fmax)).
+//  * tensorwise:  scale = amax / fmax (1 when amax == 0), q = fp8(clamp(x / scale, -fmax, fmax));
+//                 optionally with the transposed copy q^T of each matrix of a batch (weights).
 //  * MX, grouped: groups of rows (the token axis) padded to multiples of 32 rows; per 32-row block
 //                 and column, X = floor(log2(fl32(amax_blk / fmax))) clamped to [-127, 127]
 //                 (0 for an all-zero block), e8m0 byte X + 127, q = fp8(clamp(x * 2^-X, +-fmax));
