@@ -6,7 +6,8 @@ bf16 and accumulating into an fp32 main-grad -- are captured once and replayed s
 eager work of the same library between replays (as a training loop would interleave it), and every
 replay is compared with the eager results bit for bit, including a replay after the inputs were
 overwritten in place (the graph reads its inputs, not copies). The launches record no memset: the
-amax result is cleared by a fill kernel.
+amax result is cleared by a fill kernel. A second test captures the autograd op's forward and
+backward (torch.autograd.grad) in one graph.
 """
 import numpy as np
 import pytest
@@ -91,3 +92,50 @@ def test_graph_replays_match_eager(pkg, cuda):
         assert torch.equal(_bits(a), _bits(b)), name
     assert torch.equal(main_grad, want32)
     assert not torch.equal(_bits(want[2]), _bits(ref[2]))   # the inputs did change the result
+
+
+def test_graph_captures_autograd_layer(pkg, cuda):
+    """The autograd op's forward and backward (torch.autograd.grad) captured in one graph: replays
+    equal eager out, dx and dw bit for bit, also after the inputs are overwritten in place."""
+    from ggemm_asm_amd.autograd import grouped_linear_fp8
+    lens, K, N = [257, 0, 96, 400], 192, 320
+    G, M = len(lens), sum(lens)
+    g = torch.Generator(device=cuda).manual_seed(1)
+    x = torch.randn((M, K), generator=g, device=cuda).to(torch.bfloat16).requires_grad_(True)
+    w = (torch.randn((G, N, K), generator=g, device=cuda) * 0.05).to(torch.bfloat16).requires_grad_(True)
+    dy = (torch.randn((M, N), generator=g, device=cuda) * 1e-2).to(torch.bfloat16)
+    offs = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64, device=cuda)
+
+    def step():
+        out = grouped_linear_fp8(x, w, offs)
+        dx, dw = torch.autograd.grad(out, (x, w), dy)
+        return out.detach(), dx, dw
+
+    _say("graph autograd: eager")
+    ref = [t.clone() for t in step()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    _say("graph autograd: capturing")
+    with torch.cuda.graph(graph):
+        static = step()
+    for r in range(2):
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("out", "dx", "dw"), static, ref):
+            assert torch.equal(_bits(a), _bits(b)), (r, name)
+    _say("graph autograd: new inputs")
+    with torch.no_grad():
+        x.mul_(-0.5)
+        w.add_(0.01)
+        dy.mul_(2.0)
+    want = [t.clone() for t in step()]
+    graph.replay()
+    torch.cuda.synchronize()
+    for name, a, b in zip(("out", "dx", "dw"), static, want):
+        assert torch.equal(_bits(a), _bits(b)), name
