@@ -54,13 +54,16 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="gate_up_wgrad",
-                    choices=["gate_up_wgrad", "down_wgrad", "gate_up_zipf", "gate_up_mx", "constant", *FWD_SITES,
-                             *QUANT_CONFIGS, *LAYER_CONFIGS])
+                    choices=["gate_up_wgrad", "down_wgrad", "gate_up_zipf", "gate_up_mx", "plumbing", "constant",
+                             *FWD_SITES, *QUANT_CONFIGS, *LAYER_CONFIGS])
     ap.add_argument("--mfma", default="k128", choices=["k128", "k32"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU work for the cpu_baseline sample (0 disables)")
     ap.add_argument("--extra", action="store_true", help="also time the other configs (not part of the line)")
+    ap.add_argument("--info", action="store_true",
+                    help="print the registers, spills, LDS and MFMA counts of this build's code objects and exit "
+                         "(no GPU needed)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="only run a plain device-to-device copy of this many MiB (steps times): the "
                          "known-size reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -79,14 +82,36 @@ def copy_calibration(mib, steps):
 
 
 def read_traffic(name):
-    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE), if recorded."""
+    """(HBM bytes per launch, where they come from): the rocprofv3 --pmc measurement (FETCH_SIZE +
+    WRITE_SIZE, calibrated) recorded in profiles/traffic_<name>.txt with the kernel revision it was
+    taken at, or (None, None). Not measured by this run."""
+    value, rev = None, None
     try:
         for line in open(traffic_file(name)):
             if line.startswith("traffic_bytes_per_launch:"):
-                return float(line.split(":", 1)[1])
+                value = float(line.split(":", 1)[1])
+            elif line.startswith("kernel_revision:"):
+                rev = line.split(":", 1)[1].strip()
     except OSError:
-        pass
-    return None
+        return None, None
+    src = f"profiles/traffic_{name}.txt (rocprofv3 --pmc, kernel revision {rev or 'unrecorded'})"
+    return value, (src if value is not None else None)
+
+
+def host_cores():
+    """CPU cores this process may run on (its affinity set), the host share the CPU baseline has."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
+def print_info(pkg):
+    """Resources of this build's code objects (the counterpart of the reference's kernel info
+    printout, bench.py:544-589)."""
+    from ggemm_asm_amd import harness
+    for path in (pkg.CODE_OBJECT_PATH, *pkg.PERSISTENT_CODE_OBJECT_PATHS.values()):
+        print(json.dumps(harness.kernel_info(path)), flush=True)
 
 
 def make_runner(pkg, p, dev, mfma):
@@ -153,7 +178,7 @@ def cpu_baseline_fwd(p, seconds):
         if t_total >= seconds:
             break
     return {"value": round(done_flops / t_total / 1e12, 4), "unit": "TFLOPS", "cores": int(threads),
-            "kind": "port",
+            "host_cores": host_cores(), "kind": "port",
             "sample": f"{groups} of {p.G} groups ({rows} rows, {done_flops / 1e12:.2f} TFLOP) of {p.name}: "
                       f"numpy fp32 dequantize + OpenBLAS sgemm + bf16 RNE, {t_total:.1f} s"}
 
@@ -182,7 +207,7 @@ def cpu_baseline(p, seconds):
         if t_total >= seconds:
             break
     return {"value": round(done_flops / t_total / 1e12, 4), "unit": "TFLOPS", "cores": int(threads),
-            "kind": "port",
+            "host_cores": host_cores(), "kind": "port",
             "sample": f"{groups} of {p.G} groups ({tokens} tokens, {done_flops / 1e12:.2f} TFLOP) of {p.name}: "
                       f"numpy fp32 dequantize + OpenBLAS sgemm + bf16 RNE, {t_total:.1f} s"}
 
@@ -236,7 +261,8 @@ def quant_workload(pkg, name, seed, dev):
                 orq.quantize_mx_grouped(xc, np.array([0, rows], np.int64), "e5m2", out_rows=rows)
             t_total += time.perf_counter() - t0
             done += xc.size
-        return {"value": round(done * (nbytes / n) / t_total / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+        return {"value": round(done * (nbytes / n) / t_total / 1e9, 3), "unit": "GB/s", "cores": 1,
+                "host_cores": host_cores(), "kind": "port",
                 "sample": f"{done // xc.size} x {rows} rows of {name}'s input through the numpy oracle, "
                           f"{t_total:.1f} s"}
 
@@ -252,7 +278,8 @@ def main_quant(args, pkg, dev):
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16->fp8",
             "data": "synthetic", "config": cfg,
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic(args.config)},
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic(args.config)[0],
+                         "traffic_source": read_traffic(args.config)[1]},
             "cpu_baseline": cpu(args.cpu_seconds) if args.cpu_seconds > 0 else None}
     print(json.dumps(line), flush=True)
 
@@ -299,9 +326,12 @@ def main():
     if args.copy_calibration_mb:
         copy_calibration(args.copy_calibration_mb, args.steps)
         return
-    import torch
     from __graft_entry__ import load_package
     pkg = load_package()
+    if args.info:
+        print_info(pkg)
+        return
+    import torch
     dev = torch.device("cuda:0")
     if args.config in QUANT_CONFIGS:
         main_quant(args, pkg, dev)
@@ -320,7 +350,7 @@ def main():
     run = make_runner(pkg, p, dev, args.mfma)
     ms = time_steps(run, args.steps, args.warmup)
     tflops = p.flops / (ms * 1e-3) / 1e12
-    traffic = read_traffic(args.config)
+    traffic, traffic_source = read_traffic(args.config)
     if fwd:
         geo = pkg.launch_geometry(p.N)
         config = {"workload": p.name, "G": p.G, "M_total": p.M, "K": p.K, "N": p.N,
@@ -338,9 +368,11 @@ def main():
                   "kernel": "hip gfx950 persistent {tile_m}x{tile_n} tiles, mfma {mfma}".format(
                       mfma=args.mfma, **pkg.launch_geometry(p.OUT_N)),
                   "baseline_number": "reference optimized ASM 3.515 ms / 1237 TFLOPS (README.md:60)"}
-        vs_baseline = round(tflops / REF_OPT_ASM_TFLOPS, 4)
+        vs_baseline = round(tflops / REF_OPT_ASM_TFLOPS, 4) if p.name == "gate_up_wgrad" else None
     line = {
-        "metric": f"ms + TFLOPS (% FP8 peak) for {p.name if fwd else 'gate_up_wgrad'} G=32 M=131072 on 1 MI355X",
+        "metric": (f"ms + TFLOPS (% FP8 peak) for {p.name} G=32 M=131072 on 1 MI355X" if fwd else
+                   "ms + TFLOPS (% FP8 peak) for gate_up_wgrad G=32 M=131072 on 1 MI355X" if p.G == 32 else
+                   f"ms + TFLOPS (% FP8 peak) for {p.name} G={p.G} M={p.M} on 1 MI355X"),
         "value": round(tflops, 2),
         "unit": "TFLOPS",
         "n_gpus": 1,
@@ -354,7 +386,8 @@ def main():
         "data": "synthetic",
         "config": config,
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP8_DENSE_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tflops / FP8_DENSE_PEAK_TFLOPS, 4), "traffic": traffic},
+                     "unit": "TFLOP/s", "frac": round(tflops / FP8_DENSE_PEAK_TFLOPS, 4), "traffic": traffic,
+                     "traffic_source": traffic_source},
     }
     if args.extra:
         extra = {}

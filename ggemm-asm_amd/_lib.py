@@ -23,6 +23,7 @@ EXPORTS = (
 
 PERSISTENT_EXPORTS = (
     "ggemm_persistent_fp8",
+    "ggemm_persistent_clear_tail",
     "ggemm_persistent_transpose_u8",
 )
 
@@ -47,7 +48,9 @@ class GGemmError(RuntimeError):
 
 
 def library_path() -> str:
-    return _build.SO_PATH
+    """The in-tree library, or the one GGEMM_VARK_LIBRARY names (a variant build of the same
+    sources, e.g. the host-sanitizer build the CPU tests run the C ABI's validation under)."""
+    return os.environ.get("GGEMM_VARK_LIBRARY") or _build.SO_PATH
 
 
 def load():
@@ -66,9 +69,9 @@ def load():
         f = getattr(lib, name)
         f.argtypes = tw
         f.restype = ctypes.c_int
-    lib.ggemm_vark_wgrad_fp8_out.argtypes = tw[:-1] + [i32, vp]
+    lib.ggemm_vark_wgrad_fp8_out.argtypes = tw[:-1] + [i32, ctypes.c_int64, vp]
     lib.ggemm_vark_wgrad_fp8_out.restype = ctypes.c_int
-    lib.ggemm_vark_wgrad_mxfp8.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 10 + [vp]
+    lib.ggemm_vark_wgrad_mxfp8.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 10 + [ctypes.c_int64, vp]
     lib.ggemm_vark_wgrad_mxfp8.restype = ctypes.c_int
     lib.ggemm_vark_check_offsets.argtypes = [i64p, i32, ctypes.c_int64, i32]
     lib.ggemm_vark_check_offsets.restype = ctypes.c_int
@@ -82,6 +85,8 @@ def load():
     lib.ggemm_vark_launch_geometry.restype = None
     lib.ggemm_persistent_fp8.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 9 + [ctypes.c_int64, vp]
     lib.ggemm_persistent_fp8.restype = ctypes.c_int
+    lib.ggemm_persistent_clear_tail.argtypes = [vp, i32, i32, vp, i32, ctypes.c_int64, vp]
+    lib.ggemm_persistent_clear_tail.restype = ctypes.c_int
     lib.ggemm_persistent_transpose_u8.argtypes = [vp, i32, i32, i32, ctypes.c_int64, ctypes.c_int64, vp,
                                                   ctypes.c_int64, ctypes.c_int64, vp]
     lib.ggemm_persistent_transpose_u8.restype = ctypes.c_int

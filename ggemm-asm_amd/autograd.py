@@ -10,7 +10,8 @@ the autograd wiring left to the framework (Primus-Turbo, not vendored).
 * forward: x -> e4m3 and w -> e4m3 (per-tensor amax scales, the quantization producer; when x
   needs a gradient the weight pass also writes qw^T [G, K, N], the data-gradient GEMM's B); every
   fp8 operand is written with rows starting on 128-byte lines (padded row stride);
-  ``out = grouped_gemm_fp8_tensorwise(qx, qw, sx, sw, offs)`` (persistent kernel), bf16.
+  ``out = grouped_gemm_fp8_tensorwise(qx, qw, sx, sw, offs)`` (persistent kernel), bf16; rows
+  past offs[G] (tokens the routing dropped) are zero in out and in dx.
   Saved for backward: the fp8 tensors and their scales (1 byte per element, not the bf16 inputs).
 * backward: dy -> e5m2;
   ``dx[r] = dy[r] @ w[g]`` — the persistent kernel with B = qw^T (K-major [G, N_out=K, K_red=N],
@@ -46,7 +47,8 @@ class GroupedLinearFP8(torch.autograd.Function):
             qw, qwt, sw, _ = quantize_fp8_tensorwise_transpose(w.contiguous(), "e4m3", row_align=_LINE)
         else:
             (qw, sw, _), qwt = quantize_fp8_tensorwise(w.contiguous(), "e4m3", row_align=_LINE), None
-        out = grouped_gemm_fp8_tensorwise(qx, qw, sx, sw, group_offs)
+        # rows past offs[G] (tokens the routing dropped) come out as exact zeros
+        out = grouped_gemm_fp8_tensorwise(qx, qw, sx, sw, group_offs, zero_tail=True)
         ctx.save_for_backward(qx, sx, qwt, sw, group_offs)
         ctx.main_grad = main_grad
         ctx.x_dtype, ctx.w_dtype = x.dtype, w.dtype
@@ -59,7 +61,7 @@ class GroupedLinearFP8(torch.autograd.Function):
         dx = dw = None
         if ctx.needs_input_grad[0]:
             # dx[r] = dy[r] @ w[g]: B[g] = w[g]^T, [N_out = K, K_red = N] K-major
-            dx = grouped_gemm_fp8_tensorwise(qdy, qwt, sdy, sw, group_offs)
+            dx = grouped_gemm_fp8_tensorwise(qdy, qwt, sdy, sw, group_offs, zero_tail=True)
             dx = dx.to(ctx.x_dtype)
         if ctx.needs_input_grad[1] or ctx.main_grad is not None:
             if ctx.main_grad is not None:

@@ -74,6 +74,45 @@ def build_persistent_co(verbose: bool = False) -> dict:
     return dict(PERSISTENT_CO_PATHS)
 
 
+SANITIZE_DIR = os.path.join(os.path.dirname(PKG_DIR), "_build", "sanitize")
+
+
+def sanitizer_runtime() -> str:
+    """clang's AddressSanitizer runtime (it carries the UBSan handlers too): preloaded into a
+    process that loads a host-sanitized build."""
+    llvm = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "llvm")
+    r = subprocess.run([os.path.join(llvm, "bin", "clang"), "-print-file-name=libclang_rt.asan-x86_64.so"],
+                       capture_output=True, text=True)
+    path = r.stdout.strip()
+    if r.returncode != 0 or not os.path.isabs(path) or not os.path.exists(path):
+        import glob
+        hits = sorted(glob.glob(os.path.join(llvm, "lib", "clang", "*", "lib", "linux", "libclang_rt.asan-x86_64.so")))
+        path = hits[-1] if hits else ""
+    return path
+
+
+def build_host_sanitized(verbose: bool = False) -> dict:
+    """Host-side AddressSanitizer + UndefinedBehaviorSanitizer builds for the CPU tests: the
+    library (its C ABI validation and launch code instrumented; device code built as usual, GPU
+    sanitizers are not used) and the oracle's C restatement, both against clang's shared sanitizer
+    runtime. Outputs under _build/sanitize/."""
+    os.makedirs(SANITIZE_DIR, exist_ok=True)
+    lib = os.path.join(SANITIZE_DIR, "libggemm_vark.so")
+    host = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+            "-Xarch_host", "-fno-omit-frame-pointer", "-Xarch_host", "-fno-sanitize-recover=undefined"]
+    _run([hipcc(), *DEVICE_FLAGS, "-g", "-fPIC", "-shared", "-shared-libsan", *host,
+          os.path.join(CSRC, "vark_capi.hip"), os.path.join(CSRC, "persistent_capi.hip"),
+          os.path.join(CSRC, "quant_capi.hip"), "-o", lib + ".tmp"], verbose)
+    os.replace(lib + ".tmp", lib)
+    clang = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "llvm", "bin", "clang")
+    oracle_c = os.path.join(os.path.dirname(PKG_DIR), "oracle", "vark_oracle.c")
+    orc = os.path.join(SANITIZE_DIR, "libvark_oracle_c.so")
+    _run([clang, "-O1", "-g", "-std=c11", "-fPIC", "-shared", "-shared-libsan", "-fsanitize=address,undefined",
+          "-fno-omit-frame-pointer", "-fno-sanitize-recover=undefined", oracle_c, "-o", orc + ".tmp", "-lm"], verbose)
+    os.replace(orc + ".tmp", orc)
+    return {"library": lib, "oracle_c": orc, "runtime": sanitizer_runtime()}
+
+
 def build_all(verbose: bool = False) -> tuple[str, str]:
     so, co = build_so(verbose), build_co(verbose)
     build_persistent_co(verbose)

@@ -9,8 +9,8 @@
 #include "capi_common.h"
 #include "persistent_kernel.h"
 
-GGEMM_DEFINE_PERSISTENT_KERNEL(_grouped_fp8_persistent_gemm_kernel, false)
-GGEMM_DEFINE_PERSISTENT_KERNEL(_grouped_fp8_persistent_gemm_kernel_e5m2, true)
+GGEMM_DEFINE_PERSISTENT_LIB_KERNEL(_grouped_fp8_persistent_gemm_kernel, false)
+GGEMM_DEFINE_PERSISTENT_LIB_KERNEL(_grouped_fp8_persistent_gemm_kernel_e5m2, true)
 
 static_assert(GGEMM_PERSISTENT_MAX_GROUPS == ggemm::nt::kMaxGroups, "header and kernel agree");
 
@@ -87,6 +87,24 @@ __global__ void __launch_bounds__(kXThreads) transpose_u8_kernel(const uint8_t* 
   }
 }
 
+// Zeroes rows [clamp(offs[G]), m_total) of a bf16 [m_total, N] output (ggemm_persistent_clear_tail):
+// the row range comes from the device copy of the offsets, so no host synchronisation is needed;
+// rows are dealt to workgroups round robin, 16-byte chunks of a row to threads (N is a multiple of
+// 16, rows 16-byte aligned).
+constexpr int kTailThreads = 256;
+
+__global__ void __launch_bounds__(kTailThreads) clear_tail_kernel(uint16_t* out, int64_t stride_cm, int N,
+                                                                  const int64_t* group_offs, int G,
+                                                                  int64_t m_total) {
+  int64_t r0 = group_offs[G];
+  r0 = r0 < 0 ? 0 : (r0 > m_total ? m_total : r0);
+  const int chunks = N / 8;
+  for (int64_t r = r0 + blockIdx.x; r < m_total; r += gridDim.x) {
+    xv4u* row = reinterpret_cast<xv4u*>(out + r * stride_cm);
+    for (int c = threadIdx.x; c < chunks; c += kTailThreads) row[c] = xv4u{0u, 0u, 0u, 0u};
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -106,7 +124,23 @@ int ggemm_persistent_fp8(const void* a, const void* b, void* out, const float* a
                                          : _grouped_fp8_persistent_gemm_kernel;
   hipLaunchKernelGGL(kern, dim3(cus), dim3(ggemm::kThreads), ggemm::kDynLdsBytes, (hipStream_t)stream,
                      (const uint8_t*)a, (const uint8_t*)b, (uint16_t*)out, a_scale, b_scale, group_offs, G, N, K,
-                     stride_am, stride_bg, stride_bn, stride_cm, stride_cn, (void*)nullptr, (void*)nullptr);
+                     stride_am, stride_bg, stride_bn, stride_cm, stride_cn, (void*)nullptr, (void*)nullptr, M_total);
+  return (int)hipGetLastError();
+}
+
+int ggemm_persistent_clear_tail(void* out, int32_t N, int32_t stride_cm, const int64_t* group_offs, int32_t G,
+                                int64_t M_total, void* stream) {
+  if (!out || !group_offs) return GGEMM_E_NULL;
+  if (G <= 0 || G > ggemm::nt::kMaxGroups || N <= 0 || N % 16 || M_total < 0 || M_total > ggemm::nt::kMaxRow)
+    return GGEMM_E_SHAPE;
+  if (stride_cm < N || stride_cm % 8) return GGEMM_E_STRIDE;
+  if (!aligned(out, 16)) return GGEMM_E_ALIGN;
+  int cus = 0;
+  const int rc = device_cus(&cus);
+  if (rc) return rc;
+  if (M_total == 0) return GGEMM_OK;
+  hipLaunchKernelGGL(clear_tail_kernel, dim3(4 * cus), dim3(kTailThreads), 0, (hipStream_t)stream,
+                     static_cast<uint16_t*>(out), (int64_t)stride_cm, N, group_offs, G, M_total);
   return (int)hipGetLastError();
 }
 

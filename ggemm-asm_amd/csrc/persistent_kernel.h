@@ -58,6 +58,10 @@ struct Args {
   const int64_t* group_offs;
   int G, N, K;
   int stride_am, stride_bg, stride_bn, stride_cm, stride_cn;
+  // Rows of A and C: group offsets are clamped to [0, m_total] on the device, so no row outside
+  // the tensors is read or written whatever group_offs holds. kMaxRow from the drop-in code
+  // object, whose kernarg carries no row count; the library passes the real one.
+  int64_t m_total;
 };
 
 struct Tile {
@@ -127,6 +131,9 @@ __device__ __forceinline__ void persistent_body(const Args& a, GG_LDS uint8_t* l
     int64_t o[kPer + 1];
 #pragma unroll
     for (int k = 0; k <= kPer; ++k) o[k] = a.group_offs[min(tid * kPer + k, G)];
+    // rows past the tensors are neither read nor written: offsets clamp to m_total (<= kMaxRow)
+#pragma unroll
+    for (int k = 0; k <= kPer; ++k) o[k] = o[k] > a.m_total ? a.m_total : o[k];
     int64_t mine[kPer];
     int64_t sum = 0;
     bool bad = false;
@@ -364,16 +371,34 @@ __device__ __forceinline__ void persistent_body(const Args& a, GG_LDS uint8_t* l
   }
 }
 
+// A launch whose dynamic LDS is short of 64 KiB or not placed right after the static array
+// computes nothing; it fills the rows a valid launch writes, [offs[0], offs[G]) clamped to
+// [0, m_total], with NaN (0x7FC0) instead, so the mistake shows in the result rather than as a
+// fast run over stale output (offsets outside [0, kMaxRow] or decreasing ones leave out as it is,
+// as a valid launch with them does). Rows are dealt to workgroups round robin, columns to threads.
+__device__ void poison_out(const Args& a) {
+  const int64_t lo = a.group_offs[0], hi = a.group_offs[a.G];
+  if (lo < 0 || hi > kMaxRow || hi < lo) return;
+  const int64_t r0 = lo < a.m_total ? lo : a.m_total, r1 = hi < a.m_total ? hi : a.m_total;
+  const hsa_kernel_dispatch_packet_t* pkt = dispatch_packet();
+  const int64_t num_wg = (pkt->grid_size_x + pkt->workgroup_size_x - 1) / pkt->workgroup_size_x;
+  for (int64_t r = r0 + blockIdx.x; r < r1; r += num_wg)
+    for (int n = threadIdx.x; n < a.N; n += (int)pkt->workgroup_size_x) a.c[r * a.stride_cm + (int64_t)n * a.stride_cn] = 0x7fc0u;
+}
+
 template <bool kAE5M2>
 __device__ __forceinline__ void persistent_entry(const Args& a, GG_LDS uint8_t* dyn) {
   __shared__ __attribute__((aligned(1024))) uint8_t static_lds[kStaticLdsBytes];
   const hsa_kernel_dispatch_packet_t* pkt = dispatch_packet();
-  // The launch must provide the contracted dynamic LDS; otherwise do nothing (the host validates).
-  if (pkt->group_segment_size < __builtin_amdgcn_groupstaticsize() + (uint32_t)kDynLdsBytes) return;
   if (a.G <= 0 || a.G > kMaxGroups || a.K <= 0 || a.N <= 0) return;
   GG_LDS uint8_t* st = (GG_LDS uint8_t*)static_lds;
-  // The stage slots span both arrays: the dynamic window must follow the static one directly.
-  if (lds_u32(dyn) != lds_u32(st) + (uint32_t)kStaticLdsBytes) return;
+  // The launch must provide the contracted dynamic LDS, and the stage slots span both arrays: the
+  // dynamic window must follow the static one directly. Otherwise out becomes NaN (poison_out).
+  if (pkt->group_segment_size < __builtin_amdgcn_groupstaticsize() + (uint32_t)kDynLdsBytes ||
+      lds_u32(dyn) != lds_u32(st) + (uint32_t)kStaticLdsBytes) {
+    poison_out(a);
+    return;
+  }
   if (wide_tiles(a.N, false))
     persistent_body<kAE5M2, 384>(a, st);
   else
@@ -386,14 +411,28 @@ __device__ __forceinline__ void persistent_entry(const Args& a, GG_LDS uint8_t* 
 // Kernel entry point with the reference's 16-argument / 96-byte kernarg for the persistent kernel
 // (6 pointers; 8 x i32 G, N, K, stride_am, stride_bg, stride_bn, stride_cm, stride_cn at offsets
 // 48-76; two unused scratch pointers at 80 and 88; reference bench.py:312-337).
+#define GGEMM_PERSISTENT_PARAMS                                                                         \
+  const uint8_t *a, const uint8_t *b, uint16_t *c, const float *a_scale, const float *b_scale,          \
+      const int64_t *group_offs, int G, int N, int K, int stride_am, int stride_bg, int stride_bn,      \
+      int stride_cm, int stride_cn, void *global_scratch, void *profile_scratch
+
 #define GGEMM_DEFINE_PERSISTENT_KERNEL(NAME, AE5M2)                                                      \
-  extern "C" __global__ __launch_bounds__(ggemm::kThreads) void NAME(                                   \
-      const uint8_t* a, const uint8_t* b, uint16_t* c, const float* a_scale, const float* b_scale,     \
-      const int64_t* group_offs, int G, int N, int K, int stride_am, int stride_bg, int stride_bn,      \
-      int stride_cm, int stride_cn, void* global_scratch, void* profile_scratch) {                     \
+  extern "C" __global__ __launch_bounds__(ggemm::kThreads) void NAME(GGEMM_PERSISTENT_PARAMS) {          \
     extern __shared__ __attribute__((aligned(1024))) uint8_t ggemm_dyn_lds[];                           \
     ggemm::nt::Args args{a, b, c, a_scale, b_scale, group_offs, G, N, K,                                 \
-                         stride_am, stride_bg, stride_bn, stride_cm, stride_cn};                         \
+                         stride_am, stride_bg, stride_bn, stride_cm, stride_cn, ggemm::nt::kMaxRow};     \
+    (void)global_scratch; (void)profile_scratch;                                                        \
+    ggemm::nt::persistent_entry<AE5M2>(args, (GG_LDS uint8_t*)ggemm_dyn_lds);                             \
+  }
+
+// Library kernel: the same 16 arguments plus M_total, the row count of A and C (offsets clamped to
+// [0, M_total] on the device).
+#define GGEMM_DEFINE_PERSISTENT_LIB_KERNEL(NAME, AE5M2)                                                  \
+  extern "C" __global__ __launch_bounds__(ggemm::kThreads) void NAME(GGEMM_PERSISTENT_PARAMS,            \
+                                                                     int64_t m_total) {                  \
+    extern __shared__ __attribute__((aligned(1024))) uint8_t ggemm_dyn_lds[];                           \
+    ggemm::nt::Args args{a, b, c, a_scale, b_scale, group_offs, G, N, K,                                 \
+                         stride_am, stride_bg, stride_bn, stride_cm, stride_cn, m_total};                \
     (void)global_scratch; (void)profile_scratch;                                                        \
     ggemm::nt::persistent_entry<AE5M2>(args, (GG_LDS uint8_t*)ggemm_dyn_lds);                             \
   }

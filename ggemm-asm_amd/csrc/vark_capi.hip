@@ -10,11 +10,11 @@
 #include "capi_common.h"
 #include "vark_kernel.h"
 
-GGEMM_DEFINE_TENSORWISE_KERNEL(_grouped_variable_k_gemm_kernel, false)
-GGEMM_DEFINE_TENSORWISE_KERNEL(_grouped_variable_k_gemm_kernel_k32, true)
+GGEMM_DEFINE_TENSORWISE_LIB_KERNEL(_grouped_variable_k_gemm_kernel, false, uint16_t, ggemm::kOutBF16)
+GGEMM_DEFINE_TENSORWISE_LIB_KERNEL(_grouped_variable_k_gemm_kernel_k32, true, uint16_t, ggemm::kOutBF16)
 GGEMM_DEFINE_MX_KERNEL(_grouped_variable_k_mxfp8_gemm_kernel)
-GGEMM_DEFINE_TENSORWISE_F32_KERNEL(_grouped_variable_k_gemm_kernel_f32, ggemm::kOutF32)
-GGEMM_DEFINE_TENSORWISE_F32_KERNEL(_grouped_variable_k_gemm_kernel_f32_acc, ggemm::kOutF32Acc)
+GGEMM_DEFINE_TENSORWISE_LIB_KERNEL(_grouped_variable_k_gemm_kernel_f32, false, float, ggemm::kOutF32)
+GGEMM_DEFINE_TENSORWISE_LIB_KERNEL(_grouped_variable_k_gemm_kernel_f32_acc, false, float, ggemm::kOutF32Acc)
 
 namespace {
 
@@ -44,20 +44,23 @@ int validate_common(const void* lhs, const void* rhs, const void* out, const voi
 
 extern "C" {
 
+// m_total: the token count group offsets are clamped to on the device (INT64_MAX for the entry
+// points with the reference's argument list, which carries none).
 static int launch_tensorwise(bool legacy, const void* lhs, const void* rhs, void* out, const float* lhs_scale,
                              const float* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
                              int32_t OUT_N, int32_t slm, int32_t srm, int32_t scg, int32_t scm, int32_t scn,
-                             void* stream) {
+                             int64_t m_total, void* stream) {
   int rc = validate_common(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, slm, srm, scg, scm,
                            scn);
   if (rc) return rc;
+  if (m_total < 0) return GGEMM_E_SHAPE;
   int cus = 0;
   rc = device_cus(&cus);
   if (rc) return rc;
   auto kern = legacy ? _grouped_variable_k_gemm_kernel_k32 : _grouped_variable_k_gemm_kernel;
   hipLaunchKernelGGL(kern, dim3(cus), dim3(ggemm::kThreads), ggemm::kDynLdsBytes, (hipStream_t)stream,
                      (const uint8_t*)lhs, (const uint8_t*)rhs, (uint16_t*)out, lhs_scale, rhs_scale, group_offs, G,
-                     OUT_M, OUT_N, slm, srm, scg, scm, scn, (void*)nullptr, (void*)nullptr);
+                     OUT_M, OUT_N, slm, srm, scg, scm, scn, (void*)nullptr, (void*)nullptr, m_total);
   return (int)hipGetLastError();
 }
 
@@ -66,7 +69,7 @@ int ggemm_vark_wgrad_fp8(const void* lhs, const void* rhs, void* out, const floa
                          int32_t stride_rhs_m, int32_t stride_cg, int32_t stride_cm, int32_t stride_cn,
                          void* stream) {
   return launch_tensorwise(false, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
-                           stride_rhs_m, stride_cg, stride_cm, stride_cn, stream);
+                           stride_rhs_m, stride_cg, stride_cm, stride_cn, INT64_MAX, stream);
 }
 
 int ggemm_vark_wgrad_fp8_k32(const void* lhs, const void* rhs, void* out, const float* lhs_scale,
@@ -74,20 +77,22 @@ int ggemm_vark_wgrad_fp8_k32(const void* lhs, const void* rhs, void* out, const 
                              int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
                              int32_t stride_cm, int32_t stride_cn, void* stream) {
   return launch_tensorwise(true, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
-                           stride_rhs_m, stride_cg, stride_cm, stride_cn, stream);
+                           stride_rhs_m, stride_cg, stride_cm, stride_cn, INT64_MAX, stream);
 }
 
 int ggemm_vark_wgrad_fp8_out(const void* lhs, const void* rhs, void* out, const float* lhs_scale,
                              const float* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
                              int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
-                             int32_t stride_cm, int32_t stride_cn, int32_t out_mode, void* stream) {
+                             int32_t stride_cm, int32_t stride_cn, int32_t out_mode, int64_t M_total,
+                             void* stream) {
   if (out_mode == GGEMM_OUT_BF16)
     return launch_tensorwise(false, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
-                             stride_rhs_m, stride_cg, stride_cm, stride_cn, stream);
+                             stride_rhs_m, stride_cg, stride_cm, stride_cn, M_total, stream);
   if (out_mode != GGEMM_OUT_F32 && out_mode != GGEMM_OUT_F32_ACCUM) return GGEMM_E_FORMAT;
   int rc = validate_common(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
                            stride_rhs_m, stride_cg, stride_cm, stride_cn);
   if (rc) return rc;
+  if (M_total < 0) return GGEMM_E_SHAPE;
   if (!aligned(out, 16)) return GGEMM_E_ALIGN;    // 16-byte fp32 row segments
   int cus = 0;
   rc = device_cus(&cus);
@@ -95,7 +100,8 @@ int ggemm_vark_wgrad_fp8_out(const void* lhs, const void* rhs, void* out, const 
   auto kern = out_mode == GGEMM_OUT_F32 ? _grouped_variable_k_gemm_kernel_f32 : _grouped_variable_k_gemm_kernel_f32_acc;
   hipLaunchKernelGGL(kern, dim3(cus), dim3(ggemm::kThreads), ggemm::kDynLdsBytes, (hipStream_t)stream,
                      (const uint8_t*)lhs, (const uint8_t*)rhs, (float*)out, lhs_scale, rhs_scale, group_offs, G, OUT_M,
-                     OUT_N, stride_lhs_m, stride_rhs_m, stride_cg, stride_cm, stride_cn, (void*)nullptr, (void*)nullptr);
+                     OUT_N, stride_lhs_m, stride_rhs_m, stride_cg, stride_cm, stride_cn, (void*)nullptr, (void*)nullptr,
+                     M_total);
   return (int)hipGetLastError();
 }
 
@@ -103,10 +109,11 @@ int ggemm_vark_wgrad_mxfp8(const void* lhs, const void* rhs, void* out, const ui
                            const uint8_t* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
                            int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
                            int32_t stride_cm, int32_t stride_cn, int32_t stride_lhs_scale, int32_t stride_rhs_scale,
-                           void* stream) {
+                           int64_t M_total, void* stream) {
   int rc = validate_common(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
                            stride_rhs_m, stride_cg, stride_cm, stride_cn);
   if (rc) return rc;
+  if (M_total < 0) return GGEMM_E_SHAPE;
   if (stride_lhs_scale < OUT_M || stride_rhs_scale < OUT_N || stride_lhs_scale % 16 || stride_rhs_scale % 16)
     return GGEMM_E_STRIDE;
   if (!aligned(lhs_scale, 16) || !aligned(rhs_scale, 16)) return GGEMM_E_ALIGN;
@@ -116,7 +123,7 @@ int ggemm_vark_wgrad_mxfp8(const void* lhs, const void* rhs, void* out, const ui
   hipLaunchKernelGGL(_grouped_variable_k_mxfp8_gemm_kernel, dim3(cus), dim3(ggemm::kThreads), ggemm::kDynLdsBytes,
                      (hipStream_t)stream, (const uint8_t*)lhs, (const uint8_t*)rhs, (uint16_t*)out, lhs_scale,
                      rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m, stride_rhs_m, stride_cg, stride_cm,
-                     stride_cn, stride_lhs_scale, stride_rhs_scale, (void*)nullptr, (void*)nullptr);
+                     stride_cn, stride_lhs_scale, stride_rhs_scale, (void*)nullptr, (void*)nullptr, M_total);
   return (int)hipGetLastError();
 }
 

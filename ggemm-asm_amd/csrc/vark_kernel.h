@@ -364,7 +364,15 @@ struct VarKArgs {
   int stride_lhs_m, stride_rhs_m;
   int stride_cg, stride_cm, stride_cn;
   int stride_lhs_scale, stride_rhs_scale;  // MX only
+  // Token count of LHS/RHS: group offsets are clamped to [0, m_total] on the device, so no load
+  // leaves the tensors whatever group_offs holds. INT64_MAX from the drop-in code object, whose
+  // kernarg carries no token count (reference launcher.cpp:16-33); the library passes the real one.
+  int64_t m_total;
 };
+
+__device__ __forceinline__ int64_t clamp_off(int64_t o, int64_t m_total) {
+  return o < 0 ? 0 : (o > m_total ? m_total : o);
+}
 
 struct Tile {
   int g, m0, n0, nsteps;
@@ -447,9 +455,11 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 // Groups are sorted (and their offsets kept in LDS, so the tile loop reads them there instead of
 // issuing a global load whose wait would drain the prefetched stage) when G <= kMaxSortG and every
 // offset fits 31 bits; otherwise natural order with offsets read from memory.
-template <int kTN, int kK, int kEpiW = 1>
+// kTM / kNT: tile height (OUT_M) and workgroup threads of the calling kernel.
+template <int kTN, int kK, int kEpiW = 1, int kTM = kTileM, int kNT = kThreads>
 __device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_order, GG_LDS int* s_kb,
                                             GG_LDS int* s_flag, GG_LDS int64_t* s_bound) {
+  constexpr int kNW = kNT / 64;
   Sched S;
   const hsa_kernel_dispatch_packet_t* pkt = dispatch_packet();
   const int num_wg = (int)((pkt->grid_size_x + pkt->workgroup_size_x - 1) / pkt->workgroup_size_x);
@@ -460,16 +470,16 @@ __device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_ord
   if (S.sorted) {
     if (tid == 0) *s_flag = 0;
     __syncthreads();
-    for (int g = tid; g <= G; g += kThreads) {
-      const int64_t o = a.group_offs[g];
-      if (o < 0 || o > 0x7fffffff) *s_flag = 1;
+    for (int g = tid; g <= G; g += kNT) {
+      const int64_t o = clamp_off(a.group_offs[g], a.m_total);
+      if (o > 0x7fffffff) *s_flag = 1;
       s_kb[g] = (int)o;
     }
     __syncthreads();
     S.sorted = *s_flag == 0;
   }
   if (S.sorted) {
-    for (int g = tid; g < G; g += kThreads) {
+    for (int g = tid; g < G; g += kNT) {
       const int my = group_size(s_kb, g);
       int rank = 0;
       for (int h = 0; h < G; ++h) {
@@ -481,7 +491,7 @@ __device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_ord
     __syncthreads();
   }
 
-  S.n_tm = (a.OUT_M + kTileM - 1) / kTileM;
+  S.n_tm = (a.OUT_M + kTM - 1) / kTM;
   S.n_tn = (a.OUT_N + kTN - 1) / kTN;
   S.tiles_per_group = S.n_tm * S.n_tn;
   const int64_t total = (int64_t)G * S.tiles_per_group;
@@ -524,7 +534,7 @@ __device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_ord
   GG_LDS uint64_t* s_pred = (GG_LDS uint64_t*)((GG_LDS uint8_t*)s_order + kPredOffset);
   const bool choose = S.sorted && n_xcd > 1;
   if (choose)
-    for (int sl = tid; sl < G; sl += kThreads) s_w[sl] = (group_size(s_kb, s_order[sl]) + kK - 1) / kK + kEpiW;
+    for (int sl = tid; sl < G; sl += kNT) s_w[sl] = (group_size(s_kb, s_order[sl]) + kK - 1) / kK + kEpiW;
   __syncthreads();
   // workgroup w's tiles under each deal; in the rounds deal, XCD x holds positions [32x, 32x + 32)
   // of a round, and a round's position p is followed by the next round's num_wg - 1 - p
@@ -540,7 +550,7 @@ __device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_ord
   bool rounds = false;
   if (choose) {
     uint64_t mx[2] = {0, 0};
-    for (int w = tid; w < 2 * num_wg; w += kThreads) {
+    for (int w = tid; w < 2 * num_wg; w += kNT) {
       const int d = w >= num_wg, q = w - d * num_wg;
       const uint64_t v = deal_weight(s_w, tpg, d ? rounds_deal(q) : slice_deal(q));
       mx[d] = v > mx[d] ? v : mx[d];
@@ -555,7 +565,7 @@ __device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_ord
     __syncthreads();
     uint64_t m0 = 0, m1 = 0;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < kNW; ++w) {
       m0 = s_pred[2 * w] > m0 ? s_pred[2 * w] : m0;
       m1 = s_pred[2 * w + 1] > m1 ? s_pred[2 * w + 1] : m1;
     }
@@ -575,7 +585,7 @@ __device__ __forceinline__ Sched make_sched(const VarKArgs& a, GG_LDS int* s_ord
   return S;
 }
 
-template <int kTN, int kK>
+template <int kTN, int kK, int kTM = kTileM>
 __device__ __forceinline__ Tile tile_at(const Sched& S, const VarKArgs& a, const GG_LDS int* s_order,
                                         const GG_LDS int* s_kb, int t) {
   constexpr int kBandN = 4;
@@ -588,7 +598,7 @@ __device__ __forceinline__ Tile tile_at(const Sched& S, const VarKArgs& a, const
   const int bw = min(kBandN, S.n_tn - band * kBandN);
   const int tm = r / bw;
   const int tn = band * kBandN + (r - tm * bw);
-  T.m0 = tm * kTileM;
+  T.m0 = tm * kTM;
   T.n0 = tn * kTN;
   // wave-uniform values in scalar registers either way
   T.g = __builtin_amdgcn_readfirstlane(T.g);
@@ -597,8 +607,8 @@ __device__ __forceinline__ Tile tile_at(const Sched& S, const VarKArgs& a, const
     T.kb = __builtin_amdgcn_readfirstlane(s_kb[T.g]);
     ke = __builtin_amdgcn_readfirstlane(s_kb[T.g + 1]);
   } else {
-    T.kb = uniform64(a.group_offs[T.g]);
-    ke = uniform64(a.group_offs[T.g + 1]);
+    T.kb = clamp_off(uniform64(a.group_offs[T.g]), a.m_total);
+    ke = clamp_off(uniform64(a.group_offs[T.g + 1]), a.m_total);
   }
   T.klen = ke > T.kb ? ke - T.kb : 0;
   T.nsteps = (int)((T.klen + kK - 1) / kK);
@@ -608,6 +618,29 @@ __device__ __forceinline__ Tile tile_at(const Sched& S, const VarKArgs& a, const
 // Output modes of the tensorwise kernel's epilogue: bf16 C (the reference contract), fp32 C, and
 // fp32 C accumulated in place (C += result: the main-grad accumulation of a training step).
 enum OutMode : int { kOutBF16 = 0, kOutF32 = 1, kOutF32Acc = 2 };
+
+// A launch that breaks the contract (dynamic LDS short of 64 KiB or not placed right after the
+// static array, more output tiles than 32-bit indices cover) computes nothing; it fills C[0:G]
+// with NaN instead (bf16 0x7FC0, fp32 0x7FC00000), the extent a valid launch writes, so the
+// mistake shows in the result: a caller that never re-zeroes C between launches (reference
+// launcher.cpp:108,163-169) would otherwise time stale results as a fast valid run. Rows are
+// dealt to workgroups round robin, columns to threads.
+template <int kOut>
+__device__ void poison_c(const VarKArgs& a) {
+  const hsa_kernel_dispatch_packet_t* pkt = dispatch_packet();
+  const int64_t num_wg = (pkt->grid_size_x + pkt->workgroup_size_x - 1) / pkt->workgroup_size_x;
+  const int64_t rows = (int64_t)a.G * a.OUT_M;
+  for (int64_t r = blockIdx.x; r < rows; r += num_wg) {
+    const int64_t g = r / a.OUT_M, m = r - g * a.OUT_M;
+    const int64_t base = g * a.stride_cg + m * a.stride_cm;
+    for (int n = threadIdx.x; n < a.OUT_N; n += (int)pkt->workgroup_size_x) {
+      if constexpr (kOut == kOutBF16)
+        static_cast<uint16_t*>(a.out)[base + (int64_t)n * a.stride_cn] = 0x7fc0u;
+      else
+        static_cast<uint32_t*>(a.out)[base + (int64_t)n * a.stride_cn] = 0x7fc00000u;
+    }
+  }
+}
 // Schedule weight of a tile's epilogue in 128-token stages (bf16: 1): an fp32 C tile stores twice
 // the bytes, and the accumulating epilogue also waits for the old values to arrive.
 constexpr int kEpiWF32 = 2, kEpiWF32Acc = 4;
@@ -631,7 +664,10 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
 
   const Sched S = make_sched<kTN, kKStep, kOut == kOutBF16 ? 1 : kOut == kOutF32 ? kEpiWF32 : kEpiWF32Acc>(
       a, s_order, s_kb, s_flag, s_bound);
-  if (!S.valid) return;
+  if (!S.valid) {
+    poison_c<kOut>(a);
+    return;
+  }
   auto tile_at_ = [&](int t) { return tile_at<kTN, kKStep>(S, a, s_order, s_kb, t); };
 
   float alpha = 1.0f;
@@ -958,7 +994,10 @@ __device__ __forceinline__ void vark_body32(const VarKArgs& a, GG_LDS uint8_t* l
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   const Sched S = make_sched<kTN, kKStep>(a, s_order, s_kb, s_flag, s_bound);
-  if (!S.valid) return;
+  if (!S.valid) {
+    poison_c<kOutBF16>(a);
+    return;
+  }
 
   const int wm = wave & 1;   // wave row (OUT_M) in the 2 x 4 wave grid
   const int wn = wave >> 1;  // wave column (OUT_N)
@@ -1123,12 +1162,15 @@ template <bool kMX, bool kLegacyK32, int kOut = kOutBF16>
 __device__ __forceinline__ void vark_entry(const VarKArgs& a, GG_LDS uint8_t* dyn) {
   __shared__ __attribute__((aligned(1024))) uint8_t static_lds[kStaticLdsBytes];
   const hsa_kernel_dispatch_packet_t* pkt = dispatch_packet();
-  // The launch must provide the contracted dynamic LDS; otherwise do nothing (host validates).
-  if (pkt->group_segment_size < __builtin_amdgcn_groupstaticsize() + (uint32_t)kDynLdsBytes) return;
   if (a.G <= 0) return;
   GG_LDS uint8_t* st = (GG_LDS uint8_t*)static_lds;
-  // The stage slots span both arrays: the dynamic window must follow the static one directly.
-  if (lds_u32(dyn) != lds_u32(st) + (uint32_t)kStaticLdsBytes) return;
+  // The launch must provide the contracted dynamic LDS, and the stage slots span both arrays: the
+  // dynamic window must follow the static one directly. Otherwise C becomes NaN (poison_c).
+  if (pkt->group_segment_size < __builtin_amdgcn_groupstaticsize() + (uint32_t)kDynLdsBytes ||
+      lds_u32(dyn) != lds_u32(st) + (uint32_t)kStaticLdsBytes) {
+    poison_c<kOut>(a);
+    return;
+  }
   if (wide_tiles(a.OUT_N, kMX)) {
     if constexpr (kMX)
       vark_body32(a, st);
@@ -1144,32 +1186,32 @@ __device__ __forceinline__ void vark_entry(const VarKArgs& a, GG_LDS uint8_t* dy
 // Kernel entry points. The tensorwise one keeps the reference's 16-argument / 96-byte kernarg
 // (6 pointers, 8 x i32 at offsets 48-76, two unused scratch pointers at 80 and 88) so code that
 // launches the reference code object drives it unchanged (reference launcher.cpp:16-33,123-171;
-// bench.py:364-413).
+// bench.py:364-413). That kernarg carries no token count, so group offsets are only clamped at 0.
+#define GGEMM_VARK_TW_PARAMS(CT)                                                                        \
+  const uint8_t *lhs, const uint8_t *rhs, CT *out, const float *lhs_scale, const float *rhs_scale,     \
+      const int64_t *group_offs, int G, int OUT_M, int OUT_N, int stride_lhs_m, int stride_rhs_m,        \
+      int stride_cg, int stride_cm, int stride_cn, void *global_scratch, void *profile_scratch
+
 #define GGEMM_DEFINE_TENSORWISE_KERNEL(NAME, LEGACY)                                                    \
-  extern "C" __global__ __launch_bounds__(ggemm::kThreads) void NAME(                                   \
-      const uint8_t* lhs, const uint8_t* rhs, uint16_t* out, const float* lhs_scale,                    \
-      const float* rhs_scale, const int64_t* group_offs, int G, int OUT_M, int OUT_N,                    \
-      int stride_lhs_m, int stride_rhs_m, int stride_cg, int stride_cm, int stride_cn,                    \
-      void* global_scratch, void* profile_scratch) {                                                     \
+  extern "C" __global__ __launch_bounds__(ggemm::kThreads) void NAME(GGEMM_VARK_TW_PARAMS(uint16_t)) {  \
     extern __shared__ __attribute__((aligned(1024))) uint8_t ggemm_dyn_lds[];                           \
     ggemm::VarKArgs a{lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N,                  \
-                      stride_lhs_m, stride_rhs_m, stride_cg, stride_cm, stride_cn, 0, 0};                \
+                      stride_lhs_m, stride_rhs_m, stride_cg, stride_cm, stride_cn, 0, 0, INT64_MAX};     \
     (void)global_scratch; (void)profile_scratch;                                                        \
     ggemm::vark_entry<false, LEGACY>(a, (GG_LDS uint8_t*)ggemm_dyn_lds);                                  \
   }
 
-// Tensorwise kernels with an fp32 output mode (kOutF32 / kOutF32Acc): same 16 arguments, C an fp32
-// tensor (strides in fp32 elements). Library entry points only; not part of the reference contract.
-#define GGEMM_DEFINE_TENSORWISE_F32_KERNEL(NAME, OUT)                                                   \
-  extern "C" __global__ __launch_bounds__(ggemm::kThreads) void NAME(                                   \
-      const uint8_t* lhs, const uint8_t* rhs, float* out, const float* lhs_scale, const float* rhs_scale, \
-      const int64_t* group_offs, int G, int OUT_M, int OUT_N, int stride_lhs_m, int stride_rhs_m,        \
-      int stride_cg, int stride_cm, int stride_cn, void* global_scratch, void* profile_scratch) {        \
+// Library kernels: the same 16 arguments plus the token count M_total (group offsets clamped to
+// [0, M_total] on the device). CT / OUT: bf16 C (kOutBF16), or an fp32 C for the fp32 output
+// modes (kOutF32 / kOutF32Acc, strides in fp32 elements).
+#define GGEMM_DEFINE_TENSORWISE_LIB_KERNEL(NAME, LEGACY, CT, OUT)                                       \
+  extern "C" __global__ __launch_bounds__(ggemm::kThreads) void NAME(GGEMM_VARK_TW_PARAMS(CT),           \
+                                                                     int64_t m_total) {                  \
     extern __shared__ __attribute__((aligned(1024))) uint8_t ggemm_dyn_lds[];                           \
     ggemm::VarKArgs a{lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N,                  \
-                      stride_lhs_m, stride_rhs_m, stride_cg, stride_cm, stride_cn, 0, 0};                \
+                      stride_lhs_m, stride_rhs_m, stride_cg, stride_cm, stride_cn, 0, 0, m_total};       \
     (void)global_scratch; (void)profile_scratch;                                                        \
-    ggemm::vark_entry<false, false, OUT>(a, (GG_LDS uint8_t*)ggemm_dyn_lds);                              \
+    ggemm::vark_entry<false, LEGACY, OUT>(a, (GG_LDS uint8_t*)ggemm_dyn_lds);                             \
   }
 
 #define GGEMM_DEFINE_MX_KERNEL(NAME)                                                                    \
@@ -1177,11 +1219,12 @@ __device__ __forceinline__ void vark_entry(const VarKArgs& a, GG_LDS uint8_t* dy
       const uint8_t* lhs, const uint8_t* rhs, uint16_t* out, const uint8_t* lhs_scale,                  \
       const uint8_t* rhs_scale, const int64_t* group_offs, int G, int OUT_M, int OUT_N,                  \
       int stride_lhs_m, int stride_rhs_m, int stride_cg, int stride_cm, int stride_cn,                    \
-      int stride_lhs_scale, int stride_rhs_scale, void* global_scratch, void* profile_scratch) {         \
+      int stride_lhs_scale, int stride_rhs_scale, void* global_scratch, void* profile_scratch,           \
+      int64_t m_total) {                                                                                 \
     extern __shared__ __attribute__((aligned(1024))) uint8_t ggemm_dyn_lds[];                           \
     ggemm::VarKArgs a{lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N,                  \
                       stride_lhs_m, stride_rhs_m, stride_cg, stride_cm, stride_cn,                      \
-                      stride_lhs_scale, stride_rhs_scale};                                              \
+                      stride_lhs_scale, stride_rhs_scale, m_total};                                     \
     (void)global_scratch; (void)profile_scratch;                                                        \
     ggemm::vark_entry<true, false>(a, (GG_LDS uint8_t*)ggemm_dyn_lds);                                    \
   }

@@ -1,8 +1,8 @@
 """Code-object launch harness: drives the build's `.co` files the way the reference drives its own.
 
 Mirrors the reference's HIP module path (reference bench.py:43-143 ``load_kernel`` /
-``_detect_kernel_name`` / ``unload_kernel``; bench.py:288-309,364-413 ``_pack_args`` /
-``prepare_variable_k_args`` / ``launch_variable_k_kernel``; bench.py:312-361
+``_detect_kernel_name`` / ``unload_kernel``; bench.py:288-309,364-413 the kernelParams array
+of ``prepare_variable_k_args`` / ``launch_variable_k_kernel``; bench.py:312-361
 ``prepare_persistent_args`` / ``launch_persistent_kernel``; launcher.cpp:16-33,123-171 the
 96-byte ``KernelArgs`` record passed with HIP_LAUNCH_PARAM_BUFFER_POINTER). It exists to show
 the build's code objects are drop-ins for that launch surface; the library entry points in
@@ -115,42 +115,75 @@ def unload_kernel(module) -> None:
     load_hip().hipModuleUnload(module)
 
 
+def _llvm_tool(name: str) -> str:
+    cand = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "llvm", "bin", name)
+    return cand if os.path.exists(cand) else name
+
+
+_INFO_KEYS = ("vgpr_count", "agpr_count", "sgpr_count", "vgpr_spill_count", "sgpr_spill_count",
+              "group_segment_fixed_size", "private_segment_fixed_size", "kernarg_segment_size",
+              "max_flat_workgroup_size", "wavefront_size")
+
+
+def kernel_info(co_path: str) -> dict:
+    """Resource usage of a code object built here, per kernel, the counterpart of the reference's
+    ``print_kernel_info`` (bench.py:544-589): registers, spills, LDS, scratch and kernarg bytes from
+    the AMDGPU metadata note (llvm-readelf --notes), plus instruction and MFMA counts from the
+    disassembly (llvm-objdump). Only for this build's own code objects."""
+    import re
+    import subprocess
+    notes = subprocess.run([_llvm_tool("llvm-readelf"), "--notes", co_path], capture_output=True, text=True,
+                           timeout=60).stdout
+    kernels = {}
+    for chunk in re.split(r"\n\s*- \.agpr_count:", notes)[1:]:
+        chunk = ".agpr_count:" + chunk
+        name = re.search(r"\.name:\s+(\S+)", chunk).group(1)
+        info = {k: int(m.group(1)) for k in _INFO_KEYS
+                if (m := re.search(rf"\.{k}:\s+(\d+)", chunk))}
+        kernels[name] = info
+    dis = subprocess.run([_llvm_tool("llvm-objdump"), "-d", "--mcpu=gfx950", co_path], capture_output=True, text=True,
+                         timeout=120).stdout
+    current = None
+    for line in dis.splitlines():
+        m = re.match(r"^[0-9a-f]+ <(\S+)>:", line)
+        if m:
+            current = kernels.setdefault(m.group(1), {})
+            current.update(instructions=0, mfma=0, s_nop=0, lds_dma=0)
+            continue
+        ins = line.split("//")[0].strip()
+        if current is None or not ins or not line[:1].isspace():
+            continue
+        current["instructions"] += 1
+        current["mfma"] += ins.startswith("v_mfma")
+        current["s_nop"] += ins.startswith("s_nop")
+        current["lds_dma"] += ins.startswith("buffer_load") and ins.endswith(" lds")
+    return {"file": co_path, "bytes": os.path.getsize(co_path), "kernels": kernels}
+
+
 def get_num_cus(device: int = 0) -> int:
     return torch.cuda.get_device_properties(device).multi_processor_count
 
 
-def _pack_args(args):
-    """16-entry kernelParams array (reference bench.py:296-309 packs the same way)."""
-    arr = (ctypes.c_void_p * len(args))()
-    storage = []
-    for i, a in enumerate(args):
-        if isinstance(a, ctypes.c_void_p):
-            p = ctypes.c_uint64(a.value or 0)
-        elif isinstance(a, ctypes.c_int32):
-            p = ctypes.c_int32(a.value)
-        else:
-            raise TypeError(f"unexpected argument type {type(a)}")
-        storage.append(p)
-        arr[i] = ctypes.cast(ctypes.pointer(p), ctypes.c_void_p)
-    return arr, storage
+# Byte offsets of the 16 kernarg fields (six pointers, eight int32, two scratch pointers; reference
+# launcher.cpp:16-33): hipModuleLaunchKernel's kernelParams entry i points at field i.
+_FIELD_OFFSETS = tuple(range(0, 48, 8)) + tuple(range(48, 80, 4)) + (80, 88)
 
 
-def _arg_list(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N):
-    P, I = (lambda t: ctypes.c_void_p(t.data_ptr())), (lambda v: ctypes.c_int32(int(v)))
-    return [P(lhs), P(rhs), P(out), P(lhs_scale), P(rhs_scale), P(group_offs),
-            I(G), I(OUT_M), I(OUT_N), I(lhs.stride(0)), I(rhs.stride(0)),
-            I(out.stride(0)), I(out.stride(1)), I(out.stride(2)),
-            ctypes.c_void_p(0), ctypes.c_void_p(0)]
+def _kernel_params(record: bytes):
+    """kernelParams array over one 96-byte kernarg record; the buffer must outlive the launch."""
+    buf = ctypes.create_string_buffer(record, KERNARG_SIZE)
+    base = ctypes.addressof(buf)
+    return (ctypes.c_void_p * len(_FIELD_OFFSETS))(*(base + o for o in _FIELD_OFFSETS)), buf
 
 
 def prepare_variable_k_args(func, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N,
                             num_sms, shared_mem=SHARED_MEM):
     """Closure launching with a kernelParams array on the null stream (bench.py:364-402)."""
     hip = load_hip()
-    packed, storage = _pack_args(_arg_list(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N))
+    params, storage = _kernel_params(kernarg_buffer(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N))
 
     def launch():
-        check_hip(hip.hipModuleLaunchKernel(func, num_sms, 1, 1, BLOCK, 1, 1, shared_mem, None, packed, None),
+        check_hip(hip.hipModuleLaunchKernel(func, num_sms, 1, 1, BLOCK, 1, 1, shared_mem, None, params, None),
                   "launching variable-K kernel")
 
     return launch, storage
@@ -163,22 +196,22 @@ def launch_variable_k_kernel(func, lhs, rhs, out, lhs_scale, rhs_scale, group_of
     launch()
 
 
-def _persistent_arg_list(a, b, out, a_scale, b_scale, group_offs, G, N, K):
-    """Reference bench.py:317-336: strides from the tensors (b as [G, N, K], out as [M, N])."""
-    P, I = (lambda t: ctypes.c_void_p(t.data_ptr())), (lambda v: ctypes.c_int32(int(v)))
-    return [P(a), P(b), P(out), P(a_scale), P(b_scale), P(group_offs),
-            I(G), I(N), I(K), I(a.stride(0)), I(b.stride(0)), I(b.stride(1)),
-            I(out.stride(0)), I(out.stride(1)), ctypes.c_void_p(0), ctypes.c_void_p(0)]
+def persistent_kernarg_buffer(a, b, out, a_scale, b_scale, group_offs, G, N, K) -> bytes:
+    """The persistent kernel's 96-byte record (reference bench.py:317-336): strides from the
+    tensors, b as [G, N, K], out as [M, N]."""
+    return struct.pack("<6Q8i2Q", a.data_ptr(), b.data_ptr(), out.data_ptr(), a_scale.data_ptr(),
+                       b_scale.data_ptr(), group_offs.data_ptr(), G, N, K, a.stride(0), b.stride(0),
+                       b.stride(1), out.stride(0), out.stride(1), 0, 0)
 
 
 def prepare_persistent_args(func, a, b, out, a_scale, b_scale, group_offs, G, N, K, num_sms,
                             shared_mem=SHARED_MEM):
     """Closure launching the persistent fwd/dgrad kernel on the null stream (bench.py:312-351)."""
     hip = load_hip()
-    packed, storage = _pack_args(_persistent_arg_list(a, b, out, a_scale, b_scale, group_offs, G, N, K))
+    params, storage = _kernel_params(persistent_kernarg_buffer(a, b, out, a_scale, b_scale, group_offs, G, N, K))
 
     def launch():
-        check_hip(hip.hipModuleLaunchKernel(func, num_sms, 1, 1, BLOCK, 1, 1, shared_mem, None, packed, None),
+        check_hip(hip.hipModuleLaunchKernel(func, num_sms, 1, 1, BLOCK, 1, 1, shared_mem, None, params, None),
                   "launching persistent kernel")
 
     return launch, storage

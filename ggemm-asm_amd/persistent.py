@@ -58,7 +58,8 @@ def transpose_b(b: torch.Tensor) -> torch.Tensor:
 
 def grouped_gemm_fp8_tensorwise(a: torch.Tensor, b: torch.Tensor, a_scale: torch.Tensor, b_scale: torch.Tensor,
                                 group_offs: torch.Tensor, trans_b: bool = True, out: torch.Tensor | None = None,
-                                *, a_format: str | None = None, validate: bool = False) -> torch.Tensor:
+                                *, a_format: str | None = None, validate: bool = False,
+                                zero_tail: bool = False) -> torch.Tensor:
     """``out[r] = a_scale * b_scale * a[r] @ B[g]^T`` for ``offs[g] <= r < offs[g+1]`` (bf16).
 
     a: float8_e4m3fn (forward) or float8_e5m2 (data gradient) [M_total, K]; b: float8_e4m3fn
@@ -66,8 +67,10 @@ def grouped_gemm_fp8_tensorwise(a: torch.Tensor, b: torch.Tensor, a_scale: torch
     (``trans_b=False``: transposed into a contiguous [G, N, K] copy first by the library's byte
     transpose -- a weight quantized with ``quantize_fp8_tensorwise_transpose`` already has that
     layout); scales: single-element
-    fp32 tensors on the device; group_offs: int64 [G+1]. Rows outside ``[0, offs[G])`` of a new
-    ``out`` are left unwritten. ``validate=True`` checks group_offs on the host first (a sync).
+    fp32 tensors on the device; group_offs: int64 [G+1]. Rows outside ``[0, offs[G])`` of ``out``
+    are left unwritten, or set to zero with ``zero_tail=True`` (the library's device-side clear, no
+    sync: dropped tokens get exact zeros). ``validate=True`` checks group_offs on the host first (a
+    sync). Offsets past M_total are clamped to it on the device.
     """
     if a.dim() != 2 or b.dim() != 3:
         raise ValueError("a must be 2-D [M_total, K] and b 3-D [G, N, K] (trans_b) or [G, K, N]")
@@ -110,7 +113,11 @@ def grouped_gemm_fp8_tensorwise(a: torch.Tensor, b: torch.Tensor, a_scale: torch
         rc = lib.ggemm_persistent_fp8(
             a.data_ptr(), b.data_ptr(), out.data_ptr(), a_scale.data_ptr(), b_scale.data_ptr(), group_offs.data_ptr(),
             G, N, K, a.stride(0), b.stride(0), b.stride(1), out.stride(0), out.stride(1), fmt, M_total, _stream(dev))
-    _lib.check(rc, "ggemm_persistent_fp8")
+        _lib.check(rc, "ggemm_persistent_fp8")
+        if zero_tail:
+            rc = lib.ggemm_persistent_clear_tail(out.data_ptr(), N, out.stride(0), group_offs.data_ptr(), G, M_total,
+                                                 _stream(dev))
+            _lib.check(rc, "ggemm_persistent_clear_tail")
     return out
 
 

@@ -30,7 +30,17 @@ def _as_2d(x: torch.Tensor) -> torch.Tensor:
         x = x.reshape(-1, x.shape[-1])
     if x.stride(1) != 1:
         raise ValueError("x must be contiguous along its last dimension")
+    if x.shape[0] > 1 and x.stride(0) < x.shape[1]:
+        # overlapping rows (an expanded or otherwise aliased view): the kernels read rows * cols
+        # distinct elements, so hand them a copy that holds them
+        x = x.contiguous()
     return x
+
+
+def _row_stride(x2: torch.Tensor) -> int:
+    """Row stride to hand the library for a 2-D view from ``_as_2d``: its own, except for a view of
+    at most one row, whose stride(0) torch leaves arbitrary and the kernels never use."""
+    return x2.stride(0) if x2.shape[0] > 1 else x2.shape[1]
 
 
 def _ptr(x2: torch.Tensor) -> int:
@@ -58,7 +68,7 @@ def amax(x: torch.Tensor) -> torch.Tensor:
     x2 = _as_2d(x)
     out = torch.empty((), dtype=torch.float32, device=x.device)
     with torch.cuda.device(x.device):
-        rc = _lib.load().ggemm_quant_amax(_ptr(x2), _IN[x.dtype], x2.shape[0], x2.shape[1], max(x2.stride(0), x2.shape[1]),
+        rc = _lib.load().ggemm_quant_amax(_ptr(x2), _IN[x.dtype], x2.shape[0], x2.shape[1], _row_stride(x2),
                                           out.data_ptr(), _stream(x.device))
     _lib.check(rc, "ggemm_quant_amax")
     return out
@@ -94,8 +104,8 @@ def quantize_fp8_tensorwise(x: torch.Tensor, fmt: str = "e4m3", row_align: int |
     qp = q2 if q2.shape[0] > 0 else torch.empty((1, x.shape[-1]), dtype=dt, device=x.device)
     with torch.cuda.device(x.device):
         rc = _lib.load().ggemm_quant_fp8_tensorwise(
-            _ptr(x2), _IN[x.dtype], x2.shape[0], x2.shape[1], max(x2.stride(0), x2.shape[1]), code, qp.data_ptr(),
-            max(qp.stride(0), qp.shape[1]), scale.data_ptr(), am.data_ptr(), _stream(x.device))
+            _ptr(x2), _IN[x.dtype], x2.shape[0], x2.shape[1], _row_stride(x2), code, qp.data_ptr(),
+            _row_stride(qp), scale.data_ptr(), am.data_ptr(), _stream(x.device))
     _lib.check(rc, "ggemm_quant_fp8_tensorwise")
     return q, scale, am
 
@@ -152,6 +162,7 @@ def quantize_mxfp8_grouped(x: torch.Tensor, group_offs: torch.Tensor, fmt: str =
     _check(x, fmt)
     if x.dim() != 2 or x.stride(1) != 1:
         raise ValueError("x must be 2-D [M, N], contiguous along N")
+    x = _as_2d(x)
     if group_offs.dtype != torch.int64 or group_offs.dim() != 1 or group_offs.numel() < 2:
         raise ValueError("group_offs must be int64 [G+1]")
     if group_offs.device != x.device:
@@ -165,7 +176,7 @@ def quantize_mxfp8_grouped(x: torch.Tensor, group_offs: torch.Tensor, fmt: str =
     padded = torch.empty(G + 1, dtype=torch.int64, device=x.device)
     with torch.cuda.device(x.device):
         rc = _lib.load().ggemm_quant_mxfp8_grouped(
-            _ptr(x), _IN[x.dtype], M, N, max(x.stride(0), N), group_offs.data_ptr(), G, code, q.data_ptr(),
+            _ptr(x), _IN[x.dtype], M, N, _row_stride(x), group_offs.data_ptr(), G, code, q.data_ptr(),
             q.stride(0), rows_out, scales.data_ptr(), scales.stride(0), padded.data_ptr(), _stream(x.device))
     _lib.check(rc, "ggemm_quant_mxfp8_grouped")
     return q, scales, padded

@@ -4,8 +4,9 @@
 ``grouped_gemm_fp8_tensorwise_variable_k_triton_kernel(lhs, rhs, lhs_scale, rhs_scale,
 group_offs)`` (reference bench.py:241-246, 262-269): same argument order and meaning, a new
 bf16 ``[G, OUT_M, OUT_N]`` tensor as the result. The launch goes through
-``ggemm_vark_wgrad_fp8`` in libggemm_vark.so on torch's current stream; there is no
-fallback: a missing library or a non-gfx950 device raises.
+``ggemm_vark_wgrad_fp8_out`` in libggemm_vark.so on torch's current stream, bounded by the
+tensors' token count (group offsets past it are clamped on the device); there is no fallback: a
+missing library or a non-gfx950 device raises.
 """
 from __future__ import annotations
 
@@ -102,23 +103,27 @@ def grouped_gemm_fp8_tensorwise_variable_k(lhs: torch.Tensor, rhs: torch.Tensor,
         _validate_offsets(group_offs, M_total, mx=False)
     lhs, rhs = _nonempty(lhs), _nonempty(rhs)
     lib = _lib.load()
-    if out_dtype == torch.float32:
-        if mfma != "k128":
-            raise ValueError("the fp32 output modes use the K=128 MFMA kernel")
-        mode = 2 if accumulate else 1
+    if mfma == "k128":
+        mode = 2 if accumulate else (1 if out_dtype == torch.float32 else 0)
         with torch.cuda.device(lhs.device):
             rc = lib.ggemm_vark_wgrad_fp8_out(
                 lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), lhs_scale.data_ptr(), rhs_scale.data_ptr(),
                 group_offs.data_ptr(), G, OUT_M, OUT_N, lhs.stride(0), rhs.stride(0), out.stride(0), out.stride(1),
-                out.stride(2), mode, _stream(lhs.device))
+                out.stride(2), mode, M_total, _stream(lhs.device))
         _lib.check(rc, "ggemm_vark_wgrad_fp8_out")
         return out
-    fn = {"k128": lib.ggemm_vark_wgrad_fp8, "k32": lib.ggemm_vark_wgrad_fp8_k32}[mfma]
+    if mfma != "k32":
+        raise ValueError("mfma must be 'k128' or 'k32'")
+    if out_dtype == torch.float32:
+        raise ValueError("the fp32 output modes use the K=128 MFMA kernel")
+    # the K=32 kernel keeps the reference's argument list (no token count): offsets must end
+    # within the tensors, as with the reference kernel
     with torch.cuda.device(lhs.device):
-        rc = fn(lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), lhs_scale.data_ptr(), rhs_scale.data_ptr(),
-                group_offs.data_ptr(), G, OUT_M, OUT_N, lhs.stride(0), rhs.stride(0), out.stride(0),
-                out.stride(1), out.stride(2), _stream(lhs.device))
-    _lib.check(rc, "ggemm_vark_wgrad_fp8" if mfma == "k128" else "ggemm_vark_wgrad_fp8_k32")
+        rc = lib.ggemm_vark_wgrad_fp8_k32(
+            lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), lhs_scale.data_ptr(), rhs_scale.data_ptr(),
+            group_offs.data_ptr(), G, OUT_M, OUT_N, lhs.stride(0), rhs.stride(0), out.stride(0), out.stride(1),
+            out.stride(2), _stream(lhs.device))
+    _lib.check(rc, "ggemm_vark_wgrad_fp8_k32")
     return out
 
 
@@ -150,7 +155,7 @@ def grouped_gemm_mxfp8_variable_k(lhs: torch.Tensor, rhs: torch.Tensor, lhs_scal
         rc = lib.ggemm_vark_wgrad_mxfp8(
             lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), lhs_scale.data_ptr(), rhs_scale.data_ptr(),
             group_offs.data_ptr(), G, OUT_M, OUT_N, lhs.stride(0), rhs.stride(0), out.stride(0), out.stride(1),
-            out.stride(2), lhs_scale.stride(0), rhs_scale.stride(0), _stream(lhs.device))
+            out.stride(2), lhs_scale.stride(0), rhs_scale.stride(0), M_total, _stream(lhs.device))
     _lib.check(rc, "ggemm_vark_wgrad_mxfp8")
     return out
 

@@ -39,7 +39,10 @@ extern "C" {
  *   a_scale / b_scale: fp32 scalars; group_offs: int64 [G+1], offs[0] = 0, non-decreasing,
  *   offs[G] <= M_total. Rows of out outside [0, offs[G]) are not written.
  * M_total (rows of a and out) is not part of the reference kernarg; it bounds the 32-bit row and
- * tile indices here (M_total < 2^31 - 256, at most 2^30 output tiles of 192 x 320).
+ * tile indices here (M_total < 2^31 - 256, at most 2^30 output tiles of 192 x 320), and the
+ * kernel clamps every group offset to M_total on the device, so offsets past it read and write no
+ * row outside a and out (group g covers rows [min(offs[g], M_total), min(offs[g+1], M_total)));
+ * a negative or decreasing offset array writes nothing.
  * Requirements: 1 <= G <= GGEMM_PERSISTENT_MAX_GROUPS; N, K > 0 and multiples of 16; row strides
  * >= K and multiples of 16, stride_bg >= (N-1)*stride_bn + K and a multiple of 16, stride_cm >= N
  * and a multiple of 8; 192*stride_am and 384*stride_bn below 2^31 - 2^16; a, b, out 16-byte
@@ -48,6 +51,17 @@ int ggemm_persistent_fp8(const void* a, const void* b, void* out, const float* a
                          const int64_t* group_offs, int32_t G, int32_t N, int32_t K, int32_t stride_am,
                          int32_t stride_bg, int32_t stride_bn, int32_t stride_cm, int32_t stride_cn,
                          int32_t a_format, int64_t M_total, void* stream);
+
+/* Zeroes rows [min(offs[G], M_total), M_total) of out (bf16 [M_total, N], row stride stride_cm):
+ * the rows ggemm_persistent_fp8 leaves unwritten when routing drops tokens (offs[G] < M_total).
+ * offs[G] is read on the device, so the call needs no host synchronisation and can be captured in
+ * a graph; with no row past offs[G] it costs one small launch. No reference counterpart (the
+ * reference harness always routes every row, bench.py:205-218); the autograd layer's forward
+ * output and input gradient use it so that dropped rows are exact zeros. Requirements:
+ * 1 <= G <= GGEMM_PERSISTENT_MAX_GROUPS, N > 0 and a multiple of 16, 0 <= M_total < 2^31 - 256,
+ * stride_cm >= N and a multiple of 8, out 16-byte aligned. */
+int ggemm_persistent_clear_tail(void* out, int32_t N, int32_t stride_cm, const int64_t* group_offs, int32_t G,
+                                int64_t M_total, void* stream);
 
 /* Byte transpose of a batch of matrices: dst[b][c][r] = src[b][r][c] for b < batch, r < rows,
  * c < cols, element addresses src + b*src_bstride + r*src_rstride + c and dst + b*dst_bstride +

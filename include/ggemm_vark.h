@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define GGEMM_VARK_ABI_VERSION 2
+#define GGEMM_VARK_ABI_VERSION 3
 
 enum {
   GGEMM_OK = 0,
@@ -39,7 +39,9 @@ enum {
  * lhs: e4m3fn [M_total, OUT_M] (row stride stride_lhs_m); rhs: e5m2 [M_total, OUT_N]
  * (row stride stride_rhs_m); out: bf16 [G, OUT_M, OUT_N] (strides stride_cg, stride_cm,
  * stride_cn == 1); lhs_scale / rhs_scale: fp32 scalars; group_offs: int64 [G+1], offs[0] = 0,
- * non-decreasing. Every element of out[0:G] is written, empty groups with zeros.
+ * non-decreasing, offs[G] <= M_total (the caller's guarantee, as with the reference kernel: this
+ * argument list carries no token count; ggemm_vark_wgrad_fp8_out with GGEMM_OUT_BF16 is the same
+ * launch bounded by M_total). Every element of out[0:G] is written, empty groups with zeros.
  * Requirements: OUT_M, OUT_N, stride_lhs_m, stride_rhs_m multiples of 16; stride_cm,
  * stride_cg multiples of 4; lhs/rhs 16-byte aligned, out 8-byte aligned. */
 int ggemm_vark_wgrad_fp8(const void* lhs, const void* rhs, void* out, const float* lhs_scale,
@@ -65,26 +67,30 @@ int ggemm_vark_wgrad_fp8_k32(const void* lhs, const void* rhs, void* out, const 
  * training step (beta = 1), with the product rounded once to fp32 before the addition. No
  * reference counterpart: the reference kernel writes bf16 only (reference launcher.cpp:16-33);
  * the modes are the epilogue variants a training framework needs around it. Same arguments as
- * ggemm_vark_wgrad_fp8 with strides in elements of C's type; fp32 C must be 16-byte aligned,
- * stride_cm and stride_cg multiples of 4. Accumulate mode reads and writes every element of
- * C[0:G] once per launch (empty groups add zero), so a launch is deterministic. GGEMM_OUT_BF16
- * is the plain ggemm_vark_wgrad_fp8. */
+ * ggemm_vark_wgrad_fp8 with strides in elements of C's type, plus M_total >= 0, the token count
+ * of lhs and rhs: every group offset is clamped to [0, M_total] on the device, so no load leaves
+ * the tensors whatever group_offs holds (group g covers tokens [clamp(offs[g]), clamp(offs[g+1]))).
+ * fp32 C must be 16-byte aligned, stride_cm and stride_cg multiples of 4. Accumulate mode reads
+ * and writes every element of C[0:G] once per launch (empty groups add zero), so a launch is
+ * deterministic. GGEMM_OUT_BF16 is ggemm_vark_wgrad_fp8 bounded by M_total. */
 int ggemm_vark_wgrad_fp8_out(const void* lhs, const void* rhs, void* out, const float* lhs_scale,
                              const float* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
                              int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
-                             int32_t stride_cm, int32_t stride_cn, int32_t out_mode, void* stream);
+                             int32_t stride_cm, int32_t stride_cn, int32_t out_mode, int64_t M_total,
+                             void* stream);
 
 /* MXFP8 block-scaled grouped wgrad (no reference counterpart: the reference imports only the
  * tensorwise kernels, reference bench.py:241-246). lhs_scale: e8m0 bytes [ceil(M_total/32), OUT_M]
  * with row stride stride_lhs_scale; rhs_scale: e8m0 [ceil(M_total/32), OUT_N], row stride
  * stride_rhs_scale. Token block b (tokens 32b..32b+31) of a column is multiplied by
- * 2^(scale[b][col]-127). Every group must start at a multiple of 32 tokens (checked when
- * host_group_offs is given, otherwise the caller's responsibility). */
+ * 2^(scale[b][col]-127). Every group must start at a multiple of 32 tokens (ggemm_vark_check_offsets
+ * with mx = 1 checks a host copy; otherwise the caller's responsibility). Group offsets are
+ * clamped to [0, M_total] on the device, as in ggemm_vark_wgrad_fp8_out. */
 int ggemm_vark_wgrad_mxfp8(const void* lhs, const void* rhs, void* out, const uint8_t* lhs_scale,
                            const uint8_t* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
                            int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
                            int32_t stride_cm, int32_t stride_cn, int32_t stride_lhs_scale,
-                           int32_t stride_rhs_scale, void* stream);
+                           int32_t stride_rhs_scale, int64_t M_total, void* stream);
 
 /* Host-side check of a group-offset array (host memory, G+1 entries) against M_total; MX also
  * checks 32-token alignment of group starts. Mirrors the invariants the reference generator

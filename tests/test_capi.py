@@ -93,21 +93,25 @@ def test_validation_rejects(pkg, kw, rc):
 @pytest.mark.parametrize("mode,kw,rc", [
     (3, {}, -8), (-1, {}, -8), (1, dict(out=FAKE + 8), -4), (2, dict(out=FAKE + 8), -4), (1, dict(scn=2), -3),
     (2, dict(scm=5762), -3), (1, dict(lhs=0), -1),
+    # a negative token count, in every output mode
+    (0, dict(M=-1), -2), (1, dict(M=-1), -2), (2, dict(M=-5), -2),
 ])
 def test_fp32_out_validation_rejects(pkg, mode, kw, rc):
     lib = pkg.load_library()
     a = dict(lhs=FAKE, rhs=FAKE, out=FAKE, ls=FAKE, rs=FAKE, offs=FAKE, G=32, OUT_M=2880, OUT_N=5760,
-             slm=2880, srm=5760, scg=2880 * 5760, scm=5760, scn=1)
+             slm=2880, srm=5760, scg=2880 * 5760, scm=5760, scn=1, M=131072)
     a.update(kw)
     assert lib.ggemm_vark_wgrad_fp8_out(a["lhs"], a["rhs"], a["out"], a["ls"], a["rs"], a["offs"], a["G"], a["OUT_M"],
-                                        a["OUT_N"], a["slm"], a["srm"], a["scg"], a["scm"], a["scn"], mode, None) == rc
+                                        a["OUT_N"], a["slm"], a["srm"], a["scg"], a["scm"], a["scn"], mode, a["M"],
+                                        None) == rc
 
 
 def test_mx_validation_rejects(pkg):
     lib = pkg.load_library()
     args = [FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 4, 64, 128, 64, 128, 64 * 128, 128, 1]
-    assert lib.ggemm_vark_wgrad_mxfp8(*args, 60, 128, None) == -3      # scale stride < OUT_M
-    assert lib.ggemm_vark_wgrad_mxfp8(*args[:3], FAKE + 4, *args[4:], 64, 128, None) == -4
+    assert lib.ggemm_vark_wgrad_mxfp8(*args, 60, 128, 512, None) == -3      # scale stride < OUT_M
+    assert lib.ggemm_vark_wgrad_mxfp8(*args[:3], FAKE + 4, *args[4:], 64, 128, 512, None) == -4
+    assert lib.ggemm_vark_wgrad_mxfp8(*args, 64, 128, -1, None) == -2       # negative token count
 
 
 def test_python_op_refuses_cpu_tensors(pkg):
@@ -229,3 +233,17 @@ def test_m0_only_feeds_lds_dma(pkg):
             assert ins[k + 1].startswith("buffer_load_dwordx4") and ins[k + 1].rstrip().endswith("lds"), ins[k + 1]
             n_dma += 1
     assert n_dma >= 8
+
+
+def test_code_object_resources(pkg):
+    """The drop-in wgrad code object keeps its registers: no VGPR spills and no scratch (a spill
+    would put scratch traffic in the stage loop), at most 256 VGPRs (two 64-lane waves per SIMD,
+    the 512-thread launch contract), the 96 KiB static LDS, the 96-byte kernarg; and it is built on
+    the MFMA and LDS-DMA instructions it is designed around."""
+    from ggemm_asm_amd import harness
+    info = harness.kernel_info(pkg.CODE_OBJECT_PATH)["kernels"]["_grouped_variable_k_gemm_kernel"]
+    assert info["vgpr_spill_count"] == 0 and info["private_segment_fixed_size"] == 0, info
+    assert info["vgpr_count"] + info["agpr_count"] <= 256, info
+    assert info["group_segment_fixed_size"] == 98304 and info["kernarg_segment_size"] == 96, info
+    assert info["max_flat_workgroup_size"] == 512 and info["wavefront_size"] == 64, info
+    assert info["mfma"] >= 36 and info["lds_dma"] >= 9, info

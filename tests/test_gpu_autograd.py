@@ -95,3 +95,35 @@ def test_grouped_linear_fp8_main_grad(pkg, orc, cuda):
     f32 = pkg.grouped_gemm_fp8_tensorwise_variable_k(qx, qdy, sx, sdy, offs, out_dtype=torch.float32)
     torch.cuda.synchronize()
     assert torch.equal(mg, c0 + f32)
+
+
+def test_grouped_linear_fp8_dropped_tokens_are_zero(pkg, orc, orp, cuda):
+    """Routing that drops tokens (offs[G] < M): the rows past offs[G] of out and of x.grad are exact
+    zeros, also when the buffers torch hands out held other values before (the first call fills
+    the caching allocator's blocks with a full-routing run)."""
+    from ggemm_asm_amd.autograd import grouped_linear_fp8
+    lens, K, N, M = [100, 0, 157], 256, 384, 400
+    g = torch.Generator().manual_seed(17)
+    G = len(lens)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16).to(cuda).requires_grad_(True)
+    w = (torch.randn((G, N, K), generator=g) * 0.05).to(torch.bfloat16).to(cuda).requires_grad_(True)
+    dy = (torch.randn((M, N), generator=g) * 1e-2).to(torch.bfloat16).to(cuda)
+    full = torch.tensor([0, 100, 100, M], dtype=torch.int64, device=cuda)
+    _say("grouped linear fp8 with dropped tokens")
+    grouped_linear_fp8(x, w, full).backward(dy)      # leaves nonzero values in freed blocks
+    x.grad = None
+    w.grad = None
+    offs = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64, device=cuda)
+    out = grouped_linear_fp8(x, w, offs)
+    out.backward(dy)
+    torch.cuda.synchronize()
+    end = int(sum(lens))
+    assert bool((out[end:].view(torch.int16) == 0).all())
+    assert bool((x.grad[end:].view(torch.int16) == 0).all())
+    qx, sx, _ = pkg.quantize_fp8_tensorwise(x.detach(), "e4m3")
+    qw, sw, _ = pkg.quantize_fp8_tensorwise(w.detach(), "e4m3")
+    o = offs.cpu().numpy()
+    ref_out = orp.grouped_fp8(_bytes(qx)[:end], _bytes(qw), float(sx), float(sw), o, "e4m3")
+    m = orc.compare(pkg.as_bf16_bits(out)[:end], ref_out)
+    _say(f"forward rows within offs[G]: {m}")
+    assert orc.parity_ok(m)

@@ -2,10 +2,11 @@
 drop-in code object).
 
 Bar (from the north-star statement): cosine >= 0.99999, max relative error <= 2e-2 over
-|C| > 1e-3 * max|C|, empty groups exactly zero, no non-finite values. Small and ragged cases are
-compared in full with the oracle; full-size configurations are compared with the oracle on
-selected groups plus the size-independent row-sum identity
-``C[g] @ 1 = sL*sR * LHS_g^T (RHS_g @ 1)`` evaluated on every row of every group.
+|C| > 1e-3 * max|C|, empty groups exactly zero, no non-finite values. Every case, the full-size
+configurations included, compares its whole output with the oracle; the full-size ones also check
+the size-independent row-sum and column-sum identities
+``C[g] @ 1 = sL*sR * LHS_g^T (RHS_g @ 1)`` and ``1^T C[g] = sL*sR * (1^T LHS_g^T) RHS_g`` on every
+row and column of every group.
 """
 import os
 import re
@@ -62,26 +63,12 @@ def _rand_bytes_problem(lens, om, on, seed, mx=False, dist="normal"):
 
 
 def _error_bound_ok(orc, got_bits, lhs, rhs, offs, sl, sr, label, lsc=None, rsc=None):
-    """Rigorous check for adversarial inputs: |got - exact| <= 2^-8 |exact| (bf16 output rounding)
-    + the fp8-MFMA accumulation bound (oracle.fp8_mfma_error_bound) + fp32 scale rounding."""
-    L, R, o = lhs.numpy(), rhs.numpy(), offs.numpy()
-    lv = np.nan_to_num(orc.decode_e4m3(L).astype(np.float64))
-    rv = np.nan_to_num(orc.decode_e5m2(R).astype(np.float64))
-    if lsc is not None:
-        blk = np.arange(L.shape[0]) // 32
-        lv = lv * orc.decode_e8m0(lsc.numpy()[blk]).astype(np.float64)
-        rv = rv * orc.decode_e8m0(rsc.numpy()[blk]).astype(np.float64)
-        exact = orc.vark_wgrad_mxfp8_f32(L, R, lsc.numpy(), rsc.numpy(), o, acc_dtype=np.float64)
-        scale = 1.0
-    else:
-        exact = orc.vark_wgrad_tensorwise_f32(L, R, sl, sr, o, acc_dtype=np.float64)
-        scale = float(np.float32(sl)) * float(np.float32(sr))
-    bound = orc.fp8_mfma_error_bound(lv, rv, o, scale)
-    mag = orc.fp8_mfma_error_bound(np.abs(lv), np.abs(rv), o, scale)  # >= 2^-24 sum|t| scale terms
-    got = orc.bf16_bits_to_f32(got_bits).astype(np.float64)
-    lim = 2.0 ** -8 * np.abs(exact) + 1.01 * bound + 4 * 2.0 ** -24 * mag + 1e-38
-    viol = np.abs(got - exact) > lim
-    worst = float(np.max(np.abs(got - exact) / lim))
+    """Rigorous check for adversarial inputs (oracle.mfma_bound_violations, pinned on the CPU by
+    tests/test_oracle_mfma.py): |got - exact| <= 2^-8 |exact| (bf16 output rounding) + the fp8-MFMA
+    accumulation bound + fp32 scale rounding, on every element."""
+    viol, worst = orc.mfma_bound_violations(
+        orc.bf16_bits_to_f32(got_bits), lhs.numpy(), rhs.numpy(), offs.numpy(), sl, sr,
+        None if lsc is None else lsc.numpy(), None if rsc is None else rsc.numpy())
     _say(f"{label}: error-bound violations {int(viol.sum())} of {viol.size}, worst ratio {worst:.3f}")
     assert not viol.any()
 
@@ -359,31 +346,64 @@ def _rowsum_identity(pkg, p, out, dev):
     return worst
 
 
-def _oracle_groups(pkg, orc, p, out, groups):
-    """Oracle comparison of selected groups; the 1e-3 * max|C| threshold of the bar is taken over
-    the whole output tensor, as the bar defines it."""
+def _colsum_identity(pkg, p, out, dev):
+    """max over (g, n) of |sum_m C[m,n] - sL sR (sum_m L[k,m]) . R[k,n]| / (sum_m |C| + eps): the
+    column sums pin where each OUT_N column landed (the row sums pin the OUT_M rows)."""
+    worst = 0.0
+    offs = p.group_offs.cpu().tolist()
+    for g in range(p.G):
+        lo, hi = offs[g], offs[g + 1]
+        if hi == lo:
+            continue
+        c = out[g].float()
+        lhs_cols = c.sum(dim=0).double()
+        if p.is_mx:
+            blk = torch.arange(lo, hi, device=dev) // 32
+            L = p.lhs[lo:hi].view(torch.float8_e4m3fn).float() * torch.exp2(p.lhs_mx[blk].float() - 127)
+            R = p.rhs[lo:hi].view(torch.float8_e5m2).float() * torch.exp2(p.rhs_mx[blk].float() - 127)
+            rhs_cols = L.double().sum(dim=1) @ R.double()
+        else:
+            L = p.lhs[lo:hi].view(torch.float8_e4m3fn).double()
+            R = p.rhs[lo:hi].view(torch.float8_e5m2).double()
+            rhs_cols = (L.sum(dim=1) @ R) * p.lhs_scale * p.rhs_scale
+        denom = c.abs().sum(dim=0).double() + 1e-30
+        worst = max(worst, float(((lhs_cols - rhs_cols).abs() / denom).max()))
+    return worst
+
+
+def _oracle_whole(pkg, orc, p, out):
+    """Every group of the full-size output against the oracle, with the bar over the whole tensor
+    (cosine over all of C, the 1e-3 * max|C| threshold from the whole reference, as the reference's
+    own check takes it, reference bench.py:641-646); empty groups exactly zero."""
     offs = p.group_offs.cpu().numpy()
-    cmax = float(out.float().abs().max())
-    for g in groups:
+    L_all, R_all = p.lhs.cpu().numpy(), p.rhs.cpu().numpy()
+    if p.is_mx:
+        LS, RS = p.lhs_mx.cpu().numpy(), p.rhs_mx.cpu().numpy()
+    got = pkg.as_bf16_bits(out)
+    refs = []
+    for g in range(p.G):
         lo, hi = int(offs[g]), int(offs[g + 1])
-        sub_offs = np.array([0, hi - lo], dtype=np.int64)
-        L = p.lhs[lo:hi].cpu().numpy()
-        R = p.rhs[lo:hi].cpu().numpy()
+        sub = np.array([0, hi - lo], dtype=np.int64)
         if p.is_mx:
             b0, b1 = lo // 32, (hi + 31) // 32
-            ref = orc.vark_wgrad_mxfp8(L, R, p.lhs_mx[b0:b1].cpu().numpy(), p.rhs_mx[b0:b1].cpu().numpy(), sub_offs)
+            ref = orc.vark_wgrad_mxfp8(L_all[lo:hi], R_all[lo:hi], LS[b0:b1], RS[b0:b1], sub)[0]
         else:
-            ref = orc.vark_wgrad_tensorwise(L, R, p.lhs_scale, p.rhs_scale, sub_offs)
-        m = orc.compare(pkg.as_bf16_bits(out[g:g + 1]), ref, sub_offs, ref_absmax=cmax)
-        _say(f"{p.name} group {g} K={hi - lo}: {m}")
-        assert orc.parity_ok(m), (p.name, g, m)
+            ref = orc.vark_wgrad_tensorwise(L_all[lo:hi], R_all[lo:hi], p.lhs_scale, p.rhs_scale, sub)[0]
+        refs.append(ref)
+        if hi == lo:
+            assert np.all((got[g] & 0x7FFF) == 0), (p.name, "empty group", g)
+    amax = max(float(np.abs(orc.bf16_bits_to_f32(r)).max()) for r in refs)
+    m = orc.compare_parts(((got[g], refs[g]) for g in range(p.G)), amax)
+    _say(f"{p.name}: whole C ({p.G} groups) vs oracle: {m}")
+    assert orc.parity_ok(m), (p.name, m)
 
 
 @pytest.mark.parametrize("name", ["down_wgrad", "gate_up_wgrad", "gate_up_zipf", "gate_up_mx", "gate_up_reference_lens"])
 def test_full_size_config(pkg, orc, cuda, name):
-    """Full-size configurations. gate_up_zipf and gate_up_reference_lens (the reference's seed-42
-    exponential group sizes) are skewed enough that the kernel deals its tiles in boustrophedon
-    rounds rather than XCD-pair slices (tests/test_vark_schedule_host.py models the choice)."""
+    """Full-size configurations, the whole output against the oracle. gate_up_zipf and
+    gate_up_reference_lens (the reference's seed-42 exponential group sizes) are skewed enough that
+    the kernel deals its tiles in boustrophedon rounds rather than XCD-pair slices
+    (tests/test_vark_schedule_host.py models the choice)."""
     _say(f"full-size {name}")
     if name == "gate_up_reference_lens":
         p = pkg.inputs.make_problem("gate_up_wgrad", seed=0, device=cuda,
@@ -404,11 +424,10 @@ def test_full_size_config(pkg, orc, cuda, name):
     worst = _rowsum_identity(pkg, p, out, cuda)
     _say(f"{name}: row-sum identity worst relative residual {worst:.3e}")
     assert worst < 2 ** -6
-    lens = np.diff(p.group_offs.cpu().numpy())
-    order = np.argsort(-lens, kind="stable")
-    picks = {int(order[0]), int(order[len(order) // 2])}
-    picks |= {int(g) for g in np.nonzero((lens > 0) & (lens < 32))[0][:4]}
-    _oracle_groups(pkg, orc, p, out, sorted(picks))
+    worst = _colsum_identity(pkg, p, out, cuda)
+    _say(f"{name}: column-sum identity worst relative residual {worst:.3e}")
+    assert worst < 2 ** -6
+    _oracle_whole(pkg, orc, p, out)
 
 
 # ----------------------------------------------------------------------------- fp32 epilogues
@@ -480,3 +499,73 @@ def test_fp32_accumulate_full_size(pkg, orc, cuda, routing):
     torch.cuda.synchronize()
     assert torch.equal(acc, c0 + f32)
     assert torch.equal(f32.to(torch.bfloat16).view(torch.int16), bf.view(torch.int16))
+
+
+# ----------------------------------------------------------------------------- launch contract
+
+@pytest.mark.parametrize("kind", ["bf16", "f32", "f32_acc", "mx"])
+def test_offsets_past_token_count_are_clamped(pkg, orc, cuda, kind):
+    """Group offsets past M_total (the tensors' token count) are clamped on the device: lhs and
+    rhs are views of the first M rows of larger buffers whose extra rows hold 0x38 (1.0 / 0.5), so
+    any read past row M would change the result, which must equal the oracle on the clamped
+    offsets (a negative first offset clamps to 0; a group wholly past M is empty)."""
+    mx = kind == "mx"
+    M = 448 if mx else 457
+    offs = torch.tensor([0, 96, 96, 384, 640, 800] if mx else [-64, 100, 100, 400, 600, 800], dtype=torch.int64)
+    clamped = offs.clamp(min=0, max=M)
+    _say(f"wgrad offsets past M_total ({kind}): M={M} offs={offs.tolist()}")
+    lens = torch.diff(clamped).tolist()
+    lhs, rhs, _, sc, (sl, sr) = _rand_bytes_problem(lens, 208, 384, seed=41, mx=mx)
+    pad = 512
+    lhs_full = torch.cat([lhs, torch.full((pad, lhs.shape[1]), 0x38, dtype=torch.uint8)])
+    rhs_full = torch.cat([rhs, torch.full((pad, rhs.shape[1]), 0x38, dtype=torch.uint8)])
+    dl, dr = lhs_full.to(cuda)[:M], rhs_full.to(cuda)[:M]
+    if mx:
+        lsc = torch.cat([sc[0], torch.full((pad // 32, sc[0].shape[1]), 127, dtype=torch.uint8)])
+        rsc = torch.cat([sc[1], torch.full((pad // 32, sc[1].shape[1]), 127, dtype=torch.uint8)])
+        out = pkg.grouped_gemm_mxfp8_variable_k(dl, dr, lsc.to(cuda)[:M // 32], rsc.to(cuda)[:M // 32], offs.to(cuda))
+        torch.cuda.synchronize()
+        ref = orc.vark_wgrad_mxfp8(lhs.numpy(), rhs.numpy(), sc[0].numpy(), sc[1].numpy(), clamped.numpy())
+        _assert_parity(orc, pkg.as_bf16_bits(out), ref, clamped.numpy(), "clamp/mx")
+        return
+    s1 = torch.tensor(sl, dtype=torch.float32, device=cuda)
+    s2 = torch.tensor(sr, dtype=torch.float32, device=cuda)
+    if kind == "bf16":
+        out = pkg.grouped_gemm_fp8_tensorwise_variable_k(dl, dr, s1, s2, offs.to(cuda))
+        torch.cuda.synchronize()
+        ref = orc.vark_wgrad_tensorwise(lhs.numpy(), rhs.numpy(), sl, sr, clamped.numpy())
+        _assert_parity(orc, pkg.as_bf16_bits(out), ref, clamped.numpy(), "clamp/bf16")
+        return
+    c0 = torch.zeros((5, 208, 384), dtype=torch.float32, device=cuda)
+    out = pkg.grouped_gemm_fp8_tensorwise_variable_k(dl, dr, s1, s2, offs.to(cuda), out=c0,
+                                                     out_dtype=torch.float32, accumulate=kind == "f32_acc")
+    torch.cuda.synchronize()
+    ref = orc.vark_wgrad_tensorwise_f32(lhs.numpy(), rhs.numpy(), sl, sr, clamped.numpy(), acc_dtype=np.float64)
+    _f32_parity(orc, out.cpu().numpy(), ref, f"clamp/{kind}")
+    for g in (1, 4):
+        assert bool((out[g] == 0).all()), g
+
+
+@pytest.mark.parametrize("dyn_lds", [32768, 0])
+def test_code_object_short_dynamic_lds_writes_nan(pkg, cuda, dyn_lds):
+    """A launch with less than the contracted 64 KiB of dynamic LDS computes nothing and fills
+    C[0:G] with NaN (0x7FC0) instead of leaving it stale: the reference launcher never re-zeroes C
+    between launches (launcher.cpp:108,163-169), so a mis-launch must not time as a valid run. A
+    normal kernel exit, not a fault; a padded C shows nothing outside C[0:G] is written."""
+    from ggemm_asm_amd import harness
+    _say(f"wgrad code object with {dyn_lds} B dynamic LDS")
+    lhs, rhs, offs, _, _ = _rand_bytes_problem([96, 0, 160], 192, 384, seed=23)
+    dl, dr, do = lhs.to(cuda), rhs.to(cuda), offs.to(cuda)
+    s = torch.tensor(0.1, device=cuda)
+    big = torch.full((4, 200, 400), 0x1234, dtype=torch.int16, device=cuda)
+    out = big.view(torch.bfloat16)[:3, :192, :384]
+    module, func, _ = harness.load_kernel(pkg.CODE_OBJECT_PATH)
+    try:
+        harness.launch_variable_k_kernel(func, dl, dr, out, s, s, do, 3, 192, 384, harness.get_num_cus(0),
+                                         shared_mem=dyn_lds)
+        torch.cuda.synchronize()
+    finally:
+        harness.unload_kernel(module)
+    assert bool((out.view(torch.int16) == 0x7FC0).all())
+    big[:3, :192, :384] = 0x1234
+    assert bool((big == 0x1234).all())

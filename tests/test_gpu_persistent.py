@@ -4,8 +4,8 @@ the C ABI or the drop-in code objects).
 Bar (from the north-star statement, applied to this kernel): cosine >= 0.99999, max relative error
 <= 2e-2 over |C| > 1e-3 * max|C|, no non-finite values. Small and ragged cases are compared in full
 with the oracle; adversarial all-codes inputs against a rigorous error bound of the exact result;
-the full-size call sites with the oracle on selected groups plus the size-independent row-sum
-identity ``out[r] @ 1 = s_a s_b A[r] (B[g]^T 1)`` on every row.
+the full-size call sites with the oracle on every row plus the size-independent row-sum identity
+``out[r] @ 1 = s_a s_b A[r] (B[g]^T 1)`` on every row.
 """
 import numpy as np
 import pytest
@@ -306,18 +306,68 @@ def test_full_size_site(pkg, orc, orp, cuda, name):
     worst = _rowsum_identity(p, out, cuda)
     _say(f"{name}: row-sum identity worst relative residual {worst:.3e}")
     assert worst < 2 ** -6
-    # oracle on the smallest, a median and the largest group: first 400 and last 200 rows of each
+    # every row of every group against the oracle, the bar over the whole output
     offs = p.group_offs.cpu().numpy()
-    lens = np.diff(offs)
-    order = np.argsort(lens, kind="stable")
-    cmax = float(out.float().abs().max())
-    for g in sorted({int(order[0]), int(order[len(order) // 2]), int(order[-1])}):
+    a_all, b_all = p.a.cpu().numpy(), p.b.cpu().numpy()
+    got = pkg.as_bf16_bits(out)
+    refs = []
+    for g in range(p.G):
         lo, hi = int(offs[g]), int(offs[g + 1])
-        rows = np.unique(np.concatenate([np.arange(lo, min(hi, lo + 400)), np.arange(max(lo, hi - 200), hi)]))
-        a_rows = p.a[torch.from_numpy(rows).to(cuda)].cpu().numpy()
-        ref = orp.grouped_fp8(a_rows, p.b[g:g + 1].cpu().numpy(), p.a_scale, p.b_scale,
-                              np.array([0, rows.size]), p.a_format)
-        got = pkg.as_bf16_bits(out[torch.from_numpy(rows).to(cuda)])
-        m = orc.compare(got, ref, ref_absmax=cmax)
-        _say(f"{name} group {g} rows={hi - lo} (checked {rows.size}): {m}")
-        assert orc.parity_ok(m), (name, g, m)
+        refs.append(orp.grouped_fp8(a_all[lo:hi], b_all[g:g + 1], p.a_scale, p.b_scale,
+                                    np.array([0, hi - lo]), p.a_format))
+    amax = max(float(np.abs(orc.bf16_bits_to_f32(r)).max()) if r.size else 0.0 for r in refs)
+    m = orc.compare_parts(((got[offs[g]:offs[g + 1]], refs[g]) for g in range(p.G)), amax)
+    _say(f"{name}: all {int(offs[-1])} rows vs oracle: {m}")
+    assert orc.parity_ok(m), (name, m)
+
+
+def test_offsets_past_row_count_are_clamped(pkg, orc, orp, cuda):
+    """Group offsets past M_total (the rows of a and out) are clamped on the device: a and out are
+    views of the first M rows of larger buffers whose extra rows hold 0x38 (A) and a sentinel
+    (out); no row past M may be read (it would change the result) or written (the sentinel stays),
+    and the rows within M equal the oracle on the clamped offsets. zero_tail clears the rows past
+    the clamped offs[G] and only those."""
+    M, K, N = 457, 272, 384
+    offs = torch.tensor([0, 100, 100, 400, 600, 800], dtype=torch.int64)
+    clamped = offs.clamp(max=M).numpy()
+    _say(f"persistent offsets past M_total: M={M} offs={offs.tolist()}")
+    g = torch.Generator().manual_seed(31)
+    a_full = torch.full((M + 512, K), 0x38, dtype=torch.uint8)
+    a_full[:M] = torch.randn((M, K), generator=g).to(torch.float8_e4m3fn).view(torch.uint8)
+    b = torch.randn((5, N, K), generator=g).to(torch.float8_e4m3fn).view(torch.uint8)
+    da = a_full.to(cuda)[:M].view(torch.float8_e4m3fn)
+    s = torch.tensor(0.25, device=cuda)
+    for zero_tail in (False, True):
+        out_full = torch.full((M + 512, N), 0x1234, dtype=torch.int16, device=cuda)
+        out = out_full.view(torch.bfloat16)[:M]
+        pkg.grouped_gemm_fp8_tensorwise(da, b.to(cuda).view(torch.float8_e4m3fn), s, s, offs.to(cuda), out=out,
+                                        zero_tail=zero_tail)
+        torch.cuda.synchronize()
+        assert bool((out_full[M:] == 0x1234).all()), "a row past M_total was written"
+        ref = orp.grouped_fp8(a_full[:M].numpy(), b.numpy(), 0.25, 0.25, clamped, "e4m3")
+        m = orc.compare(pkg.as_bf16_bits(out)[:int(clamped[-1])], ref[:int(clamped[-1])])
+        _say(f"zero_tail={zero_tail}: {m}")
+        assert orc.parity_ok(m)
+
+
+def test_code_object_short_dynamic_lds_writes_nan(pkg, cuda):
+    """A launch with less than the contracted 64 KiB of dynamic LDS computes nothing and fills the
+    rows a valid launch writes, [0, offs[G]), with NaN (0x7FC0), so the mistake cannot pass for a
+    fast valid run; rows past offs[G] stay untouched. A normal kernel exit, not a fault."""
+    from ggemm_asm_amd import harness
+    M, K, N = 300, 256, 384
+    offs = torch.tensor([0, 120, 120, 250], dtype=torch.int64, device=cuda)
+    a = torch.zeros((M, K), dtype=torch.uint8, device=cuda)
+    b = torch.zeros((3, N, K), dtype=torch.uint8, device=cuda)
+    s = torch.tensor(1.0, device=cuda)
+    _say("persistent code object with 32 KiB dynamic LDS")
+    module, func, _ = harness.load_kernel(pkg.PERSISTENT_CODE_OBJECT_PATHS["e4m3"])
+    try:
+        out = torch.full((M, N), 0x1234, dtype=torch.int16, device=cuda)
+        harness.launch_persistent_kernel(func, a, b, out, s, s, offs, 3, N, K, harness.get_num_cus(0),
+                                         shared_mem=32768)
+        torch.cuda.synchronize()
+    finally:
+        harness.unload_kernel(module)
+    assert bool((out[:250] == 0x7FC0).all())
+    assert bool((out[250:] == 0x1234).all())

@@ -182,7 +182,8 @@ def test_mx_oracle_reduces_to_tensorwise_and_is_blockwise_linear(orc):
 # ----------------------------------------------------------------------------- C restatement
 
 def _c_oracle():
-    path = os.path.join(ROOT, "oracle", "_build", "libvark_oracle_c.so")
+    # GGEMM_ORACLE_C_LIBRARY: a variant build of vark_oracle.c (the host-sanitizer run)
+    path = os.environ.get("GGEMM_ORACLE_C_LIBRARY") or os.path.join(ROOT, "oracle", "_build", "libvark_oracle_c.so")
     if not os.path.exists(path):
         from oracle import build
         build.build_c()

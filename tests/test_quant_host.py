@@ -156,3 +156,22 @@ def _transpose_model(B, R, C, q_stride, t_stride):
 def test_transpose_tile_index_model(B, R, C, qs, ts):
     _transpose_model(B, R, C, qs, ts)
 
+
+
+def test_overlapping_rows_are_copied_not_read_past():
+    """An input whose rows overlap (an expanded view: stride 0) is copied before the library sees
+    it, and the row stride handed to the library is the tensor's own -- never a stride the view
+    does not have (the kernels read rows * cols distinct elements); a view of one row passes its
+    width (its stride(0) is arbitrary and unused)."""
+    import torch
+    from ggemm_asm_amd import quant
+    x = torch.randn(1, 256).expand(1024, 256)
+    x2 = quant._as_2d(x)
+    assert x2.is_contiguous() and x2.stride(0) == 256 and torch.equal(x2, x)
+    assert quant._row_stride(x2) == 256
+    y = torch.randn(64, 512)[:, :256]                  # padded rows: the stride is kept
+    assert quant._row_stride(quant._as_2d(y)) == 512
+    z = torch.randn(300, 1, 256).expand(300, 2, 256).reshape(-1, 256)   # reshape copies already
+    assert quant._row_stride(quant._as_2d(z)) == 256
+    one = torch.randn(1, 2, 256)[:, 0]                 # one row, stride(0) = 512
+    assert quant._row_stride(quant._as_2d(one)) == 256
