@@ -801,16 +801,82 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
       cur ^= 1;
     }
 
-    if constexpr (kOut != kOutBF16) {
-      // ---- fp32 epilogue: a lane's 4 consecutive columns of one C row are already a 16-byte
-      // row segment, so it stores them directly (no LDS staging). Accumulate mode reads the old
-      // values one m-block ahead of their use.
+    if constexpr (kOut != kOutBF16 && kTN == 384) {
+      // ---- fp32 epilogue, 384-wide tiles. Lane holds C[m][n..n+3] for m = m0+96wm+16i+s16,
+      // n = n0+96wn+16j+4q: 64-byte pieces of 16 rows. Each m-block goes through a private 6 KiB
+      // region of the freed slot (16 rows of 96 floats, 16-byte chunk c of row r at c ^ ((r>>1)&7))
+      // and comes back as whole 128-byte lines: instruction (h, k) gives lane l row (l>>3) + 8h,
+      // chunk (l&7) + 8k. Both the 16 rows of a write and the 2 rows x 8 chunks of a read then hit
+      // 16 distinct bank groups. So each old-value load and each store covers 8 whole lines of C
+      // (a wave's 96 floats of a row start on a line boundary), half the line requests of storing
+      // the 64-byte pieces directly. Accumulate mode loads the old values one m-block ahead. One
+      // barrier first: every wave must be done with the last stage.
+      lds_barrier();
+      GG_LDS uint8_t* stg = (cur ? lm.L[0] : lm.L[1]) + wave * C::EpiRegion;
+      int el = lane;
+      asm volatile("" : "+v"(el));   // keeps the per-lane address math out of the stage loop
+      // write side: chunk 4j+q of row s16 sits at 64 (j ^ ub) + 16 (q ^ (u & 3)), u = (s16>>1)&7
+      const int u_w = (s16 >> 1) & 7, ub = (u_w >> 2) & 1;
+      const int wb = s16 * 384 + 16 * (q ^ (u_w & 3));
+      const int w_even = wb + 64 * ub, w_odd = wb - 64 * ub;
+      // read side: row r0 + 8h, chunk 8k + e sits at 128 k + 16 ((e ^ w) ^ 4h), w = r0 >> 1
+      const int r0 = el >> 3, ew = (el & 7) ^ (r0 >> 1);
+      const int rd0 = r0 * 384 + 16 * ew, rd1 = rd0 + 8 * 384 + ((ew & 4) ? -64 : 64);
+      float* cg = static_cast<float*>(a.out) + (int64_t)T.g * a.stride_cg;
+      float* cl = cg + (int64_t)(T.m0 + wm * kWaveM + r0) * a.stride_cm + T.n0 + wn * C::WaveN + 4 * (el & 7);
+      const int mrow = T.m0 + wm * kWaveM + r0, ncol = T.n0 + wn * C::WaveN + 4 * (el & 7);
+      // A full tile (every tile at the measured shapes) runs without per-element bounds checks:
+      // with them the compiler cannot count outstanding memory operations across the branches and
+      // drains them all before every store.
+      auto epilogue = [&](auto kFullTile) {
+        constexpr bool kFull = decltype(kFullTile)::value;
+        auto in = [&](int i, int h, int k) {
+          return kFull || (mrow + 16 * i + 8 * h < a.OUT_M && ncol + 32 * k < a.OUT_N);
+        };
+        auto ptr = [&](int i, int h, int k) { return cl + (int64_t)(16 * i + 8 * h) * a.stride_cm + 32 * k; };
+        v4f old[2][6];
+        auto load_old = [&](int i, v4f* dst) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int k = 0; k < 3; ++k)
+              dst[3 * h + k] = in(i, h, k) ? *(const v4f*)ptr(i, h, k) : v4f{0.f, 0.f, 0.f, 0.f};
+        };
+        if constexpr (kOut == kOutF32Acc) load_old(0, old[0]);
+#pragma unroll
+        for (int i = 0; i < kMB; ++i) {
+          if constexpr (kOut == kOutF32Acc)
+            if (i + 1 < kMB) load_old(i + 1, old[(i + 1) & 1]);
+          // the scaled product, rounded to fp32 here, is what accumulate mode adds to C: the sum
+          // equals adding the fp32-output result to C, bit for bit
+#pragma unroll
+          for (int jj = 0; jj < NB; ++jj)
+            *(GG_LDS v4f*)(stg + ((jj & 1) ? w_odd : w_even) + 64 * jj) = acc[i][jj] * alpha;
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+              v4f v = *(const GG_LDS v4f*)(stg + (h ? rd1 : rd0) + 128 * k);
+              if constexpr (kOut == kOutF32Acc) v += old[i & 1][3 * h + k];
+              if (in(i, h, k)) __builtin_nontemporal_store(v, (v4f*)ptr(i, h, k));
+            }
+        }
+      };
+      const bool full = T.m0 + kTileM <= a.OUT_M && T.n0 + kTN <= a.OUT_N;
+      if (full)
+        epilogue(std::true_type{});
+      else
+        epilogue(std::false_type{});
+      // fp32 mode: a full tile issued exactly kMB x NB stores per wave (the counted wait applies);
+      // accumulate mode: loads and stores mixed, the next tile's first wait drains everything
+      full_prev = kOut == kOutF32 && full;
+    } else if constexpr (kOut != kOutBF16) {
+      // ---- fp32 epilogue, 320-wide tiles: a lane's 4 consecutive columns of one C row are a
+      // 16-byte row segment, stored directly. Accumulate mode reads the old values one m-block
+      // ahead of their use.
       float* cg = static_cast<float*>(a.out) + (int64_t)T.g * a.stride_cg;
       const int mb = T.m0 + wm * kWaveM + s16;
       const int nb = T.n0 + wn * C::WaveN + 4 * q;
-      // A full tile (every tile at the measured shapes) runs without per-element bounds checks:
-      // with them the compiler cannot count outstanding memory operations across the branches
-      // and drains them all before every store.
       auto epilogue = [&](auto kFullTile) {
         constexpr bool kFull = decltype(kFullTile)::value;
         auto in = [&](int m, int n) { return kFull || (m < a.OUT_M && n < a.OUT_N); };
@@ -830,9 +896,8 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
 #pragma unroll
           for (int j = 0; j < NB; ++j) {
             const int m = mb + 16 * i, n = nb + 16 * j;
-            // the scaled product is rounded to fp32 before the addition (the empty asm keeps the
-            // compiler from fusing them into an FMA), so accumulating equals adding the
-            // fp32-output result to C, bit for bit
+            // the product is rounded to fp32 before the addition (the empty asm keeps the compiler
+            // from fusing them into an FMA), as in the 384-wide epilogue
             v4f v = acc[i][j] * alpha;
             if constexpr (kOut == kOutF32Acc) {
               asm volatile("" : "+v"(v));
@@ -847,8 +912,6 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
         epilogue(std::true_type{});
       else
         epilogue(std::false_type{});
-      // fp32 mode: a full tile issued exactly kMB x NB stores per wave (the counted wait applies);
-      // accumulate mode: loads and stores mixed, the next tile's first wait drains everything
       full_prev = kOut == kOutF32 && full;
     } else {
       // ---- epilogue. Lane holds C[m][n..n+3] for m = m0+wm*96+i*16+s16, n = n0+wn*TN/4+j*16+4q.
