@@ -367,12 +367,13 @@ def main():
                   "inputs": "seeded N(0,1) / N(0,1e-3) quantized per-tensor, multinomial group sizes, in HBM",
                   "kernel": "hip gfx950 persistent {tile_m}x{tile_n} tiles, mfma {mfma}".format(
                       mfma=args.mfma, **pkg.launch_geometry(p.OUT_N)),
-                  "baseline_number": "reference optimized ASM 3.515 ms / 1237 TFLOPS (README.md:60)"}
+                  "baseline_number": ("reference optimized ASM 3.515 ms / 1237 TFLOPS (README.md:60)"
+                                      if p.name == "gate_up_wgrad" else "none published for this workload")}
+        if p.is_mx:
+            config["scales"] = "e8m0 per 32 tokens per column (MX block scaling)"
         vs_baseline = round(tflops / REF_OPT_ASM_TFLOPS, 4) if p.name == "gate_up_wgrad" else None
     line = {
-        "metric": (f"ms + TFLOPS (% FP8 peak) for {p.name} G=32 M=131072 on 1 MI355X" if fwd else
-                   "ms + TFLOPS (% FP8 peak) for gate_up_wgrad G=32 M=131072 on 1 MI355X" if p.G == 32 else
-                   f"ms + TFLOPS (% FP8 peak) for {p.name} G={p.G} M={p.M} on 1 MI355X"),
+        "metric": f"ms + TFLOPS (% FP8 peak) for {p.name} G={p.G} M={p.M} on 1 MI355X",
         "value": round(tflops, 2),
         "unit": "TFLOPS",
         "n_gpus": 1,
