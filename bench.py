@@ -16,6 +16,10 @@ gate_up shape (x bf16 [131072, 2880], w bf16 [32, 5760, 2880], dy bf16 [131072, 
 x and w, forward GEMM, quantize dy, dgrad GEMM, wgrad GEMM accumulated into an fp32 main-grad;
 FLOPs = 3 * 2 * M * K * N.
 
+``--site all | all_fwd | all_wgrad | <site>`` runs the reference's call sites one after the other
+with its own input recipe and prints its summary table (per-site ms, TFLOPS, share of the total)
+on stderr; the JSON line carries the sum over the sites (reference bench.py:690-858).
+
 ``--config quant_tensorwise | quant_mx`` measures the FP8 quantization producer (HBM-bound, GB/s):
 x bf16 [131072, 2880] -> per-tensor e4m3 (amax pass + quantize pass: 2 + 2 + 1 bytes per
 element), and dy bf16 [131072, 5760] -> grouped MX e5m2 with 32-token padding (2 + 1 + 1/32
@@ -41,6 +45,8 @@ REF_OPT_ASM_TFLOPS = 1237.0       # reference optimized ASM, gate_up_wgrad, C la
 FWD_SITES = ("gate_up_fwd", "down_fwd", "down_dgrad", "gate_up_dgrad")
 QUANT_CONFIGS = ("quant_tensorwise", "quant_mx", "quant_weight_transpose")
 LAYER_CONFIGS = ("gate_up_layer",)
+WGRAD_SITES = ("down_wgrad", "gate_up_wgrad")
+SITE_GROUPS = {"all": (*FWD_SITES, *WGRAD_SITES), "all_fwd": FWD_SITES, "all_wgrad": WGRAD_SITES}
 HBM_PEAK_GBS = 8000.0             # MI355X HBM3E
 
 
@@ -56,6 +62,9 @@ def parse_args():
     ap.add_argument("--config", default="gate_up_wgrad",
                     choices=["gate_up_wgrad", "down_wgrad", "gate_up_zipf", "gate_up_mx", "plumbing", "constant",
                              *FWD_SITES, *QUANT_CONFIGS, *LAYER_CONFIGS])
+    ap.add_argument("--site", default=None, choices=[*SITE_GROUPS, *FWD_SITES, *WGRAD_SITES],
+                    help="time the reference's call sites (one, or a group) with its own input recipe and print "
+                         "a per-site summary table; replaces --config")
     ap.add_argument("--mfma", default="k128", choices=["k128", "k32"])
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -303,6 +312,21 @@ def main_layer(args, pkg, dev):
     ms = time_steps(step, args.steps, args.warmup)
     flops = 3 * 2.0 * M * K * N
     tflops = flops / (ms * 1e-3) / 1e12
+    extra = None
+    if args.extra:
+        # gradient accumulation: the weight is unchanged between micro-batches, so its fp8 copy
+        # (and q^T) comes from the cache and the weight quantization pass drops out of the step
+        from ggemm_asm_amd.autograd import FP8WeightCache
+        cache = FP8WeightCache()
+
+        def step_cached():
+            x.grad = None
+            out = grouped_linear_fp8(x, w, offs, main_grad=main_grad, weight_cache=cache)
+            out.backward(dy)
+
+        t = time_steps(step_cached, max(args.steps // 2, 10), max(args.warmup // 2, 5))
+        extra = {"gate_up_layer_cached_weight": {"ms": round(t, 4), "TFLOPS": round(flops / (t * 1e-3) / 1e12, 2),
+                                                 "cache_hits": cache.hits, "cache_misses": cache.misses}}
     line = {"metric": "ms + TFLOPS of one FP8 grouped linear training step (gate_up shape) on 1 MI355X",
             "value": round(tflops, 2), "unit": "TFLOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -311,6 +335,55 @@ def main_layer(args, pkg, dev):
                        "step": "quantize x, w (e4m3) + fwd GEMM + quantize dy (e5m2) + dgrad GEMM + wgrad GEMM "
                                "accumulated into an fp32 main-grad",
                        "inputs": "seed-42 exponential group sizes, randn bf16, in HBM"},
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP8_DENSE_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tflops / FP8_DENSE_PEAK_TFLOPS, 4), "traffic": None},
+            "cpu_baseline": None}
+    if extra:
+        line["extra"] = extra
+    print(json.dumps(line), flush=True)
+
+
+def main_sites(args, pkg, dev):
+    """The reference's multi-site run (bench.py:690-858): each call site in turn with the
+    reference's input recipe (seed-42 exponential group lengths, randn bf16 cast to fp8, scales
+    0.1), then its summary table (ms, TFLOPS, TFLOP and share of the total per site, and the total)
+    on stderr. The JSON line carries the sum over the sites."""
+    import torch
+    names = SITE_GROUPS.get(args.site, (args.site,))
+    rows = []
+    for name in names:
+        if name in FWD_SITES:
+            p = pkg.inputs.make_fwd_problem(name, seed=args.seed, device=dev)
+        else:
+            p = pkg.inputs.make_wgrad_site_problem(name, seed=args.seed, device=dev)
+        torch.cuda.synchronize()
+        run = make_runner(pkg, p, dev, args.mfma)
+        ms = time_steps(run, args.steps, args.warmup)
+        rows.append({"site": name, "ms": round(ms, 4), "TFLOPS": round(p.flops / (ms * 1e-3) / 1e12, 2),
+                     "TFLOP": round(p.flops / 1e12, 4)})
+        print(f"  {name}: {ms:.4f} ms", file=sys.stderr, flush=True)
+        del p, run
+    total_ms = sum(r["ms"] for r in rows)
+    total_tflop = sum(r["TFLOP"] for r in rows)
+    tflops = total_tflop / (total_ms * 1e-3)
+    bar = "=" * 64
+    print(bar, file=sys.stderr)
+    print(f"{'Site':<16s} {'ms':>9} {'TFLOPS':>9} {'TFLOP':>8} {'% total':>8}", file=sys.stderr)
+    print("-" * 64, file=sys.stderr)
+    for r in rows:
+        print(f"{r['site']:<16s} {r['ms']:9.4f} {r['TFLOPS']:9.1f} {r['TFLOP']:8.3f} "
+              f"{100 * r['ms'] / total_ms:7.1f}%", file=sys.stderr)
+    print("-" * 64, file=sys.stderr)
+    print(f"{'TOTAL':<16s} {total_ms:9.4f} {tflops:9.1f} {total_tflop:8.3f} {'100.0':>7s}%", file=sys.stderr)
+    print(bar, file=sys.stderr, flush=True)
+    line = {"metric": f"ms + TFLOPS (% FP8 peak) summed over the {args.site} call sites on 1 MI355X",
+            "value": round(tflops, 2), "unit": "TFLOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(total_ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "fp8", "data": "synthetic",
+            "config": {"workload": args.site, "sites": rows,
+                       "inputs": "reference recipe: seed-42 exponential group sizes, randn bf16 cast to fp8, "
+                                 "scales 0.1, in HBM",
+                       "step": "one launch of each site's grouped GEMM, sites run one after the other"},
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP8_DENSE_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(tflops / FP8_DENSE_PEAK_TFLOPS, 4), "traffic": None},
             "cpu_baseline": None}
@@ -333,6 +406,9 @@ def main():
         return
     import torch
     dev = torch.device("cuda:0")
+    if args.site:
+        main_sites(args, pkg, dev)
+        return
     if args.config in QUANT_CONFIGS:
         main_quant(args, pkg, dev)
         return

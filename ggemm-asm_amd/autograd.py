@@ -20,9 +20,15 @@ the autograd wiring left to the framework (Primus-Turbo, not vendored).
   RHS, C [G, K, N]) and the gradient is its transpose ([G, N, K], a view). With
   ``main_grad=`` an fp32 [G, K, N] tensor, dW is accumulated into it instead (the fp32 epilogue,
   beta = 1) and the returned weight gradient is None.
+* ``weight_cache=FP8WeightCache()``: the weight's quantization (qw, qw^T, scale) is kept between
+  calls and redone only when the weight changes (its storage, shape or version counter: an
+  optimizer's in-place update bumps it). With gradient accumulation over several micro-batches
+  the weight pass then runs once per update instead of once per step.
 There is no CPU path: the tensors must live on a gfx950 GPU.
 """
 from __future__ import annotations
+
+import weakref
 
 import torch
 
@@ -33,9 +39,54 @@ from .vark import grouped_gemm_fp8_tensorwise_variable_k
 _LINE = 128   # bytes per cache line
 
 
+def _quantize_weight(w, with_transpose):
+    """(qw, qw^T or None, scale) of a [G, N, K] weight, rows on 128-byte lines."""
+    if with_transpose:
+        qw, qwt, sw, _ = quantize_fp8_tensorwise_transpose(w.contiguous(), "e4m3", row_align=_LINE)
+        return qw, qwt, sw
+    qw, sw, _ = quantize_fp8_tensorwise(w.contiguous(), "e4m3", row_align=_LINE)
+    return qw, None, sw
+
+
+class FP8WeightCache:
+    """One weight's e4m3 quantization, kept while the weight is unchanged.
+
+    An entry is reused only for the same tensor object (held by a weak reference, so a new tensor
+    that happens to reuse the old one's memory never hits) with the same storage address, shape,
+    strides, dtype and version counter; any in-place write to the weight (an optimizer step,
+    ``copy_``, ``add_``) bumps the version and the next call quantizes again. A cached entry
+    without q^T is upgraded when a call needs the data gradient. ``hits`` / ``misses`` count
+    lookups."""
+
+    def __init__(self):
+        self._ref = None
+        self._key = None
+        self._val = None
+        self.hits = 0
+        self.misses = 0
+
+    @staticmethod
+    def _key_of(w):
+        return (w.data_ptr(), tuple(w.shape), tuple(w.stride()), w.dtype, str(w.device), w._version)
+
+    def get(self, w, with_transpose):
+        key = self._key_of(w)
+        same = self._ref is not None and self._ref() is w and self._key == key
+        if same and (self._val[1] is not None or not with_transpose):
+            self.hits += 1
+            return self._val
+        self.misses += 1
+        self._val = _quantize_weight(w, with_transpose)
+        self._ref, self._key = weakref.ref(w), key
+        return self._val
+
+    def clear(self):
+        self._ref = self._key = self._val = None
+
+
 class GroupedLinearFP8(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, w, group_offs, main_grad):
+    def forward(ctx, x, w, group_offs, main_grad, weight_cache=None):
         if x.dim() != 2 or w.dim() != 3 or x.shape[1] != w.shape[2]:
             raise ValueError("x must be [M, K] and w [G, N, K]")
         if w.shape[0] != group_offs.numel() - 1:
@@ -43,10 +94,10 @@ class GroupedLinearFP8(torch.autograd.Function):
         # operand rows start on 128-byte lines (padded buffers): K-major rows of K = 2880 bytes
         # would otherwise straddle lines and cost the GEMMs 1.5 line requests per row segment
         qx, sx, _ = quantize_fp8_tensorwise(x.contiguous(), "e4m3", row_align=_LINE)
-        if ctx.needs_input_grad[0]:
-            qw, qwt, sw, _ = quantize_fp8_tensorwise_transpose(w.contiguous(), "e4m3", row_align=_LINE)
+        if weight_cache is not None:
+            qw, qwt, sw = weight_cache.get(w, ctx.needs_input_grad[0])
         else:
-            (qw, sw, _), qwt = quantize_fp8_tensorwise(w.contiguous(), "e4m3", row_align=_LINE), None
+            qw, qwt, sw = _quantize_weight(w, ctx.needs_input_grad[0])
         # rows past offs[G] (tokens the routing dropped) come out as exact zeros
         out = grouped_gemm_fp8_tensorwise(qx, qw, sx, sw, group_offs, zero_tail=True)
         ctx.save_for_backward(qx, sx, qwt, sw, group_offs)
@@ -70,17 +121,19 @@ class GroupedLinearFP8(torch.autograd.Function):
             else:
                 dwt = grouped_gemm_fp8_tensorwise_variable_k(qx, qdy, sx, sdy, group_offs)   # [G, K, N]
                 dw = dwt.transpose(1, 2).to(ctx.w_dtype)
-        return dx, dw, None, None
+        return dx, dw, None, None, None
 
 
 def grouped_linear_fp8(x: torch.Tensor, w: torch.Tensor, group_offs: torch.Tensor,
-                       main_grad: torch.Tensor | None = None) -> torch.Tensor:
+                       main_grad: torch.Tensor | None = None,
+                       weight_cache: FP8WeightCache | None = None) -> torch.Tensor:
     """FP8 grouped linear layer: ``out[r] = x[r] @ w[g]^T`` for the rows of group g, bf16 out.
 
     x: bf16 / fp32 [M, K] (rows grouped by expert); w: bf16 / fp32 [G, N, K]; group_offs: int64
     [G+1] on the device. Backward gives dx [M, K] and dw [G, N, K]; with ``main_grad`` (fp32
-    [G, K, N], the wgrad kernel's orientation) the weight gradient is added into it instead."""
+    [G, K, N], the wgrad kernel's orientation) the weight gradient is added into it instead. With
+    ``weight_cache`` the weight's fp8 copy is reused while the weight is unchanged."""
     if main_grad is not None:
         if main_grad.dtype != torch.float32 or tuple(main_grad.shape) != (w.shape[0], w.shape[2], w.shape[1]):
             raise ValueError(f"main_grad must be fp32 [G, K, N] = {[w.shape[0], w.shape[2], w.shape[1]]}")
-    return GroupedLinearFP8.apply(x, w, group_offs, main_grad)
+    return GroupedLinearFP8.apply(x, w, group_offs, main_grad, weight_cache)

@@ -227,6 +227,26 @@ def constant_problem(G: int = 32, M: int = M_TOTAL, OUT_M: int = F_DIM, OUT_N: i
     return VarKProblem("constant", lhs, rhs, offs, G, OUT_M, OUT_N, lhs_scale=0.1, rhs_scale=0.1)
 
 
+def make_wgrad_site_problem(name: str, seed: int = 42, device: str | torch.device = "cpu",
+                            lens: torch.Tensor | None = None) -> VarKProblem:
+    """A wgrad call site with the reference's own input recipe (reference bench.py:182-193,
+    205-223, 731-737): seed-42 exponential group lengths over 32 experts and 131072 tokens, LHS and
+    RHS torch.randn in bf16 cast straight to e4m3fn / e5m2 (no scaling), scales 0.1. ``seed``
+    seeds the values (a generator on ``device``)."""
+    if name not in WGRAD_SITES:
+        raise ValueError(f"unknown site {name!r}; choose from {tuple(WGRAD_SITES)}")
+    device = torch.device(device)
+    om, on = WGRAD_SITES[name]
+    lens_ = torch.as_tensor(lens, dtype=torch.long) if lens is not None else make_group_lens_reference()
+    offs = make_group_offs(lens_).to(device)
+    M_, G_ = int(lens_.sum()), len(lens_)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    lhs = torch.randn((M_, om), generator=gen, device=device, dtype=torch.bfloat16).to(torch.float8_e4m3fn)
+    rhs = torch.randn((M_, on), generator=gen, device=device, dtype=torch.bfloat16).to(torch.float8_e5m2)
+    return VarKProblem(name, lhs.view(torch.uint8), rhs.view(torch.uint8), offs, G_, om, on, lhs_scale=0.1,
+                       rhs_scale=0.1, meta={"seed": seed, "lens": lens_.tolist(), "recipe": "reference"})
+
+
 # ----------------------------------------------------------------------------- fwd / dgrad sites
 
 # persistent-kernel call sites (reference bench.py:153-180): K, N, A format (B is always e4m3fn,

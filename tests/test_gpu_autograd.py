@@ -127,3 +127,43 @@ def test_grouped_linear_fp8_dropped_tokens_are_zero(pkg, orc, orp, cuda):
     m = orc.compare(pkg.as_bf16_bits(out)[:end], ref_out)
     _say(f"forward rows within offs[G]: {m}")
     assert orc.parity_ok(m)
+
+
+def test_grouped_linear_fp8_weight_cache(pkg, cuda):
+    """weight_cache: the second call with an unchanged weight reuses its fp8 copy and gives the
+    same bits as an uncached call; an in-place update of the weight quantizes again; a call that
+    needs the data gradient after one that did not upgrades the entry with q^T."""
+    from ggemm_asm_amd.autograd import FP8WeightCache, grouped_linear_fp8
+    lens, K, N = [96, 0, 160], 192, 256
+    g = torch.Generator().manual_seed(23)
+    G, M = len(lens), sum(lens)
+    x = torch.randn((M, K), generator=g).to(torch.bfloat16).to(cuda)
+    w = (torch.randn((G, N, K), generator=g) * 0.05).to(torch.bfloat16).to(cuda).requires_grad_(True)
+    dy = (torch.randn((M, N), generator=g) * 1e-2).to(torch.bfloat16).to(cuda)
+    offs = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64, device=cuda)
+    cache = FP8WeightCache()
+    _say("grouped linear fp8 weight cache")
+    out0 = grouped_linear_fp8(x, w, offs, weight_cache=cache)      # x needs no grad: no q^T
+    assert (cache.hits, cache.misses) == (0, 1)
+    xg = x.clone().requires_grad_(True)
+    out1 = grouped_linear_fp8(xg, w, offs, weight_cache=cache)     # needs q^T: upgraded
+    assert (cache.hits, cache.misses) == (0, 2)
+    out1.backward(dy)
+    dx_ref = xg.grad.clone()
+    xg.grad = None
+    out2 = grouped_linear_fp8(xg, w, offs, weight_cache=cache)     # hit
+    assert (cache.hits, cache.misses) == (1, 2)
+    out2.backward(dy)
+    ref = grouped_linear_fp8(x, w.detach(), offs)                  # uncached
+    torch.cuda.synchronize()
+    for o in (out0, out1, out2):
+        assert torch.equal(o.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(xg.grad.view(torch.int16), dx_ref.view(torch.int16))
+    with torch.no_grad():
+        w.mul_(2.0)                                                # an optimizer-like in-place step
+    out3 = grouped_linear_fp8(x, w, offs, weight_cache=cache)
+    assert (cache.hits, cache.misses) == (1, 3)
+    ref3 = grouped_linear_fp8(x, w.detach(), offs)
+    torch.cuda.synchronize()
+    assert torch.equal(out3.view(torch.int16), ref3.view(torch.int16))
+    assert not torch.equal(out3.view(torch.int16), ref.view(torch.int16))

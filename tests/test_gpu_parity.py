@@ -305,8 +305,29 @@ def test_reference_launcher_runs_code_object(pkg):
                        capture_output=True, text=True, timeout=120)
     _say(r.stdout.strip().replace("\n", " | "))
     assert r.returncode == 0, r.stderr
+    assert re.search(r"Site: gate_up_wgrad\s+E=32 M=131072 OUT_M=2880 OUT_N=5760", r.stdout)
     m = re.search(r"Kernel:\s+([\d.]+) ms\s+([\d.]+) TFLOPS", r.stdout)
     assert m and float(m.group(1)) > 0
+    # the same inputs through the library entry point, timed the same way (events around 10
+    # launches after 3): the code object under the reference's launcher runs the same kernel body
+    dev = torch.device("cuda:0")
+    p = pkg.inputs.constant_problem(device=dev)
+    s = torch.tensor(0.1, device=dev)
+    out = torch.empty((p.G, p.OUT_M, p.OUT_N), dtype=torch.bfloat16, device=dev)
+    run = lambda: pkg.grouped_gemm_fp8_tensorwise_variable_k(p.lhs, p.rhs, s, s, p.group_offs, out=out)
+    for _ in range(3):
+        run()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    lib_ms = e0.elapsed_time(e1) / 10
+    ratio = float(m.group(1)) / lib_ms
+    _say(f"launcher {float(m.group(1)):.3f} ms, library {lib_ms:.3f} ms, ratio {ratio:.3f}")
+    assert bool((out.view(torch.int16) == 0x41A4).all())
+    assert 0.7 < ratio < 1.4
 
 
 # ----------------------------------------------------------------------------- full-size configs

@@ -236,6 +236,21 @@ def test_reference_group_lens_seed42(pkg):
     assert offs[0] == 0 and offs[-1] == 131072 and offs.dtype == torch.int64
 
 
+def test_wgrad_site_reference_recipe(pkg):
+    """reference bench.py:221-223,731-737: randn bf16 cast straight to e4m3fn / e5m2, scales 0.1,
+    the seed-42 lengths unless overridden."""
+    p = pkg.inputs.make_wgrad_site_problem("down_wgrad", seed=5, lens=[40, 0, 24])
+    assert (p.G, p.M, p.OUT_M, p.OUT_N) == (3, 64, 2880, 2880)
+    assert p.lhs_scale == p.rhs_scale == 0.1 and p.group_offs.tolist() == [0, 40, 40, 64]
+    gen = torch.Generator().manual_seed(5)
+    ref_l = torch.randn((64, 2880), generator=gen, dtype=torch.bfloat16).to(torch.float8_e4m3fn)
+    ref_r = torch.randn((64, 2880), generator=gen, dtype=torch.bfloat16).to(torch.float8_e5m2)
+    assert torch.equal(p.lhs, ref_l.view(torch.uint8)) and torch.equal(p.rhs, ref_r.view(torch.uint8))
+    assert pkg.inputs.make_wgrad_site_problem.__defaults__[0] == 42
+    with pytest.raises(ValueError):
+        pkg.inputs.make_wgrad_site_problem("gate_up_fwd")
+
+
 def test_config_length_recipes(pkg):
     g = torch.Generator().manual_seed(0)
     z = pkg.inputs.zipf_lens(32, 131072, g)
