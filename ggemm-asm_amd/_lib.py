@@ -13,6 +13,7 @@ EXPORTS = (
     "ggemm_vark_wgrad_fp8",
     "ggemm_vark_wgrad_fp8_k32",
     "ggemm_vark_wgrad_fp8_out",
+    "ggemm_vark_wgrad_fp8_wide",
     "ggemm_vark_wgrad_mxfp8",
     "ggemm_vark_check_offsets",
     "ggemm_vark_num_cus",
@@ -71,6 +72,8 @@ def load():
         f.restype = ctypes.c_int
     lib.ggemm_vark_wgrad_fp8_out.argtypes = tw[:-1] + [i32, ctypes.c_int64, vp]
     lib.ggemm_vark_wgrad_fp8_out.restype = ctypes.c_int
+    lib.ggemm_vark_wgrad_fp8_wide.argtypes = tw[:-1] + [ctypes.c_int64, vp]
+    lib.ggemm_vark_wgrad_fp8_wide.restype = ctypes.c_int
     lib.ggemm_vark_wgrad_mxfp8.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 10 + [ctypes.c_int64, vp]
     lib.ggemm_vark_wgrad_mxfp8.restype = ctypes.c_int
     lib.ggemm_vark_check_offsets.argtypes = [i64p, i32, ctypes.c_int64, i32]

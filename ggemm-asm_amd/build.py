@@ -45,7 +45,18 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(err, flush=True)
 
 
+def generate_wide_asm() -> str:
+    """Rewrite csrc/vark_wide_asm.inc (the wide-tile kernel's per-tile assembly) from its generator."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("gen_vark_wide", os.path.join(CSRC, "gen_vark_wide.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    mod.main()
+    return mod.OUT
+
+
 def build_so(verbose: bool = False) -> str:
+    generate_wide_asm()
     os.makedirs(LIB_DIR, exist_ok=True)
     tmp = SO_PATH + ".tmp"
     _run([hipcc(), *DEVICE_FLAGS, "-fPIC", "-shared", os.path.join(CSRC, "vark_capi.hip"),

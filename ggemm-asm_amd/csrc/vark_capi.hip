@@ -9,12 +9,14 @@
 #include "../../include/ggemm_vark.h"
 #include "capi_common.h"
 #include "vark_kernel.h"
+#include "vark_wide.h"
 
 GGEMM_DEFINE_TENSORWISE_LIB_KERNEL(_grouped_variable_k_gemm_kernel, false, uint16_t, ggemm::kOutBF16)
 GGEMM_DEFINE_TENSORWISE_LIB_KERNEL(_grouped_variable_k_gemm_kernel_k32, true, uint16_t, ggemm::kOutBF16)
 GGEMM_DEFINE_MX_KERNEL(_grouped_variable_k_mxfp8_gemm_kernel)
 GGEMM_DEFINE_TENSORWISE_LIB_KERNEL(_grouped_variable_k_gemm_kernel_f32, false, float, ggemm::kOutF32)
 GGEMM_DEFINE_TENSORWISE_LIB_KERNEL(_grouped_variable_k_gemm_kernel_f32_acc, false, float, ggemm::kOutF32Acc)
+GGEMM_DEFINE_WIDE_KERNEL(_grouped_variable_k_gemm_kernel_wide)
 
 namespace {
 
@@ -40,6 +42,13 @@ int validate_common(const void* lhs, const void* rhs, const void* out, const voi
   return GGEMM_OK;
 }
 
+// Shapes the wide-tile kernel takes: OUT_N a multiple of its 384-wide tile (N-ragged tiles would
+// need per-lane store masks; rows past OUT_M fall outside its C buffer resource), and a group of C
+// addressable with 32-bit byte offsets.
+bool wide_shape_ok(int OUT_M, int OUT_N, int scm) {
+  return OUT_N % ggemm::wide::kTN == 0 && (int64_t)OUT_M * scm * 2 < INT32_MAX;
+}
+
 }  // namespace
 
 extern "C" {
@@ -61,6 +70,28 @@ static int launch_tensorwise(bool legacy, const void* lhs, const void* rhs, void
   hipLaunchKernelGGL(kern, dim3(cus), dim3(ggemm::kThreads), ggemm::kDynLdsBytes, (hipStream_t)stream,
                      (const uint8_t*)lhs, (const uint8_t*)rhs, (uint16_t*)out, lhs_scale, rhs_scale, group_offs, G,
                      OUT_M, OUT_N, slm, srm, scg, scm, scn, (void*)nullptr, (void*)nullptr, m_total);
+  return (int)hipGetLastError();
+}
+
+int ggemm_vark_wgrad_fp8_wide(const void* lhs, const void* rhs, void* out, const float* lhs_scale,
+                              const float* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
+                              int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
+                              int32_t stride_cm, int32_t stride_cn, int64_t M_total, void* stream) {
+  int rc = validate_common(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
+                           stride_rhs_m, stride_cg, stride_cm, stride_cn);
+  if (rc) return rc;
+  if (M_total < 0) return GGEMM_E_SHAPE;
+  if (!wide_shape_ok(OUT_M, OUT_N, stride_cm)) return GGEMM_E_SHAPE;
+  if (!aligned(out, 16)) return GGEMM_E_ALIGN;    // 16-byte stores of whole row chunks
+  int cus = 0;
+  rc = device_cus(&cus);
+  if (rc) return rc;
+  // the kernel keeps token counts in 32 bits: a group never exceeds 2^31 - 1 tokens
+  const int64_t m_total = M_total < INT32_MAX ? M_total : INT32_MAX;
+  hipLaunchKernelGGL(_grouped_variable_k_gemm_kernel_wide, dim3(cus), dim3(ggemm::wide::kNT), 0, (hipStream_t)stream,
+                     (const uint8_t*)lhs, (const uint8_t*)rhs, (uint16_t*)out, lhs_scale, rhs_scale, group_offs, G,
+                     OUT_M, OUT_N, stride_lhs_m, stride_rhs_m, stride_cg, stride_cm, stride_cn, (void*)nullptr,
+                     (void*)nullptr, m_total);
   return (int)hipGetLastError();
 }
 

@@ -79,6 +79,18 @@ int ggemm_vark_wgrad_fp8_out(const void* lhs, const void* rhs, void* out, const 
                              int32_t stride_cm, int32_t stride_cn, int32_t out_mode, int64_t M_total,
                              void* stream);
 
+/* Tensorwise FP8 grouped wgrad, bf16 C, on the wide-tile kernel: 256 x 384 output tiles on
+ * 256-thread workgroups (one wave per SIMD, 512 registers per wave), outside the reference's
+ * 512-thread launch contract; no reference counterpart (it replaces the same launch as
+ * ggemm_vark_wgrad_fp8, reference launcher.cpp:123-171, for the shapes it takes). Same arguments
+ * and result as ggemm_vark_wgrad_fp8_out with GGEMM_OUT_BF16, group offsets clamped to
+ * [0, min(M_total, 2^31 - 1)]. Shapes: OUT_N a multiple of 384, OUT_M * stride_cm * 2 < 2^31,
+ * out 16-byte aligned; otherwise GGEMM_E_SHAPE / GGEMM_E_ALIGN and nothing is launched. */
+int ggemm_vark_wgrad_fp8_wide(const void* lhs, const void* rhs, void* out, const float* lhs_scale,
+                              const float* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
+                              int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
+                              int32_t stride_cm, int32_t stride_cn, int64_t M_total, void* stream);
+
 /* MXFP8 block-scaled grouped wgrad (no reference counterpart: the reference imports only the
  * tensorwise kernels, reference bench.py:241-246). lhs_scale: e8m0 bytes [ceil(M_total/32), OUT_M]
  * with row stride stride_lhs_scale; rhs_scale: e8m0 [ceil(M_total/32), OUT_N], row stride
