@@ -15,7 +15,7 @@ include/ggemm_persistent.h. Modules:
 * ``build``      -- in-tree hipcc build of the library and the drop-in code objects
 """
 from . import build, inputs  # noqa: F401
-from ._lib import GGemmError, launch_geometry, library_path, load as load_library  # noqa: F401
+from ._lib import GGemmError, bf16_kernel, launch_geometry, library_path, load as load_library  # noqa: F401
 from .autograd import FP8WeightCache, GroupedLinearFP8, grouped_linear_fp8  # noqa: F401
 from .persistent import grouped_gemm_fp8_tensorwise  # noqa: F401
 from .quant import (amax, padded_rows, quantize_fp8_tensorwise, quantize_fp8_tensorwise_transpose,  # noqa: F401

@@ -19,6 +19,7 @@ EXPORTS = (
     "ggemm_vark_num_cus",
     "ggemm_vark_strerror",
     "ggemm_vark_abi_version",
+    "ggemm_vark_bf16_kernel",
     "ggemm_vark_launch_geometry",
 )
 
@@ -84,6 +85,8 @@ def load():
     lib.ggemm_vark_strerror.restype = ctypes.c_char_p
     lib.ggemm_vark_abi_version.argtypes = []
     lib.ggemm_vark_abi_version.restype = i32
+    lib.ggemm_vark_bf16_kernel.argtypes = [i32, i32, i32, vp]
+    lib.ggemm_vark_bf16_kernel.restype = ctypes.c_int32
     lib.ggemm_vark_launch_geometry.argtypes = [i32] + [ctypes.POINTER(i32)] * 5
     lib.ggemm_vark_launch_geometry.restype = None
     lib.ggemm_persistent_fp8.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 9 + [ctypes.c_int64, vp]
@@ -116,6 +119,13 @@ def strerror(code: int) -> str:
 def check(code: int, what: str) -> None:
     if code != 0:
         raise GGemmError(code, what)
+
+
+def bf16_kernel(out_m: int, out_n: int, stride_cm: int | None = None) -> str:
+    """Which kernel the bf16 wgrad entry points run for this shape (a 256-byte aligned C assumed):
+    "wide" (256 x 384 tiles, one wave per SIMD) or "192-row" (the reference launch geometry)."""
+    sel = load().ggemm_vark_bf16_kernel(int(out_m), int(out_n), int(stride_cm or out_n), 256)
+    return "wide" if sel == 1 else "192-row"
 
 
 def launch_geometry(out_n: int = 5760) -> dict:

@@ -49,6 +49,27 @@ bool wide_shape_ok(int OUT_M, int OUT_N, int scm) {
   return OUT_N % ggemm::wide::kTN == 0 && (int64_t)OUT_M * scm * 2 < INT32_MAX;
 }
 
+// The bf16 entry points run the wide-tile kernel where it takes the shape and the problem is
+// large enough to fill its tiles (OUT_M >= 1024: at most one partial 256-row tile in four);
+// otherwise the 192 x 384 / 192 x 320 kernel.
+bool wide_selected(int OUT_M, int OUT_N, int scm, const void* out) {
+  return OUT_M >= 1024 && wide_shape_ok(OUT_M, OUT_N, scm) && aligned(out, 16);
+}
+
+int launch_wide(const void* lhs, const void* rhs, void* out, const float* lhs_scale, const float* rhs_scale,
+                const int64_t* group_offs, int32_t G, int32_t OUT_M, int32_t OUT_N, int32_t slm, int32_t srm,
+                int32_t scg, int32_t scm, int32_t scn, int64_t M_total, void* stream) {
+  int cus = 0;
+  int rc = device_cus(&cus);
+  if (rc) return rc;
+  // the kernel keeps token counts in 32 bits: a group never exceeds 2^31 - 1 tokens
+  const int64_t m_total = M_total < INT32_MAX ? M_total : INT32_MAX;
+  hipLaunchKernelGGL(_grouped_variable_k_gemm_kernel_wide, dim3(cus), dim3(ggemm::wide::kNT), 0, (hipStream_t)stream,
+                     (const uint8_t*)lhs, (const uint8_t*)rhs, (uint16_t*)out, lhs_scale, rhs_scale, group_offs, G,
+                     OUT_M, OUT_N, slm, srm, scg, scm, scn, (void*)nullptr, (void*)nullptr, m_total);
+  return (int)hipGetLastError();
+}
+
 }  // namespace
 
 extern "C" {
@@ -63,6 +84,9 @@ static int launch_tensorwise(bool legacy, const void* lhs, const void* rhs, void
                            scn);
   if (rc) return rc;
   if (m_total < 0) return GGEMM_E_SHAPE;
+  if (!legacy && wide_selected(OUT_M, OUT_N, scm, out))
+    return launch_wide(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, slm, srm, scg, scm, scn,
+                       m_total, stream);
   int cus = 0;
   rc = device_cus(&cus);
   if (rc) return rc;
@@ -83,16 +107,8 @@ int ggemm_vark_wgrad_fp8_wide(const void* lhs, const void* rhs, void* out, const
   if (M_total < 0) return GGEMM_E_SHAPE;
   if (!wide_shape_ok(OUT_M, OUT_N, stride_cm)) return GGEMM_E_SHAPE;
   if (!aligned(out, 16)) return GGEMM_E_ALIGN;    // 16-byte stores of whole row chunks
-  int cus = 0;
-  rc = device_cus(&cus);
-  if (rc) return rc;
-  // the kernel keeps token counts in 32 bits: a group never exceeds 2^31 - 1 tokens
-  const int64_t m_total = M_total < INT32_MAX ? M_total : INT32_MAX;
-  hipLaunchKernelGGL(_grouped_variable_k_gemm_kernel_wide, dim3(cus), dim3(ggemm::wide::kNT), 0, (hipStream_t)stream,
-                     (const uint8_t*)lhs, (const uint8_t*)rhs, (uint16_t*)out, lhs_scale, rhs_scale, group_offs, G,
-                     OUT_M, OUT_N, stride_lhs_m, stride_rhs_m, stride_cg, stride_cm, stride_cn, (void*)nullptr,
-                     (void*)nullptr, m_total);
-  return (int)hipGetLastError();
+  return launch_wide(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m, stride_rhs_m,
+                     stride_cg, stride_cm, stride_cn, M_total, stream);
 }
 
 int ggemm_vark_wgrad_fp8(const void* lhs, const void* rhs, void* out, const float* lhs_scale, const float* rhs_scale,
@@ -198,6 +214,10 @@ const char* ggemm_vark_strerror(int32_t code) {
 }
 
 int32_t ggemm_vark_abi_version(void) { return GGEMM_VARK_ABI_VERSION; }
+
+int32_t ggemm_vark_bf16_kernel(int32_t OUT_M, int32_t OUT_N, int32_t stride_cm, const void* out) {
+  return wide_selected(OUT_M, OUT_N, stride_cm, out) ? 1 : 0;
+}
 
 void ggemm_vark_launch_geometry(int32_t out_n, int32_t* block_threads, int32_t* dynamic_lds, int32_t* tile_m,
                                 int32_t* tile_n, int32_t* k_step) {

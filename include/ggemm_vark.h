@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define GGEMM_VARK_ABI_VERSION 3
+#define GGEMM_VARK_ABI_VERSION 4
 
 enum {
   GGEMM_OK = 0,
@@ -123,6 +123,12 @@ int32_t ggemm_vark_abi_version(void);
 /* Launch geometry the library uses (and the drop-in code object expects) for a problem of width
  * OUT_N = out_n: block threads, dynamic LDS bytes, output tile (OUT_M x OUT_N; the N tile is 384
  * when out_n is a multiple of 384, else 320) and tokens per pipeline stage. */
+/* Which kernel the bf16 entry points (ggemm_vark_wgrad_fp8, ggemm_vark_wgrad_fp8_out with
+ * GGEMM_OUT_BF16) run for a shape: 1 = the wide-tile kernel (OUT_M >= 1024, the shapes
+ * ggemm_vark_wgrad_fp8_wide takes, out 16-byte aligned), 0 = the 192-row-tile kernel of the
+ * reference launch geometry. No reference counterpart. Touches no device. */
+int32_t ggemm_vark_bf16_kernel(int32_t OUT_M, int32_t OUT_N, int32_t stride_cm, const void* out);
+
 void ggemm_vark_launch_geometry(int32_t out_n, int32_t* block_threads, int32_t* dynamic_lds, int32_t* tile_m,
                                 int32_t* tile_n, int32_t* k_step);
 
