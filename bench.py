@@ -441,9 +441,10 @@ def main():
         config = {"workload": p.name, "G": p.G, "M_total": p.M, "OUT_M": p.OUT_M, "OUT_N": p.OUT_N,
                   "lhs": "e4m3fn", "rhs": "e5m2", "out": "bf16", "acc": "fp32",
                   "inputs": "seeded N(0,1) / N(0,1e-3) quantized per-tensor, multinomial group sizes, in HBM",
-                  "kernel": ("hip gfx950 persistent 256x384 tiles, 256-thread workgroups (one wave per SIMD, "
-                             "hand-placed accumulators), mfma 32x32x64"
-                             if args.mfma == "k128" and not p.is_mx and pkg.bf16_kernel(p.OUT_M, p.OUT_N) == "wide"
+                  "kernel": ("hip gfx950 persistent {}x{} tiles, 256-thread workgroups (one wave per SIMD, "
+                             "hand-placed accumulators), mfma 32x32x64".format(
+                                 *((320, 320) if pkg.bf16_kernel(p.OUT_M, p.OUT_N) == "wide320" else (256, 384)))
+                             if args.mfma == "k128" and not p.is_mx and pkg.bf16_kernel(p.OUT_M, p.OUT_N) != "192-row"
                              else "hip gfx950 persistent {tile_m}x{tile_n} tiles, mfma {mfma}".format(
                                  mfma=args.mfma, **pkg.launch_geometry(p.OUT_N))),
                   "baseline_number": ("reference optimized ASM 3.515 ms / 1237 TFLOPS (README.md:60)"

@@ -73,7 +73,7 @@ def load():
         f.restype = ctypes.c_int
     lib.ggemm_vark_wgrad_fp8_out.argtypes = tw[:-1] + [i32, ctypes.c_int64, vp]
     lib.ggemm_vark_wgrad_fp8_out.restype = ctypes.c_int
-    lib.ggemm_vark_wgrad_fp8_wide.argtypes = tw[:-1] + [ctypes.c_int64, vp]
+    lib.ggemm_vark_wgrad_fp8_wide.argtypes = tw[:-1] + [ctypes.c_int64, i32, vp]
     lib.ggemm_vark_wgrad_fp8_wide.restype = ctypes.c_int
     lib.ggemm_vark_wgrad_mxfp8.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 10 + [ctypes.c_int64, vp]
     lib.ggemm_vark_wgrad_mxfp8.restype = ctypes.c_int
@@ -123,9 +123,10 @@ def check(code: int, what: str) -> None:
 
 def bf16_kernel(out_m: int, out_n: int, stride_cm: int | None = None) -> str:
     """Which kernel the bf16 wgrad entry points run for this shape (a 256-byte aligned C assumed):
-    "wide" (256 x 384 tiles, one wave per SIMD) or "192-row" (the reference launch geometry)."""
+    "wide320" / "wide256" (320 x 320 / 256 x 384 tiles, one wave per SIMD) or "192-row" (the
+    reference launch geometry)."""
     sel = load().ggemm_vark_bf16_kernel(int(out_m), int(out_n), int(stride_cm or out_n), 256)
-    return "wide" if sel == 1 else "192-row"
+    return {320: "wide320", 256: "wide256"}.get(sel, "192-row")
 
 
 def launch_geometry(out_n: int = 5760) -> dict:

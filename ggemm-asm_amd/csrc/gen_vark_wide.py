@@ -1,31 +1,34 @@
 #!/usr/bin/env python3
-"""Writes vark_wide_asm.inc: the per-tile body of the wide-tile FP8 grouped wgrad kernel
-(vark_wide.h) as one gfx950 inline-assembly statement.
+"""Writes vark_wide_asm.inc: the per-tile body of the wide-tile FP8 grouped wgrad kernels
+(vark_wide.h), one gfx950 inline-assembly statement per tile configuration.
 
-Why assembly: a 256 x 384 output tile on four waves (one per SIMD) needs 384 fp32 accumulators
-per wave, 256 in AGPRs and 128 in VGPRs. The compiler gives every MFMA of a kernel the same
-accumulator register class (at most 256 AGPRs), so it cannot build this kernel without spilling;
-written out here, the accumulators sit in fixed registers for the whole K loop.
+Why assembly: a wide output tile on four waves (one per SIMD) needs 384 (256 x 384) or 400
+(320 x 320) fp32 accumulators per wave, 256 in AGPRs and the rest in VGPRs. The compiler gives
+every MFMA of a kernel the same accumulator register class (at most 256 AGPRs), so it cannot build
+these kernels without spilling; written out here, the accumulators sit in fixed registers for the
+whole K loop.
 
 One statement computes one tile of one group (the HIP code around it walks the schedule, see
 vark_wide.h) and keeps the operand pipeline running across tiles:
-  * the token axis in stages of 64: LDS holds three stage slots of 40 KiB (64 rows of 256 LHS
-    bytes, then 64 rows of 384 RHS bytes), filled by LDS-DMA (buffer_load_dwordx4 ... lds, 1 KiB per
-    wave-instruction, 4 LHS + 6 RHS per wave and stage), bounded by the buffer's num_records so
-    tokens past the group end read as zero;
+  * the token axis in stages of 64: LDS holds three stage slots (64 rows of the tile's LHS bytes,
+    then 64 rows of its RHS bytes, 40 KiB), filled by LDS-DMA (buffer_load_dwordx4 ... lds, 1 KiB
+    per wave-instruction, 10 per wave and stage), bounded by the buffer's num_records so tokens
+    past the group end read as zero;
   * an issue cursor walks this tile's stages, then the next tile's first two: at each stage's
     barrier the slot just released takes the cursor's next stage, so up to three stages are in
     flight; counted vmcnt waits use a per-wave model of outstanding vector-memory operations
     (in/out operands, so it survives between tiles);
-  * per stage and wave 24 v_mfma_f32_32x32x64_f8f6f4 (4 LHS blocks x 6 RHS blocks of 32, A = RHS
-    e5m2 with cbsz 1, B = LHS e4m3), operands read with ds_read_b64_tr_b8 as the MFMAs release
-    their registers, the barrier that publishes the next stage placed after the first column;
-  * the epilogue scales by s_lhs * s_rhs, converts to bf16 (RNE), stages each 32 x 64 piece
-    through the freed slot (XOR swizzle, conflict-free) and stores whole 128-byte row segments
-    non-temporally; rows past OUT_M fall outside the C buffer resource and are dropped.
+  * per stage and wave BM x BN v_mfma_f32_32x32x64_f8f6f4 (BM LHS blocks x BN RHS blocks of 32;
+    A = RHS e5m2 with cbsz 1, B = LHS e4m3), operands read with ds_read_b64_tr_b8 as the MFMAs
+    release their registers, the barrier that publishes the next stage after the first row of
+    MFMAs, the next stage's LDS-DMA one instruction per MFMA gap;
+  * the epilogue scales by s_lhs * s_rhs, converts to bf16 (RNE), stages 32-row pieces through the
+    freed slot (XOR swizzle, conflict-free) and stores whole row chunks non-temporally; rows past
+    OUT_M fall outside the C buffer resource and are dropped.
 
-Operands (numbered as the asm statement in vark_wide.h passes them) are listed in OPERANDS; run
-this script to rewrite the include after changing it (build.py runs it before every build).
+Each configuration's operands (numbered as the asm statement in vark_wide.h passes them) are
+listed by Config.operands; run this script to rewrite the include after changing it (build.py runs
+it before every build).
 """
 from __future__ import annotations
 
@@ -35,26 +38,10 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 OUT = os.path.join(HERE, "vark_wide_asm.inc")
 
-SLOT = 40960                 # bytes per stage slot
 SLOTS = 3
-RHS_OFF = 16384              # RHS rows follow 64 rows of 256 LHS bytes
 WORD3 = 0x00020000           # raw buffer resource word 3 (32-bit data format)
-E_STORES = 48                # C stores per wave and tile (12 passes x 4)
-LOADS = 10                   # LDS-DMA instructions per wave and stage
-
-# in/out ("+s") then inputs: (name, constraint)
-OPERANDS = [
-    ("c0", "+s"), ("nis", "+s"), ("vmt", "+s"), ("q0", "+s"), ("q1", "+s"), ("q2", "+s"), ("np", "+s"),
-    ("lds_base", "s"), ("w1k", "s"),
-    ("bLT_lo", "s"), ("bLT_hi", "s"), ("bRT_lo", "s"), ("bRT_hi", "s"), ("klenT", "s"), ("m0T", "s"), ("n0T", "s"),
-    ("bLN_lo", "s"), ("bLN_hi", "s"), ("bRN_lo", "s"), ("bRN_hi", "s"), ("klenN", "s"), ("m0N", "s"), ("n0N", "s"),
-    ("cT_lo", "s"), ("cT_hi", "s"), ("crecT", "s"),
-    ("stride_l", "s"), ("stride_r", "s"), ("cm2", "s"), ("alpha", "s"), ("sw_epi", "s"),
-    ("voffL0", "v"), *[(f"voffR{j}", "v") for j in range(6)], *[(f"amb{i}", "v") for i in range(4)],
-    *[(f"bnb{j}", "v") for j in range(6)], ("ew_base", "v"), ("ew_s", "v"), ("rb_even", "v"), ("rb_odd", "v"),
-    ("gb", "v"),
-]
-OP = {name: f"%{i}" for i, (name, _) in enumerate(OPERANDS)}
+KS = 64                      # tokens per stage
+TOK_OFFS = (0, 8, 32, 40)    # token offsets of the four transposed reads of a 32x32x64 operand
 
 # scalar temporaries (clobbered): buffer resources in aligned quads, then state
 SGPR = dict(
@@ -63,37 +50,112 @@ SGPR = dict(
     RC="s[64:67]", RC0="s64", RC1="s65", RC2="s66", RC3="s67",
     S="s68", K="s69", INT="s70", IDX="s71", REM="s72", LIM="s73",
     BL0="s74", BL1="s75", BR0="s76", BR1="s77", CM0="s78", CN0="s79",
-    ISLOT="s80", CS="s81", NS="s82", T="s83", T2="s84", L16="s85", NEED="s86", LIMTOP="s87", EPI="s88",
-    IB="s89",
+    ISLOT="s80", CS="s81", NS="s82", T="s83", T2="s84", NEED="s85", LIMTOP="s86", EPI="s87", IB="s88",
 )
-SGPR_CLOBBER = list(range(56, 90))
-VGPR_CLOBBER = list(range(36, 256))      # v36-v47 temps, v48-v127 operands, v128-v255 accumulators
-VT, VT2 = "v36", "v37"                   # address temporaries
+SGPR_CLOBBER = list(range(56, 89))
 
 
-def acc(i, j):
-    """Accumulator registers of block (m-block i, n-block j): blocks 0-15 in AGPRs, 16-23 in VGPRs."""
-    b = 6 * i + j
-    if b < 16:
-        return "a", 16 * b
-    return "v", 128 + 16 * (b - 16)
+def swizzle(pitch):
+    """Chunk swizzle of a token row of `pitch` bytes (a function of the token index): the 8 tokens
+    x 2 chunks x 2 halves a 32-lane half of a transposed read touches land in 32 distinct 8-byte
+    bank pairs, and tokens t + 8, t + 32, t + 40 share t's swizzle."""
+    if pitch == 256:
+        return lambda t: (t & 7) << 1
+    if pitch == 384:
+        return lambda t: ((t >> 1) & 3) << 1
+    if pitch == 320:
+        return lambda t: ((t >> 2) & 1) << 1
+    raise ValueError(pitch)
 
 
-def acc_range(i, j):
-    kind, base = acc(i, j)
-    return f"{kind}[{base}:{base + 15}]"
+class Config:
+    def __init__(self, tm, tn):
+        self.tm, self.tn = tm, tn
+        self.name = f"{tm}x{tn}"
+        self.bm, self.bn = tm // 64, tn // 64           # 32-wide blocks per wave (2 x 2 waves)
+        self.rhs_off = KS * tm
+        self.slot = KS * (tm + tn)
+        self.nl = KS * tm // 1024 // 4                  # LHS / RHS LDS-DMA instructions per wave
+        self.nr = KS * tn // 1024 // 4
+        self.loads = self.nl + self.nr
+        nblk = self.bm * self.bn
+        self.vacc0 = 256 - 16 * (nblk - 16)             # first VGPR accumulator
+        self.vop0 = self.vacc0 - 8 * (self.bm + self.bn)
+        self.vt, self.vt2 = f"v{self.vop0 - 2}", f"v{self.vop0 - 1}"
+        self.vgpr_clobber = list(range(self.vop0 - 2, 256))
+        self.pairs = [(2 * p, 2 * p + 1) if 2 * p + 1 < self.bn else (2 * p,) for p in range((self.bn + 1) // 2)]
+        self.e_stores = self.bm * sum(4 if len(pr) == 2 else 2 for pr in self.pairs)
+        # read bases: one per block, or (320-byte rows, one-bit swizzle) two per side by parity
+        self.parity_bases = tm == 320 and tn == 320
+        ops = [("c0", "+s"), ("nis", "+s"), ("vmt", "+s"), ("q0", "+s"), ("q1", "+s"), ("q2", "+s"), ("np", "+s"),
+               ("lds_base", "s"), ("w1k", "s"),
+               ("bLT_lo", "s"), ("bLT_hi", "s"), ("bRT_lo", "s"), ("bRT_hi", "s"), ("klenT", "s"), ("m0T", "s"),
+               ("n0T", "s"),
+               ("bLN_lo", "s"), ("bLN_hi", "s"), ("bRN_lo", "s"), ("bRN_hi", "s"), ("klenN", "s"), ("m0N", "s"),
+               ("n0N", "s"),
+               ("cT_lo", "s"), ("cT_hi", "s"), ("crecT", "s"),
+               ("stride_l", "s"), ("stride_r", "s"), ("cm2", "s"), ("alpha", "s"), ("sw_epi", "s")]
+        ops += [(f"voffL{j}", "v") for j in range(self.nl)] + [(f"voffR{j}", "v") for j in range(self.nr)]
+        if self.parity_bases:
+            ops += [("amb0", "v"), ("amb1", "v"), ("bnb0", "v"), ("bnb1", "v")]
+        else:
+            ops += [(f"amb{i}", "v") for i in range(self.bm)] + [(f"bnb{j}", "v") for j in range(self.bn)]
+        ops += [("ew_base", "v"), ("ew_s", "v"), ("rb_even", "v"), ("rb_odd", "v"), ("gb", "v")]
+        if self.bn % 2:
+            ops += [("rb1", "v"), ("gb1", "v")]
+        self.operands = ops
+        self.op = {name: f"%{i}" for i, (name, _) in enumerate(ops)}
+        # MFMA order within a stage: m-block 0 across all n-blocks first, then the other m-blocks
+        # column by column; m-block 0's registers free up after its row, an n-block's after its
+        # column, so the next stage's operands are read spread over the stage.
+        self.order = [(0, j) for j in range(self.bn)] + [(i, j) for j in range(self.bn) for i in range(1, self.bm)]
+        pos = {ij: n for n, ij in enumerate(self.order)}
+        self.barrier_after = self.bn - 1
+        reads = {self.bn - 1: [("am", 0)]}
+        for j in range(self.bn):
+            reads.setdefault(pos[(self.bm - 1, j)], []).append(("bn", j))
+        for i in range(1, self.bm):
+            reads.setdefault(pos[(i, self.bn - 1)], []).append(("am", i))
+        self.reads_after = reads
+        free = [n for n in range(self.bn, len(self.order) - 1) if n not in reads]
+        assert len(free) >= self.loads, self.name
+        self.dma_after = free[:self.loads]
+        self.setup_after = (0, 1, 2)
+        assert self.vop0 - 2 >= 28 and self.e_stores + self.loads <= 63
+        assert self.nl * 4 * 1024 == KS * tm and self.nr * 4 * 1024 == KS * tn
+
+    def acc(self, i, j):
+        """Accumulator registers of block (m-block i, n-block j): blocks 0-15 in AGPRs, the rest in
+        VGPRs from vacc0 up."""
+        b = self.bn * i + j
+        if b < 16:
+            return "a", 16 * b
+        return "v", self.vacc0 + 16 * (b - 16)
+
+    def acc_range(self, i, j):
+        kind, base = self.acc(i, j)
+        return f"{kind}[{base}:{base + 15}]"
+
+    def am(self, i):
+        return self.vop0 + 8 * i
+
+    def bn_reg(self, j):
+        return self.vop0 + 8 * self.bm + 8 * j
+
+    def read_base(self, side, b):
+        """(base operand, extra immediate) of block b's first transposed read."""
+        if self.parity_bases:
+            return self.op[f"{side}b{b & 1}"], 32 * b
+        return self.op[f"{side}b{b}"], 0
 
 
-def am(i):
-    return 48 + 8 * i
-
-
-def bn(j):
-    return 80 + 8 * j
+CONFIGS = (Config(256, 384), Config(320, 320))
 
 
 class Gen:
-    def __init__(self):
+    def __init__(self, cfg=CONFIGS[0]):
+        self.cfg = cfg
+        self.OP = cfg.op
         self.lines = []
         self.nlabel = 0
 
@@ -104,34 +166,6 @@ class Gen:
         self.nlabel += 1
         return f".Lggw_{stem}{self.nlabel}_%="
 
-    # ---------------------------------------------------------------- vm model
-
-    def wait_oldest(self):
-        """Wait for the oldest issued, not yet awaited stage; pop it from the model. vmcnt is
-        rounded down to one of the counts this kernel can produce (a stricter wait is safe)."""
-        s = SGPR
-        self.emit(f"s_sub_u32 {s['NEED']}, {OP['vmt']}, {OP['q0']}")
-        self.emit(f"s_mov_b32 {OP['q0']}, {OP['q1']}")
-        self.emit(f"s_mov_b32 {OP['q1']}, {OP['q2']}")
-        self.emit(f"s_sub_u32 {OP['np']}, {OP['np']}, 1")
-        counts = [E_STORES + LOADS, E_STORES, 2 * LOADS, LOADS]
-        done = self.label("wdone")
-        tgt = {c: self.label(f"w{c}_") for c in counts}
-        self.emit(f"s_cmp_eq_u32 {s['NEED']}, {LOADS}")        # the steady state: one stage behind
-        self.emit(f"s_cbranch_scc1 {tgt[LOADS]}")
-        for c in counts:
-            self.emit(f"s_cmp_ge_u32 {s['NEED']}, {c}")
-            self.emit(f"s_cbranch_scc1 {tgt[c]}")
-        self.emit("s_waitcnt vmcnt(0)")
-        self.emit(f"s_branch {done}")
-        for c in counts:
-            self.emit(f"{tgt[c]}:")
-            self.emit(f"s_waitcnt vmcnt({c})")
-            self.emit(f"s_branch {done}")
-        self.emit(f"{done}:")
-
-    # ---------------------------------------------------------------- issue
-
     def capture(self, fn, *args):
         """The lines fn would emit, without emitting them."""
         saved, self.lines = self.lines, []
@@ -139,11 +173,38 @@ class Gen:
         out, self.lines = self.lines, saved
         return out
 
+    # ---------------------------------------------------------------- vm model
+
+    def wait_oldest(self):
+        """Wait for the oldest issued, not yet awaited stage; pop it from the model. vmcnt is
+        rounded down to one of the counts this kernel can produce (a stricter wait is safe)."""
+        s, OP, c = SGPR, self.OP, self.cfg
+        self.emit(f"s_sub_u32 {s['NEED']}, {OP['vmt']}, {OP['q0']}")
+        self.emit(f"s_mov_b32 {OP['q0']}, {OP['q1']}")
+        self.emit(f"s_mov_b32 {OP['q1']}, {OP['q2']}")
+        self.emit(f"s_sub_u32 {OP['np']}, {OP['np']}, 1")
+        counts = [c.e_stores + c.loads, c.e_stores, 2 * c.loads, c.loads]
+        done = self.label("wdone")
+        tgt = {n: self.label(f"w{n}_") for n in counts}
+        self.emit(f"s_cmp_eq_u32 {s['NEED']}, {c.loads}")        # the steady state: one stage behind
+        self.emit(f"s_cbranch_scc1 {tgt[c.loads]}")
+        for n in counts:
+            self.emit(f"s_cmp_ge_u32 {s['NEED']}, {n}")
+            self.emit(f"s_cbranch_scc1 {tgt[n]}")
+        self.emit("s_waitcnt vmcnt(0)")
+        self.emit(f"s_branch {done}")
+        for n in counts:
+            self.emit(f"{tgt[n]}:")
+            self.emit(f"s_waitcnt vmcnt({n})")
+            self.emit(f"s_branch {done}")
+        self.emit(f"{done}:")
+
+    # ---------------------------------------------------------------- issue
+
     def issue_setup(self):
         """Buffer resources of the cursor's stage and this wave's LDS-DMA base in slot ISLOT."""
-        s = SGPR
-        e = self.emit
-        e(f"s_min_i32 {s['T']}, {s['REM']}, 64")
+        s, OP, e = SGPR, self.OP, self.emit
+        e(f"s_min_i32 {s['T']}, {s['REM']}, {KS}")
         e(f"s_max_i32 {s['T']}, {s['T']}, 0")
         e(f"s_mul_i32 {s['RL2']}, {s['T']}, {OP['stride_l']}")
         e(f"s_sub_u32 {s['RL2']}, {s['RL2']}, {s['CM0']}")
@@ -159,51 +220,44 @@ class Gen:
         e(f"s_add_u32 {s['IB']}, {s['IB']}, {OP['w1k']}")
 
     def issue_dma(self, j):
-        """LDS-DMA instruction j of the stage (0-3: LHS rows, 4-9: RHS rows)."""
-        s = SGPR
-        e = self.emit
-        if j < 4:
+        """LDS-DMA instruction j of the stage (first the nl LHS rows, then the nr RHS rows)."""
+        s, OP, e, c = SGPR, self.OP, self.emit, self.cfg
+        if j < c.nl:
             e(f"s_add_u32 m0, {s['IB']}, {4096 * j}")
-            if j == 0:
-                e("s_nop 0")
-                e(f"buffer_load_dwordx4 {OP['voffL0']}, {s['RL']}, 0 offen lds")
-            else:
-                e(f"s_mul_i32 {s['T2']}, {s['L16']}, {j}")
-                e(f"v_add_u32 {VT2}, {s['T2']}, {OP['voffL0']}")
-                e(f"buffer_load_dwordx4 {VT2}, {s['RL']}, 0 offen lds")
+            e("s_nop 0")
+            e(f"buffer_load_dwordx4 {OP[f'voffL{j}']}, {s['RL']}, 0 offen lds")
         else:
-            jj = j - 4
-            e(f"s_add_u32 m0, {s['IB']}, {RHS_OFF + 4096 * jj}")
+            jj = j - c.nl
+            e(f"s_add_u32 m0, {s['IB']}, {c.rhs_off + 4096 * jj}")
             e("s_nop 0")
             e(f"buffer_load_dwordx4 {OP[f'voffR{jj}']}, {s['RR']}, 0 offen lds")
 
     def issue_finish(self):
-        """Model: LOADS more operations, the count right after this stage remembered; advance the
+        """Model: loads more operations, the count right after this stage remembered; advance the
         cursor to its next stage and slot."""
-        s = SGPR
-        e = self.emit
-        e(f"s_add_u32 {OP['vmt']}, {OP['vmt']}, {LOADS}")
+        s, OP, e, c = SGPR, self.OP, self.emit, self.cfg
+        e(f"s_add_u32 {OP['vmt']}, {OP['vmt']}, {c.loads}")
         for n, q in enumerate(("q0", "q1", "q2")):
             e(f"s_cmp_eq_u32 {OP['np']}, {n}")
             e(f"s_cselect_b32 {OP[q]}, {OP['vmt']}, {OP[q]}")
         e(f"s_add_u32 {OP['np']}, {OP['np']}, 1")
         e(f"s_add_u32 {s['IDX']}, {s['IDX']}, 1")
-        e(f"s_sub_i32 {s['REM']}, {s['REM']}, 64")
+        e(f"s_sub_i32 {s['REM']}, {s['REM']}, {KS}")
         e(f"s_lshl_b32 {s['T']}, {OP['stride_l']}, 6")
         e(f"s_add_u32 {s['BL0']}, {s['BL0']}, {s['T']}")
         e(f"s_addc_u32 {s['BL1']}, {s['BL1']}, 0")
         e(f"s_lshl_b32 {s['T']}, {OP['stride_r']}, 6")
         e(f"s_add_u32 {s['BR0']}, {s['BR0']}, {s['T']}")
         e(f"s_addc_u32 {s['BR1']}, {s['BR1']}, 0")
-        e(f"s_add_u32 {s['ISLOT']}, {s['ISLOT']}, {SLOT}")
-        e(f"s_cmp_ge_u32 {s['ISLOT']}, {SLOT * SLOTS}")
-        e(f"s_cselect_b32 {s['T']}, {SLOT * SLOTS}, 0")
+        e(f"s_add_u32 {s['ISLOT']}, {s['ISLOT']}, {c.slot}")
+        e(f"s_cmp_ge_u32 {s['ISLOT']}, {c.slot * SLOTS}")
+        e(f"s_cselect_b32 {s['T']}, {c.slot * SLOTS}, 0")
         e(f"s_sub_u32 {s['ISLOT']}, {s['ISLOT']}, {s['T']}")
 
     def issue_core(self):
         """Issue the cursor's stage into slot ISLOT and advance the cursor."""
         self.issue_setup()
-        for j in range(LOADS):
+        for j in range(self.cfg.loads):
             self.issue_dma(j)
         self.issue_finish()
 
@@ -211,8 +265,7 @@ class Gen:
         """Before a stage that may issue: move the cursor to the next tile once this one is fully
         issued (the next tile's first two stages are the cursor's limit there); SCC = the cursor
         has a stage to issue."""
-        s = SGPR
-        e = self.emit
+        s, OP, e = SGPR, self.OP, self.emit
         nosw = self.label("nosw")
         e(f"s_cmp_eq_u32 {s['INT']}, 1")
         e(f"s_cbranch_scc0 {nosw}")
@@ -221,7 +274,7 @@ class Gen:
         e(f"s_mov_b32 {s['INT']}, 0")
         e(f"s_mov_b32 {s['IDX']}, 0")
         e(f"s_mov_b32 {s['REM']}, {OP['klenN']}")
-        e(f"s_add_u32 {s['T']}, {OP['klenN']}, 63")
+        e(f"s_add_u32 {s['T']}, {OP['klenN']}, {KS - 1}")
         e(f"s_lshr_b32 {s['T']}, {s['T']}, 6")
         e(f"s_min_u32 {s['LIM']}, {s['T']}, 2")
         e(f"s_mov_b32 {s['BL0']}, {OP['bLN_lo']}")
@@ -235,78 +288,63 @@ class Gen:
 
     # ---------------------------------------------------------------- operands
 
-    def read_am(self, i, slot):
-        e = self.emit
-        e(f"v_add_u32 {VT}, {slot}, {OP[f'amb{i}']}")
-        for n, off in enumerate((0, 8 * 256, 32 * 256, 40 * 256)):
-            r = am(i) + 2 * n
-            e(f"ds_read_b64_tr_b8 v[{r}:{r + 1}], {VT} offset:{off}")
-
-    def read_bn(self, j, slot):
-        e = self.emit
-        e(f"v_add_u32 {VT}, {slot}, {OP[f'bnb{j}']}")
-        for n, off in enumerate((0, 8 * 384, 32 * 384, 40 * 384)):
-            r = bn(j) + 2 * n
-            e(f"ds_read_b64_tr_b8 v[{r}:{r + 1}], {VT} offset:{off}")
+    def read_block(self, side, b, slot):
+        c, e = self.cfg, self.emit
+        base, extra = c.read_base(side, b)
+        pitch = c.tm if side == "am" else c.tn
+        reg0 = c.am(b) if side == "am" else c.bn_reg(b)
+        e(f"v_add_u32 {c.vt}, {slot}, {base}")
+        for n, dt in enumerate(TOK_OFFS):
+            r = reg0 + 2 * n
+            e(f"ds_read_b64_tr_b8 v[{r}:{r + 1}], {c.vt} offset:{extra + dt * pitch}")
 
     def mfma(self, i, j, first):
-        d = acc_range(i, j)
-        c = "0" if first else d
-        self.emit(f"v_mfma_f32_32x32x64_f8f6f4 {d}, v[{bn(j)}:{bn(j) + 7}], v[{am(i)}:{am(i) + 7}], {c} cbsz:1")
+        c = self.cfg
+        d = c.acc_range(i, j)
+        src = "0" if first else d
+        a, b = c.bn_reg(j), c.am(i)
+        self.emit(f"v_mfma_f32_32x32x64_f8f6f4 {d}, v[{a}:{a + 7}], v[{b}:{b + 7}], {src} cbsz:1")
 
     # ---------------------------------------------------------------- one stage
 
-    # MFMA order within a stage: m-block 0 across all six n-blocks first, then the other three
-    # m-blocks column by column. m-block 0's registers free up after six MFMAs and the n-blocks'
-    # after their column, so the next stage's operands are read spread over the stage; the next
-    # stage begins with m-block 0, whose operands were read earliest.
-    ORDER = [(0, j) for j in range(6)] + [(i, j) for j in range(6) for i in (1, 2, 3)]
-    BARRIER_AFTER = 4                                   # MFMA index after which the barrier sits
-    READS_AFTER = {5: [("am", 0)], 8: [("bn", 0)], 11: [("bn", 1)], 14: [("bn", 2)], 17: [("bn", 3)],
-                   20: [("bn", 4)], 21: [("am", 1)], 22: [("am", 2)], 23: [("bn", 5), ("am", 3)]}
-    DMA_AFTER = [6, 7, 9, 10, 12, 13, 15, 16, 18, 19]   # LDS-DMA instruction j after MFMA DMA_AFTER[j]
-    SETUP_AFTER = (0, 1, 2)                             # buffer resources, in three pieces
-    FINISH_AFTER = 20
-
     def stage(self, first, last, issue):
         """Stage k: its operands are in registers (read during stage k-1, or at tile entry for the
-        first stage); CS = its slot. Unless last: after MFMA 4 every read of slot CS has completed,
-        the wave waits for stage k+1's loads and passes the barrier (stage k+1 published, slot CS
-        free); stage k+1's operands are then read as their registers free up, and with issue the
-        cursor's next stage goes into slot CS one LDS-DMA instruction per MFMA gap."""
-        s = SGPR
-        e = self.emit
+        first stage); CS = its slot. After the first row of MFMAs every read of slot CS has
+        completed; unless last, the wave then waits for stage k+1's loads and passes the barrier
+        (stage k+1 published, slot CS free); stage k+1's operands are read as their registers free
+        up, and with issue the cursor's next stage goes into slot CS one LDS-DMA instruction per
+        MFMA gap."""
+        s, e, c = SGPR, self.emit, self.cfg
         if not last:
-            e(f"s_add_u32 {s['NS']}, {s['CS']}, {SLOT}")
-            e(f"s_cmp_ge_u32 {s['NS']}, {SLOT * SLOTS}")
-            e(f"s_cselect_b32 {s['T']}, {SLOT * SLOTS}, 0")
+            e(f"s_add_u32 {s['NS']}, {s['CS']}, {c.slot}")
+            e(f"s_cmp_ge_u32 {s['NS']}, {c.slot * SLOTS}")
+            e(f"s_cselect_b32 {s['T']}, {c.slot * SLOTS}, 0")
             e(f"s_sub_u32 {s['NS']}, {s['NS']}, {s['T']}")
         setup = self.capture(self.issue_setup) if issue else []
         pieces = [setup[:5], setup[5:10], setup[10:]]
+        # the previous stage's reads ended with the last n-block and the last m-block (4 reads each)
         e("s_waitcnt lgkmcnt(0)" if first else "s_waitcnt lgkmcnt(15)")
-        for n, (i, j) in enumerate(self.ORDER):
-            if not first:
-                # previous stage's reads ended ... bn4, am1, am2, bn5, am3 (4 reads each)
-                if n == 5:
-                    e("s_waitcnt lgkmcnt(4)")
+        for n, (i, j) in enumerate(c.order):
+            if not first and n == c.bn - 1:
+                e("s_waitcnt lgkmcnt(4)")
             self.mfma(i, j, first)
-            if issue and n in self.SETUP_AFTER:
-                for line in pieces[self.SETUP_AFTER.index(n)]:
+            if issue and n in c.setup_after:
+                for line in pieces[c.setup_after.index(n)]:
                     e(line)
-            if n == self.BARRIER_AFTER:
-                # every read of slot CS (this stage's operands) has completed in this wave
+            if n == c.barrier_after:
                 e("s_waitcnt lgkmcnt(0)")
                 if not last:
                     self.wait_oldest()
                     e("s_barrier")
             if last:
                 continue
-            for kind, b in self.READS_AFTER.get(n, []):
-                (self.read_am if kind == "am" else self.read_bn)(b, s["NS"])
-            if issue and n in self.DMA_AFTER:
-                self.issue_dma(self.DMA_AFTER.index(n))
-            if issue and n == self.FINISH_AFTER:
-                self.issue_finish()
+            for side, b in c.reads_after.get(n, []):
+                self.read_block(side, b, s["NS"])
+            if issue and n in c.dma_after:
+                k = c.dma_after.index(n)
+                self.issue_dma(k)
+                if k == c.loads - 1:
+                    self.issue_finish()
 
     def variant_pair(self, first):
         """A stage that is not the tile's last: with or without a stage to issue."""
@@ -323,26 +361,36 @@ class Gen:
     # ---------------------------------------------------------------- epilogue
 
     def c_resource(self):
-        s = SGPR
-        e = self.emit
+        s, OP, e = SGPR, self.OP, self.emit
         e(f"s_mov_b32 {s['RC0']}, {OP['cT_lo']}")
         e(f"s_and_b32 {s['RC1']}, {OP['cT_hi']}, 0xffff")
         e(f"s_mov_b32 {s['RC2']}, {OP['crecT']}")
         e(f"s_mov_b32 {s['RC3']}, 0x{WORD3:x}")
 
-    def store_offset(self, i, k, p):
-        """T = this wave's byte offset of tile rows 128 wm + 32 i + 8 k, columns 192 wn + 64 p."""
-        s = SGPR
-        e = self.emit
-        e(f"s_mul_i32 {s['T']}, {OP['cm2']}, {32 * i + 8 * k}")
+    def store_offset(self, i, row, p, lane_base):
+        """vt2 = byte offset of this wave's tile row 32 i + row (lane part in lane_base), columns
+        from 64 p on."""
+        s, OP, e, c = SGPR, self.OP, self.emit, self.cfg
+        e(f"s_mul_i32 {s['T']}, {OP['cm2']}, {32 * i + row}")
         e(f"s_add_u32 {s['T']}, {s['T']}, {OP['sw_epi']}")
         if p:
             e(f"s_add_u32 {s['T']}, {s['T']}, {128 * p}")
-        e(f"v_add_u32 {VT2}, {s['T']}, {OP['gb']}")
+        e(f"v_add_u32 {c.vt2}, {s['T']}, {OP[lane_base]}")
+
+    @staticmethod
+    def pass_stores(nblk):
+        """(row offset, read base index, read immediate, lane base) of a pass's stores: two-block
+        passes read rows 8 k + l / 8, chunk l % 8 (k = 0..3); one-block passes rows 16 k + l / 4,
+        chunk l % 4 (k = 0, 1)."""
+        if nblk == 2:
+            return [(8 * k, k % 2, 2048 if k >= 2 else 0, "gb") for k in range(4)]
+        return [(16 * k, 2, 2048 * k, "gb1") for k in range(2)]
 
     def epilogue(self):
-        s = SGPR
-        e = self.emit
+        s, OP, e, c = SGPR, self.OP, self.emit, self.cfg
+        v0 = c.vop0                      # the operand registers are free here
+        tacc, tmul, tcvt = v0, v0 + 4, v0 + 8
+        waddr, rbase, dset = v0 + 10, v0 + 18, (v0 + 24, v0 + 40)
         e("s_nop 7")
         e("s_nop 7")
         e("s_nop 7")
@@ -350,76 +398,75 @@ class Gen:
         e(f"s_add_u32 {s['EPI']}, {OP['lds_base']}, {s['CS']}")
         e(f"s_lshl_b32 {s['T']}, {OP['w1k']}, 2")
         e(f"s_add_u32 {s['EPI']}, {s['EPI']}, {s['T']}")
-        # staging write addresses of chunk c = 4 jj + g: row l % 32, chunk c ^ swz, half l / 32
-        for c in range(8):
-            e(f"v_xor_b32 v38, {c}, {OP['ew_s']}")
-            e("v_lshlrev_b32 v38, 4, v38")
-            e(f"v_add3_u32 v{112 + c}, v38, {OP['ew_base']}, {s['EPI']}")
-        e(f"v_add_u32 v120, {s['EPI']}, {OP['rb_even']}")
-        e(f"v_add_u32 v121, {s['EPI']}, {OP['rb_odd']}")
+        # staging write address of chunk cc: row l % 32, chunk cc ^ swz(row), half l / 32
+        for cc in range(8):
+            e(f"v_xor_b32 v{tcvt}, {cc}, {OP['ew_s']}")
+            e(f"v_lshlrev_b32 v{tcvt}, 4, v{tcvt}")
+            e(f"v_add3_u32 v{waddr + cc}, v{tcvt}, {OP['ew_base']}, {s['EPI']}")
+        e(f"v_add_u32 v{rbase}, {s['EPI']}, {OP['rb_even']}")
+        e(f"v_add_u32 v{rbase + 1}, {s['EPI']}, {OP['rb_odd']}")
+        if c.bn % 2:
+            e(f"v_add_u32 v{rbase + 2}, {s['EPI']}, {OP['rb1']}")
         self.c_resource()
         npass = 0
-        for i in range(4):
-            for p in range(3):
-                dbase = 80 if npass % 2 == 0 else 96
+        for i in range(c.bm):
+            for p, blocks in enumerate(c.pairs):
+                dbase = dset[npass % 2]
                 npass += 1
-                for jj in range(2):
-                    j = 2 * p + jj
-                    kind, base = acc(i, j)
+                for jj, j in enumerate(blocks):
+                    kind, base = c.acc(i, j)
                     for g in range(4):
                         src = []
                         for r in range(4):
                             reg = base + 4 * g + r
                             if kind == "a":
-                                e(f"v_accvgpr_read_b32 v{40 + r}, a{reg}")
-                                src.append(f"v{40 + r}")
+                                e(f"v_accvgpr_read_b32 v{tacc + r}, a{reg}")
+                                src.append(f"v{tacc + r}")
                             else:
                                 src.append(f"v{reg}")
                         for r in range(4):
-                            e(f"v_mul_f32 v{44 + r}, {OP['alpha']}, {src[r]}")
-                        e("v_cvt_pk_bf16_f32 v38, v44, v45")
-                        e("v_cvt_pk_bf16_f32 v39, v46, v47")
-                        e(f"ds_write_b64 v{112 + 4 * jj + g}, v[38:39]")
-                for k in range(4):
-                    base_v = "v120" if k % 2 == 0 else "v121"
-                    off = 2048 if k >= 2 else 0
+                            e(f"v_mul_f32 v{tmul + r}, {OP['alpha']}, {src[r]}")
+                        e(f"v_cvt_pk_bf16_f32 v{tcvt}, v{tmul}, v{tmul + 1}")
+                        e(f"v_cvt_pk_bf16_f32 v{tcvt + 1}, v{tmul + 2}, v{tmul + 3}")
+                        e(f"ds_write_b64 v{waddr + 4 * jj + g}, v[{tcvt}:{tcvt + 1}]")
+                stores = self.pass_stores(len(blocks))
+                for k, (_, rb, off, _) in enumerate(stores):
                     d = dbase + 4 * k
-                    e(f"ds_read_b128 v[{d}:{d + 3}], {base_v} offset:{off}")
+                    e(f"ds_read_b128 v[{d}:{d + 3}], v{rbase + rb} offset:{off}")
                 e("s_waitcnt lgkmcnt(0)")
-                for k in range(4):
+                for k, (row, _, _, lb) in enumerate(stores):
                     d = dbase + 4 * k
-                    self.store_offset(i, k, p)
-                    e(f"buffer_store_dwordx4 v[{d}:{d + 3}], {VT2}, {s['RC']}, 0 offen nt")
-        e(f"s_add_u32 {OP['vmt']}, {OP['vmt']}, {E_STORES}")
+                    self.store_offset(i, row, p, lb)
+                    e(f"buffer_store_dwordx4 v[{d}:{d + 3}], {c.vt2}, {s['RC']}, 0 offen nt")
+        e(f"s_add_u32 {OP['vmt']}, {OP['vmt']}, {c.e_stores}")
 
     def zero_epilogue(self):
-        """A tile without tokens: zeros straight from registers, the same 48 stores per wave."""
-        e = self.emit
-        for r in range(80, 84):
+        """A tile without tokens: zeros straight from registers, the same stores per wave."""
+        e, c = self.emit, self.cfg
+        z = c.vop0 + 24
+        for r in range(z, z + 4):
             e(f"v_mov_b32 v{r}, 0")
         self.c_resource()
-        for i in range(4):
-            for p in range(3):
-                for k in range(4):
-                    self.store_offset(i, k, p)
-                    e(f"buffer_store_dwordx4 v[80:83], {VT2}, {SGPR['RC']}, 0 offen nt")
-        e(f"s_add_u32 {OP['vmt']}, {OP['vmt']}, {E_STORES}")
+        for i in range(c.bm):
+            for p, blocks in enumerate(c.pairs):
+                for row, _, _, lb in self.pass_stores(len(blocks)):
+                    self.store_offset(i, row, p, lb)
+                    e(f"buffer_store_dwordx4 v[{z}:{z + 3}], {c.vt2}, {SGPR['RC']}, 0 offen nt")
+        e(f"s_add_u32 {self.OP['vmt']}, {self.OP['vmt']}, {c.e_stores}")
 
     # ---------------------------------------------------------------- whole tile
 
     def tile(self):
-        s = SGPR
-        e = self.emit
+        s, OP, e, c = SGPR, self.OP, self.emit, self.cfg
         e("s_nop 4")   # inputs may come from v_readfirstlane (VALU-written SGPRs) just before
-        e(f"s_add_u32 {s['S']}, {OP['klenT']}, 63")
+        e(f"s_add_u32 {s['S']}, {OP['klenT']}, {KS - 1}")
         e(f"s_lshr_b32 {s['S']}, {s['S']}, 6")
-        e(f"s_lshl_b32 {s['L16']}, {OP['stride_l']}, 4")
-        e(f"s_mul_i32 {s['CS']}, {OP['c0']}, {SLOT}")
+        e(f"s_mul_i32 {s['CS']}, {OP['c0']}, {c.slot}")
         e(f"s_add_u32 {s['T']}, {OP['c0']}, {OP['nis']}")
         e(f"s_cmp_ge_u32 {s['T']}, {SLOTS}")
         e(f"s_cselect_b32 {s['T2']}, {SLOTS}, 0")
         e(f"s_sub_u32 {s['T']}, {s['T']}, {s['T2']}")
-        e(f"s_mul_i32 {s['ISLOT']}, {s['T']}, {SLOT}")
+        e(f"s_mul_i32 {s['ISLOT']}, {s['T']}, {c.slot}")
         # cursor: this tile, at its first stage not yet issued
         e(f"s_mov_b32 {s['INT']}, 1")
         e(f"s_mov_b32 {s['IDX']}, {OP['nis']}")
@@ -451,10 +498,10 @@ class Gen:
         e(f"s_cbranch_scc1 {zero}")
         self.wait_oldest()
         e("s_barrier")
-        for i in range(4):
-            self.read_am(i, s["CS"])
-        for j in range(6):
-            self.read_bn(j, s["CS"])
+        for i in range(c.bm):
+            self.read_block("am", i, s["CS"])
+        for j in range(c.bn):
+            self.read_block("bn", j, s["CS"])
         first_last, loop, steady_last, epi = (self.label(x) for x in ("fl", "loop", "sl", "epi"))
         e(f"s_cmp_eq_u32 {s['S']}, 1")
         e(f"s_cbranch_scc1 {first_last}")
@@ -486,24 +533,26 @@ class Gen:
 
 
 def render():
-    g = Gen()
-    g.tile()
-    text = "\\n\\t".join(g.lines)
-    clob = ([f'"a{r}"' for r in range(256)] + [f'"v{r}"' for r in VGPR_CLOBBER]
-            + [f'"s{r}"' for r in SGPR_CLOBBER] + ['"m0"', '"scc"', '"memory"'])
-    order = ", ".join(f"{i}:{n}" for i, (n, _) in enumerate(OPERANDS))
-    out = [
-        "// Generated by gen_vark_wide.py; do not edit. Per-tile body of the wide-tile FP8 grouped",
-        "// wgrad kernel (vark_wide.h): gfx950 assembly for one inline asm statement.",
-        f"// Operands: {order}",
-        f"#define GGEMM_WIDE_NOPERANDS {len(OPERANDS)}",
-        f"#define GGEMM_WIDE_E_STORES {E_STORES}",
-        f"#define GGEMM_WIDE_LOADS {LOADS}",
-        f"#define GGEMM_WIDE_ASM \"{text}\"",
-        "#define GGEMM_WIDE_CLOBBERS " + ", ".join(clob),
-        "",
-    ]
-    return "\n".join(out), len(g.lines)
+    out = ["// Generated by gen_vark_wide.py; do not edit. Per-tile bodies of the wide-tile FP8 grouped",
+           "// wgrad kernels (vark_wide.h): gfx950 assembly, one inline asm statement per tile shape."]
+    total = 0
+    for c in CONFIGS:
+        g = Gen(c)
+        g.tile()
+        total += len(g.lines)
+        text = "\\n\\t".join(g.lines)
+        clob = ([f'"a{r}"' for r in range(256)] + [f'"v{r}"' for r in c.vgpr_clobber]
+                + [f'"s{r}"' for r in SGPR_CLOBBER] + ['"m0"', '"scc"', '"memory"'])
+        order = ", ".join(f"{i}:{n}" for i, (n, _) in enumerate(c.operands))
+        t = c.name
+        out += [
+            f"// {t} operands: {order}",
+            f"#define GGEMM_WIDE_NOPERANDS_{t} {len(c.operands)}",
+            f"#define GGEMM_WIDE_E_STORES_{t} {c.e_stores}",
+            f"#define GGEMM_WIDE_ASM_{t} \"{text}\"",
+            f"#define GGEMM_WIDE_CLOBBERS_{t} " + ", ".join(clob),
+        ]
+    return "\n".join(out) + "\n", total
 
 
 def main(path=OUT):

@@ -16,7 +16,8 @@ GGEMM_DEFINE_TENSORWISE_LIB_KERNEL(_grouped_variable_k_gemm_kernel_k32, true, ui
 GGEMM_DEFINE_MX_KERNEL(_grouped_variable_k_mxfp8_gemm_kernel)
 GGEMM_DEFINE_TENSORWISE_LIB_KERNEL(_grouped_variable_k_gemm_kernel_f32, false, float, ggemm::kOutF32)
 GGEMM_DEFINE_TENSORWISE_LIB_KERNEL(_grouped_variable_k_gemm_kernel_f32_acc, false, float, ggemm::kOutF32Acc)
-GGEMM_DEFINE_WIDE_KERNEL(_grouped_variable_k_gemm_kernel_wide)
+GGEMM_DEFINE_WIDE_KERNEL(_grouped_variable_k_gemm_kernel_wide, 256, 384)
+GGEMM_DEFINE_WIDE_KERNEL(_grouped_variable_k_gemm_kernel_wide320, 320, 320)
 
 namespace {
 
@@ -42,31 +43,35 @@ int validate_common(const void* lhs, const void* rhs, const void* out, const voi
   return GGEMM_OK;
 }
 
-// Shapes the wide-tile kernel takes: OUT_N a multiple of its 384-wide tile (N-ragged tiles would
-// need per-lane store masks; rows past OUT_M fall outside its C buffer resource), and a group of C
-// addressable with 32-bit byte offsets.
-bool wide_shape_ok(int OUT_M, int OUT_N, int scm) {
-  return OUT_N % ggemm::wide::kTN == 0 && (int64_t)OUT_M * scm * 2 < INT32_MAX;
+// Wide-tile kernels (tile = its OUT_M height): 320 x 320 where it divides both output dims (no
+// partial tiles), else 256 x 384 where OUT_N is a multiple of 384 (N-ragged tiles would need
+// per-lane store masks; rows past OUT_M fall outside the C buffer resource); a group of C must be
+// addressable with 32-bit byte offsets. 0: no wide kernel takes the shape.
+int wide_tile_for(int OUT_M, int OUT_N, int scm) {
+  if ((int64_t)OUT_M * scm * 2 >= INT32_MAX) return 0;
+  if (OUT_M % 320 == 0 && OUT_N % 320 == 0) return 320;
+  if (OUT_N % 384 == 0) return 256;
+  return 0;
 }
 
-// The bf16 entry points run the wide-tile kernel where it takes the shape and the problem is
-// large enough to fill its tiles (OUT_M >= 1024: at most one partial 256-row tile in four);
-// otherwise the 192 x 384 / 192 x 320 kernel.
-bool wide_selected(int OUT_M, int OUT_N, int scm, const void* out) {
-  return OUT_M >= 1024 && wide_shape_ok(OUT_M, OUT_N, scm) && aligned(out, 16);
+// The bf16 entry points run a wide-tile kernel where one takes the shape and the problem is large
+// enough to fill its tiles (OUT_M >= 1024); otherwise the 192 x 384 / 192 x 320 kernel.
+int wide_selected(int OUT_M, int OUT_N, int scm, const void* out) {
+  return OUT_M >= 1024 && aligned(out, 16) ? wide_tile_for(OUT_M, OUT_N, scm) : 0;
 }
 
-int launch_wide(const void* lhs, const void* rhs, void* out, const float* lhs_scale, const float* rhs_scale,
-                const int64_t* group_offs, int32_t G, int32_t OUT_M, int32_t OUT_N, int32_t slm, int32_t srm,
-                int32_t scg, int32_t scm, int32_t scn, int64_t M_total, void* stream) {
+int launch_wide(int tile, const void* lhs, const void* rhs, void* out, const float* lhs_scale,
+                const float* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M, int32_t OUT_N,
+                int32_t slm, int32_t srm, int32_t scg, int32_t scm, int32_t scn, int64_t M_total, void* stream) {
   int cus = 0;
   int rc = device_cus(&cus);
   if (rc) return rc;
-  // the kernel keeps token counts in 32 bits: a group never exceeds 2^31 - 1 tokens
+  // the kernels keep token counts in 32 bits: a group never exceeds 2^31 - 1 tokens
   const int64_t m_total = M_total < INT32_MAX ? M_total : INT32_MAX;
-  hipLaunchKernelGGL(_grouped_variable_k_gemm_kernel_wide, dim3(cus), dim3(ggemm::wide::kNT), 0, (hipStream_t)stream,
-                     (const uint8_t*)lhs, (const uint8_t*)rhs, (uint16_t*)out, lhs_scale, rhs_scale, group_offs, G,
-                     OUT_M, OUT_N, slm, srm, scg, scm, scn, (void*)nullptr, (void*)nullptr, m_total);
+  auto kern = tile == 320 ? _grouped_variable_k_gemm_kernel_wide320 : _grouped_variable_k_gemm_kernel_wide;
+  hipLaunchKernelGGL(kern, dim3(cus), dim3(ggemm::wide::kNT), 0, (hipStream_t)stream, (const uint8_t*)lhs,
+                     (const uint8_t*)rhs, (uint16_t*)out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, slm, srm,
+                     scg, scm, scn, (void*)nullptr, (void*)nullptr, m_total);
   return (int)hipGetLastError();
 }
 
@@ -84,9 +89,9 @@ static int launch_tensorwise(bool legacy, const void* lhs, const void* rhs, void
                            scn);
   if (rc) return rc;
   if (m_total < 0) return GGEMM_E_SHAPE;
-  if (!legacy && wide_selected(OUT_M, OUT_N, scm, out))
-    return launch_wide(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, slm, srm, scg, scm, scn,
-                       m_total, stream);
+  if (const int tile = legacy ? 0 : wide_selected(OUT_M, OUT_N, scm, out))
+    return launch_wide(tile, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, slm, srm, scg, scm,
+                       scn, m_total, stream);
   int cus = 0;
   rc = device_cus(&cus);
   if (rc) return rc;
@@ -100,15 +105,20 @@ static int launch_tensorwise(bool legacy, const void* lhs, const void* rhs, void
 int ggemm_vark_wgrad_fp8_wide(const void* lhs, const void* rhs, void* out, const float* lhs_scale,
                               const float* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
                               int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
-                              int32_t stride_cm, int32_t stride_cn, int64_t M_total, void* stream) {
+                              int32_t stride_cm, int32_t stride_cn, int64_t M_total, int32_t tile_m,
+                              void* stream) {
   int rc = validate_common(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
                            stride_rhs_m, stride_cg, stride_cm, stride_cn);
   if (rc) return rc;
   if (M_total < 0) return GGEMM_E_SHAPE;
-  if (!wide_shape_ok(OUT_M, OUT_N, stride_cm)) return GGEMM_E_SHAPE;
+  const int fit = wide_tile_for(OUT_M, OUT_N, stride_cm);
+  int tile = tile_m == 0 ? fit : tile_m;
+  if (tile == 320 && (OUT_M % 320 || OUT_N % 320)) tile = 0;
+  if (tile == 256 && OUT_N % 384) tile = 0;
+  if ((tile != 256 && tile != 320) || fit == 0) return GGEMM_E_SHAPE;
   if (!aligned(out, 16)) return GGEMM_E_ALIGN;    // 16-byte stores of whole row chunks
-  return launch_wide(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m, stride_rhs_m,
-                     stride_cg, stride_cm, stride_cn, M_total, stream);
+  return launch_wide(tile, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
+                     stride_rhs_m, stride_cg, stride_cm, stride_cn, M_total, stream);
 }
 
 int ggemm_vark_wgrad_fp8(const void* lhs, const void* rhs, void* out, const float* lhs_scale, const float* rhs_scale,
@@ -216,7 +226,7 @@ const char* ggemm_vark_strerror(int32_t code) {
 int32_t ggemm_vark_abi_version(void) { return GGEMM_VARK_ABI_VERSION; }
 
 int32_t ggemm_vark_bf16_kernel(int32_t OUT_M, int32_t OUT_N, int32_t stride_cm, const void* out) {
-  return wide_selected(OUT_M, OUT_N, stride_cm, out) ? 1 : 0;
+  return wide_selected(OUT_M, OUT_N, stride_cm, out);
 }
 
 void ggemm_vark_launch_geometry(int32_t out_n, int32_t* block_threads, int32_t* dynamic_lds, int32_t* tile_m,

@@ -76,15 +76,16 @@ def grouped_gemm_fp8_tensorwise_variable_k(lhs: torch.Tensor, rhs: torch.Tensor,
                                            rhs_scale: torch.Tensor, group_offs: torch.Tensor,
                                            out: torch.Tensor | None = None, *, mfma: str = "k128",
                                            validate: bool = False, out_dtype: torch.dtype = torch.bfloat16,
-                                           accumulate: bool = False, wide: bool = False) -> torch.Tensor:
+                                           accumulate: bool = False, wide: bool | int = False) -> torch.Tensor:
     """``out[g] = lhs_scale * rhs_scale * lhs[offs[g]:offs[g+1]]^T @ rhs[offs[g]:offs[g+1]]`` (bf16).
 
     lhs: float8_e4m3fn [M_total, OUT_M]; rhs: float8_e5m2 [M_total, OUT_N]; scales: fp32 scalar
     tensors on the device; group_offs: int64 [G+1]. ``mfma="k32"`` selects the kernel built on the
     K=32 MFMA the reference uses; ``validate=True`` checks group_offs on the host first (a sync).
     ``out_dtype=torch.float32`` writes an fp32 C; ``accumulate=True`` adds the result into the fp32
-    ``out`` given (the main-grad accumulation, beta = 1). ``wide=True`` runs the wide-tile kernel
-    (256 x 384 tiles, bf16 C, OUT_N a multiple of 384).
+    ``out`` given (the main-grad accumulation, beta = 1). ``wide=True`` runs a wide-tile kernel
+    (bf16 C; 320 x 320 tiles where OUT_M and OUT_N are multiples of 320, else 256 x 384 with OUT_N a
+    multiple of 384); ``wide=320`` / ``wide=256`` picks the tile height.
     """
     _check_inputs(lhs, rhs, group_offs)
     for s in (lhs_scale, rhs_scale):
@@ -111,7 +112,7 @@ def grouped_gemm_fp8_tensorwise_variable_k(lhs: torch.Tensor, rhs: torch.Tensor,
             rc = lib.ggemm_vark_wgrad_fp8_wide(
                 lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), lhs_scale.data_ptr(), rhs_scale.data_ptr(),
                 group_offs.data_ptr(), G, OUT_M, OUT_N, lhs.stride(0), rhs.stride(0), out.stride(0), out.stride(1),
-                out.stride(2), M_total, _stream(lhs.device))
+                out.stride(2), M_total, 0 if wide is True else int(wide), _stream(lhs.device))
         _lib.check(rc, "ggemm_vark_wgrad_fp8_wide")
         return out
     if mfma == "k128":

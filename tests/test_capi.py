@@ -23,16 +23,20 @@ def _header_functions():
 
 
 def test_bf16_kernel_selection(pkg):
-    """The bf16 entry points take the wide-tile kernel for large OUT_M with OUT_N a multiple of 384
-    and a 16-byte aligned C; every other shape keeps the 192-row-tile kernel."""
+    """The bf16 entry points take a wide-tile kernel for large OUT_M: 320 x 320 where both output
+    dims are multiples of 320, else 256 x 384 with OUT_N a multiple of 384, with a 16-byte aligned
+    C; every other shape keeps the 192-row-tile kernel."""
     lib = pkg.load_library()
-    assert lib.ggemm_vark_bf16_kernel(2880, 5760, 5760, 4096) == 1
-    assert lib.ggemm_vark_bf16_kernel(1024, 384, 384, 4096) == 1
-    assert lib.ggemm_vark_bf16_kernel(2880, 2880, 2880, 4096) == 0      # OUT_N not a multiple of 384
+    assert lib.ggemm_vark_bf16_kernel(2880, 5760, 5760, 4096) == 320
+    assert lib.ggemm_vark_bf16_kernel(2880, 2880, 2880, 4096) == 320
+    assert lib.ggemm_vark_bf16_kernel(1024, 384, 384, 4096) == 256
+    assert lib.ggemm_vark_bf16_kernel(3072, 5376, 5376, 4096) == 256
+    assert lib.ggemm_vark_bf16_kernel(2048, 2000, 2000, 4096) == 0      # neither tile divides OUT_N
     assert lib.ggemm_vark_bf16_kernel(1008, 5760, 5760, 4096) == 0      # small OUT_M
     assert lib.ggemm_vark_bf16_kernel(2880, 5760, 5760, 4104) == 0      # C only 8-byte aligned
     assert lib.ggemm_vark_bf16_kernel(65536, 384, 65536, 4096) == 0     # group past 32-bit offsets
-    assert pkg.bf16_kernel(2880, 5760) == "wide" and pkg.bf16_kernel(2880, 2880) == "192-row"
+    assert pkg.bf16_kernel(2880, 5760) == "wide320" and pkg.bf16_kernel(1024, 768) == "wide256"
+    assert pkg.bf16_kernel(1000, 2880) == "192-row"
 
 
 def test_library_exports_every_header_symbol(pkg):

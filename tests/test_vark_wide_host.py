@@ -1,5 +1,5 @@
-"""CPU checks of the wide-tile wgrad kernel's generated assembly (ggemm-asm_amd/csrc/gen_vark_wide.py,
-vark_wide.h), before any GPU launch.
+"""CPU checks of the wide-tile wgrad kernels' generated assembly (ggemm-asm_amd/csrc/gen_vark_wide.py,
+vark_wide.h; both tile shapes, 256 x 384 and 320 x 320), before any GPU launch.
 
 The per-tile assembly statement is executed by a small interpreter of its scalar instructions
 (SALU arithmetic, compares, branches, m0) that records the vector-memory, LDS and MFMA
@@ -12,9 +12,9 @@ long groups) the recorded program must:
     wave reads it, and never DMA into a slot before a barrier that follows the last reads of its
     previous stage or of the epilogue staged there, nor stage C in a slot before a barrier that
     follows every read of its stage;
-  * issue 24 MFMAs per stage covering the 4 x 6 blocks once (zero accumulator input in a tile's
-    first stage), each after the LDS reads of its operands completed (in-order lgkmcnt), and 48 C
-    stores per tile whose row/column offsets cover the wave's quadrant;
+  * issue BM x BN MFMAs per stage covering the blocks once (zero accumulator input in a tile's
+    first stage), each after the LDS reads of its operands completed (in-order lgkmcnt), and the C
+    stores of every epilogue pass, whose row/column offsets cover the wave's quadrant;
   * take the same branches and barriers in every wave.
 Per-lane address maps (operand reads, LDS-DMA placement, epilogue staging) are checked against
 the 32x32x64 operand layout and for LDS bank conflicts.
@@ -42,8 +42,8 @@ GEN = _gen()
 M32 = 0xFFFFFFFF
 
 
-def _program():
-    g = GEN.Gen()
+def _program(cfg):
+    g = GEN.Gen(cfg)
     g.tile()
     prog, labels = [], {}
     for line in g.lines:
@@ -56,7 +56,8 @@ def _program():
     return prog, labels
 
 
-PROG, LABELS = _program()
+CFGS = {c.name: c for c in GEN.CONFIGS}
+PROGS = {name: _program(c) for name, c in CFGS.items()}
 
 
 def _s32(x):
@@ -67,7 +68,9 @@ def _s32(x):
 class Block:
     """Runs the per-tile statement for one wave with given operand values."""
 
-    def __init__(self, ops, events, scal):
+    def __init__(self, cfg, ops, events, scal, prog=None):
+        self.cfg = cfg
+        self.prog, self.labels = prog or PROGS[cfg.name]
         self.ops = ops          # operand name -> value (SGPR operands) / name (VGPR operands)
         self.ev = events
         self.s = scal           # persistent scalar temporaries (s56..s88), as on the GPU
@@ -76,7 +79,7 @@ class Block:
 
     def val(self, a):
         if a.startswith("%"):
-            name = GEN.OPERANDS[int(a[1:])][0]
+            name = self.cfg.operands[int(a[1:])][0]
             return self.ops[name]
         if a == "m0":
             return self.s.get("m0", 0)
@@ -89,8 +92,8 @@ class Block:
     def setr(self, a, x):
         x &= M32
         if a.startswith("%"):
-            name = GEN.OPERANDS[int(a[1:])][0]
-            assert GEN.OPERANDS[int(a[1:])][1] == "+s", f"write to input operand {name}"
+            name = self.cfg.operands[int(a[1:])][0]
+            assert self.cfg.operands[int(a[1:])][1] == "+s", f"write to input operand {name}"
             self.ops[name] = x
         else:
             assert a == "m0" or re.fullmatch(r"s\d+", a), a
@@ -103,6 +106,7 @@ class Block:
 
     def run(self):
         pc = 0
+        PROG, LABELS = self.prog, self.labels
         while pc < len(PROG):
             op, a = PROG[pc]
             pc += 1
@@ -183,7 +187,7 @@ class Block:
 LHS, RHS, OUT = 0x7F0000000000, 0x7E0000000000, 0x7D0000000000
 
 
-def _run_tiles(tiles, wave, stride_l=2880, stride_r=5760, stride_cm=5760, OUT_M=2880):
+def _run_tiles(cfg, tiles, wave, stride_l=2880, stride_r=5760, stride_cm=5760, OUT_M=2880, prog=None):
     """tiles: list of (g, m0, n0, kb, klen). Returns (events, per-tile event slices, final state)."""
     ev = []
     scal = {f"s{r}": 0 for r in GEN.SGPR_CLOBBER}
@@ -203,9 +207,9 @@ def _run_tiles(tiles, wave, stride_l=2880, stride_r=5760, stride_cm=5760, OUT_M=
                    cT_lo=(OUT + 2 * (m0 * stride_cm + n0)) & M32, cT_hi=(OUT + 2 * (m0 * stride_cm + n0)) >> 32,
                    crecT=((OUT_M - m0) * stride_cm - n0) * 2,
                    stride_l=stride_l, stride_r=stride_r, cm2=2 * stride_cm, alpha=0x3F800000,
-                   sw_epi=(128 * (wave & 1) * stride_cm + 192 * (wave >> 1)) * 2)
+                   sw_epi=(32 * cfg.bm * (wave & 1) * stride_cm + 32 * cfg.bn * (wave >> 1)) * 2)
         start = len(ev)
-        Block(ops, ev, scal).run()
+        Block(cfg, ops, ev, scal, prog).run()
         spans.append((start, len(ev)))
         for k in state:
             state[k] = ops[k]
@@ -213,46 +217,52 @@ def _run_tiles(tiles, wave, stride_l=2880, stride_r=5760, stride_cm=5760, OUT_M=
     return ev, spans, state
 
 
-def _check(tiles, wave=0, stride_l=2880, stride_r=5760, stride_cm=5760, OUT_M=2880):
-    ev, spans, state = _run_tiles(tiles, wave, stride_l, stride_r, stride_cm, OUT_M)
+def _check(cfg, tiles, wave=0, stride_l=2880, stride_r=5760, stride_cm=5760, OUT_M=2880, prog=None):
+    ev, spans, state = _run_tiles(cfg, tiles, wave, stride_l, stride_r, stride_cm, OUT_M, prog)
+    op = lambda name: "%" + str([n for n, _ in cfg.operands].index(name))
+    L = cfg.loads
     stages = [(n, s) for n, t in enumerate(tiles) for s in range((t[4] + 63) // 64)]
     slot_of = {st: k % 3 for k, st in enumerate(stages)}
-    # ---- DMA: one group of 4 LHS + 6 RHS loads per stage, in stage order
+    # ---- DMA: one group of nl LHS + nr RHS loads per stage, in stage order
     dmas = [(i, e) for i, e in enumerate(ev) if e[0] == "dma"]
-    assert len(dmas) == 10 * len(stages)
+    assert len(dmas) == L * len(stages)
     issue_pos = {}
     for k, (n, s) in enumerate(stages):
         g, m0, n0, kb, klen = tiles[n]
-        grp = dmas[10 * k:10 * k + 10]
+        grp = dmas[L * k:L * k + L]
         issue_pos[(n, s)] = (grp[0][0], grp[-1][0])
         rv = min(64, klen - 64 * s)
         for j, (_, e) in enumerate(grp):
             _, m0v, (base, nrec, stride_bits, w3), voff, _ = e
             assert stride_bits == 0 and w3 == GEN.WORD3
-            if j < 4:
+            if j < cfg.nl:
                 assert base == LHS + (kb + 64 * s) * stride_l + m0
                 assert nrec == rv * stride_l - m0
-                assert m0v == slot_of[(n, s)] * GEN.SLOT + 1024 * wave + 4096 * j
-                assert voff == ((0, "%" + str(_opidx("voffL0"))) if j == 0 else (16 * stride_l * j, _op("voffL0")))
+                assert m0v == slot_of[(n, s)] * cfg.slot + 1024 * wave + 4096 * j
+                assert voff == (0, op(f"voffL{j}"))
             else:
-                jj = j - 4
+                jj = j - cfg.nl
                 assert base == RHS + (kb + 64 * s) * stride_r + n0
                 assert nrec == rv * stride_r - n0
-                assert m0v == slot_of[(n, s)] * GEN.SLOT + GEN.RHS_OFF + 1024 * wave + 4096 * jj
-                assert voff == (0, _op(f"voffR{jj}"))
-    # ---- reads: groups of 40 in compute order, from the stage's slot
+                assert m0v == slot_of[(n, s)] * cfg.slot + cfg.rhs_off + 1024 * wave + 4096 * jj
+                assert voff == (0, op(f"voffR{jj}"))
+    # ---- reads: groups of 4 (bm + bn) in compute order, from the stage's slot
+    R = 4 * (cfg.bm + cfg.bn)
     reads = [(i, e) for i, e in enumerate(ev) if e[0] == "read"]
-    assert len(reads) == 40 * len(stages)
+    assert len(reads) == R * len(stages)
     read_span = {}
+    want = []
+    for side, nb, pitch in (("am", cfg.bm, cfg.tm), ("bn", cfg.bn, cfg.tn)):
+        for b in range(nb):
+            base, extra = cfg.read_base(side, b)
+            want += [(base, extra + dt * pitch) for dt in GEN.TOK_OFFS]
     for k, st in enumerate(stages):
-        grp = reads[40 * k:40 * k + 40]
+        grp = reads[R * k:R * k + R]
         read_span[st] = (grp[0][0], grp[-1][0])
         names = []
         for _, (_, (slot_off, name), off, dst) in grp:
-            assert slot_off == slot_of[st] * GEN.SLOT, (st, slot_off)
+            assert slot_off == slot_of[st] * cfg.slot, (st, slot_off)
             names.append((name, off))
-        want = [(_op(f"amb{i}"), o) for i in range(4) for o in (0, 2048, 8192, 10240)]
-        want += [(_op(f"bnb{j}"), o) for j in range(6) for o in (0, 3072, 12288, 15360)]
         assert sorted(names) == sorted(want)
     # ---- completion model: in-order vmcnt, barriers
     issued = []            # event index of each vector-memory op, in order
@@ -279,7 +289,7 @@ def _check(tiles, wave=0, stride_l=2880, stride_r=5760, stride_cm=5760, OUT_M=28
     for e in ev:
         if e[0] == "read":
             pending.append(regs(e[3]))
-        elif e[0] in ("ds_write_b64",):
+        elif e[0] == "ds_write_b64":
             pending.append(set())
         elif e[0] == "ds_read_b128":
             pending.append(regs(e[1][0]))
@@ -292,11 +302,6 @@ def _check(tiles, wave=0, stride_l=2880, stride_r=5760, stride_cm=5760, OUT_M=28
             assert not any(regs(e[3]) & p for p in pending), "store of pending LDS data"
     # ---- slot reuse: a DMA into a slot follows a barrier that follows every read of the previous
     # stage in that slot and every epilogue staging access there
-    last_use = {0: -1, 1: -1, 2: -1}
-    occupant = {}
-    stage_at_dma = {}
-    for k, st in enumerate(stages):
-        stage_at_dma[issue_pos[st][0]] = st
     epi_slot_events = []
     for n, (a, b) in enumerate(spans):
         if (tiles[n][4] + 63) // 64 > 0:
@@ -304,19 +309,14 @@ def _check(tiles, wave=0, stride_l=2880, stride_r=5760, stride_cm=5760, OUT_M=28
             for i in range(a, b):
                 if ev[i][0] in ("ds_write_b64", "ds_read_b128"):
                     epi_slot_events.append((i, slot_of[last]))
-    uses = []
+    uses = sorted([(read_span[st][1], slot_of[st]) for st in stages] + epi_slot_events)
     for st in stages:
-        uses.append((read_span[st][1], slot_of[st]))
-    uses += epi_slot_events
-    uses.sort()
-    for k, st in enumerate(stages):
         pos = issue_pos[st][0]
         slot = slot_of[st]
         prior = [i for i, sl in uses if sl == slot and i < pos]
         if prior:
             assert any(max(prior) < bi < pos for bi in barriers), f"DMA of {st} into slot {slot} races a reader"
-        # and no read of this slot's previous stage after the DMA
-        later_prev = [i for i, sl in uses if sl == slot and i > pos and i < read_span[st][0]]
+        later_prev = [i for i, sl in uses if sl == slot and pos < i < read_span[st][0]]
         assert not later_prev, f"slot {slot} read after DMA of {st}"
     # the epilogue stages C in the slot of the tile's last stage: its first write follows a barrier
     # that follows every wave's reads of that stage
@@ -327,45 +327,38 @@ def _check(tiles, wave=0, stride_l=2880, stride_r=5760, stride_cm=5760, OUT_M=28
             last_r = read_span[(n, S - 1)][1]
             assert any(last_r < bi < first_w for bi in barriers), f"tile {n}: staging races operand reads"
     # ---- MFMAs and stores per tile
+    nblk = cfg.bm * cfg.bn
     for n, (a, b) in enumerate(spans):
         S = (tiles[n][4] + 63) // 64
         mf = [ev[i] for i in range(a, b) if ev[i][0] == "mfma"]
-        assert len(mf) == 24 * S
+        assert len(mf) == nblk * S
         for s in range(S):
-            blk = mf[24 * s:24 * s + 24]
-            dsts = {e[1] for e in blk}
-            assert len(dsts) == 24
+            blk = mf[nblk * s:nblk * s + nblk]
+            assert len({e[1] for e in blk}) == nblk
             for e in blk:
                 assert (e[4] == "0") == (s == 0) and (e[4] == "0" or e[4] == e[1])
         st_ev = [ev[i] for i in range(a, b) if ev[i][0] == "store"]
-        assert len(st_ev) == GEN.E_STORES
+        assert len(st_ev) == cfg.e_stores
         g, m0, n0, kb, klen = tiles[n]
-        offs = sorted(e[1][0] for e in st_ev)
-        sw = (128 * (wave & 1) * stride_cm + 192 * (wave >> 1)) * 2
-        want = sorted(sw + (32 * i + 8 * k) * 2 * stride_cm + 128 * p for i in range(4) for k in range(4)
-                      for p in range(3))
-        assert offs == want
+        sw = (32 * cfg.bm * (wave & 1) * stride_cm + 32 * cfg.bn * (wave >> 1)) * 2
+        want_st = []
+        for i in range(cfg.bm):
+            for pidx, blocks in enumerate(cfg.pairs):
+                for row, _, _, lb in GEN.Gen.pass_stores(len(blocks)):
+                    want_st.append((sw + (32 * i + row) * 2 * stride_cm + 128 * pidx, op(lb)))
+        assert sorted((e[1][0], e[1][1]) for e in st_ev) == sorted(want_st)
         for e in st_ev:
             base, nrec, _, _ = e[2]
             assert base == OUT + 2 * (m0 * stride_cm + n0) and nrec == ((OUT_M - m0) * stride_cm - n0) * 2
-            assert e[1][1] == _op("gb")
     assert state["np"] == 0 and state["nis"] == 0
     return ev
 
 
-def _opidx(name):
-    return [n for n, _ in GEN.OPERANDS].index(name)
-
-
-def _op(name):
-    return "%" + str(_opidx(name))
-
-
-def _tiles(klens, seed=0):
+def _tiles(cfg, klens, seed=0):
     rng = np.random.default_rng(seed)
     out, kb = [], 0
     for n, k in enumerate(klens):
-        out.append((n % 7, 256 * int(rng.integers(0, 11)), 384 * int(rng.integers(0, 15)), kb, int(k)))
+        out.append((n % 7, cfg.tm * int(rng.integers(0, 9)), cfg.tn * int(rng.integers(0, 15)), kb, int(k)))
         kb += int(k)
     return out
 
@@ -377,141 +370,177 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("cfg", list(CFGS))
 @pytest.mark.parametrize("klens", CASES, ids=[f"case{i}" for i in range(len(CASES))])
-def test_wide_pipeline_program(klens):
-    _check(_tiles(klens, seed=len(klens)))
+def test_wide_pipeline_program(cfg, klens):
+    c = CFGS[cfg]
+    _check(c, _tiles(c, klens, seed=len(klens)), stride_cm=5760 if cfg == "256x384" else 5760)
 
 
-def test_wide_pipeline_random_sequences():
+@pytest.mark.parametrize("cfg", list(CFGS))
+def test_wide_pipeline_random_sequences(cfg):
+    c = CFGS[cfg]
     rng = np.random.default_rng(7)
     for trial in range(40):
         n = int(rng.integers(1, 9))
         klens = [int(x) for x in rng.choice([0, 1, 31, 63, 64, 65, 127, 128, 129, 190, 320, 777], size=n)]
-        _check(_tiles(klens, seed=trial), wave=trial % 4)
+        _check(c, _tiles(c, klens, seed=trial), wave=trial % 4)
 
 
-def test_waves_take_the_same_path():
-    tiles = _tiles([130, 0, 1, 63, 64, 65, 300], seed=3)
+@pytest.mark.parametrize("cfg", list(CFGS))
+def test_waves_take_the_same_path(cfg):
+    c = CFGS[cfg]
+    tiles = _tiles(c, [130, 0, 1, 63, 64, 65, 300], seed=3)
     seqs = []
     for w in range(4):
-        ev, _, _ = _run_tiles(tiles, w)
+        ev, _, _ = _run_tiles(c, tiles, w)
         seqs.append([e[0] for e in ev if e[0] in ("barrier", "mfma", "dma", "store", "read")])
-    assert all(s == seqs[0] for s in seqs)
+    assert all(sq == seqs[0] for sq in seqs)
+
+
+def test_generated_include_is_current():
+    """vark_wide_asm.inc in the tree is what the generator writes (the build regenerates it)."""
+    text, _ = GEN.render()
+    assert open(GEN.OUT).read() == text
+
+
+def test_asm_writes_only_clobbered_registers():
+    for c in GEN.CONFIGS:
+        g = GEN.Gen(c)
+        g.tile()
+        for line in g.lines:
+            for m in re.finditer(r"\b([sva])\[?(\d+)(?::(\d+)\])?", line):
+                k, lo = m.group(1), int(m.group(2))
+                hi = int(m.group(3)) if m.group(3) else lo
+                if k == "s":
+                    assert GEN.SGPR_CLOBBER[0] <= lo and hi <= GEN.SGPR_CLOBBER[-1], line
+                elif k == "v":
+                    assert c.vgpr_clobber[0] <= lo and hi <= 255, line
+                else:
+                    assert hi <= 255, line
 
 
 # ----------------------------------------------------------------------------- per-lane maps
+# Restated from vark_wide.h's set-up (amb / bnb / voff / epilogue bases) and checked for layout
+# and conflicts.
 
-def _swz_l(t):
-    return (t & 7) << 1
-
-
-def _swz_r(t):
-    return ((t >> 1) & 3) << 1
-
-
-def _lane_reads(w, width, lane_base_fn):
-    """(lane, read k) -> (token, logical chunk, half) of the LDS bytes a transposed read touches."""
-    out = {}
-    for lane in range(64):
-        for k, dt in enumerate((0, 8, 32, 40)):
-            out[(lane, k)] = lane_base_fn(lane, dt)
-    return out
+def _lane(lane):
+    g16, t16 = lane >> 4, lane & 15
+    return g16 & 1, 16 * (g16 >> 1) + (t16 >> 1), t16 & 1      # cb, tb0, hb
 
 
-def test_operand_reads_match_dma_placement_and_layout():
+def _block_base(cfg, side, wv, b, lane):
+    """Byte offset (slot-relative) of block b's first transposed read, as vark_wide.h forms it."""
+    cb, tb0, hb = _lane(lane)
+    pitch, nb = (cfg.tm, cfg.bm) if side == "am" else (cfg.tn, cfg.bn)
+    off = 0 if side == "am" else cfg.rhs_off
+    swz = GEN.swizzle(pitch)
+    return off + tb0 * pitch + 16 * ((2 * nb * wv + 2 * b + cb) ^ swz(tb0)) + 8 * hb
+
+
+@pytest.mark.parametrize("cfg", list(CFGS))
+def test_operand_reads_match_dma_placement_and_layout(cfg):
     """For every lane and read, the physical LDS address it reads holds (token, logical column
     chunk, half) = the 32x32x64 operand element the MFMA needs: row l % 32 of the block, tokens
-    16 h + 0..15 in bytes 0-15 and 32 + 16 h + 0..15 in bytes 16-31 (h = l / 32)."""
-    for side, width, swz, nblk in (("lhs", 256, _swz_l, 4), ("rhs", 384, _swz_r, 6)):
-        for wv in range(2):   # wm for LHS, wn for RHS
-            for blk in range(nblk):
+    16 h + 0..15 in bytes 0-15 and 32 + 16 h + 0..15 in bytes 16-31 (h = l / 32). With parity
+    bases, block b's address is base[b & 1] + 32 b as the assembly forms it."""
+    c = CFGS[cfg]
+    for side, nb, pitch in (("am", c.bm, c.tm), ("bn", c.bn, c.tn)):
+        swz = GEN.swizzle(pitch)
+        off = 0 if side == "am" else c.rhs_off
+        for wv in range(2):
+            for b in range(nb):
                 for lane in range(64):
-                    g16, t16 = lane >> 4, lane & 15
-                    cb, hh = g16 & 1, g16 >> 1
-                    tb0, hb = 16 * hh + (t16 >> 1), t16 & 1
-                    first = (8 * wv if side == "lhs" else 12 * wv) + 2 * blk
-                    base = tb0 * width + 16 * ((first + cb) ^ swz(tb0)) + 8 * hb
-                    for dt in (0, 8, 32, 40):
-                        addr = base + dt * width
-                        t = addr // width
-                        pc = (addr % width) // 16
-                        logical = pc ^ swz(t)   # the DMA stored logical chunk pc ^ swz(t) at pc
-                        assert t == tb0 + dt and logical == first + cb and (addr % 16) // 8 == hb
-                    # the tr_b8 read of the 16-lane group gives lane l column 16 cb + l % 16 of the
-                    # block: operand row l % 32
+                    cb, tb0, hb = _lane(lane)
+                    base = _block_base(c, side, wv, b, lane)
+                    if c.parity_bases:
+                        pb = _block_base(c, side, wv, b & 1, lane) - 32 * (b & 1)
+                        assert pb + 32 * b == base
+                    first = 2 * nb * wv + 2 * b
+                    for dt in GEN.TOK_OFFS:
+                        addr = base + dt * pitch - off
+                        t, pc = addr // pitch, (addr % pitch) // 16
+                        assert t == tb0 + dt and pc ^ swz(t) == first + cb and (addr % 16) // 8 == hb
                     assert 16 * cb + (lane % 16) == lane % 32
 
 
-def test_operand_reads_conflict_free():
-    for width, swz, first_fn in ((256, _swz_l, lambda wv, b: 8 * wv + 2 * b), (384, _swz_r, lambda wv, b: 12 * wv + 2 * b)):
+@pytest.mark.parametrize("cfg", list(CFGS))
+def test_operand_reads_conflict_free(cfg):
+    c = CFGS[cfg]
+    for side, nb, pitch in (("am", c.bm, c.tm), ("bn", c.bn, c.tn)):
         for wv in range(2):
-            for blk in range(4 if width == 256 else 6):
-                for dt in (0, 8, 32, 40):
+            for b in range(nb):
+                for dt in GEN.TOK_OFFS:
                     for half in range(2):
-                        pairs = set()
-                        for lane in range(32 * half, 32 * half + 32):
-                            g16, t16 = lane >> 4, lane & 15
-                            cb, hh = g16 & 1, g16 >> 1
-                            tb0, hb = 16 * hh + (t16 >> 1), t16 & 1
-                            addr = (tb0 + dt) * width + 16 * ((first_fn(wv, blk) + cb) ^ swz(tb0)) + 8 * hb
-                            pairs.add((addr // 8) % 32)
+                        pairs = {((_block_base(c, side, wv, b, lane) + dt * pitch) // 8) % 32
+                                 for lane in range(32 * half, 32 * half + 32)}
                         assert len(pairs) == 32
 
 
-def test_dma_fills_each_slot_byte_once():
-    stride_l, stride_r = 2880, 5760
-    for width, n_inst, stride, swz in ((256, 16, stride_l, _swz_l), (384, 24, stride_r, _swz_r)):
+@pytest.mark.parametrize("cfg", list(CFGS))
+def test_dma_fills_each_slot_byte_once(cfg):
+    c = CFGS[cfg]
+    for pitch, n_inst, stride in ((c.tm, 4 * c.nl, 2880), (c.tn, 4 * c.nr, 5760)):
+        swz = GEN.swizzle(pitch)
         seen = {}
         for w in range(4):
             for j in range(n_inst // 4):
                 i = w + 4 * j
                 for lane in range(64):
                     q = 64 * i + lane
-                    row, pc = q // (width // 16), q % (width // 16)
+                    row, pc = q // (pitch // 16), q % (pitch // 16)
                     lds = 1024 * i + 16 * lane
-                    assert lds == row * width + 16 * pc
-                    if width == 256:
-                        rowl, pcl = 4 * w + (lane >> 4), lane & 15
-                        voff = rowl * stride + 16 * (pcl ^ swz(rowl)) + 16 * j * stride
-                    else:
-                        voff = row * stride + 16 * (pc ^ swz(row))
-                    seen[lds] = voff
-                    assert voff == row * stride + 16 * (pc ^ swz(row))
-        assert sorted(seen) == list(range(0, 64 * width, 16))
+                    assert lds == row * pitch + 16 * pc
+                    seen[lds] = row * stride + 16 * (pc ^ swz(row))
+        assert sorted(seen) == list(range(0, 64 * pitch, 16))
+        # the logical chunks of each row are each loaded once
+        rows = {}
+        for lds, voff in seen.items():
+            rows.setdefault(voff // stride, []).append((voff % stride) // 16)
+        assert all(sorted(v) == list(range(pitch // 16)) for v in rows.values())
+
+
+def _phys(r, cc):
+    return r * 128 + 16 * (cc ^ ((r >> 1) & 7))
 
 
 def test_epilogue_staging_and_store_coverage():
-    """Writes (row l % 32, chunk 4 jj + g, half l / 32) and read-backs (row 8 k + l / 8, chunk
-    l % 8) address the same swizzled layout, each 16-byte chunk once, conflict-free (16 lanes per
-    8-byte write cycle, 8 lanes per 16-byte read cycle); the stores then cover the 32 x 64 piece."""
-    def phys(r, c):
-        return r * 128 + 16 * (c ^ ((r >> 1) & 7))
-    writes = {}
-    for jj in range(2):
-        for g in range(4):
+    """Writes (row l % 32, chunk 4 jj + g, half l / 32) and read-backs (two-block passes: row
+    8 k + l / 8, chunk l % 8; one-block passes: row 16 k + l / 4, chunk l % 4) address the same
+    swizzled layout, each 16-byte chunk once, conflict-free (16 lanes per 8-byte write cycle, 8
+    lanes per 16-byte read cycle); the stores then cover the 32 x 64 (32 x 32) piece."""
+    for nblk in (2, 1):
+        writes = {}
+        for jj in range(nblk):
+            for g in range(4):
+                for lane in range(64):
+                    rl, hl = lane & 31, lane >> 5
+                    ew_base, ew_s = rl * 128 + 8 * hl, (rl >> 1) & 7
+                    addr = ew_base + (((4 * jj + g) ^ ew_s) << 4)
+                    assert addr == _phys(rl, 4 * jj + g) + 8 * hl
+                    writes[addr] = (rl, 32 * jj + 8 * g + 4 * hl)     # row, first column of 4
+                for q in range(4):
+                    banks = {(((lane & 31) * 128 + ((((4 * jj + g) ^ (((lane & 31) >> 1) & 7)) << 4))
+                               + 8 * (lane >> 5)) // 8) % 32 for lane in range(16 * q, 16 * q + 16)}
+                    assert len(banks) == 16
+        assert len(writes) == 32 * 8 * nblk
+        cover = set()
+        for k, (row, rb, off, lb) in enumerate(GEN.Gen.pass_stores(nblk)):
+            addrs = []
             for lane in range(64):
-                rl, hl = lane & 31, lane >> 5
-                ew_base, ew_s = rl * 128 + 8 * hl, (rl >> 1) & 7
-                addr = ew_base + (((4 * jj + g) ^ ew_s) << 4)
-                assert addr == phys(rl, 4 * jj + g) + 8 * hl
-                writes[addr] = (rl, 32 * jj + 8 * g + 4 * hl)     # row, first column of 4
-            for q in range(4):
-                banks = {((((lane & 31) * 128 + ((((4 * jj + g) ^ (((lane & 31) >> 1) & 7)) << 4)) + 8 * (lane >> 5)) // 8) % 32)
-                         for lane in range(16 * q, 16 * q + 16)}
-                assert len(banks) == 16
-    assert len(writes) == 32 * 16
-    cover = set()
-    for k in range(4):
-        for lane in range(64):
-            rr, rc, rs = lane >> 3, lane & 7, ((lane >> 3) >> 1) & 7
-            rb = (rr * 128 + 16 * (rc ^ rs)) if k % 2 == 0 else ((8 + rr) * 128 + 16 * (rc ^ (rs ^ 4)))
-            addr = rb + (2048 if k >= 2 else 0)
-            r = 8 * k + rr
-            assert addr == phys(r, rc)
-            assert writes[addr] == (r, 8 * rc) and writes[addr + 8] == (r, 8 * rc + 4)
-            cover.add((r, rc))
-        for q in range(8):
-            chunks = {(((8 * k + (lane >> 3)) * 128 + 16 * ((lane & 7) ^ (((8 * k + (lane >> 3)) >> 1) & 7))) // 16) % 8
-                      for lane in range(8 * q, 8 * q + 8)}
-            assert len(chunks) == 8
-    assert cover == {(r, c) for r in range(32) for c in range(8)}
+                if nblk == 2:
+                    rr, rc, rs = lane >> 3, lane & 7, ((lane >> 3) >> 1) & 7
+                    base = (rr * 128 + 16 * (rc ^ rs)) if rb == 0 else ((8 + rr) * 128 + 16 * (rc ^ (rs ^ 4)))
+                    r, cc = row + rr, rc
+                else:
+                    r1, c1 = lane >> 2, lane & 3
+                    base = r1 * 128 + 16 * (c1 ^ ((r1 >> 1) & 7))
+                    r, cc = row + r1, c1
+                addr = base + off
+                assert addr == _phys(r, cc)
+                assert writes[addr] == (r, 8 * cc) and writes[addr + 8] == (r, 8 * cc + 4)
+                cover.add((r, cc))
+                addrs.append(addr)
+            for q in range(8):
+                assert len({(a // 16) % 16 for a in addrs[8 * q:8 * q + 8]}) == 8   # 16-byte bank groups
+        assert cover == {(r, cc) for r in range(32) for cc in range(4 * nblk)}
