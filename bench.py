@@ -498,7 +498,15 @@ def main():
                     p.lhs, p.rhs, sl, sr, p.group_offs, out=c32, out_dtype=torch.float32, accumulate=acc)
                 t = time_steps(r, max(args.steps // 4, 10), max(args.warmup // 4, 5))
                 extra[name] = {"ms": round(t, 4), "TFLOPS": round(p.flops / (t * 1e-3) / 1e12, 2)}
-            del c32
+            # the accumulate at the reference's seed-42 exponential group lengths
+            q = pkg.inputs.make_problem("gate_up_wgrad", seed=args.seed, device=dev,
+                                        lens=pkg.inputs.make_group_lens_reference())
+            r = lambda: pkg.grouped_gemm_fp8_tensorwise_variable_k(
+                q.lhs, q.rhs, sl, sr, q.group_offs, out=c32, out_dtype=torch.float32, accumulate=True)
+            t = time_steps(r, max(args.steps // 4, 10), max(args.warmup // 4, 5))
+            extra["gate_up_reference_lens_f32_accum"] = {"ms": round(t, 4),
+                                                         "TFLOPS": round(q.flops / (t * 1e-3) / 1e12, 2)}
+            del c32, q
         line["extra"] = extra
     if args.cpu_seconds > 0 and fwd:
         line["cpu_baseline"] = cpu_baseline_fwd(p, args.cpu_seconds)

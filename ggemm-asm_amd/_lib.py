@@ -73,7 +73,7 @@ def load():
         f.restype = ctypes.c_int
     lib.ggemm_vark_wgrad_fp8_out.argtypes = tw[:-1] + [i32, ctypes.c_int64, vp]
     lib.ggemm_vark_wgrad_fp8_out.restype = ctypes.c_int
-    lib.ggemm_vark_wgrad_fp8_wide.argtypes = tw[:-1] + [ctypes.c_int64, i32, vp]
+    lib.ggemm_vark_wgrad_fp8_wide.argtypes = tw[:-1] + [ctypes.c_int64, i32, i32, vp]
     lib.ggemm_vark_wgrad_fp8_wide.restype = ctypes.c_int
     lib.ggemm_vark_wgrad_mxfp8.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 10 + [ctypes.c_int64, vp]
     lib.ggemm_vark_wgrad_mxfp8.restype = ctypes.c_int

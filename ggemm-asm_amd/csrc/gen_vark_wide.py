@@ -69,9 +69,10 @@ def swizzle(pitch):
 
 
 class Config:
-    def __init__(self, tm, tn):
+    def __init__(self, tm, tn, out="bf16"):
         self.tm, self.tn = tm, tn
-        self.name = f"{tm}x{tn}"
+        self.out = out                                  # "bf16", "f32" (fp32 C) or "f32acc" (C += result)
+        self.name = f"{tm}x{tn}" + ("" if out == "bf16" else "_" + out)
         self.bm, self.bn = tm // 64, tn // 64           # 32-wide blocks per wave (2 x 2 waves)
         self.rhs_off = KS * tm
         self.slot = KS * (tm + tn)
@@ -84,7 +85,12 @@ class Config:
         self.vt, self.vt2 = f"v{self.vop0 - 2}", f"v{self.vop0 - 1}"
         self.vgpr_clobber = list(range(self.vop0 - 2, 256))
         self.pairs = [(2 * p, 2 * p + 1) if 2 * p + 1 < self.bn else (2 * p,) for p in range((self.bn + 1) // 2)]
-        self.e_stores = self.bm * sum(4 if len(pr) == 2 else 2 for pr in self.pairs)
+        if out == "bf16":
+            self.e_stores = self.bm * sum(4 if len(pr) == 2 else 2 for pr in self.pairs)
+        else:
+            # fp32: one 32 x 32 block per pass, four 1 KiB stores (and, accumulating, four loads of
+            # the old values); the counted waits saturate at vmcnt's 63
+            self.e_stores = nblk * (8 if out == "f32acc" else 4)
         # read bases: one per block, or (320-byte rows, one-bit swizzle) two per side by parity
         self.parity_bases = tm == 320 and tn == 320
         ops = [("c0", "+s"), ("nis", "+s"), ("vmt", "+s"), ("q0", "+s"), ("q1", "+s"), ("q2", "+s"), ("np", "+s"),
@@ -100,9 +106,12 @@ class Config:
             ops += [("amb0", "v"), ("amb1", "v"), ("bnb0", "v"), ("bnb1", "v")]
         else:
             ops += [(f"amb{i}", "v") for i in range(self.bm)] + [(f"bnb{j}", "v") for j in range(self.bn)]
-        ops += [("ew_base", "v"), ("ew_s", "v"), ("rb_even", "v"), ("rb_odd", "v"), ("gb", "v")]
-        if self.bn % 2:
-            ops += [("rb1", "v"), ("gb1", "v")]
+        if out == "bf16":
+            ops += [("ew_base", "v"), ("ew_s", "v"), ("rb_even", "v"), ("rb_odd", "v"), ("gb", "v")]
+            if self.bn % 2:
+                ops += [("rb1", "v"), ("gb1", "v")]
+        else:
+            ops += [("fw_base", "v"), ("fw_s", "v"), ("frb", "v"), ("fgb", "v")]
         self.operands = ops
         self.op = {name: f"%{i}" for i, (name, _) in enumerate(ops)}
         # MFMA order within a stage: m-block 0 across all n-blocks first, then the other m-blocks
@@ -121,7 +130,7 @@ class Config:
         assert len(free) >= self.loads, self.name
         self.dma_after = free[:self.loads]
         self.setup_after = (0, 1, 2)
-        assert self.vop0 - 2 >= 28 and self.e_stores + self.loads <= 63
+        assert self.vop0 - 2 >= 28 and (out != "bf16" or self.e_stores + self.loads <= 63)
         assert self.nl * 4 * 1024 == KS * tm and self.nr * 4 * 1024 == KS * tn
 
     def acc(self, i, j):
@@ -149,7 +158,7 @@ class Config:
         return self.op[f"{side}b{b}"], 0
 
 
-CONFIGS = (Config(256, 384), Config(320, 320))
+CONFIGS = (Config(256, 384), Config(320, 320), Config(320, 320, "f32"), Config(320, 320, "f32acc"))
 
 
 class Gen:
@@ -183,7 +192,7 @@ class Gen:
         self.emit(f"s_mov_b32 {OP['q0']}, {OP['q1']}")
         self.emit(f"s_mov_b32 {OP['q1']}, {OP['q2']}")
         self.emit(f"s_sub_u32 {OP['np']}, {OP['np']}, 1")
-        counts = [c.e_stores + c.loads, c.e_stores, 2 * c.loads, c.loads]
+        counts = sorted({min(n, 63) for n in (c.e_stores + c.loads, c.e_stores, 2 * c.loads, c.loads)}, reverse=True)
         done = self.label("wdone")
         tgt = {n: self.label(f"w{n}_") for n in counts}
         self.emit(f"s_cmp_eq_u32 {s['NEED']}, {c.loads}")        # the steady state: one stage behind
@@ -387,6 +396,8 @@ class Gen:
         return [(16 * k, 2, 2048 * k, "gb1") for k in range(2)]
 
     def epilogue(self):
+        if self.cfg.out != "bf16":
+            return self.epilogue_f32()
         s, OP, e, c = SGPR, self.OP, self.emit, self.cfg
         v0 = c.vop0                      # the operand registers are free here
         tacc, tmul, tcvt = v0, v0 + 4, v0 + 8
@@ -440,9 +451,109 @@ class Gen:
                     e(f"buffer_store_dwordx4 v[{d}:{d + 3}], {c.vt2}, {s['RC']}, 0 offen nt")
         e(f"s_add_u32 {OP['vmt']}, {OP['vmt']}, {c.e_stores}")
 
+    def f32_store_offset(self, i, j, k):
+        """vt2 = byte offset of this wave's tile rows 32 i + 8 k + l / 8, columns 32 j + 4 (l % 8)
+        (fp32)."""
+        s, OP, e, c = SGPR, self.OP, self.emit, self.cfg
+        e(f"s_mul_i32 {s['T']}, {OP['cm2']}, {2 * (32 * i + 8 * k)}")
+        e(f"s_add_u32 {s['T']}, {s['T']}, {OP['sw_epi']}")
+        if j:
+            e(f"s_add_u32 {s['T']}, {s['T']}, {128 * j}")
+        e(f"v_add_u32 {c.vt2}, {s['T']}, {OP['fgb']}")
+
+    def epilogue_f32(self):
+        """fp32 C, one 32 x 32 block per pass through a private 4 KiB LDS region: lane (r = l % 32,
+        h = l / 32) writes its four 16-byte row pieces (chunk 2 g + h of row r, chunk c stored at
+        c ^ (((r >> 1) & 3) << 1)); read-back k (0..3) gives lane l row 8 k + l / 8, chunk l % 8, so
+        each 1 KiB store covers 8 whole 128-byte row segments. Accumulating, the old values of the
+        next two passes are in flight while the current pass waits for its own (counted vmcnt), and
+        the product, rounded to fp32 first, is added to them."""
+        s, OP, e, c = SGPR, self.OP, self.emit, self.cfg
+        acc_mode = c.out == "f32acc"
+        v0 = c.vop0                      # the operand registers are free here
+        tacc, tmul, waddr, rbase = v0, v0 + 4, v0 + 8, v0 + 12
+        dset = v0 + 16                   # the pass's staged results (a store reads its data at issue)
+        look = 2                         # passes of old-value loads in flight ahead of the current
+        oset = [v0 + 32 + 16 * k for k in range(look + 1)]
+        assert oset[-1] + 16 <= c.vacc0
+        e("s_nop 7")
+        e("s_nop 7")
+        e("s_nop 7")
+        e("s_barrier")   # every wave is past its reads of the last stage's slot
+        e(f"s_add_u32 {s['EPI']}, {OP['lds_base']}, {s['CS']}")
+        e(f"s_lshl_b32 {s['T']}, {OP['w1k']}, 2")
+        e(f"s_add_u32 {s['EPI']}, {s['EPI']}, {s['T']}")
+        for g in range(4):
+            e(f"v_xor_b32 v{tacc}, {g}, {OP['fw_s']}")
+            e(f"v_lshlrev_b32 v{tacc}, 5, v{tacc}")
+            e(f"v_add3_u32 v{waddr + g}, v{tacc}, {OP['fw_base']}, {s['EPI']}")
+        e(f"v_add_u32 v{rbase}, {s['EPI']}, {OP['frb']}")
+        self.c_resource()
+        blocks = [(i, j) for i in range(c.bm) for j in range(c.bn)]
+        P = len(blocks)
+
+        def load_old(n):
+            i, j = blocks[n]
+            for k in range(4):
+                o = oset[n % (look + 1)] + 4 * k
+                self.f32_store_offset(i, j, k)
+                e(f"buffer_load_dwordx4 v[{o}:{o + 3}], {c.vt2}, {s['RC']}, 0 offen")
+
+        if acc_mode:
+            for n in range(min(look, P)):
+                load_old(n)
+        for n, (i, j) in enumerate(blocks):
+            kind, base = c.acc(i, j)
+            for g in range(4):
+                src = []
+                for r in range(4):
+                    reg = base + 4 * g + r
+                    if kind == "a":
+                        e(f"v_accvgpr_read_b32 v{tacc + r}, a{reg}")
+                        src.append(f"v{tacc + r}")
+                    else:
+                        src.append(f"v{reg}")
+                for r in range(4):
+                    e(f"v_mul_f32 v{tmul + r}, {OP['alpha']}, {src[r]}")
+                e(f"ds_write_b128 v{waddr + g}, v[{tmul}:{tmul + 3}]")
+            for k in range(4):
+                e(f"ds_read_b128 v[{dset + 4 * k}:{dset + 4 * k + 3}], v{rbase} offset:{1024 * k}")
+            if acc_mode:
+                if n + look < P:
+                    load_old(n + look)
+                # issued after this pass's old values: the next passes' loads and the stores of the
+                # passes since (vector memory counts complete in issue order)
+                later = 4 * sum(1 for m in range(n + 1, n + look + 1) if m < P) + 4 * min(n, look)
+                e(f"s_waitcnt vmcnt({later})")
+            e("s_waitcnt lgkmcnt(0)")
+            if acc_mode:
+                o0 = oset[n % (look + 1)]
+                for r in range(16):
+                    e(f"v_add_f32 v{dset + r}, v{dset + r}, v{o0 + r}")
+            for k in range(4):
+                self.f32_store_offset(i, j, k)
+                e(f"buffer_store_dwordx4 v[{dset + 4 * k}:{dset + 4 * k + 3}], {c.vt2}, {s['RC']}, 0 offen nt")
+        e(f"s_add_u32 {OP['vmt']}, {OP['vmt']}, {c.e_stores}")
+
     def zero_epilogue(self):
-        """A tile without tokens: zeros straight from registers, the same stores per wave."""
+        """A tile without tokens: zeros straight from registers, the same stores per wave (fp32
+        accumulation: C += 0, nothing to do)."""
         e, c = self.emit, self.cfg
+        if c.out == "f32acc":
+            e(f"s_add_u32 {self.OP['vmt']}, {self.OP['vmt']}, 0")
+            return
+        if c.out == "f32":
+            z = c.vop0 + 16
+            for r in range(z, z + 4):
+                e(f"v_mov_b32 v{r}, 0")
+            self.c_resource()
+            for i in range(c.bm):
+                for j in range(c.bn):
+                    for k in range(4):
+                        self.f32_store_offset(i, j, k)
+                        e(f"buffer_store_dwordx4 v[{z}:{z + 3}], {c.vt2}, {SGPR['RC']}, 0 offen nt")
+            e(f"s_add_u32 {self.OP['vmt']}, {self.OP['vmt']}, {c.e_stores}")
+            return
         z = c.vop0 + 24
         for r in range(z, z + 4):
             e(f"v_mov_b32 v{r}, 0")

@@ -16,8 +16,10 @@ GGEMM_DEFINE_TENSORWISE_LIB_KERNEL(_grouped_variable_k_gemm_kernel_k32, true, ui
 GGEMM_DEFINE_MX_KERNEL(_grouped_variable_k_mxfp8_gemm_kernel)
 GGEMM_DEFINE_TENSORWISE_LIB_KERNEL(_grouped_variable_k_gemm_kernel_f32, false, float, ggemm::kOutF32)
 GGEMM_DEFINE_TENSORWISE_LIB_KERNEL(_grouped_variable_k_gemm_kernel_f32_acc, false, float, ggemm::kOutF32Acc)
-GGEMM_DEFINE_WIDE_KERNEL(_grouped_variable_k_gemm_kernel_wide, 256, 384)
-GGEMM_DEFINE_WIDE_KERNEL(_grouped_variable_k_gemm_kernel_wide320, 320, 320)
+GGEMM_DEFINE_WIDE_KERNEL(_grouped_variable_k_gemm_kernel_wide, 256, 384, uint16_t, ggemm::kOutBF16)
+GGEMM_DEFINE_WIDE_KERNEL(_grouped_variable_k_gemm_kernel_wide320, 320, 320, uint16_t, ggemm::kOutBF16)
+GGEMM_DEFINE_WIDE_KERNEL(_grouped_variable_k_gemm_kernel_wide320_f32, 320, 320, float, ggemm::kOutF32)
+GGEMM_DEFINE_WIDE_KERNEL(_grouped_variable_k_gemm_kernel_wide320_f32_acc, 320, 320, float, ggemm::kOutF32Acc)
 
 namespace {
 
@@ -60,7 +62,7 @@ int wide_selected(int OUT_M, int OUT_N, int scm, const void* out) {
   return OUT_M >= 1024 && aligned(out, 16) ? wide_tile_for(OUT_M, OUT_N, scm) : 0;
 }
 
-int launch_wide(int tile, const void* lhs, const void* rhs, void* out, const float* lhs_scale,
+int launch_wide(int tile, int out_mode, const void* lhs, const void* rhs, void* out, const float* lhs_scale,
                 const float* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M, int32_t OUT_N,
                 int32_t slm, int32_t srm, int32_t scg, int32_t scm, int32_t scn, int64_t M_total, void* stream) {
   int cus = 0;
@@ -68,10 +70,19 @@ int launch_wide(int tile, const void* lhs, const void* rhs, void* out, const flo
   if (rc) return rc;
   // the kernels keep token counts in 32 bits: a group never exceeds 2^31 - 1 tokens
   const int64_t m_total = M_total < INT32_MAX ? M_total : INT32_MAX;
-  auto kern = tile == 320 ? _grouped_variable_k_gemm_kernel_wide320 : _grouped_variable_k_gemm_kernel_wide;
-  hipLaunchKernelGGL(kern, dim3(cus), dim3(ggemm::wide::kNT), 0, (hipStream_t)stream, (const uint8_t*)lhs,
-                     (const uint8_t*)rhs, (uint16_t*)out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, slm, srm,
-                     scg, scm, scn, (void*)nullptr, (void*)nullptr, m_total);
+  const dim3 grid(cus), block(ggemm::wide::kNT);
+  if (out_mode == GGEMM_OUT_BF16) {
+    auto kern = tile == 320 ? _grouped_variable_k_gemm_kernel_wide320 : _grouped_variable_k_gemm_kernel_wide;
+    hipLaunchKernelGGL(kern, grid, block, 0, (hipStream_t)stream, (const uint8_t*)lhs, (const uint8_t*)rhs,
+                       (uint16_t*)out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, slm, srm, scg, scm, scn,
+                       (void*)nullptr, (void*)nullptr, m_total);
+  } else {
+    auto kern = out_mode == GGEMM_OUT_F32 ? _grouped_variable_k_gemm_kernel_wide320_f32
+                                          : _grouped_variable_k_gemm_kernel_wide320_f32_acc;
+    hipLaunchKernelGGL(kern, grid, block, 0, (hipStream_t)stream, (const uint8_t*)lhs, (const uint8_t*)rhs,
+                       (float*)out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, slm, srm, scg, scm, scn,
+                       (void*)nullptr, (void*)nullptr, m_total);
+  }
   return (int)hipGetLastError();
 }
 
@@ -90,8 +101,8 @@ static int launch_tensorwise(bool legacy, const void* lhs, const void* rhs, void
   if (rc) return rc;
   if (m_total < 0) return GGEMM_E_SHAPE;
   if (const int tile = legacy ? 0 : wide_selected(OUT_M, OUT_N, scm, out))
-    return launch_wide(tile, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, slm, srm, scg, scm,
-                       scn, m_total, stream);
+    return launch_wide(tile, GGEMM_OUT_BF16, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, slm,
+                       srm, scg, scm, scn, m_total, stream);
   int cus = 0;
   rc = device_cus(&cus);
   if (rc) return rc;
@@ -106,18 +117,21 @@ int ggemm_vark_wgrad_fp8_wide(const void* lhs, const void* rhs, void* out, const
                               const float* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
                               int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
                               int32_t stride_cm, int32_t stride_cn, int64_t M_total, int32_t tile_m,
-                              void* stream) {
+                              int32_t out_mode, void* stream) {
+  if (out_mode != GGEMM_OUT_BF16 && out_mode != GGEMM_OUT_F32 && out_mode != GGEMM_OUT_F32_ACCUM)
+    return GGEMM_E_FORMAT;
   int rc = validate_common(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
                            stride_rhs_m, stride_cg, stride_cm, stride_cn);
   if (rc) return rc;
   if (M_total < 0) return GGEMM_E_SHAPE;
-  const int fit = wide_tile_for(OUT_M, OUT_N, stride_cm);
+  // fp32 C: the same byte bound as a bf16 C twice as wide
+  const int fit = wide_tile_for(OUT_M, OUT_N, out_mode == GGEMM_OUT_BF16 ? stride_cm : 2 * stride_cm);
   int tile = tile_m == 0 ? fit : tile_m;
   if (tile == 320 && (OUT_M % 320 || OUT_N % 320)) tile = 0;
-  if (tile == 256 && OUT_N % 384) tile = 0;
+  if (tile == 256 && (OUT_N % 384 || out_mode != GGEMM_OUT_BF16)) tile = 0;   // fp32 epilogues: 320 x 320
   if ((tile != 256 && tile != 320) || fit == 0) return GGEMM_E_SHAPE;
   if (!aligned(out, 16)) return GGEMM_E_ALIGN;    // 16-byte stores of whole row chunks
-  return launch_wide(tile, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
+  return launch_wide(tile, out_mode, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
                      stride_rhs_m, stride_cg, stride_cm, stride_cn, M_total, stream);
 }
 
@@ -151,6 +165,10 @@ int ggemm_vark_wgrad_fp8_out(const void* lhs, const void* rhs, void* out, const 
   if (rc) return rc;
   if (M_total < 0) return GGEMM_E_SHAPE;
   if (!aligned(out, 16)) return GGEMM_E_ALIGN;    // 16-byte fp32 row segments
+  // fp32 C takes the 320 x 320 wide-tile kernel where the bf16 C of the same shape would
+  if (wide_selected(OUT_M, OUT_N, 2 * stride_cm, out) == 320)
+    return launch_wide(320, out_mode, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N,
+                       stride_lhs_m, stride_rhs_m, stride_cg, stride_cm, stride_cn, M_total, stream);
   int cus = 0;
   rc = device_cus(&cus);
   if (rc) return rc;

@@ -84,8 +84,9 @@ def grouped_gemm_fp8_tensorwise_variable_k(lhs: torch.Tensor, rhs: torch.Tensor,
     K=32 MFMA the reference uses; ``validate=True`` checks group_offs on the host first (a sync).
     ``out_dtype=torch.float32`` writes an fp32 C; ``accumulate=True`` adds the result into the fp32
     ``out`` given (the main-grad accumulation, beta = 1). ``wide=True`` runs a wide-tile kernel
-    (bf16 C; 320 x 320 tiles where OUT_M and OUT_N are multiples of 320, else 256 x 384 with OUT_N a
-    multiple of 384); ``wide=320`` / ``wide=256`` picks the tile height.
+    (320 x 320 tiles where OUT_M and OUT_N are multiples of 320, else 256 x 384 with OUT_N a
+    multiple of 384, bf16 C only); ``wide=320`` / ``wide=256`` picks the tile height. Without it the
+    library picks (a wide tile for OUT_M >= 1024 where one fits).
     """
     _check_inputs(lhs, rhs, group_offs)
     for s in (lhs_scale, rhs_scale):
@@ -106,13 +107,14 @@ def grouped_gemm_fp8_tensorwise_variable_k(lhs: torch.Tensor, rhs: torch.Tensor,
     lhs, rhs = _nonempty(lhs), _nonempty(rhs)
     lib = _lib.load()
     if wide:
-        if mfma != "k128" or out_dtype != torch.bfloat16:
-            raise ValueError("the wide-tile kernel writes bf16 C with the K=64 32x32 MFMA")
+        if mfma != "k128":
+            raise ValueError("the wide-tile kernels use the 32x32x64 MFMA (mfma='k128' family)")
+        mode = 2 if accumulate else (1 if out_dtype == torch.float32 else 0)
         with torch.cuda.device(lhs.device):
             rc = lib.ggemm_vark_wgrad_fp8_wide(
                 lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), lhs_scale.data_ptr(), rhs_scale.data_ptr(),
                 group_offs.data_ptr(), G, OUT_M, OUT_N, lhs.stride(0), rhs.stride(0), out.stride(0), out.stride(1),
-                out.stride(2), M_total, 0 if wide is True else int(wide), _stream(lhs.device))
+                out.stride(2), M_total, 0 if wide is True else int(wide), mode, _stream(lhs.device))
         _lib.check(rc, "ggemm_vark_wgrad_fp8_wide")
         return out
     if mfma == "k128":

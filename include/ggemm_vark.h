@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define GGEMM_VARK_ABI_VERSION 5
+#define GGEMM_VARK_ABI_VERSION 6
 
 enum {
   GGEMM_OK = 0,
@@ -79,19 +79,20 @@ int ggemm_vark_wgrad_fp8_out(const void* lhs, const void* rhs, void* out, const 
                              int32_t stride_cm, int32_t stride_cn, int32_t out_mode, int64_t M_total,
                              void* stream);
 
-/* Tensorwise FP8 grouped wgrad, bf16 C, on a wide-tile kernel: 320 x 320 or 256 x 384 output tiles
- * on 256-thread workgroups (one wave per SIMD, 512 registers per wave), outside the reference's
+/* Tensorwise FP8 grouped wgrad on a wide-tile kernel: 320 x 320 or 256 x 384 output tiles on
+ * 256-thread workgroups (one wave per SIMD, 512 registers per wave), outside the reference's
  * 512-thread launch contract; no reference counterpart (it replaces the same launch as
  * ggemm_vark_wgrad_fp8, reference launcher.cpp:123-171, for the shapes it takes). Same arguments
- * and result as ggemm_vark_wgrad_fp8_out with GGEMM_OUT_BF16, group offsets clamped to
+ * and result as ggemm_vark_wgrad_fp8_out with the same out_mode, group offsets clamped to
  * [0, min(M_total, 2^31 - 1)]. tile_m: 320 (OUT_M and OUT_N multiples of 320), 256 (OUT_N a
- * multiple of 384) or 0 (320 where it fits, else 256). Also OUT_M * stride_cm * 2 < 2^31 and out
- * 16-byte aligned; otherwise GGEMM_E_SHAPE / GGEMM_E_ALIGN and nothing is launched. */
+ * multiple of 384; bf16 C only) or 0 (320 where it fits, else 256). Also a group of C within 2^31
+ * bytes and out 16-byte aligned; otherwise GGEMM_E_SHAPE / GGEMM_E_ALIGN / GGEMM_E_FORMAT and
+ * nothing is launched. */
 int ggemm_vark_wgrad_fp8_wide(const void* lhs, const void* rhs, void* out, const float* lhs_scale,
                               const float* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
                               int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
                               int32_t stride_cm, int32_t stride_cn, int64_t M_total, int32_t tile_m,
-                              void* stream);
+                              int32_t out_mode, void* stream);
 
 /* MXFP8 block-scaled grouped wgrad (no reference counterpart: the reference imports only the
  * tensorwise kernels, reference bench.py:241-246). lhs_scale: e8m0 bytes [ceil(M_total/32), OUT_M]
@@ -128,8 +129,9 @@ int32_t ggemm_vark_abi_version(void);
 /* Which kernel the bf16 entry points (ggemm_vark_wgrad_fp8, ggemm_vark_wgrad_fp8_out with
  * GGEMM_OUT_BF16) run for a shape: 320 or 256 = the wide-tile kernel with that tile height
  * (OUT_M >= 1024, a shape ggemm_vark_wgrad_fp8_wide takes with tile_m = 0, out 16-byte aligned),
- * 0 = the 192-row-tile kernel of the reference launch geometry. No reference counterpart. Touches
- * no device. */
+ * 0 = the 192-row-tile kernel of the reference launch geometry. The fp32 modes of
+ * ggemm_vark_wgrad_fp8_out run the 320 x 320 kernel where this returns 320 for stride_cm twice
+ * the fp32 row stride. No reference counterpart. Touches no device. */
 int32_t ggemm_vark_bf16_kernel(int32_t OUT_M, int32_t OUT_N, int32_t stride_cm, const void* out);
 
 void ggemm_vark_launch_geometry(int32_t out_n, int32_t* block_threads, int32_t* dynamic_lds, int32_t* tile_m,

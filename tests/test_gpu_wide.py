@@ -143,3 +143,70 @@ def test_wide_full_size(pkg, orc, cuda, name, tile):
     _say(f"{name}: wide{tile} vs the 192-row-tile kernel: {m}")
     assert orc.parity_ok(m)
     _oracle_whole(pkg, orc, p, out)
+
+
+@pytest.mark.parametrize("lens,om,on", [([127, 128, 0, 255, 256, 257], 320, 640), ([300, 0, 645], 640, 960),
+                                        ([31] * 4 + [0] * 2, 320, 320)], ids=["ragged", "two_groups", "tiny"])
+def test_wide_fp32_output_and_accumulate(pkg, orc, cuda, lens, om, on):
+    """The 320 x 320 kernel's fp32 epilogues: fp32 C against the float64 oracle with the bar, empty
+    groups exact zeros over a NaN prefill, bf16 rounding of the fp32 result equal to the kernel's
+    bf16 output bit for bit, and accumulation equal to C0 + the fp32 result exactly, twice."""
+    from test_gpu_parity import _f32_parity
+    lhs, rhs, offs, _, (sl, sr) = _rand_bytes_problem(lens, om, on, seed=len(lens) + om + 3)
+    G = len(lens)
+    _say(f"wide320 fp32 out lens={lens} {om}x{on}")
+    ref = orc.vark_wgrad_tensorwise_f32(lhs.numpy(), rhs.numpy(), sl, sr, offs.numpy(), acc_dtype=np.float64)
+    dl, dr, do = lhs.to(cuda), rhs.to(cuda), offs.to(cuda)
+    s1 = torch.tensor(sl, dtype=torch.float32, device=cuda)
+    s2 = torch.tensor(sr, dtype=torch.float32, device=cuda)
+    run = pkg.grouped_gemm_fp8_tensorwise_variable_k
+    out = torch.full((G, om, on), float("nan"), dtype=torch.float32, device=cuda)
+    run(dl, dr, s1, s2, do, out=out, out_dtype=torch.float32, wide=320)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    _f32_parity(orc, got, ref, "wide320 fp32 out")
+    for g, L in enumerate(lens):
+        if L == 0:
+            assert np.all(got[g] == 0), g
+    bf = run(dl, dr, s1, s2, do, wide=320)
+    torch.cuda.synchronize()
+    assert torch.equal(out.to(torch.bfloat16).view(torch.int16), bf.view(torch.int16))
+    c0 = torch.randn((G, om, on), generator=torch.Generator().manual_seed(5)).float()
+    acc = c0.to(cuda)
+    run(dl, dr, s1, s2, do, out=acc, accumulate=True, wide=320)
+    torch.cuda.synchronize()
+    got1 = acc.cpu().numpy()
+    np.testing.assert_array_equal(got1, (c0.numpy() + got).astype(np.float32))
+    run(dl, dr, s1, s2, do, out=acc, accumulate=True, wide=320)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(acc.cpu().numpy(), (got1 + got).astype(np.float32))
+
+
+@pytest.mark.parametrize("kind", ["f32", "f32_acc"])
+def test_wide_fp32_offsets_clamped_and_partial_rows(pkg, orc, cuda, kind):
+    """fp32 modes with offsets past M_total (clamped; extra rows hold 0x38) inside a C whose groups
+    are 384 rows apart: the rows between groups keep their sentinel."""
+    M = 457
+    offs = torch.tensor([-64, 100, 100, 400, 600, 800], dtype=torch.int64)
+    clamped = offs.clamp(min=0, max=M)
+    lens = torch.diff(clamped).tolist()
+    om, on = 320, 640
+    _say(f"wide320 {kind} clamped offsets, strided C")
+    lhs, rhs, _, _, (sl, sr) = _rand_bytes_problem(lens, om, on, seed=44)
+    pad = 512
+    dl = torch.cat([lhs, torch.full((pad, om), 0x38, dtype=torch.uint8)]).to(cuda)[:M]
+    dr = torch.cat([rhs, torch.full((pad, on), 0x38, dtype=torch.uint8)]).to(cuda)[:M]
+    big = torch.full((len(lens), 384, on), 7.0, dtype=torch.float32, device=cuda)
+    c0 = torch.randn((len(lens), om, on), generator=torch.Generator().manual_seed(2)).float()
+    if kind == "f32_acc":
+        big[:, :om, :] = c0.to(cuda)
+    view = big[:, :om, :]
+    pkg.grouped_gemm_fp8_tensorwise_variable_k(dl, dr, torch.tensor(sl, device=cuda), torch.tensor(sr, device=cuda),
+                                               offs.to(cuda), out=view, out_dtype=torch.float32,
+                                               accumulate=kind == "f32_acc", wide=320)
+    torch.cuda.synchronize()
+    assert bool((big[:, om:, :] == 7.0).all())
+    from test_gpu_parity import _f32_parity
+    ref = orc.vark_wgrad_tensorwise_f32(lhs.numpy(), rhs.numpy(), sl, sr, clamped.numpy(), acc_dtype=np.float64)
+    got = view.cpu().numpy() - (c0.numpy() if kind == "f32_acc" else 0)
+    _f32_parity(orc, got, ref, f"wide320 {kind} clamped")

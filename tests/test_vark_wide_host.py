@@ -163,9 +163,11 @@ class Block:
                 self.ev.append((m.group(1), int(m.group(2))))
             elif op == "v_add_u32":
                 self.v[a[0]] = (self.val(a[1]), a[2])
-            elif op == "buffer_load_dwordx4":
+            elif op == "buffer_load_dwordx4" and a[-1].endswith("lds"):
                 voff = self.v[a[0]] if a[0] in self.v and not a[0].startswith("%") else (0, a[0])
                 self.ev.append(("dma", self.s["m0"], self.rsrc(a[1]), voff, a[-1]))
+            elif op == "buffer_load_dwordx4":      # old values of an accumulated C, into VGPRs
+                self.ev.append(("oload", self.v[a[1]], self.rsrc(a[2]), a[0]))
             elif op == "buffer_store_dwordx4":
                 self.ev.append(("store", self.v[a[1]], self.rsrc(a[2]), a[0]))
             elif op == "ds_read_b64_tr_b8":
@@ -175,7 +177,7 @@ class Block:
                 self.ev.append(("read", base, off, a[0]))
             elif op == "v_mfma_f32_32x32x64_f8f6f4":
                 self.ev.append(("mfma", a[0], a[1], a[2], a[3].split()[0]))
-            elif op in ("ds_write_b64", "ds_read_b128"):
+            elif op in ("ds_write_b64", "ds_write_b128", "ds_read_b128"):
                 self.ev.append((op, a))
             elif op.startswith("v_"):
                 pass
@@ -185,6 +187,11 @@ class Block:
 
 
 LHS, RHS, OUT = 0x7F0000000000, 0x7E0000000000, 0x7D0000000000
+
+
+def _cb(cfg):
+    """Bytes per C element."""
+    return 2 if cfg.out == "bf16" else 4
 
 
 def _run_tiles(cfg, tiles, wave, stride_l=2880, stride_r=5760, stride_cm=5760, OUT_M=2880, prog=None):
@@ -204,10 +211,11 @@ def _run_tiles(cfg, tiles, wave, stride_l=2880, stride_r=5760, stride_cm=5760, O
                    bLN_lo=(LHS + N[3] * stride_l + N[1]) & M32, bLN_hi=(LHS + N[3] * stride_l + N[1]) >> 32,
                    bRN_lo=(RHS + N[3] * stride_r + N[2]) & M32, bRN_hi=(RHS + N[3] * stride_r + N[2]) >> 32,
                    klenN=N[4] if has_next else 0, m0N=N[1], n0N=N[2],
-                   cT_lo=(OUT + 2 * (m0 * stride_cm + n0)) & M32, cT_hi=(OUT + 2 * (m0 * stride_cm + n0)) >> 32,
-                   crecT=((OUT_M - m0) * stride_cm - n0) * 2,
+                   cT_lo=(OUT + _cb(cfg) * (m0 * stride_cm + n0)) & M32,
+                   cT_hi=(OUT + _cb(cfg) * (m0 * stride_cm + n0)) >> 32,
+                   crecT=((OUT_M - m0) * stride_cm - n0) * _cb(cfg),
                    stride_l=stride_l, stride_r=stride_r, cm2=2 * stride_cm, alpha=0x3F800000,
-                   sw_epi=(32 * cfg.bm * (wave & 1) * stride_cm + 32 * cfg.bn * (wave >> 1)) * 2)
+                   sw_epi=(32 * cfg.bm * (wave & 1) * stride_cm + 32 * cfg.bn * (wave >> 1)) * _cb(cfg))
         start = len(ev)
         Block(cfg, ops, ev, scal, prog).run()
         spans.append((start, len(ev)))
@@ -269,7 +277,7 @@ def _check(cfg, tiles, wave=0, stride_l=2880, stride_r=5760, stride_cm=5760, OUT
     done_at = {}           # op index -> event index where it is known complete
     barriers = [i for i, e in enumerate(ev) if e[0] == "barrier"]
     for i, e in enumerate(ev):
-        if e[0] in ("dma", "store"):
+        if e[0] in ("dma", "store", "oload"):
             issued.append(i)
         elif e[0] == "vmcnt":
             for op_i in issued[:max(len(issued) - e[1], 0)]:
@@ -289,7 +297,7 @@ def _check(cfg, tiles, wave=0, stride_l=2880, stride_r=5760, stride_cm=5760, OUT
     for e in ev:
         if e[0] == "read":
             pending.append(regs(e[3]))
-        elif e[0] == "ds_write_b64":
+        elif e[0] in ("ds_write_b64", "ds_write_b128"):
             pending.append(set())
         elif e[0] == "ds_read_b128":
             pending.append(regs(e[1][0]))
@@ -307,7 +315,7 @@ def _check(cfg, tiles, wave=0, stride_l=2880, stride_r=5760, stride_cm=5760, OUT
         if (tiles[n][4] + 63) // 64 > 0:
             last = (n, (tiles[n][4] + 63) // 64 - 1)
             for i in range(a, b):
-                if ev[i][0] in ("ds_write_b64", "ds_read_b128"):
+                if ev[i][0] in ("ds_write_b64", "ds_write_b128", "ds_read_b128"):
                     epi_slot_events.append((i, slot_of[last]))
     uses = sorted([(read_span[st][1], slot_of[st]) for st in stages] + epi_slot_events)
     for st in stages:
@@ -323,7 +331,7 @@ def _check(cfg, tiles, wave=0, stride_l=2880, stride_r=5760, stride_cm=5760, OUT
     for n, (a, b) in enumerate(spans):
         S = (tiles[n][4] + 63) // 64
         if S:
-            first_w = next(i for i in range(a, b) if ev[i][0] == "ds_write_b64")
+            first_w = next(i for i in range(a, b) if ev[i][0] in ("ds_write_b64", "ds_write_b128"))
             last_r = read_span[(n, S - 1)][1]
             assert any(last_r < bi < first_w for bi in barriers), f"tile {n}: staging races operand reads"
     # ---- MFMAs and stores per tile
@@ -337,19 +345,32 @@ def _check(cfg, tiles, wave=0, stride_l=2880, stride_r=5760, stride_cm=5760, OUT
             assert len({e[1] for e in blk}) == nblk
             for e in blk:
                 assert (e[4] == "0") == (s == 0) and (e[4] == "0" or e[4] == e[1])
-        st_ev = [ev[i] for i in range(a, b) if ev[i][0] == "store"]
-        assert len(st_ev) == cfg.e_stores
+        st_ev = [(i, ev[i]) for i in range(a, b) if ev[i][0] == "store"]
         g, m0, n0, kb, klen = tiles[n]
-        sw = (32 * cfg.bm * (wave & 1) * stride_cm + 32 * cfg.bn * (wave >> 1)) * 2
+        cbytes = _cb(cfg)
+        sw = (32 * cfg.bm * (wave & 1) * stride_cm + 32 * cfg.bn * (wave >> 1)) * cbytes
         want_st = []
-        for i in range(cfg.bm):
-            for pidx, blocks in enumerate(cfg.pairs):
-                for row, _, _, lb in GEN.Gen.pass_stores(len(blocks)):
-                    want_st.append((sw + (32 * i + row) * 2 * stride_cm + 128 * pidx, op(lb)))
-        assert sorted((e[1][0], e[1][1]) for e in st_ev) == sorted(want_st)
-        for e in st_ev:
+        if cfg.out == "bf16":
+            for i in range(cfg.bm):
+                for pidx, blocks in enumerate(cfg.pairs):
+                    for row, _, _, lb in GEN.Gen.pass_stores(len(blocks)):
+                        want_st.append((sw + (32 * i + row) * 2 * stride_cm + 128 * pidx, op(lb)))
+        elif not (cfg.out == "f32acc" and S == 0):
+            for i in range(cfg.bm):
+                for j in range(cfg.bn):
+                    for k in range(4):
+                        want_st.append((sw + (32 * i + 8 * k) * 4 * stride_cm + 128 * j, op("fgb")))
+        assert sorted((e[1][0], e[1][1]) for _, e in st_ev) == sorted(want_st)
+        for _, e in st_ev:
             base, nrec, _, _ = e[2]
-            assert base == OUT + 2 * (m0 * stride_cm + n0) and nrec == ((OUT_M - m0) * stride_cm - n0) * 2
+            assert base == OUT + cbytes * (m0 * stride_cm + n0) and nrec == ((OUT_M - m0) * stride_cm - n0) * cbytes
+        if cfg.out == "f32acc" and S:
+            # every store follows the completed load of the old values at its offset
+            ol = [(i, ev[i]) for i in range(a, b) if ev[i][0] == "oload"]
+            assert sorted(e[1] for _, e in ol) == sorted(e[1] for _, e in st_ev)
+            for si, se in st_ev:
+                li = max(i for i, le in ol if le[1] == se[1] and i < si)
+                assert li in done_at and done_at[li] < si, "store before its old values arrived"
     assert state["np"] == 0 and state["nis"] == 0
     return ev
 
@@ -544,3 +565,39 @@ def test_epilogue_staging_and_store_coverage():
             for q in range(8):
                 assert len({(a // 16) % 16 for a in addrs[8 * q:8 * q + 8]}) == 8   # 16-byte bank groups
         assert cover == {(r, cc) for r in range(32) for cc in range(4 * nblk)}
+
+
+def test_epilogue_f32_staging_and_store_coverage():
+    """fp32 passes (one 32 x 32 block): lane (r = l % 32, h = l / 32) writes chunk 2 g + h of row r
+    at fw_base + 32 (g ^ fw_s), the layout chunk c of row r at c ^ (((r >> 1) & 3) << 1); read-back k
+    gives lane l row 8 k + l / 8, chunk l % 8 at frb + 1024 k. Each chunk written and read once,
+    16-byte accesses conflict-free 8 lanes at a time, 8 lanes per whole 128-byte row."""
+    def phys(r, cc):
+        return r * 128 + 16 * (cc ^ (((r >> 1) & 3) << 1))
+    writes = {}
+    for g in range(4):
+        addrs = []
+        for lane in range(64):
+            rl, hl = lane & 31, lane >> 5
+            fw_base, fw_s = rl * 128 + 16 * hl, (rl >> 1) & 3
+            addr = fw_base + 32 * (g ^ fw_s)
+            assert addr == phys(rl, 2 * g + hl)
+            writes[addr] = (rl, 8 * g + 4 * hl)          # row, first of 4 fp32 columns
+            addrs.append(addr)
+        for q in range(8):
+            assert len({(a // 16) % 16 for a in addrs[8 * q:8 * q + 8]}) == 8
+    assert len(writes) == 32 * 8
+    cover = set()
+    for k in range(4):
+        addrs = []
+        for lane in range(64):
+            rr, rc = lane >> 3, lane & 7
+            frb = rr * 128 + 16 * (rc ^ (((rr >> 1) & 3) << 1))
+            addr = frb + 1024 * k
+            r = 8 * k + rr
+            assert addr == phys(r, rc) and writes[addr] == (r, 4 * rc)
+            cover.add((r, rc))
+            addrs.append(addr)
+        for q in range(8):
+            assert len({(a // 16) % 16 for a in addrs[8 * q:8 * q + 8]}) == 8
+    assert cover == {(r, cc) for r in range(32) for cc in range(8)}
