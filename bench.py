@@ -444,7 +444,8 @@ def main():
                   "kernel": ("hip gfx950 persistent {}x{} tiles, 256-thread workgroups (one wave per SIMD, "
                              "hand-placed accumulators), mfma 32x32x64".format(
                                  *((320, 320) if pkg.bf16_kernel(p.OUT_M, p.OUT_N) == "wide320" else (256, 384)))
-                             if args.mfma == "k128" and not p.is_mx and pkg.bf16_kernel(p.OUT_M, p.OUT_N) != "192-row"
+                             if args.mfma == "k128" and pkg.bf16_kernel(p.OUT_M, p.OUT_N) != "192-row"
+                             and (not p.is_mx or pkg.bf16_kernel(p.OUT_M, p.OUT_N) == "wide320")
                              else "hip gfx950 persistent {tile_m}x{tile_n} tiles, mfma {mfma}".format(
                                  mfma=args.mfma, **pkg.launch_geometry(p.OUT_N))),
                   "baseline_number": ("reference optimized ASM 3.515 ms / 1237 TFLOPS (README.md:60)"
@@ -484,6 +485,13 @@ def main():
             r = make_runner(pkg, q, dev, args.mfma)
             t = time_steps(r, max(args.steps // 4, 10), max(args.warmup // 4, 5))
             extra[name] = {"ms": round(t, 4), "TFLOPS": round(q.flops / (t * 1e-3) / 1e12, 2)}
+            if name == "gate_up_mx":      # the 192-row MX kernel beside the wide one the library picks
+                o = torch.empty((q.G, q.OUT_M, q.OUT_N), dtype=torch.bfloat16, device=dev)
+                r = lambda: pkg.grouped_gemm_mxfp8_variable_k(q.lhs, q.rhs, q.lhs_mx, q.rhs_mx, q.group_offs, out=o,
+                                                              tile_m=192)
+                t = time_steps(r, max(args.steps // 4, 10), max(args.warmup // 4, 5))
+                extra["gate_up_mx_192_row"] = {"ms": round(t, 4), "TFLOPS": round(q.flops / (t * 1e-3) / 1e12, 2)}
+                del o
             del q, r
         if args.mfma == "k128" and args.config == "gate_up_wgrad":
             r = make_runner(pkg, p, dev, "k32")

@@ -15,6 +15,7 @@ EXPORTS = (
     "ggemm_vark_wgrad_fp8_out",
     "ggemm_vark_wgrad_fp8_wide",
     "ggemm_vark_wgrad_mxfp8",
+    "ggemm_vark_wgrad_mxfp8_tile",
     "ggemm_vark_check_offsets",
     "ggemm_vark_num_cus",
     "ggemm_vark_strerror",
@@ -77,6 +78,8 @@ def load():
     lib.ggemm_vark_wgrad_fp8_wide.restype = ctypes.c_int
     lib.ggemm_vark_wgrad_mxfp8.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 10 + [ctypes.c_int64, vp]
     lib.ggemm_vark_wgrad_mxfp8.restype = ctypes.c_int
+    lib.ggemm_vark_wgrad_mxfp8_tile.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 10 + [ctypes.c_int64, i32, vp]
+    lib.ggemm_vark_wgrad_mxfp8_tile.restype = ctypes.c_int
     lib.ggemm_vark_check_offsets.argtypes = [i64p, i32, ctypes.c_int64, i32]
     lib.ggemm_vark_check_offsets.restype = ctypes.c_int
     lib.ggemm_vark_num_cus.argtypes = [i32, ctypes.POINTER(i32)]

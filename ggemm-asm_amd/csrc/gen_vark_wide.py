@@ -51,8 +51,18 @@ SGPR = dict(
     S="s68", K="s69", INT="s70", IDX="s71", REM="s72", LIM="s73",
     BL0="s74", BL1="s75", BR0="s76", BR1="s77", CM0="s78", CN0="s79",
     ISLOT="s80", CS="s81", NS="s82", T="s83", T2="s84", NEED="s85", LIMTOP="s86", EPI="s87", IB="s88",
+    # MXFP8 only: the cursor's scale pointer, the scale resource, the read slot's scale offsets
+    BS0="s89", BS1="s90", NSS="s91", RS="s[92:95]", RS0="s92", RS1="s93", RS2="s94", RS3="s95", NSSR="s96",
 )
 SGPR_CLOBBER = list(range(56, 89))
+SGPR_CLOBBER_MX = list(range(56, 97))
+# MXFP8: the e8m0 rows of a stage sit in a scale slot at SCALE_OFF + (stage slot offset >> 4): the
+# LHS rows of token blocks 0 and 1 at +0 and +320, the RHS rows at +1024 and +1344. Every LDS-DMA
+# destination of these kernels stays below 128 KiB (with the scale slots at 136 KiB the results
+# came out wrong on MI355X); the schedule tables, read with plain LDS reads, move above them.
+SCALE_OFF = SLOTS * 40960
+SCALE_SLOT = 40960 >> 4
+DMA_LDS_LIMIT = 128 * 1024
 
 
 def swizzle(pitch):
@@ -69,21 +79,38 @@ def swizzle(pitch):
 
 
 class Config:
-    def __init__(self, tm, tn, out="bf16"):
+    def __init__(self, tm, tn, out="bf16", mx=False):
         self.tm, self.tn = tm, tn
         self.out = out                                  # "bf16", "f32" (fp32 C) or "f32acc" (C += result)
-        self.name = f"{tm}x{tn}" + ("" if out == "bf16" else "_" + out)
+        self.mx = mx                                    # MXFP8: e8m0 block scales, scaled MFMA
+        assert not mx or (out == "bf16" and tm == tn == 320)
+        self.name = f"{tm}x{tn}" + ("" if out == "bf16" else "_" + out) + ("_mx" if mx else "")
         self.bm, self.bn = tm // 64, tn // 64           # 32-wide blocks per wave (2 x 2 waves)
         self.rhs_off = KS * tm
         self.slot = KS * (tm + tn)
         self.nl = KS * tm // 1024 // 4                  # LHS / RHS LDS-DMA instructions per wave
         self.nr = KS * tn // 1024 // 4
-        self.loads = self.nl + self.nr
+        self.loads = self.nl + self.nr + (1 if mx else 0)   # MX: one scale row per wave
         nblk = self.bm * self.bn
         self.vacc0 = 256 - 16 * (nblk - 16)             # first VGPR accumulator
-        self.vop0 = self.vacc0 - 8 * (self.bm + self.bn)
-        self.vt, self.vt2 = f"v{self.vop0 - 2}", f"v{self.vop0 - 1}"
-        self.vgpr_clobber = list(range(self.vop0 - 2, 256))
+        # MX: the lane's e8m0 scale of each block of the stage, one register each (byte 0, read
+        # with a full-register ds_read_u8). Two blocks cannot share a register through 16-bit
+        # loads: on gfx950 a ds_read_u8_d16(_hi) zeroes the other half (measured on MI355X).
+        if mx:
+            self.scale_map = {**{("am", i): (i, 0) for i in range(self.bm)},
+                              **{("bn", j): (self.bm + j, 0) for j in range(self.bn)}}
+            self.nsl, self.nsr = self.bm, self.bn
+        else:
+            self.scale_map, self.nsl, self.nsr = {}, 0, 0
+        self.vop0 = self.vacc0 - 8 * (self.bm + self.bn)   # operand tuples (even-aligned)
+        self.vsc0 = self.vop0 - self.nsl - self.nsr        # MX scale registers below them
+        # vt: read-address temporary; vt2: the epilogue's store offset (MX: the last scale
+        # register, free by then -- the K loop never uses vt2)
+        self.vt = f"v{self.vsc0 - (1 if mx else 2)}"
+        self.vt2 = f"v{self.vop0 - 1}"
+        self.vgpr_clobber = list(range(self.vsc0 - (1 if mx else 2), 256))
+        self.sgpr_clobber = SGPR_CLOBBER_MX if mx else SGPR_CLOBBER
+        self.rb = 5 if mx else 4                        # LDS reads per operand block (MX: + its scale)
         self.pairs = [(2 * p, 2 * p + 1) if 2 * p + 1 < self.bn else (2 * p,) for p in range((self.bn + 1) // 2)]
         if out == "bf16":
             self.e_stores = self.bm * sum(4 if len(pr) == 2 else 2 for pr in self.pairs)
@@ -106,12 +133,17 @@ class Config:
             ops += [("amb0", "v"), ("amb1", "v"), ("bnb0", "v"), ("bnb1", "v")]
         else:
             ops += [(f"amb{i}", "v") for i in range(self.bm)] + [(f"bnb{j}", "v") for j in range(self.bn)]
-        if out == "bf16":
-            ops += [("ew_base", "v"), ("ew_s", "v"), ("rb_even", "v"), ("rb_odd", "v"), ("gb", "v")]
-            if self.bn % 2:
-                ops += [("rb1", "v"), ("gb1", "v")]
+        epi = (["ew_base", "ew_s", "rb_even", "rb_odd", "gb"] + (["rb1", "gb1"] if self.bn % 2 else [])
+               if out == "bf16" else ["fw_base", "fw_s", "frb", "fgb"])
+        if mx:
+            # the epilogue's per-lane bases are formed from the lane id inside the statement, in
+            # operand registers free by then (the scale registers leave too few for them as inputs)
+            self.lane_regs = {n: f"v{self.vop0 + 56 + k}" for k, n in enumerate(epi)}
+            ops += [("scT_lo", "s"), ("scT_hi", "s"), ("scN_lo", "s"), ("scN_hi", "s"), ("stride_sc", "s"),
+                    ("scrd", "s"), ("scw", "s"), ("vsc", "v"), ("vscb", "v")]
         else:
-            ops += [("fw_base", "v"), ("fw_s", "v"), ("frb", "v"), ("fgb", "v")]
+            self.lane_regs = {}
+            ops += [(n, "v") for n in epi]
         self.operands = ops
         self.op = {name: f"%{i}" for i, (name, _) in enumerate(ops)}
         # MFMA order within a stage: m-block 0 across all n-blocks first, then the other m-blocks
@@ -130,7 +162,7 @@ class Config:
         assert len(free) >= self.loads, self.name
         self.dma_after = free[:self.loads]
         self.setup_after = (0, 1, 2)
-        assert self.vop0 - 2 >= 28 and (out != "bf16" or self.e_stores + self.loads <= 63)
+        assert self.vsc0 - 2 >= (20 if mx else 28) and self.vop0 % 2 == 0 and (out != "bf16" or self.e_stores + self.loads <= 63)
         assert self.nl * 4 * 1024 == KS * tm and self.nr * 4 * 1024 == KS * tn
 
     def acc(self, i, j):
@@ -148,6 +180,16 @@ class Config:
     def am(self, i):
         return self.vop0 + 8 * i
 
+    def scale_reg(self, side, b):
+        """(register, half) holding this lane's e8m0 scale of LHS m-block b (side "am") or RHS
+        n-block b (side "bn"): bits 0-7 (half 0) or 16-23 (half 1)."""
+        r, h = self.scale_map[(side, b)]
+        return self.vsc0 + r, h
+
+    def lane_value(self, name):
+        """A per-lane epilogue base: an input operand, or (MX) the register the statement forms it in."""
+        return self.lane_regs.get(name) or self.op[name]
+
     def bn_reg(self, j):
         return self.vop0 + 8 * self.bm + 8 * j
 
@@ -158,7 +200,8 @@ class Config:
         return self.op[f"{side}b{b}"], 0
 
 
-CONFIGS = (Config(256, 384), Config(320, 320), Config(320, 320, "f32"), Config(320, 320, "f32acc"))
+CONFIGS = (Config(256, 384), Config(320, 320), Config(320, 320, "f32"), Config(320, 320, "f32acc"),
+           Config(320, 320, mx=True))
 
 
 class Gen:
@@ -167,6 +210,8 @@ class Gen:
         self.OP = cfg.op
         self.lines = []
         self.nlabel = 0
+        self.nlds = 0           # LDS reads issued in the current read sequence (MX half-load waits)
+        self.lo_at = {}
 
     def emit(self, s):
         self.lines.append(s)
@@ -227,6 +272,17 @@ class Gen:
         e(f"s_mov_b32 {s['RR3']}, 0x{WORD3:x}")
         e(f"s_add_u32 {s['IB']}, {OP['lds_base']}, {s['ISLOT']}")
         e(f"s_add_u32 {s['IB']}, {s['IB']}, {OP['w1k']}")
+        if self.cfg.mx:
+            # this wave's e8m0 row: blocks (valid tokens + 31) / 32 of the stage are in range,
+            # each 320 bytes from the tile's column (the row stride is at least 320)
+            e(f"s_add_u32 {s['T2']}, {s['T']}, 31")
+            e(f"s_lshr_b32 {s['T2']}, {s['T2']}, 5")
+            e(f"s_sub_u32 {s['T2']}, {s['T2']}, 1")
+            e(f"s_mul_i32 {s['RS2']}, {s['T2']}, {OP['stride_sc']}")
+            e(f"s_add_u32 {s['RS2']}, {s['RS2']}, 320")
+            e(f"s_mov_b32 {s['RS0']}, {s['BS0']}")
+            e(f"s_and_b32 {s['RS1']}, {s['BS1']}, 0xffff")
+            e(f"s_mov_b32 {s['RS3']}, 0x{WORD3:x}")
 
     def issue_dma(self, j):
         """LDS-DMA instruction j of the stage (first the nl LHS rows, then the nr RHS rows)."""
@@ -235,6 +291,14 @@ class Gen:
             e(f"s_add_u32 m0, {s['IB']}, {4096 * j}")
             e("s_nop 0")
             e(f"buffer_load_dwordx4 {OP[f'voffL{j}']}, {s['RL']}, 0 offen lds")
+        elif j == c.nl + c.nr:
+            # MX: lanes 0-39 carry the two 320-byte e8m0 rows of the wave's side (both waves of a side
+            # write the same bytes); the other lanes' offsets are out of range (zeros into the rest
+            # of the side's 1 KiB)
+            e(f"s_lshr_b32 {s['T']}, {s['ISLOT']}, 4")
+            e(f"s_add_u32 m0, {s['T']}, {OP['scw']}")
+            e("s_nop 0")
+            e(f"buffer_load_dwordx4 {OP['vsc']}, {s['RS']}, 0 offen lds")
         else:
             jj = j - c.nl
             e(f"s_add_u32 m0, {s['IB']}, {c.rhs_off + 4096 * jj}")
@@ -258,6 +322,10 @@ class Gen:
         e(f"s_lshl_b32 {s['T']}, {OP['stride_r']}, 6")
         e(f"s_add_u32 {s['BR0']}, {s['BR0']}, {s['T']}")
         e(f"s_addc_u32 {s['BR1']}, {s['BR1']}, 0")
+        if c.mx:
+            e(f"s_lshl_b32 {s['T']}, {OP['stride_sc']}, 1")
+            e(f"s_add_u32 {s['BS0']}, {s['BS0']}, {s['T']}")
+            e(f"s_addc_u32 {s['BS1']}, {s['BS1']}, 0")
         e(f"s_add_u32 {s['ISLOT']}, {s['ISLOT']}, {c.slot}")
         e(f"s_cmp_ge_u32 {s['ISLOT']}, {c.slot * SLOTS}")
         e(f"s_cselect_b32 {s['T']}, {c.slot * SLOTS}, 0")
@@ -292,6 +360,9 @@ class Gen:
         e(f"s_mov_b32 {s['BR1']}, {OP['bRN_hi']}")
         e(f"s_mov_b32 {s['CM0']}, {OP['m0N']}")
         e(f"s_mov_b32 {s['CN0']}, {OP['n0N']}")
+        if self.cfg.mx:
+            e(f"s_mov_b32 {s['BS0']}, {OP['scN_lo']}")
+            e(f"s_mov_b32 {s['BS1']}, {OP['scN_hi']}")
         e(f"{nosw}:")
         e(f"s_cmp_lt_u32 {s['IDX']}, {s['LIM']}")
 
@@ -306,12 +377,40 @@ class Gen:
         for n, dt in enumerate(TOK_OFFS):
             r = reg0 + 2 * n
             e(f"ds_read_b64_tr_b8 v[{r}:{r + 1}], {c.vt} offset:{extra + dt * pitch}")
+        self.nlds += len(TOK_OFFS)
+        if c.mx:
+            # the lane's e8m0 scale of block b (row l % 32, token block l / 32 of the stage)
+            reg, half = c.scale_reg(side, b)
+            sslot = SGPR["NSS"] if side == "am" else SGPR["NSSR"]
+            e(f"v_add_u32 {c.vt}, {sslot}, {self.OP['vscb']}")
+            if half:
+                # the load of the register's other half has completed (at most `after` LDS reads
+                # issued since it may still be in flight)
+                after = self.nlds - self.lo_at[reg] - 1
+                e(f"s_waitcnt lgkmcnt({min(after, 15)})")
+            else:
+                self.lo_at[reg] = self.nlds
+            e(f"ds_read_u8{'_d16_hi' if half else ''} v{reg}, {c.vt} offset:{32 * b}")
+            self.nlds += 1
+
+    def scale_slot(self, slot):
+        """NSS / NSSR = the scale slot offsets (LHS / RHS rows) that go with stage slot `slot`."""
+        s = SGPR
+        self.emit(f"s_lshr_b32 {s['NSS']}, {slot}, 4")
+        self.emit(f"s_add_u32 {s['NSSR']}, {s['NSS']}, {self.OP['scrd']}")
 
     def mfma(self, i, j, first):
         c = self.cfg
         d = c.acc_range(i, j)
         src = "0" if first else d
         a, b = c.bn_reg(j), c.am(i)
+        if c.mx:
+            # scale of A (RHS n-block j) and of B (LHS m-block i): the byte op_sel_hi picks (0 or 2)
+            ra, ha = c.scale_reg("bn", j)
+            rb, hb = c.scale_reg("am", i)
+            self.emit(f"v_mfma_scale_f32_32x32x64_f8f6f4 {d}, v[{a}:{a + 7}], v[{b}:{b + 7}], {src}, v{ra}, v{rb} "
+                      f"op_sel_hi:[{ha},{hb},0] cbsz:1")
+            return
         self.emit(f"v_mfma_f32_32x32x64_f8f6f4 {d}, v[{a}:{a + 7}], v[{b}:{b + 7}], {src} cbsz:1")
 
     # ---------------------------------------------------------------- one stage
@@ -329,13 +428,19 @@ class Gen:
             e(f"s_cmp_ge_u32 {s['NS']}, {c.slot * SLOTS}")
             e(f"s_cselect_b32 {s['T']}, {c.slot * SLOTS}, 0")
             e(f"s_sub_u32 {s['NS']}, {s['NS']}, {s['T']}")
+            if c.mx:
+                self.scale_slot(s["NS"])
         setup = self.capture(self.issue_setup) if issue else []
-        pieces = [setup[:5], setup[5:10], setup[10:]]
-        # the previous stage's reads ended with the last n-block and the last m-block (4 reads each)
+        third = (len(setup) + 2) // 3
+        pieces = [setup[:third], setup[third:2 * third], setup[2 * third:]]
+        # the previous stage's reads ended with the last n-block and the last m-block (rb reads
+        # each); lgkmcnt(15) leaves at most 15 of them in flight: m-block 0 and the n-blocks before
+        # the last are in
         e("s_waitcnt lgkmcnt(0)" if first else "s_waitcnt lgkmcnt(15)")
+        self.nlds, self.lo_at = 0, {}
         for n, (i, j) in enumerate(c.order):
             if not first and n == c.bn - 1:
-                e("s_waitcnt lgkmcnt(4)")
+                e(f"s_waitcnt lgkmcnt({c.rb})")
             self.mfma(i, j, first)
             if issue and n in c.setup_after:
                 for line in pieces[c.setup_after.index(n)]:
@@ -384,7 +489,7 @@ class Gen:
         e(f"s_add_u32 {s['T']}, {s['T']}, {OP['sw_epi']}")
         if p:
             e(f"s_add_u32 {s['T']}, {s['T']}, {128 * p}")
-        e(f"v_add_u32 {c.vt2}, {s['T']}, {OP[lane_base]}")
+        e(f"v_add_u32 {c.vt2}, {s['T']}, {c.lane_value(lane_base)}")
 
     @staticmethod
     def pass_stores(nblk):
@@ -406,18 +511,19 @@ class Gen:
         e("s_nop 7")
         e("s_nop 7")
         e("s_barrier")   # every wave is past its reads of the last stage's slot
+        self.lane_values()
         e(f"s_add_u32 {s['EPI']}, {OP['lds_base']}, {s['CS']}")
         e(f"s_lshl_b32 {s['T']}, {OP['w1k']}, 2")
         e(f"s_add_u32 {s['EPI']}, {s['EPI']}, {s['T']}")
         # staging write address of chunk cc: row l % 32, chunk cc ^ swz(row), half l / 32
         for cc in range(8):
-            e(f"v_xor_b32 v{tcvt}, {cc}, {OP['ew_s']}")
+            e(f"v_xor_b32 v{tcvt}, {cc}, {c.lane_value('ew_s')}")
             e(f"v_lshlrev_b32 v{tcvt}, 4, v{tcvt}")
-            e(f"v_add3_u32 v{waddr + cc}, v{tcvt}, {OP['ew_base']}, {s['EPI']}")
-        e(f"v_add_u32 v{rbase}, {s['EPI']}, {OP['rb_even']}")
-        e(f"v_add_u32 v{rbase + 1}, {s['EPI']}, {OP['rb_odd']}")
+            e(f"v_add3_u32 v{waddr + cc}, v{tcvt}, {c.lane_value('ew_base')}, {s['EPI']}")
+        e(f"v_add_u32 v{rbase}, {s['EPI']}, {c.lane_value('rb_even')}")
+        e(f"v_add_u32 v{rbase + 1}, {s['EPI']}, {c.lane_value('rb_odd')}")
         if c.bn % 2:
-            e(f"v_add_u32 v{rbase + 2}, {s['EPI']}, {OP['rb1']}")
+            e(f"v_add_u32 v{rbase + 2}, {s['EPI']}, {c.lane_value('rb1')}")
         self.c_resource()
         npass = 0
         for i in range(c.bm):
@@ -450,6 +556,49 @@ class Gen:
                     self.store_offset(i, row, p, lb)
                     e(f"buffer_store_dwordx4 v[{d}:{d + 3}], {c.vt2}, {s['RC']}, 0 offen nt")
         e(f"s_add_u32 {OP['vmt']}, {OP['vmt']}, {c.e_stores}")
+
+    def lane_values(self):
+        """MX: form the bf16 epilogue's per-lane bases from the lane id (the other configurations
+        take them as operands), restating vark_wide.h's set-up: staging writes at row rl = l % 32,
+        half hl = l / 32 (ew_base = 128 rl + 8 hl, ew_s = (rl / 2) % 8); read-back rows rr = l / 8,
+        chunk rc = l % 8 (rb_even = 128 rr + 16 (rc ^ rs), rb_odd = 128 (8 + rr) + 16 (rc ^ rs ^ 4),
+        rs = rr / 2; gb = rr * cm2 + 16 rc) and, for a last single n-block, r1 = l / 4, c1 = l % 4
+        (rb1 = 128 r1 + 16 (c1 ^ rr), gb1 = r1 * cm2 + 16 c1)."""
+        c, e, OP = self.cfg, self.emit, self.OP
+        if not c.lane_regs:
+            return
+        R = c.lane_regs
+        t = c.vop0 + 56 + len(R)
+        ln, t0, t1, t2, rr, rc = (f"v{t + k}" for k in range(6))
+        assert t + 6 <= c.vacc0
+        e(f"v_mbcnt_lo_u32_b32 {ln}, -1, 0")
+        e(f"v_mbcnt_hi_u32_b32 {ln}, -1, {ln}")
+        e(f"v_and_b32 {t0}, 31, {ln}")
+        e(f"v_lshrrev_b32 {t1}, 5, {ln}")
+        e(f"v_lshlrev_b32 {t0}, 7, {t0}")
+        e(f"v_lshl_add_u32 {R['ew_base']}, {t1}, 3, {t0}")
+        e(f"v_bfe_u32 {R['ew_s']}, {ln}, 1, 3")
+        e(f"v_lshrrev_b32 {rr}, 3, {ln}")
+        e(f"v_and_b32 {rc}, 7, {ln}")
+        e(f"v_lshrrev_b32 {t0}, 4, {ln}")
+        e(f"v_xor_b32 {t1}, {rc}, {t0}")
+        e(f"v_lshlrev_b32 {t1}, 4, {t1}")
+        e(f"v_lshl_add_u32 {R['rb_even']}, {rr}, 7, {t1}")
+        e(f"v_xor_b32 {t1}, 4, {t0}")
+        e(f"v_xor_b32 {t1}, {t1}, {rc}")
+        e(f"v_lshlrev_b32 {t1}, 4, {t1}")
+        e(f"v_add_u32 {t2}, 8, {rr}")
+        e(f"v_lshl_add_u32 {R['rb_odd']}, {t2}, 7, {t1}")
+        e(f"v_mul_lo_u32 {t2}, {rr}, {OP['cm2']}")
+        e(f"v_lshl_add_u32 {R['gb']}, {rc}, 4, {t2}")
+        if "rb1" in R:
+            e(f"v_lshrrev_b32 {t0}, 2, {ln}")
+            e(f"v_and_b32 {t1}, 3, {ln}")
+            e(f"v_xor_b32 {t2}, {t1}, {rr}")
+            e(f"v_lshlrev_b32 {t2}, 4, {t2}")
+            e(f"v_lshl_add_u32 {R['rb1']}, {t0}, 7, {t2}")
+            e(f"v_mul_lo_u32 {t2}, {t0}, {OP['cm2']}")
+            e(f"v_lshl_add_u32 {R['gb1']}, {t1}, 4, {t2}")
 
     def f32_store_offset(self, i, j, k):
         """vt2 = byte offset of this wave's tile rows 32 i + 8 k + l / 8, columns 32 j + 4 (l % 8)
@@ -557,6 +706,7 @@ class Gen:
         z = c.vop0 + 24
         for r in range(z, z + 4):
             e(f"v_mov_b32 v{r}, 0")
+        self.lane_values()
         self.c_resource()
         for i in range(c.bm):
             for p, blocks in enumerate(c.pairs):
@@ -594,6 +744,11 @@ class Gen:
         e(f"s_addc_u32 {s['BR1']}, {OP['bRT_hi']}, 0")
         e(f"s_mov_b32 {s['CM0']}, {OP['m0T']}")
         e(f"s_mov_b32 {s['CN0']}, {OP['n0T']}")
+        if c.mx:
+            e(f"s_lshl_b32 {s['T']}, {OP['stride_sc']}, 1")
+            e(f"s_mul_i32 {s['T']}, {s['T']}, {OP['nis']}")
+            e(f"s_add_u32 {s['BS0']}, {OP['scT_lo']}, {s['T']}")
+            e(f"s_addc_u32 {s['BS1']}, {OP['scT_hi']}, 0")
         e("s_barrier")   # the previous tile's epilogue is done with its staging slot
         # top up to three stages of this tile in flight
         e(f"s_min_u32 {s['LIMTOP']}, {s['S']}, {SLOTS}")
@@ -609,6 +764,9 @@ class Gen:
         e(f"s_cbranch_scc1 {zero}")
         self.wait_oldest()
         e("s_barrier")
+        if c.mx:
+            self.scale_slot(s["CS"])
+        self.nlds, self.lo_at = 0, {}
         for i in range(c.bm):
             self.read_block("am", i, s["CS"])
         for j in range(c.bn):
@@ -653,7 +811,7 @@ def render():
         total += len(g.lines)
         text = "\\n\\t".join(g.lines)
         clob = ([f'"a{r}"' for r in range(256)] + [f'"v{r}"' for r in c.vgpr_clobber]
-                + [f'"s{r}"' for r in SGPR_CLOBBER] + ['"m0"', '"scc"', '"memory"'])
+                + [f'"s{r}"' for r in c.sgpr_clobber] + ['"m0"', '"scc"', '"memory"'])
         order = ", ".join(f"{i}:{n}" for i, (n, _) in enumerate(c.operands))
         t = c.name
         out += [

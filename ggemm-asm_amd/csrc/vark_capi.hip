@@ -20,6 +20,7 @@ GGEMM_DEFINE_WIDE_KERNEL(_grouped_variable_k_gemm_kernel_wide, 256, 384, uint16_
 GGEMM_DEFINE_WIDE_KERNEL(_grouped_variable_k_gemm_kernel_wide320, 320, 320, uint16_t, ggemm::kOutBF16)
 GGEMM_DEFINE_WIDE_KERNEL(_grouped_variable_k_gemm_kernel_wide320_f32, 320, 320, float, ggemm::kOutF32)
 GGEMM_DEFINE_WIDE_KERNEL(_grouped_variable_k_gemm_kernel_wide320_f32_acc, 320, 320, float, ggemm::kOutF32Acc)
+GGEMM_DEFINE_WIDE_MX_KERNEL(_grouped_variable_k_mxfp8_gemm_kernel_wide320)
 
 namespace {
 
@@ -180,11 +181,13 @@ int ggemm_vark_wgrad_fp8_out(const void* lhs, const void* rhs, void* out, const 
   return (int)hipGetLastError();
 }
 
-int ggemm_vark_wgrad_mxfp8(const void* lhs, const void* rhs, void* out, const uint8_t* lhs_scale,
-                           const uint8_t* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
-                           int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
-                           int32_t stride_cm, int32_t stride_cn, int32_t stride_lhs_scale, int32_t stride_rhs_scale,
-                           int64_t M_total, void* stream) {
+// tile_m: 0 = the wide 320 x 320 kernel where the bf16 tensorwise entry would run it, else the
+// 192-row kernel; 320 / 192 = that kernel (320 only for shapes it takes)
+static int launch_mx(int32_t tile_m, const void* lhs, const void* rhs, void* out, const uint8_t* lhs_scale,
+                     const uint8_t* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M, int32_t OUT_N,
+                     int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg, int32_t stride_cm,
+                     int32_t stride_cn, int32_t stride_lhs_scale, int32_t stride_rhs_scale, int64_t M_total,
+                     void* stream) {
   int rc = validate_common(lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
                            stride_rhs_m, stride_cg, stride_cm, stride_cn);
   if (rc) return rc;
@@ -192,14 +195,47 @@ int ggemm_vark_wgrad_mxfp8(const void* lhs, const void* rhs, void* out, const ui
   if (stride_lhs_scale < OUT_M || stride_rhs_scale < OUT_N || stride_lhs_scale % 16 || stride_rhs_scale % 16)
     return GGEMM_E_STRIDE;
   if (!aligned(lhs_scale, 16) || !aligned(rhs_scale, 16)) return GGEMM_E_ALIGN;
+  if (tile_m != 0 && tile_m != 320 && tile_m != 192) return GGEMM_E_SHAPE;
+  bool wide = tile_m == 0 ? wide_selected(OUT_M, OUT_N, stride_cm, out) == 320 : tile_m == 320;
+  if (tile_m == 320) {
+    if (wide_tile_for(OUT_M, OUT_N, stride_cm) != 320) return GGEMM_E_SHAPE;
+    if (!aligned(out, 16)) return GGEMM_E_ALIGN;    // 16-byte stores of whole row chunks
+  }
   int cus = 0;
   rc = device_cus(&cus);
   if (rc) return rc;
+  if (wide) {
+    // the kernels keep token counts in 32 bits: a group never exceeds 2^31 - 1 tokens
+    const int64_t m_total = M_total < INT32_MAX ? M_total : INT32_MAX;
+    hipLaunchKernelGGL(_grouped_variable_k_mxfp8_gemm_kernel_wide320, dim3(cus), dim3(ggemm::wide::kNT), 0,
+                       (hipStream_t)stream, (const uint8_t*)lhs, (const uint8_t*)rhs, (uint16_t*)out, lhs_scale,
+                       rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m, stride_rhs_m, stride_cg, stride_cm,
+                       stride_cn, stride_lhs_scale, stride_rhs_scale, m_total);
+    return (int)hipGetLastError();
+  }
   hipLaunchKernelGGL(_grouped_variable_k_mxfp8_gemm_kernel, dim3(cus), dim3(ggemm::kThreads), ggemm::kDynLdsBytes,
                      (hipStream_t)stream, (const uint8_t*)lhs, (const uint8_t*)rhs, (uint16_t*)out, lhs_scale,
                      rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m, stride_rhs_m, stride_cg, stride_cm,
                      stride_cn, stride_lhs_scale, stride_rhs_scale, (void*)nullptr, (void*)nullptr, M_total);
   return (int)hipGetLastError();
+}
+
+int ggemm_vark_wgrad_mxfp8(const void* lhs, const void* rhs, void* out, const uint8_t* lhs_scale,
+                           const uint8_t* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
+                           int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
+                           int32_t stride_cm, int32_t stride_cn, int32_t stride_lhs_scale, int32_t stride_rhs_scale,
+                           int64_t M_total, void* stream) {
+  return launch_mx(0, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m, stride_rhs_m,
+                   stride_cg, stride_cm, stride_cn, stride_lhs_scale, stride_rhs_scale, M_total, stream);
+}
+
+int ggemm_vark_wgrad_mxfp8_tile(const void* lhs, const void* rhs, void* out, const uint8_t* lhs_scale,
+                                const uint8_t* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
+                                int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
+                                int32_t stride_cm, int32_t stride_cn, int32_t stride_lhs_scale,
+                                int32_t stride_rhs_scale, int64_t M_total, int32_t tile_m, void* stream) {
+  return launch_mx(tile_m, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
+                   stride_rhs_m, stride_cg, stride_cm, stride_cn, stride_lhs_scale, stride_rhs_scale, M_total, stream);
 }
 
 int ggemm_vark_check_offsets(const int64_t* offs, int32_t G, int64_t M_total, int32_t mx) {

@@ -143,10 +143,13 @@ def grouped_gemm_fp8_tensorwise_variable_k(lhs: torch.Tensor, rhs: torch.Tensor,
 
 def grouped_gemm_mxfp8_variable_k(lhs: torch.Tensor, rhs: torch.Tensor, lhs_scale: torch.Tensor,
                                   rhs_scale: torch.Tensor, group_offs: torch.Tensor,
-                                  out: torch.Tensor | None = None, *, validate: bool = False) -> torch.Tensor:
+                                  out: torch.Tensor | None = None, *, validate: bool = False,
+                                  tile_m: int = 0) -> torch.Tensor:
     """MXFP8 variant: ``lhs_scale``/``rhs_scale`` are e8m0 bytes [ceil(M/32), OUT_M] / [.., OUT_N]
     (uint8 or float8_e8m0fnu); token block b of a column is scaled by 2^(scale-127). Group starts
-    must be multiples of 32 (``validate=True`` checks it on the host)."""
+    must be multiples of 32 (``validate=True`` checks it on the host). ``tile_m``: 0 lets the
+    library pick (the 320 x 320 wide-tile kernel for OUT_M >= 1024 where both output dims are
+    multiples of 320), 320 / 192 force the wide / the 192-row-tile kernel."""
     _check_inputs(lhs, rhs, group_offs)
     M_total, OUT_M = lhs.shape
     OUT_N = rhs.shape[1]
@@ -166,11 +169,11 @@ def grouped_gemm_mxfp8_variable_k(lhs: torch.Tensor, rhs: torch.Tensor, lhs_scal
     lhs_scale, rhs_scale = _nonempty(lhs_scale), _nonempty(rhs_scale)
     lib = _lib.load()
     with torch.cuda.device(lhs.device):
-        rc = lib.ggemm_vark_wgrad_mxfp8(
+        rc = lib.ggemm_vark_wgrad_mxfp8_tile(
             lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), lhs_scale.data_ptr(), rhs_scale.data_ptr(),
             group_offs.data_ptr(), G, OUT_M, OUT_N, lhs.stride(0), rhs.stride(0), out.stride(0), out.stride(1),
-            out.stride(2), lhs_scale.stride(0), rhs_scale.stride(0), M_total, _stream(lhs.device))
-    _lib.check(rc, "ggemm_vark_wgrad_mxfp8")
+            out.stride(2), lhs_scale.stride(0), rhs_scale.stride(0), M_total, int(tile_m), _stream(lhs.device))
+    _lib.check(rc, "ggemm_vark_wgrad_mxfp8_tile")
     return out
 
 

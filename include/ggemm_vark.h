@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define GGEMM_VARK_ABI_VERSION 6
+#define GGEMM_VARK_ABI_VERSION 7
 
 enum {
   GGEMM_OK = 0,
@@ -100,12 +100,24 @@ int ggemm_vark_wgrad_fp8_wide(const void* lhs, const void* rhs, void* out, const
  * stride_rhs_scale. Token block b (tokens 32b..32b+31) of a column is multiplied by
  * 2^(scale[b][col]-127). Every group must start at a multiple of 32 tokens (ggemm_vark_check_offsets
  * with mx = 1 checks a host copy; otherwise the caller's responsibility). Group offsets are
- * clamped to [0, M_total] on the device, as in ggemm_vark_wgrad_fp8_out. */
+ * clamped to [0, M_total] on the device, as in ggemm_vark_wgrad_fp8_out. Runs the 320 x 320
+ * wide-tile kernel where ggemm_vark_bf16_kernel returns 320 for the shape, else the 192-row one. */
 int ggemm_vark_wgrad_mxfp8(const void* lhs, const void* rhs, void* out, const uint8_t* lhs_scale,
                            const uint8_t* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
                            int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
                            int32_t stride_cm, int32_t stride_cn, int32_t stride_lhs_scale,
                            int32_t stride_rhs_scale, int64_t M_total, void* stream);
+
+/* ggemm_vark_wgrad_mxfp8 on a chosen kernel (no reference counterpart): tile_m 320 = the 320 x 320
+ * wide-tile kernel (OUT_M and OUT_N multiples of 320, a group of C within 2^31 bytes, out 16-byte
+ * aligned, group offsets clamped to [0, min(M_total, 2^31 - 1)]; otherwise GGEMM_E_SHAPE /
+ * GGEMM_E_ALIGN and nothing is launched), 192 = the 192-row-tile kernel, 0 = the choice of
+ * ggemm_vark_wgrad_mxfp8. Same arguments and result otherwise. */
+int ggemm_vark_wgrad_mxfp8_tile(const void* lhs, const void* rhs, void* out, const uint8_t* lhs_scale,
+                                const uint8_t* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
+                                int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
+                                int32_t stride_cm, int32_t stride_cn, int32_t stride_lhs_scale,
+                                int32_t stride_rhs_scale, int64_t M_total, int32_t tile_m, void* stream);
 
 /* Host-side check of a group-offset array (host memory, G+1 entries) against M_total; MX also
  * checks 32-token alignment of group starts. Mirrors the invariants the reference generator
@@ -123,17 +135,18 @@ const char* ggemm_vark_strerror(int32_t code);
 /* GGEMM_VARK_ABI_VERSION of the loaded library. */
 int32_t ggemm_vark_abi_version(void);
 
-/* Launch geometry the library uses (and the drop-in code object expects) for a problem of width
- * OUT_N = out_n: block threads, dynamic LDS bytes, output tile (OUT_M x OUT_N; the N tile is 384
- * when out_n is a multiple of 384, else 320) and tokens per pipeline stage. */
 /* Which kernel the bf16 entry points (ggemm_vark_wgrad_fp8, ggemm_vark_wgrad_fp8_out with
  * GGEMM_OUT_BF16) run for a shape: 320 or 256 = the wide-tile kernel with that tile height
  * (OUT_M >= 1024, a shape ggemm_vark_wgrad_fp8_wide takes with tile_m = 0, out 16-byte aligned),
  * 0 = the 192-row-tile kernel of the reference launch geometry. The fp32 modes of
  * ggemm_vark_wgrad_fp8_out run the 320 x 320 kernel where this returns 320 for stride_cm twice
- * the fp32 row stride. No reference counterpart. Touches no device. */
+ * the fp32 row stride, ggemm_vark_wgrad_mxfp8 its MX variant where this returns 320. No reference
+ * counterpart. Touches no device. */
 int32_t ggemm_vark_bf16_kernel(int32_t OUT_M, int32_t OUT_N, int32_t stride_cm, const void* out);
 
+/* Launch geometry the library uses (and the drop-in code object expects) for a problem of width
+ * OUT_N = out_n: block threads, dynamic LDS bytes, output tile (OUT_M x OUT_N; the N tile is 384
+ * when out_n is a multiple of 384, else 320) and tokens per pipeline stage. */
 void ggemm_vark_launch_geometry(int32_t out_n, int32_t* block_threads, int32_t* dynamic_lds, int32_t* tile_m,
                                 int32_t* tile_n, int32_t* k_step);
 

@@ -7,13 +7,17 @@ Same bar as the other wgrad kernels: cosine >= 0.99999, max relative error <= 2e
 groups (1-64-token groups, K tails of every residue class mod 64), OUT_M not a multiple of 256 (a
 partial last M-tile, whose rows past OUT_M the kernel must not write), several N tiles, G up to
 1100 (natural group order), offsets past M_total (clamped), a NaN-prefilled C, the full gate_up
-problem compared whole, and agreement with the 192 x 384 kernel.
+problem compared whole, and agreement with the 192 x 384 kernel. The MXFP8 variant (320 x 320,
+e8m0 block scales in the scaled MFMA) runs the MX cases: ragged groups, random fp8 codes with random
+scales under the rigorous error bound, offsets past M_total, the full gate_up_mx problem against
+the 192-row MX kernel.
 """
 import numpy as np
 import pytest
 import torch
 
-from test_gpu_parity import _assert_parity, _assert_parity_small_k, _oracle_whole, _rand_bytes_problem
+from test_gpu_parity import (_assert_parity, _assert_parity_small_k, _error_bound_ok, _oracle_whole,
+                             _rand_bytes_problem)
 
 pytestmark = pytest.mark.gpu
 
@@ -210,3 +214,95 @@ def test_wide_fp32_offsets_clamped_and_partial_rows(pkg, orc, cuda, kind):
     ref = orc.vark_wgrad_tensorwise_f32(lhs.numpy(), rhs.numpy(), sl, sr, clamped.numpy(), acc_dtype=np.float64)
     got = view.cpu().numpy() - (c0.numpy() if kind == "f32_acc" else 0)
     _f32_parity(orc, got, ref, f"wide320 {kind} clamped")
+
+
+# ----------------------------------------------------------------------------- MXFP8, 320 x 320
+
+MX_WIDE_CASES = [
+    ([64, 0, 96, 45], 320, 320),
+    ([32] * 5 + [0, 128, 256], 640, 320),
+    ([512, 0, 64, 33], 320, 960),
+    ([32, 64, 96, 128, 160, 192, 224, 257], 960, 640),
+    ([4096 + 64, 7], 640, 640),
+]
+
+
+def _run_mx(pkg, lhs, rhs, sc, offs, dev, out=None, tile_m=320):
+    return pkg.grouped_gemm_mxfp8_variable_k(lhs.to(dev), rhs.to(dev), sc[0].to(dev), sc[1].to(dev), offs.to(dev),
+                                             out=out, validate=True, tile_m=tile_m)
+
+
+@pytest.mark.parametrize("lens,om,on", MX_WIDE_CASES, ids=[f"mx{i}" for i in range(len(MX_WIDE_CASES))])
+def test_wide_mx_vs_oracle(pkg, orc, cuda, lens, om, on):
+    _say(f"wide320 mx lens={lens} OUT_M={om} OUT_N={on}")
+    lhs, rhs, offs, sc, _ = _rand_bytes_problem(lens, om, on, seed=sum(lens) + om + 11, mx=True)
+    c = torch.full((len(lens), om, on), float("nan"), dtype=torch.bfloat16, device=cuda)
+    out = _run_mx(pkg, lhs, rhs, sc, offs, cuda, out=c)
+    torch.cuda.synchronize()
+    ref = orc.vark_wgrad_mxfp8(lhs.numpy(), rhs.numpy(), sc[0].numpy(), sc[1].numpy(), offs.numpy())
+    _assert_parity(orc, pkg.as_bf16_bits(out), ref, offs.numpy(), "wide/mx")
+
+
+@pytest.mark.parametrize("on", [320, 1920])
+def test_wide_mx_all_codes_random_scales(pkg, orc, cuda, on):
+    """Uniformly random finite fp8 codes and random e8m0 scales (2^-7 .. 2^7): every element within
+    the rigorous error bound of the exact block-scaled product."""
+    lens = [96, 0, 64, 160, 33]
+    _say(f"wide320 mx all-codes random scales OUT_N={on}")
+    lhs, rhs, offs, (sl, sr), _ = _rand_bytes_problem(lens, 320, on, seed=12, mx=True, dist="codes")
+    out = _run_mx(pkg, lhs, rhs, (sl, sr), offs, cuda)
+    torch.cuda.synchronize()
+    _error_bound_ok(orc, pkg.as_bf16_bits(out), lhs, rhs, offs, 1.0, 1.0, "wide mx codes", lsc=sl, rsc=sr)
+
+
+def test_wide_mx_offsets_past_token_count_are_clamped(pkg, orc, cuda):
+    """As the 192-row MX kernel's test: rows and scale rows past M_total hold 0x38 / 127, so any
+    read past the token count changes the result."""
+    M = 448
+    offs = torch.tensor([0, 96, 96, 384, 640, 800], dtype=torch.int64)
+    clamped = offs.clamp(min=0, max=M)
+    _say(f"wide320 mx offsets past M_total: M={M} offs={offs.tolist()}")
+    lens = torch.diff(clamped).tolist()
+    lhs, rhs, _, sc, _ = _rand_bytes_problem(lens, 320, 640, seed=45, mx=True)
+    pad = 512
+    lhs_full = torch.cat([lhs, torch.full((pad, lhs.shape[1]), 0x38, dtype=torch.uint8)])
+    rhs_full = torch.cat([rhs, torch.full((pad, rhs.shape[1]), 0x38, dtype=torch.uint8)])
+    lsc = torch.cat([sc[0], torch.full((pad // 32, sc[0].shape[1]), 127, dtype=torch.uint8)])
+    rsc = torch.cat([sc[1], torch.full((pad // 32, sc[1].shape[1]), 127, dtype=torch.uint8)])
+    out = pkg.grouped_gemm_mxfp8_variable_k(lhs_full.to(cuda)[:M], rhs_full.to(cuda)[:M], lsc.to(cuda)[:M // 32],
+                                            rsc.to(cuda)[:M // 32], offs.to(cuda), tile_m=320)
+    torch.cuda.synchronize()
+    ref = orc.vark_wgrad_mxfp8(lhs.numpy(), rhs.numpy(), sc[0].numpy(), sc[1].numpy(), clamped.numpy())
+    _assert_parity(orc, pkg.as_bf16_bits(out), ref, clamped.numpy(), "wide/mx clamp")
+
+
+def test_wide_mx_rejects_unsupported_shapes(pkg, cuda):
+    lhs = torch.zeros((64, 320), dtype=torch.uint8, device=cuda)
+    rhs = torch.zeros((64, 336), dtype=torch.uint8, device=cuda)
+    sl = torch.full((2, 320), 127, dtype=torch.uint8, device=cuda)
+    sr = torch.full((2, 336), 127, dtype=torch.uint8, device=cuda)
+    offs = torch.tensor([0, 64], dtype=torch.int64, device=cuda)
+    with pytest.raises(Exception, match="ggemm_vark_wgrad_mxfp8_tile"):
+        pkg.grouped_gemm_mxfp8_variable_k(lhs, rhs, sl, sr, offs, tile_m=320)
+
+
+def test_wide_mx_full_size(pkg, orc, cuda):
+    """gate_up_mx at full size: the library picks the wide MX kernel; deterministic, the whole C
+    against the oracle, and within the bar of the 192-row MX kernel (same scaled 32x32x64 MFMA
+    sequence per block, so normally bit-identical)."""
+    _say("wide320 mx full-size gate_up_mx")
+    p = pkg.inputs.make_problem("gate_up_mx", seed=0, device=cuda)
+    assert pkg.bf16_kernel(p.OUT_M, p.OUT_N) == "wide320"
+    run = lambda t: pkg.grouped_gemm_mxfp8_variable_k(p.lhs, p.rhs, p.lhs_mx, p.rhs_mx, p.group_offs, tile_m=t)
+    out = run(0)
+    out2 = run(320)
+    narrow = run(192)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16)), "non-deterministic output"
+    assert bool(torch.isfinite(out).all())
+    same = float((out.view(torch.int16) == narrow.view(torch.int16)).float().mean())
+    _say(f"gate_up_mx: wide vs 192-row kernel bit-identical fraction {same:.6f}")
+    m = orc.compare(pkg.as_bf16_bits(out), pkg.as_bf16_bits(narrow))
+    _say(f"gate_up_mx: wide vs 192-row kernel {m}")
+    assert orc.parity_ok(m)
+    _oracle_whole(pkg, orc, p, out)

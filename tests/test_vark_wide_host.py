@@ -16,8 +16,12 @@ long groups) the recorded program must:
     first stage), each after the LDS reads of its operands completed (in-order lgkmcnt), and the C
     stores of every epilogue pass, whose row/column offsets cover the wave's quadrant;
   * take the same branches and barriers in every wave.
-Per-lane address maps (operand reads, LDS-DMA placement, epilogue staging) are checked against
-the 32x32x64 operand layout and for LDS bank conflicts.
+The MXFP8 configuration also issues one e8m0 row per wave and stage (checked like the operand
+rows), and every scaled MFMA must find, in the register half its op_sel_hi picks, the completed
+scale read of its own block and stage.
+Per-lane address maps (operand reads, LDS-DMA placement, epilogue staging, MX scale rows and the
+epilogue bases the MX statement forms from the lane id) are checked against the 32x32x64 operand
+layout and for LDS bank conflicts.
 """
 import importlib.util
 import os
@@ -177,6 +181,16 @@ class Block:
                 self.ev.append(("read", base, off, a[0]))
             elif op == "v_mfma_f32_32x32x64_f8f6f4":
                 self.ev.append(("mfma", a[0], a[1], a[2], a[3].split()[0]))
+            elif op == "v_mfma_scale_f32_32x32x64_f8f6f4":
+                hi = re.search(r"op_sel_hi:\[(\d),(\d),(\d)\]", ",".join(a[5:])).groups()
+                assert re.search(r"\bcbsz:1\b", ",".join(a[5:])) and "op_sel:" not in ",".join(a[5:])
+                self.ev.append(("mfma", a[0], a[1], a[2], a[3], a[4], a[5].split()[0], (int(hi[0]), int(hi[1]))))
+            elif op in ("ds_read_u8", "ds_read_u8_d16", "ds_read_u8_d16_hi"):
+                reg, mod = a[1].split()
+                # register halves written: (half, holds the byte) -- a full load zero-fills bits 16-31
+                halves = {"ds_read_u8": ((0, True), (1, False)), "ds_read_u8_d16": ((0, True),),
+                          "ds_read_u8_d16_hi": ((1, True),)}[op]
+                self.ev.append(("sread", self.v[reg], int(mod.split(":")[1]), a[0], halves))
             elif op in ("ds_write_b64", "ds_write_b128", "ds_read_b128"):
                 self.ev.append((op, a))
             elif op.startswith("v_"):
@@ -187,6 +201,8 @@ class Block:
 
 
 LHS, RHS, OUT = 0x7F0000000000, 0x7E0000000000, 0x7D0000000000
+LSC, RSC = 0x7C0000000000, 0x7B0000000000       # MX e8m0 scales
+STRIDE_LSC, STRIDE_RSC = 2896, 5776             # their row strides (at least the width, 16-aligned)
 
 
 def _cb(cfg):
@@ -197,7 +213,7 @@ def _cb(cfg):
 def _run_tiles(cfg, tiles, wave, stride_l=2880, stride_r=5760, stride_cm=5760, OUT_M=2880, prog=None):
     """tiles: list of (g, m0, n0, kb, klen). Returns (events, per-tile event slices, final state)."""
     ev = []
-    scal = {f"s{r}": 0 for r in GEN.SGPR_CLOBBER}
+    scal = {f"s{r}": 0 for r in cfg.sgpr_clobber}
     state = dict(c0=0, nis=0, vmt=0, q0=0, q1=0, q2=0, np=0)
     spans = []
     for n, (g, m0, n0, kb, klen) in enumerate(tiles):
@@ -216,6 +232,13 @@ def _run_tiles(cfg, tiles, wave, stride_l=2880, stride_r=5760, stride_cm=5760, O
                    crecT=((OUT_M - m0) * stride_cm - n0) * _cb(cfg),
                    stride_l=stride_l, stride_r=stride_r, cm2=2 * stride_cm, alpha=0x3F800000,
                    sw_epi=(32 * cfg.bm * (wave & 1) * stride_cm + 32 * cfg.bn * (wave >> 1)) * _cb(cfg))
+        if cfg.mx:
+            side = wave >> 1
+            base_sc, st_sc = (RSC, STRIDE_RSC) if side else (LSC, STRIDE_LSC)
+            sct = base_sc + (kb >> 5) * st_sc + (n0 if side else m0)
+            scn = base_sc + (N[3] >> 5) * st_sc + (N[2] if side else N[1])
+            ops.update(scT_lo=sct & M32, scT_hi=sct >> 32, scN_lo=scn & M32, scN_hi=scn >> 32, stride_sc=st_sc,
+                       scrd=(1024 + 160 * ((wave >> 1) - (wave & 1))) & M32, scw=GEN.SCALE_OFF + 1024 * side)
         start = len(ev)
         Block(cfg, ops, ev, scal, prog).run()
         spans.append((start, len(ev)))
@@ -243,11 +266,20 @@ def _check(cfg, tiles, wave=0, stride_l=2880, stride_r=5760, stride_cm=5760, OUT
         for j, (_, e) in enumerate(grp):
             _, m0v, (base, nrec, stride_bits, w3), voff, _ = e
             assert stride_bits == 0 and w3 == GEN.WORD3
+            assert m0v + 1024 <= GEN.DMA_LDS_LIMIT          # LDS-DMA destinations below 128 KiB
             if j < cfg.nl:
                 assert base == LHS + (kb + 64 * s) * stride_l + m0
                 assert nrec == rv * stride_l - m0
                 assert m0v == slot_of[(n, s)] * cfg.slot + 1024 * wave + 4096 * j
                 assert voff == (0, op(f"voffL{j}"))
+            elif j == cfg.nl + cfg.nr:
+                # MX: the e8m0 rows of this wave's side (wave / 2) for the stage's two token blocks
+                side = wave >> 1
+                base_sc, st_sc = (RSC, STRIDE_RSC) if side else (LSC, STRIDE_LSC)
+                assert base == base_sc + ((kb + 64 * s) >> 5) * st_sc + (n0 if side else m0)
+                assert nrec == ((rv + 31) // 32 - 1) * st_sc + 320
+                assert m0v == GEN.SCALE_OFF + ((slot_of[(n, s)] * cfg.slot) >> 4) + 1024 * side
+                assert voff == (0, op("vsc"))
             else:
                 jj = j - cfg.nl
                 assert base == RHS + (kb + 64 * s) * stride_r + n0
@@ -289,22 +321,50 @@ def _check(cfg, tiles, wave=0, stride_l=2880, stride_r=5760, stride_cm=5760, OUT
         assert all(i in done_at and done_at[i] < first_read for i in loads), f"stage {st} read before its loads"
         last_done = max(done_at[i] for i in loads)
         assert any(last_done < bi < first_read for bi in barriers), f"stage {st}: no barrier after its wait"
-    # ---- operand data: every MFMA's A and B registers hold completed reads (in-order lgkmcnt)
+    # ---- operand data: every MFMA's A and B registers (and MX scale registers) hold completed reads
+    # (in-order lgkmcnt); registers are tracked in 16-bit halves. No LDS load is issued into a
+    # register another LDS load still in flight writes (a 16-bit load does not keep the other
+    # half's value if the two overlap)
     def regs(r):
         m = re.fullmatch(r"v\[(\d+):(\d+)\]", r)
-        return set(range(int(m.group(1)), int(m.group(2)) + 1))
-    pending = []           # (regs written) of issued, not known complete LDS reads
+        return {(x, h) for x in range(int(m.group(1)), int(m.group(2)) + 1) for h in (0, 1)}
+    pending = []           # (register halves written) of issued, not known complete LDS reads
+    last_w = {}            # register half -> (slot value, base, offset) of the last scale read into it
+    mfma_k = 0
+    blk_of = {cfg.acc_range(i, j): (i, j) for i in range(cfg.bm) for j in range(cfg.bn)}
+    def whole(hs):
+        return {x for x, _ in hs}
+
+    def issue_load(hs):
+        assert not any(whole(hs) & whole(p) for p in pending), "two LDS loads in flight to one register"
+        pending.append(hs)
     for e in ev:
         if e[0] == "read":
-            pending.append(regs(e[3]))
+            issue_load(regs(e[3]))
+        elif e[0] == "sread":
+            r = int(e[3][1:])
+            issue_load({(r, h) for h, _ in e[4]})
+            for h, data in e[4]:
+                last_w[(r, h)] = (e[1][0], e[1][1], e[2]) if data else ("zero", e[1][1], e[2])
         elif e[0] in ("ds_write_b64", "ds_write_b128"):
             pending.append(set())
         elif e[0] == "ds_read_b128":
-            pending.append(regs(e[1][0]))
+            issue_load(regs(e[1][0]))
         elif e[0] == "lgkmcnt":
             pending = pending[len(pending) - e[1]:] if e[1] < len(pending) else pending
         elif e[0] == "mfma":
             need = regs(e[2]) | regs(e[3])
+            if cfg.mx:
+                (i, j), st = blk_of[e[1]], stages[mfma_k // (cfg.bm * cfg.bn)]
+                ra, ha = cfg.scale_reg("bn", j)
+                rb, hb = cfg.scale_reg("am", i)
+                assert (e[5], e[6], e[7]) == (f"v{ra}", f"v{rb}", (ha, hb)), e
+                sslot = (slot_of[st] * cfg.slot) >> 4
+                scrd = (1024 + 160 * ((wave >> 1) - (wave & 1))) & M32
+                assert last_w.get((rb, hb)) == (sslot, op("vscb"), 32 * i), f"MFMA {e}: LHS scale of {st}"
+                assert last_w.get((ra, ha)) == ((sslot + scrd) & M32, op("vscb"), 32 * j), f"MFMA {e}: RHS scale"
+                need |= {(ra, ha), (rb, hb)}
+            mfma_k += 1
             assert not any(need & p for p in pending), f"MFMA {e} reads registers of a pending LDS read"
         elif e[0] == "store":
             assert not any(regs(e[3]) & p for p in pending), "store of pending LDS data"
@@ -354,7 +414,8 @@ def _check(cfg, tiles, wave=0, stride_l=2880, stride_r=5760, stride_cm=5760, OUT
             for i in range(cfg.bm):
                 for pidx, blocks in enumerate(cfg.pairs):
                     for row, _, _, lb in GEN.Gen.pass_stores(len(blocks)):
-                        want_st.append((sw + (32 * i + row) * 2 * stride_cm + 128 * pidx, op(lb)))
+                        want_st.append((sw + (32 * i + row) * 2 * stride_cm + 128 * pidx,
+                                        cfg.lane_regs.get(lb) or op(lb)))
         elif not (cfg.out == "f32acc" and S == 0):
             for i in range(cfg.bm):
                 for j in range(cfg.bn):
@@ -434,7 +495,7 @@ def test_asm_writes_only_clobbered_registers():
                 k, lo = m.group(1), int(m.group(2))
                 hi = int(m.group(3)) if m.group(3) else lo
                 if k == "s":
-                    assert GEN.SGPR_CLOBBER[0] <= lo and hi <= GEN.SGPR_CLOBBER[-1], line
+                    assert c.sgpr_clobber[0] <= lo and hi <= c.sgpr_clobber[-1], line
                 elif k == "v":
                     assert c.vgpr_clobber[0] <= lo and hi <= 255, line
                 else:
@@ -601,3 +662,140 @@ def test_epilogue_f32_staging_and_store_coverage():
         for q in range(8):
             assert len({(a // 16) % 16 for a in addrs[8 * q:8 * q + 8]}) == 8
     assert cover == {(r, cc) for r in range(32) for cc in range(8)}
+
+
+# ----------------------------------------------------------------------------- MXFP8 per-lane maps
+
+MXC = CFGS["320x320_mx"]
+
+
+def test_mx_scale_rows_reach_each_lane():
+    """The scale slot as the four waves' LDS-DMA fills it (vark_wide.h: both waves of side v / 2
+    carry that side's two rows, lane l < 40 chunk l % 20 of row l / 20 with vsc = (l / 20) stride +
+    16 (l % 20) to scw + 16 l, the other lanes out of range), read as the statement reads it (vscb +
+    32 b, RHS + scrd): every lane of every wave gets, for each m-block i / n-block j, the e8m0 byte
+    of row l % 32 of that block in token block l / 32 -- the lane the scaled 32x32x64 MFMA takes the
+    scale of (row l % 32, K-block l / 32) from, K-block 0 being the stage's tokens 0-31 (bytes 0-15
+    of both lane halves). The two waves of a side write identical bytes, and all of it lies below
+    128 KiB and inside the slot's 2.5 KiB."""
+    rng = np.random.default_rng(11)
+    for st_l, st_r, m0, n0, blk0 in ((2896, 5776, 320 * 3, 320 * 7, 5), (320, 320, 0, 0, 0)):
+        lsc = rng.integers(0, 255, size=(blk0 + 2, st_l), dtype=np.uint8)
+        rsc = rng.integers(0, 255, size=(blk0 + 2, st_r), dtype=np.uint8)
+        for slot_idx in range(3):
+            sbase = GEN.SCALE_OFF + ((slot_idx * MXC.slot) >> 4)
+            lds = {}
+            for v in range(4):
+                side = v >> 1
+                sc, st, col = (rsc, st_r, n0) if side else (lsc, st_l, m0)
+                flat = sc.reshape(-1)
+                nrec = 1 * st + 320                       # both blocks valid
+                scw = GEN.SCALE_OFF + 1024 * side
+                for lane in range(64):
+                    vsc = (lane // 20) * st + 16 * (lane % 20) if lane < 40 else 0x80000000
+                    data = flat[blk0 * st + col + vsc:][:16] if vsc + 16 <= nrec else np.zeros(16, np.uint8)
+                    assert (vsc + 16 <= nrec) == (lane < 40)
+                    dst = scw + ((slot_idx * MXC.slot) >> 4) + 16 * lane
+                    assert sbase <= dst and dst + 16 <= sbase + GEN.SCALE_SLOT and dst + 16 <= GEN.DMA_LDS_LIMIT
+                    for k in range(16):
+                        assert lds.setdefault(dst + k, int(data[k])) == int(data[k])   # same bytes from both waves
+            for w in range(4):
+                wm, wn = w & 1, w >> 1
+                scrd = 1024 + 160 * (wn - wm)
+                for lane in range(64):
+                    vscb = GEN.SCALE_OFF + 320 * (lane >> 5) + 160 * wm + (lane & 31)
+                    kb, row = lane >> 5, lane & 31
+                    for b in range(MXC.bm):
+                        assert lds[sbase - GEN.SCALE_OFF + vscb + 32 * b] == lsc[blk0 + kb, m0 + 160 * wm + 32 * b + row]
+                    for b in range(MXC.bn):
+                        assert (lds[sbase - GEN.SCALE_OFF + vscb + scrd + 32 * b]
+                                == rsc[blk0 + kb, n0 + 160 * wn + 32 * b + row])
+
+
+def test_mx_scale_reads_conflict_free():
+    """One scale read (ds_read_u8, 64 lanes): the 32 lanes of a half read 32 consecutive bytes of
+    one row, so at most 4 lanes share a 4-byte bank word and no two lanes hit one bank in
+    different words."""
+    for w in range(4):
+        wm, wn = w & 1, w >> 1
+        for extra in [32 * b for b in range(5)] + [1024 + 160 * (wn - wm) + 32 * b for b in range(5)]:
+            for half in range(2):
+                addrs = [320 * (lane >> 5) + 160 * wm + (lane & 31) + extra for lane in range(32 * half, 32 * half + 32)]
+                words = {}
+                for a in addrs:
+                    words.setdefault((a // 4) % 64, set()).add(a // 4)
+                assert all(len(v) == 1 for v in words.values())
+
+
+def _eval_lane_values(cfg, stride_cm):
+    """Runs the statement's lane-id sequence (Gen.lane_values) for every lane."""
+    g = GEN.Gen(cfg)
+    g.lane_values()
+    ops = {cfg.op["cm2"]: 2 * stride_cm}
+    out = []
+    for lane in range(64):
+        v = {}
+
+        def val(x):
+            if x in ops:
+                return ops[x]
+            if x.startswith("v"):
+                return v[x]
+            return int(x, 0)
+        for line in g.lines:
+            op, _, rest = line.partition(" ")
+            a = [t.strip() for t in rest.split(",")]
+            if op == "v_mbcnt_lo_u32_b32":
+                assert a[1:] == ["-1", "0"]
+                v[a[0]] = min(lane, 32)
+            elif op == "v_mbcnt_hi_u32_b32":
+                assert a[1] == "-1"
+                v[a[0]] = val(a[2]) + max(lane - 32, 0)
+            elif op == "v_and_b32":
+                v[a[0]] = val(a[1]) & val(a[2])
+            elif op == "v_xor_b32":
+                v[a[0]] = val(a[1]) ^ val(a[2])
+            elif op == "v_lshrrev_b32":
+                v[a[0]] = val(a[2]) >> val(a[1])
+            elif op == "v_lshlrev_b32":
+                v[a[0]] = (val(a[2]) << val(a[1])) & M32
+            elif op == "v_lshl_add_u32":
+                v[a[0]] = ((val(a[1]) << val(a[2])) + val(a[3])) & M32
+            elif op == "v_bfe_u32":
+                v[a[0]] = (val(a[1]) >> val(a[2])) & ((1 << val(a[3])) - 1)
+            elif op == "v_add_u32":
+                v[a[0]] = (val(a[1]) + val(a[2])) & M32
+            elif op == "v_mul_lo_u32":
+                v[a[0]] = (val(a[1]) * val(a[2])) & M32
+            else:
+                raise AssertionError(op)
+        out.append({n: v[r] for n, r in cfg.lane_regs.items()})
+    return out
+
+
+@pytest.mark.parametrize("stride_cm", [5760, 2880, 320])
+def test_mx_epilogue_lane_values(stride_cm):
+    """The epilogue bases the MX statement forms from the lane id equal the values vark_wide.h
+    passes the other configurations as operands."""
+    got = _eval_lane_values(MXC, stride_cm)
+    for lane in range(64):
+        rl, hl = lane & 31, lane >> 5
+        rr, rc = lane >> 3, lane & 7
+        rs = (rr >> 1) & 7
+        r1, c1 = lane >> 2, lane & 3
+        want = dict(ew_base=rl * 128 + 8 * hl, ew_s=(rl >> 1) & 7, rb_even=rr * 128 + 16 * (rc ^ rs),
+                    rb_odd=(8 + rr) * 128 + 16 * (rc ^ (rs ^ 4)), gb=(rr * stride_cm + 8 * rc) * 2,
+                    rb1=r1 * 128 + 16 * (c1 ^ ((r1 >> 1) & 7)), gb1=(r1 * stride_cm + 8 * c1) * 2)
+        assert got[lane] == want, lane
+
+
+def test_mx_lane_value_registers_are_free():
+    """The registers the MX epilogue forms its bases (and temporaries) in lie in the operand
+    registers, clear of the staging registers the bf16 epilogue uses (vop0 .. vop0 + 55) and of the
+    accumulators."""
+    regs = {int(r[1:]) for r in MXC.lane_regs.values()}
+    g = GEN.Gen(MXC)
+    g.lane_values()
+    for line in g.lines:
+        regs |= {int(m) for m in re.findall(r"\bv(\d+)\b", line.split(" ", 1)[1].split(",")[0])}
+    assert min(regs) >= MXC.vop0 + 56 and max(regs) < MXC.vacc0
