@@ -58,8 +58,9 @@ SGPR_CLOBBER = list(range(56, 89))
 SGPR_CLOBBER_MX = list(range(56, 97))
 # MXFP8: the e8m0 rows of a stage sit in a scale slot at SCALE_OFF + (stage slot offset >> 4): the
 # LHS rows of token blocks 0 and 1 at +0 and +320, the RHS rows at +1024 and +1344. Every LDS-DMA
-# destination of these kernels stays below 128 KiB (with the scale slots at 136 KiB the results
-# came out wrong on MI355X); the schedule tables, read with plain LDS reads, move above them.
+# destination of these kernels stays below 128 KiB, the range the operand slots have always used
+# (the DMA's M0 offset is not exercised above it); the schedule tables, read with plain LDS reads,
+# move above the scale slots.
 SCALE_OFF = SLOTS * 40960
 SCALE_SLOT = 40960 >> 4
 DMA_LDS_LIMIT = 128 * 1024
