@@ -66,6 +66,11 @@ def parse_args():
                     help="time the reference's call sites (one, or a group) with its own input recipe and print "
                          "a per-site summary table; replaces --config")
     ap.add_argument("--mfma", default="k128", choices=["k128", "k32"])
+    ap.add_argument("--out", default="bf16", choices=["bf16", "f32", "f32_accum"],
+                    help="tensorwise wgrad configs: C bf16, fp32, or fp32 accumulated in place (C += result)")
+    ap.add_argument("--lens", default="multinomial", choices=["multinomial", "reference"],
+                    help="tensorwise wgrad configs: the configuration's group sizes, or the reference's seed-42 "
+                         "exponential ones (reference bench.py:205-223)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU work for the cpu_baseline sample (0 disables)")
@@ -416,17 +421,32 @@ def main():
         main_layer(args, pkg, dev)
         return
     fwd = args.config in FWD_SITES
+    tw_wgrad = args.config in ("gate_up_wgrad", "down_wgrad", "gate_up_zipf")
+    if (args.out != "bf16" or args.lens != "multinomial") and not tw_wgrad:
+        raise SystemExit("--out / --lens apply to the tensorwise wgrad configs (gate_up_wgrad, down_wgrad, "
+                         "gate_up_zipf)")
     if args.config == "constant":
         p = pkg.inputs.constant_problem(device=dev)
     elif fwd:
         p = pkg.inputs.make_fwd_problem(args.config, seed=args.seed, device=dev)
     else:
-        p = pkg.inputs.make_problem(args.config, seed=args.seed, device=dev)
+        lens = pkg.inputs.make_group_lens_reference() if args.lens == "reference" else None
+        p = pkg.inputs.make_problem(args.config, seed=args.seed, device=dev, lens=lens)
     torch.cuda.synchronize()
-    run = make_runner(pkg, p, dev, args.mfma)
+    if args.out != "bf16":
+        sl = torch.tensor(p.lhs_scale, dtype=torch.float32, device=dev)
+        sr = torch.tensor(p.rhs_scale, dtype=torch.float32, device=dev)
+        c32 = torch.zeros((p.G, p.OUT_M, p.OUT_N), dtype=torch.float32, device=dev)
+        run = lambda: pkg.grouped_gemm_fp8_tensorwise_variable_k(p.lhs, p.rhs, sl, sr, p.group_offs, out=c32,
+                                                                  out_dtype=torch.float32,
+                                                                  accumulate=args.out == "f32_accum")
+    else:
+        run = make_runner(pkg, p, dev, args.mfma)
     ms = time_steps(run, args.steps, args.warmup)
     tflops = p.flops / (ms * 1e-3) / 1e12
-    traffic, traffic_source = read_traffic(args.config)
+    # traffic measured for this exact variant (profiles/traffic_<config>[_<out>][_reference_lens].txt)
+    traffic, traffic_source = read_traffic(args.config + ("" if args.out == "bf16" else "_" + args.out)
+                                           + ("" if args.lens == "multinomial" else "_reference_lens"))
     if fwd:
         geo = pkg.launch_geometry(p.N)
         config = {"workload": p.name, "G": p.G, "M_total": p.M, "K": p.K, "N": p.N,
@@ -439,8 +459,13 @@ def main():
         vs_baseline = None
     else:
         config = {"workload": p.name, "G": p.G, "M_total": p.M, "OUT_M": p.OUT_M, "OUT_N": p.OUT_N,
-                  "lhs": "e4m3fn", "rhs": "e5m2", "out": "bf16", "acc": "fp32",
-                  "inputs": "seeded N(0,1) / N(0,1e-3) quantized per-tensor, multinomial group sizes, in HBM",
+                  "lhs": "e4m3fn", "rhs": "e5m2",
+                  "out": {"bf16": "bf16", "f32": "fp32", "f32_accum": "fp32, accumulated in place (C += result)"}[
+                      args.out],
+                  "acc": "fp32",
+                  "inputs": "seeded N(0,1) / N(0,1e-3) quantized per-tensor, {} group sizes, in HBM".format(
+                      "the reference's seed-42 exponential" if args.lens == "reference" else
+                      {"gate_up_zipf": "Zipf-skewed"}.get(p.name, "multinomial")),
                   "kernel": ("hip gfx950 persistent {}x{} tiles, 256-thread workgroups (one wave per SIMD, "
                              "hand-placed accumulators), mfma 32x32x64".format(
                                  *((320, 320) if pkg.bf16_kernel(p.OUT_M, p.OUT_N) == "wide320" else (256, 384)))
@@ -452,9 +477,12 @@ def main():
                                       if p.name == "gate_up_wgrad" else "none published for this workload")}
         if p.is_mx:
             config["scales"] = "e8m0 per 32 tokens per column (MX block scaling)"
-        vs_baseline = round(tflops / REF_OPT_ASM_TFLOPS, 4) if p.name == "gate_up_wgrad" else None
+        vs_baseline = (round(tflops / REF_OPT_ASM_TFLOPS, 4) if p.name == "gate_up_wgrad" and args.out == "bf16"
+                       else None)
+    variant = "".join(f" {k}={v}" for k, v, d in (("out", args.out, "bf16"), ("lens", args.lens, "multinomial"))
+                      if v != d)
     line = {
-        "metric": f"ms + TFLOPS (% FP8 peak) for {p.name} G={p.G} M={p.M} on 1 MI355X",
+        "metric": f"ms + TFLOPS (% FP8 peak) for {p.name}{variant} G={p.G} M={p.M} on 1 MI355X",
         "value": round(tflops, 2),
         "unit": "TFLOPS",
         "n_gpus": 1,
