@@ -113,6 +113,11 @@ class Config:
         self.sgpr_clobber = SGPR_CLOBBER_MX if mx else SGPR_CLOBBER
         self.rb = 5 if mx else 4                        # LDS reads per operand block (MX: + its scale)
         self.pairs = [(2 * p, 2 * p + 1) if 2 * p + 1 < self.bn else (2 * p,) for p in range((self.bn + 1) // 2)]
+        # bf16 passes of the waves in the right half (wn = 1): with an odd block count their columns
+        # start half a 128-byte line into the tile row, so the single block goes first and every
+        # two-block pass stores whole lines (only the line the two halves share is split)
+        self.pairs_wn1 = ([(0,)] + [(2 * q + 1, 2 * q + 2) for q in range((self.bn - 1) // 2)]
+                          if self.bn % 2 else self.pairs)
         if out == "bf16":
             self.e_stores = self.bm * sum(4 if len(pr) == 2 else 2 for pr in self.pairs)
         else:
@@ -482,15 +487,31 @@ class Gen:
         e(f"s_mov_b32 {s['RC2']}, {OP['crecT']}")
         e(f"s_mov_b32 {s['RC3']}, 0x{WORD3:x}")
 
-    def store_offset(self, i, row, p, lane_base):
+    def store_offset(self, i, row, j0, lane_base):
         """vt2 = byte offset of this wave's tile row 32 i + row (lane part in lane_base), columns
-        from 64 p on."""
+        from block j0 (32 j0) on."""
         s, OP, e, c = SGPR, self.OP, self.emit, self.cfg
         e(f"s_mul_i32 {s['T']}, {OP['cm2']}, {32 * i + row}")
         e(f"s_add_u32 {s['T']}, {s['T']}, {OP['sw_epi']}")
-        if p:
-            e(f"s_add_u32 {s['T']}, {s['T']}, {128 * p}")
+        if j0:
+            e(f"s_add_u32 {s['T']}, {s['T']}, {64 * j0}")
         e(f"v_add_u32 {c.vt2}, {s['T']}, {c.lane_value(lane_base)}")
+
+    def by_half(self, body):
+        """body(pairs) for this wave's bf16 pass order: the right-half waves (wn = bit 11 of w1k)
+        take pairs_wn1 where it differs."""
+        c, e = self.cfg, self.emit
+        if c.pairs_wn1 == c.pairs:
+            body(c.pairs)
+            return
+        right, done = self.label("wn1_"), self.label("wndone")
+        e(f"s_bitcmp1_b32 {self.OP['w1k']}, 11")
+        e(f"s_cbranch_scc1 {right}")
+        body(c.pairs)
+        e(f"s_branch {done}")
+        e(f"{right}:")
+        body(c.pairs_wn1)
+        e(f"{done}:")
 
     @staticmethod
     def pass_stores(nblk):
@@ -526,36 +547,39 @@ class Gen:
         if c.bn % 2:
             e(f"v_add_u32 v{rbase + 2}, {s['EPI']}, {c.lane_value('rb1')}")
         self.c_resource()
-        npass = 0
-        for i in range(c.bm):
-            for p, blocks in enumerate(c.pairs):
-                dbase = dset[npass % 2]
-                npass += 1
-                for jj, j in enumerate(blocks):
-                    kind, base = c.acc(i, j)
-                    for g in range(4):
-                        src = []
-                        for r in range(4):
-                            reg = base + 4 * g + r
-                            if kind == "a":
-                                e(f"v_accvgpr_read_b32 v{tacc + r}, a{reg}")
-                                src.append(f"v{tacc + r}")
-                            else:
-                                src.append(f"v{reg}")
-                        for r in range(4):
-                            e(f"v_mul_f32 v{tmul + r}, {OP['alpha']}, {src[r]}")
-                        e(f"v_cvt_pk_bf16_f32 v{tcvt}, v{tmul}, v{tmul + 1}")
-                        e(f"v_cvt_pk_bf16_f32 v{tcvt + 1}, v{tmul + 2}, v{tmul + 3}")
-                        e(f"ds_write_b64 v{waddr + 4 * jj + g}, v[{tcvt}:{tcvt + 1}]")
-                stores = self.pass_stores(len(blocks))
-                for k, (_, rb, off, _) in enumerate(stores):
-                    d = dbase + 4 * k
-                    e(f"ds_read_b128 v[{d}:{d + 3}], v{rbase + rb} offset:{off}")
-                e("s_waitcnt lgkmcnt(0)")
-                for k, (row, _, _, lb) in enumerate(stores):
-                    d = dbase + 4 * k
-                    self.store_offset(i, row, p, lb)
-                    e(f"buffer_store_dwordx4 v[{d}:{d + 3}], {c.vt2}, {s['RC']}, 0 offen nt")
+
+        def passes(pairs):
+            npass = 0
+            for i in range(c.bm):
+                for blocks in pairs:
+                    dbase = dset[npass % 2]
+                    npass += 1
+                    for jj, j in enumerate(blocks):
+                        kind, base = c.acc(i, j)
+                        for g in range(4):
+                            src = []
+                            for r in range(4):
+                                reg = base + 4 * g + r
+                                if kind == "a":
+                                    e(f"v_accvgpr_read_b32 v{tacc + r}, a{reg}")
+                                    src.append(f"v{tacc + r}")
+                                else:
+                                    src.append(f"v{reg}")
+                            for r in range(4):
+                                e(f"v_mul_f32 v{tmul + r}, {OP['alpha']}, {src[r]}")
+                            e(f"v_cvt_pk_bf16_f32 v{tcvt}, v{tmul}, v{tmul + 1}")
+                            e(f"v_cvt_pk_bf16_f32 v{tcvt + 1}, v{tmul + 2}, v{tmul + 3}")
+                            e(f"ds_write_b64 v{waddr + 4 * jj + g}, v[{tcvt}:{tcvt + 1}]")
+                    stores = self.pass_stores(len(blocks))
+                    for k, (_, rb, off, _) in enumerate(stores):
+                        d = dbase + 4 * k
+                        e(f"ds_read_b128 v[{d}:{d + 3}], v{rbase + rb} offset:{off}")
+                    e("s_waitcnt lgkmcnt(0)")
+                    for k, (row, _, _, lb) in enumerate(stores):
+                        d = dbase + 4 * k
+                        self.store_offset(i, row, blocks[0], lb)
+                        e(f"buffer_store_dwordx4 v[{d}:{d + 3}], {c.vt2}, {s['RC']}, 0 offen nt")
+        self.by_half(passes)
         e(f"s_add_u32 {OP['vmt']}, {OP['vmt']}, {c.e_stores}")
 
     def lane_values(self):
@@ -709,11 +733,14 @@ class Gen:
             e(f"v_mov_b32 v{r}, 0")
         self.lane_values()
         self.c_resource()
-        for i in range(c.bm):
-            for p, blocks in enumerate(c.pairs):
-                for row, _, _, lb in self.pass_stores(len(blocks)):
-                    self.store_offset(i, row, p, lb)
-                    e(f"buffer_store_dwordx4 v[{z}:{z + 3}], {c.vt2}, {SGPR['RC']}, 0 offen nt")
+
+        def zeros(pairs):
+            for i in range(c.bm):
+                for blocks in pairs:
+                    for row, _, _, lb in self.pass_stores(len(blocks)):
+                        self.store_offset(i, row, blocks[0], lb)
+                        e(f"buffer_store_dwordx4 v[{z}:{z + 3}], {c.vt2}, {SGPR['RC']}, 0 offen nt")
+        self.by_half(zeros)
         e(f"s_add_u32 {self.OP['vmt']}, {self.OP['vmt']}, {c.e_stores}")
 
     # ---------------------------------------------------------------- whole tile

@@ -148,6 +148,8 @@ class Block:
             elif op in ("s_cmp_eq_u32", "s_cmp_lt_u32", "s_cmp_ge_u32"):
                 x, y = self.val(a[0]) & M32, self.val(a[1]) & M32
                 self.scc = int(x == y if op == "s_cmp_eq_u32" else x < y if op == "s_cmp_lt_u32" else x >= y)
+            elif op == "s_bitcmp1_b32":
+                self.scc = (self.val(a[0]) >> int(a[1])) & 1
             elif op == "s_cselect_b32":
                 self.setr(a[0], self.val(a[1]) if self.scc else self.val(a[2]))
             elif op == "s_cbranch_scc1":
@@ -411,10 +413,11 @@ def _check(cfg, tiles, wave=0, stride_l=2880, stride_r=5760, stride_cm=5760, OUT
         sw = (32 * cfg.bm * (wave & 1) * stride_cm + 32 * cfg.bn * (wave >> 1)) * cbytes
         want_st = []
         if cfg.out == "bf16":
+            # the right-half waves' passes start with the single block (line-aligned pairs)
             for i in range(cfg.bm):
-                for pidx, blocks in enumerate(cfg.pairs):
+                for blocks in (cfg.pairs_wn1 if wave >> 1 else cfg.pairs):
                     for row, _, _, lb in GEN.Gen.pass_stores(len(blocks)):
-                        want_st.append((sw + (32 * i + row) * 2 * stride_cm + 128 * pidx,
+                        want_st.append((sw + (32 * i + row) * 2 * stride_cm + 64 * blocks[0],
                                         cfg.lane_regs.get(lb) or op(lb)))
         elif not (cfg.out == "f32acc" and S == 0):
             for i in range(cfg.bm):
@@ -799,3 +802,20 @@ def test_mx_lane_value_registers_are_free():
     for line in g.lines:
         regs |= {int(m) for m in re.findall(r"\bv(\d+)\b", line.split(" ", 1)[1].split(",")[0])}
     assert min(regs) >= MXC.vop0 + 56 and max(regs) < MXC.vacc0
+
+
+@pytest.mark.parametrize("cfg", [n for n, c in CFGS.items() if c.out == "bf16"])
+def test_bf16_two_block_passes_store_whole_lines(cfg):
+    """Every two-block bf16 pass of every wave stores 128-byte row pieces that start on a 128-byte
+    boundary of the tile row (a C row starts on one at the MoE shapes), so only the line shared by
+    the left and right half of an odd block count is written in two pieces."""
+    c = CFGS[cfg]
+    for wn in range(2):
+        for blocks in (c.pairs_wn1 if wn else c.pairs):
+            start = 2 * (32 * c.bn * wn + 32 * blocks[0])          # bytes into the tile row
+            if len(blocks) == 2:
+                assert start % 128 == 0, (wn, blocks)
+            else:
+                assert start % 64 == 0
+        got = sorted(j for blocks in (c.pairs_wn1 if wn else c.pairs) for j in blocks)
+        assert got == list(range(c.bn))
