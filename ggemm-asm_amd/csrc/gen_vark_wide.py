@@ -112,14 +112,17 @@ class Config:
         self.vgpr_clobber = list(range(self.vsc0 - (1 if mx else 2), 256))
         self.sgpr_clobber = SGPR_CLOBBER_MX if mx else SGPR_CLOBBER
         self.rb = 5 if mx else 4                        # LDS reads per operand block (MX: + its scale)
-        self.pairs = [(2 * p, 2 * p + 1) if 2 * p + 1 < self.bn else (2 * p,) for p in range((self.bn + 1) // 2)]
-        # bf16 passes of the waves in the right half (wn = 1): with an odd block count their columns
-        # start half a 128-byte line into the tile row, so the single block goes first and every
-        # two-block pass stores whole lines (only the line the two halves share is split)
-        self.pairs_wn1 = ([(0,)] + [(2 * q + 1, 2 * q + 2) for q in range((self.bn - 1) // 2)]
-                          if self.bn % 2 else self.pairs)
+        # bf16 passes of two blocks (64 columns: one 128-byte C line per row). With an odd block count
+        # the right-half waves (wn = 1) start half a line into the tile row: the left half pairs
+        # blocks (0, 1), (2, 3), ..., the right half (1, 2), (3, 4), ..., and the line the two halves
+        # share (left block bn - 1, right block 0) goes through a joint pass: both waves stage their
+        # block in one LDS region, and after a barrier each stores half of its rows as whole lines.
+        self.joint = self.bn % 2 == 1
+        self.pairs = [(2 * q, 2 * q + 1) for q in range(self.bn // 2)]
+        self.pairs_wn1 = [(2 * q + 1, 2 * q + 2) for q in range(self.bn // 2)] if self.joint else self.pairs
+        self.joint_block = (self.bn - 1, 0)            # (left wave's block, right wave's block)
         if out == "bf16":
-            self.e_stores = self.bm * sum(4 if len(pr) == 2 else 2 for pr in self.pairs)
+            self.e_stores = self.bm * (4 * len(self.pairs) + (2 if self.joint else 0))
         else:
             # fp32: one 32 x 32 block per pass, four 1 KiB stores (and, accumulating, four loads of
             # the old values); the counted waits saturate at vmcnt's 63
@@ -139,8 +142,8 @@ class Config:
             ops += [("amb0", "v"), ("amb1", "v"), ("bnb0", "v"), ("bnb1", "v")]
         else:
             ops += [(f"amb{i}", "v") for i in range(self.bm)] + [(f"bnb{j}", "v") for j in range(self.bn)]
-        epi = (["ew_base", "ew_s", "rb_even", "rb_odd", "gb"] + (["rb1", "gb1"] if self.bn % 2 else [])
-               if out == "bf16" else ["fw_base", "fw_s", "frb", "fgb"])
+        epi = (["ew_base", "ew_s", "rb_even", "rb_odd", "gb"] if out == "bf16"
+               else ["fw_base", "fw_s", "frb", "fgb"])
         if mx:
             # the epilogue's per-lane bases are formed from the lane id inside the statement, in
             # operand registers free by then (the scale registers leave too few for them as inputs)
@@ -493,34 +496,41 @@ class Gen:
         s, OP, e, c = SGPR, self.OP, self.emit, self.cfg
         e(f"s_mul_i32 {s['T']}, {OP['cm2']}, {32 * i + row}")
         e(f"s_add_u32 {s['T']}, {s['T']}, {OP['sw_epi']}")
-        if j0:
+        if j0 > 0:
             e(f"s_add_u32 {s['T']}, {s['T']}, {64 * j0}")
+        elif j0 < 0:
+            e(f"s_sub_u32 {s['T']}, {s['T']}, {-64 * j0}")
         e(f"v_add_u32 {c.vt2}, {s['T']}, {c.lane_value(lane_base)}")
 
     def by_half(self, body):
-        """body(pairs) for this wave's bf16 pass order: the right-half waves (wn = bit 11 of w1k)
-        take pairs_wn1 where it differs."""
+        """body(wn) for this wave's half of the tile's columns: the right-half waves (wn = bit 11
+        of w1k) run their own code where the two halves' passes differ (an odd block count)."""
         c, e = self.cfg, self.emit
-        if c.pairs_wn1 == c.pairs:
-            body(c.pairs)
+        if not c.joint:
+            body(0)
             return
         right, done = self.label("wn1_"), self.label("wndone")
         e(f"s_bitcmp1_b32 {self.OP['w1k']}, 11")
         e(f"s_cbranch_scc1 {right}")
-        body(c.pairs)
+        body(0)
         e(f"s_branch {done}")
         e(f"{right}:")
-        body(c.pairs_wn1)
+        body(1)
         e(f"{done}:")
 
+    # stores of a two-block pass: (row offset, read base index, read immediate); read-back k gives
+    # lane l row 8 k + l / 8, chunk l % 8 (rows 16.. at +2048 of the rows-0.. bases)
+    PAIR_STORES = [(8 * k, k % 2, 2048 if k >= 2 else 0) for k in range(4)]
+
     @staticmethod
-    def pass_stores(nblk):
-        """(row offset, read base index, read immediate, lane base) of a pass's stores: two-block
-        passes read rows 8 k + l / 8, chunk l % 8 (k = 0..3); one-block passes rows 16 k + l / 4,
-        chunk l % 4 (k = 0, 1)."""
-        if nblk == 2:
-            return [(8 * k, k % 2, 2048 if k >= 2 else 0, "gb") for k in range(4)]
-        return [(16 * k, 2, 2048 * k, "gb1") for k in range(2)]
+    def joint_stores(wn):
+        """The joint pass's stores of wave half wn: rows 0-15 (left) or 16-31 (right) of the shared
+        line, as (row offset, read base index, read immediate)."""
+        return Gen.PAIR_STORES[2 * wn:2 * wn + 2]
+
+    def joint_col(self, wn):
+        """First block of the shared line in this wave's column frame (the right half's is -1)."""
+        return self.cfg.bn - 1 if wn == 0 else -1
 
     def epilogue(self):
         if self.cfg.out != "bf16":
@@ -544,40 +554,75 @@ class Gen:
             e(f"v_add3_u32 v{waddr + cc}, v{tcvt}, {c.lane_value('ew_base')}, {s['EPI']}")
         e(f"v_add_u32 v{rbase}, {s['EPI']}, {c.lane_value('rb_even')}")
         e(f"v_add_u32 v{rbase + 1}, {s['EPI']}, {c.lane_value('rb_odd')}")
-        if c.bn % 2:
-            e(f"v_add_u32 v{rbase + 2}, {s['EPI']}, {c.lane_value('rb1')}")
         self.c_resource()
+        xw, xr = v0 + 70, v0 + 74        # joint pass: write and read addresses in the shared region
+        if c.joint:
+            # IB (free in the epilogue) = the shared region of this wave row: slot + 16 KiB +
+            # wm * 8 KiB, two 4 KiB buffers by m-block parity; T2 = its distance from EPI
+            e(f"s_and_b32 {s['T']}, {OP['w1k']}, 1024")
+            e(f"s_lshl_b32 {s['T']}, {s['T']}, 3")
+            e(f"s_add_u32 {s['IB']}, {OP['lds_base']}, {s['CS']}")
+            e(f"s_add_u32 {s['IB']}, {s['IB']}, {s['T']}")
+            e(f"s_add_u32 {s['IB']}, {s['IB']}, 16384")
+            e(f"s_sub_u32 {s['T2']}, {s['IB']}, {s['EPI']}")
+            e(f"v_add_u32 v{xr}, {s['IB']}, {c.lane_value('rb_even')}")
+            e(f"v_add_u32 v{xr + 1}, {s['IB']}, {c.lane_value('rb_odd')}")
 
-        def passes(pairs):
+        def block_to_lds(i, j, addr, off=0):
+            """Scale, round to bf16 and write block (i, j): lane (r, h) writes half h of chunks
+            addr[0..3] of row r."""
+            kind, base = c.acc(i, j)
+            for g in range(4):
+                src = []
+                for r in range(4):
+                    reg = base + 4 * g + r
+                    if kind == "a":
+                        e(f"v_accvgpr_read_b32 v{tacc + r}, a{reg}")
+                        src.append(f"v{tacc + r}")
+                    else:
+                        src.append(f"v{reg}")
+                for r in range(4):
+                    e(f"v_mul_f32 v{tmul + r}, {OP['alpha']}, {src[r]}")
+                e(f"v_cvt_pk_bf16_f32 v{tcvt}, v{tmul}, v{tmul + 1}")
+                e(f"v_cvt_pk_bf16_f32 v{tcvt + 1}, v{tmul + 2}, v{tmul + 3}")
+                e(f"ds_write_b64 v{addr[g]}, v[{tcvt}:{tcvt + 1}]" + (f" offset:{off}" if off else ""))
+
+        def passes(wn):
+            pairs = c.pairs_wn1 if wn else c.pairs
+            if c.joint:
+                # this half's chunks of the shared line: 0-3 (left) or 4-7 (right) of each row
+                for g in range(4):
+                    e(f"v_add_u32 v{xw + g}, {s['T2']}, v{waddr + 4 * wn + g}")
             npass = 0
             for i in range(c.bm):
+                if c.joint:
+                    off = 4096 * (i % 2)
+                    block_to_lds(i, c.joint_block[wn], [xw + g for g in range(4)], off)
+                    e("s_waitcnt lgkmcnt(0)")
+                    e("s_barrier")   # both halves' blocks of the shared line are in LDS
+                    dbase = dset[npass % 2]
+                    npass += 1
+                    stores = self.joint_stores(wn)
+                    for k, (_, rb, imm) in enumerate(stores):
+                        d = dbase + 4 * k
+                        e(f"ds_read_b128 v[{d}:{d + 3}], v{xr + rb} offset:{off + imm}")
+                    e("s_waitcnt lgkmcnt(0)")
+                    for k, (row, _, _) in enumerate(stores):
+                        d = dbase + 4 * k
+                        self.store_offset(i, row, self.joint_col(wn), "gb")
+                        e(f"buffer_store_dwordx4 v[{d}:{d + 3}], {c.vt2}, {s['RC']}, 0 offen nt")
                 for blocks in pairs:
                     dbase = dset[npass % 2]
                     npass += 1
                     for jj, j in enumerate(blocks):
-                        kind, base = c.acc(i, j)
-                        for g in range(4):
-                            src = []
-                            for r in range(4):
-                                reg = base + 4 * g + r
-                                if kind == "a":
-                                    e(f"v_accvgpr_read_b32 v{tacc + r}, a{reg}")
-                                    src.append(f"v{tacc + r}")
-                                else:
-                                    src.append(f"v{reg}")
-                            for r in range(4):
-                                e(f"v_mul_f32 v{tmul + r}, {OP['alpha']}, {src[r]}")
-                            e(f"v_cvt_pk_bf16_f32 v{tcvt}, v{tmul}, v{tmul + 1}")
-                            e(f"v_cvt_pk_bf16_f32 v{tcvt + 1}, v{tmul + 2}, v{tmul + 3}")
-                            e(f"ds_write_b64 v{waddr + 4 * jj + g}, v[{tcvt}:{tcvt + 1}]")
-                    stores = self.pass_stores(len(blocks))
-                    for k, (_, rb, off, _) in enumerate(stores):
+                        block_to_lds(i, j, [waddr + 4 * jj + g for g in range(4)])
+                    for k, (_, rb, imm) in enumerate(self.PAIR_STORES):
                         d = dbase + 4 * k
-                        e(f"ds_read_b128 v[{d}:{d + 3}], v{rbase + rb} offset:{off}")
+                        e(f"ds_read_b128 v[{d}:{d + 3}], v{rbase + rb} offset:{imm}")
                     e("s_waitcnt lgkmcnt(0)")
-                    for k, (row, _, _, lb) in enumerate(stores):
+                    for k, (row, _, _) in enumerate(self.PAIR_STORES):
                         d = dbase + 4 * k
-                        self.store_offset(i, row, blocks[0], lb)
+                        self.store_offset(i, row, blocks[0], "gb")
                         e(f"buffer_store_dwordx4 v[{d}:{d + 3}], {c.vt2}, {s['RC']}, 0 offen nt")
         self.by_half(passes)
         e(f"s_add_u32 {OP['vmt']}, {OP['vmt']}, {c.e_stores}")
@@ -587,8 +632,7 @@ class Gen:
         take them as operands), restating vark_wide.h's set-up: staging writes at row rl = l % 32,
         half hl = l / 32 (ew_base = 128 rl + 8 hl, ew_s = (rl / 2) % 8); read-back rows rr = l / 8,
         chunk rc = l % 8 (rb_even = 128 rr + 16 (rc ^ rs), rb_odd = 128 (8 + rr) + 16 (rc ^ rs ^ 4),
-        rs = rr / 2; gb = rr * cm2 + 16 rc) and, for a last single n-block, r1 = l / 4, c1 = l % 4
-        (rb1 = 128 r1 + 16 (c1 ^ rr), gb1 = r1 * cm2 + 16 c1)."""
+        rs = rr / 2; gb = rr * cm2 + 16 rc)."""
         c, e, OP = self.cfg, self.emit, self.OP
         if not c.lane_regs:
             return
@@ -616,14 +660,6 @@ class Gen:
         e(f"v_lshl_add_u32 {R['rb_odd']}, {t2}, 7, {t1}")
         e(f"v_mul_lo_u32 {t2}, {rr}, {OP['cm2']}")
         e(f"v_lshl_add_u32 {R['gb']}, {rc}, 4, {t2}")
-        if "rb1" in R:
-            e(f"v_lshrrev_b32 {t0}, 2, {ln}")
-            e(f"v_and_b32 {t1}, 3, {ln}")
-            e(f"v_xor_b32 {t2}, {t1}, {rr}")
-            e(f"v_lshlrev_b32 {t2}, 4, {t2}")
-            e(f"v_lshl_add_u32 {R['rb1']}, {t0}, 7, {t2}")
-            e(f"v_mul_lo_u32 {t2}, {t0}, {OP['cm2']}")
-            e(f"v_lshl_add_u32 {R['gb1']}, {t1}, 4, {t2}")
 
     def f32_store_offset(self, i, j, k):
         """vt2 = byte offset of this wave's tile rows 32 i + 8 k + l / 8, columns 32 j + 4 (l % 8)
@@ -734,11 +770,15 @@ class Gen:
         self.lane_values()
         self.c_resource()
 
-        def zeros(pairs):
+        def zeros(wn):
             for i in range(c.bm):
-                for blocks in pairs:
-                    for row, _, _, lb in self.pass_stores(len(blocks)):
-                        self.store_offset(i, row, blocks[0], lb)
+                if c.joint:
+                    for row, _, _ in self.joint_stores(wn):
+                        self.store_offset(i, row, self.joint_col(wn), "gb")
+                        e(f"buffer_store_dwordx4 v[{z}:{z + 3}], {c.vt2}, {SGPR['RC']}, 0 offen nt")
+                for blocks in (c.pairs_wn1 if wn else c.pairs):
+                    for row, _, _ in self.PAIR_STORES:
+                        self.store_offset(i, row, blocks[0], "gb")
                         e(f"buffer_store_dwordx4 v[{z}:{z + 3}], {c.vt2}, {SGPR['RC']}, 0 offen nt")
         self.by_half(zeros)
         e(f"s_add_u32 {self.OP['vmt']}, {self.OP['vmt']}, {c.e_stores}")

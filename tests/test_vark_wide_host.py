@@ -413,12 +413,18 @@ def _check(cfg, tiles, wave=0, stride_l=2880, stride_r=5760, stride_cm=5760, OUT
         sw = (32 * cfg.bm * (wave & 1) * stride_cm + 32 * cfg.bn * (wave >> 1)) * cbytes
         want_st = []
         if cfg.out == "bf16":
-            # the right-half waves' passes start with the single block (line-aligned pairs)
+            # line-aligned pairs per wave half; with an odd block count the shared line's rows 0-15
+            # (left half) or 16-31 (right half), from block bn - 1 / -1 of the wave's columns
+            wn = wave >> 1
+            gb = cfg.lane_regs.get("gb") or op("gb")
             for i in range(cfg.bm):
-                for blocks in (cfg.pairs_wn1 if wave >> 1 else cfg.pairs):
-                    for row, _, _, lb in GEN.Gen.pass_stores(len(blocks)):
-                        want_st.append((sw + (32 * i + row) * 2 * stride_cm + 64 * blocks[0],
-                                        cfg.lane_regs.get(lb) or op(lb)))
+                if cfg.joint:
+                    j0 = cfg.bn - 1 if wn == 0 else -1
+                    for row, _, _ in GEN.Gen.joint_stores(wn):
+                        want_st.append((sw + (32 * i + row) * 2 * stride_cm + 64 * j0, gb))
+                for blocks in (cfg.pairs_wn1 if wn else cfg.pairs):
+                    for row, _, _ in GEN.Gen.PAIR_STORES:
+                        want_st.append((sw + (32 * i + row) * 2 * stride_cm + 64 * blocks[0], gb))
         elif not (cfg.out == "f32acc" and S == 0):
             for i in range(cfg.bm):
                 for j in range(cfg.bn):
@@ -590,45 +596,71 @@ def _phys(r, cc):
 
 
 def test_epilogue_staging_and_store_coverage():
-    """Writes (row l % 32, chunk 4 jj + g, half l / 32) and read-backs (two-block passes: row
-    8 k + l / 8, chunk l % 8; one-block passes: row 16 k + l / 4, chunk l % 4) address the same
-    swizzled layout, each 16-byte chunk once, conflict-free (16 lanes per 8-byte write cycle, 8
-    lanes per 16-byte read cycle); the stores then cover the 32 x 64 (32 x 32) piece."""
-    for nblk in (2, 1):
-        writes = {}
-        for jj in range(nblk):
-            for g in range(4):
-                for lane in range(64):
-                    rl, hl = lane & 31, lane >> 5
-                    ew_base, ew_s = rl * 128 + 8 * hl, (rl >> 1) & 7
-                    addr = ew_base + (((4 * jj + g) ^ ew_s) << 4)
-                    assert addr == _phys(rl, 4 * jj + g) + 8 * hl
-                    writes[addr] = (rl, 32 * jj + 8 * g + 4 * hl)     # row, first column of 4
-                for q in range(4):
-                    banks = {(((lane & 31) * 128 + ((((4 * jj + g) ^ (((lane & 31) >> 1) & 7)) << 4))
-                               + 8 * (lane >> 5)) // 8) % 32 for lane in range(16 * q, 16 * q + 16)}
-                    assert len(banks) == 16
-        assert len(writes) == 32 * 8 * nblk
-        cover = set()
-        for k, (row, rb, off, lb) in enumerate(GEN.Gen.pass_stores(nblk)):
-            addrs = []
+    """Writes (row l % 32, chunk 4 jj + g, half l / 32) and read-backs (row 8 k + l / 8, chunk
+    l % 8) address the same swizzled layout, each 16-byte chunk once, conflict-free (16 lanes per
+    8-byte write cycle, 8 lanes per 16-byte read cycle); the stores then cover the 32 x 64 piece."""
+    writes = {}
+    for jj in range(2):
+        for g in range(4):
             for lane in range(64):
-                if nblk == 2:
-                    rr, rc, rs = lane >> 3, lane & 7, ((lane >> 3) >> 1) & 7
-                    base = (rr * 128 + 16 * (rc ^ rs)) if rb == 0 else ((8 + rr) * 128 + 16 * (rc ^ (rs ^ 4)))
-                    r, cc = row + rr, rc
-                else:
-                    r1, c1 = lane >> 2, lane & 3
-                    base = r1 * 128 + 16 * (c1 ^ ((r1 >> 1) & 7))
-                    r, cc = row + r1, c1
-                addr = base + off
-                assert addr == _phys(r, cc)
-                assert writes[addr] == (r, 8 * cc) and writes[addr + 8] == (r, 8 * cc + 4)
-                cover.add((r, cc))
-                addrs.append(addr)
-            for q in range(8):
-                assert len({(a // 16) % 16 for a in addrs[8 * q:8 * q + 8]}) == 8   # 16-byte bank groups
-        assert cover == {(r, cc) for r in range(32) for cc in range(4 * nblk)}
+                rl, hl = lane & 31, lane >> 5
+                ew_base, ew_s = rl * 128 + 8 * hl, (rl >> 1) & 7
+                addr = ew_base + (((4 * jj + g) ^ ew_s) << 4)
+                assert addr == _phys(rl, 4 * jj + g) + 8 * hl
+                writes[addr] = (rl, 32 * jj + 8 * g + 4 * hl)     # row, first column of 4
+            for q in range(4):
+                banks = {(((lane & 31) * 128 + ((((4 * jj + g) ^ (((lane & 31) >> 1) & 7)) << 4))
+                           + 8 * (lane >> 5)) // 8) % 32 for lane in range(16 * q, 16 * q + 16)}
+                assert len(banks) == 16
+    assert len(writes) == 32 * 8 * 2
+    cover = set()
+    for k, (row, rb, off) in enumerate(GEN.Gen.PAIR_STORES):
+        addrs = []
+        for lane in range(64):
+            rr, rc, rs = lane >> 3, lane & 7, ((lane >> 3) >> 1) & 7
+            base = (rr * 128 + 16 * (rc ^ rs)) if rb == 0 else ((8 + rr) * 128 + 16 * (rc ^ (rs ^ 4)))
+            r, cc = row + rr, rc
+            addr = base + off
+            assert addr == _phys(r, cc)
+            assert writes[addr] == (r, 8 * cc) and writes[addr + 8] == (r, 8 * cc + 4)
+            cover.add((r, cc))
+            addrs.append(addr)
+        for q in range(8):
+            assert len({(a // 16) % 16 for a in addrs[8 * q:8 * q + 8]}) == 8   # 16-byte bank groups
+    assert cover == {(r, cc) for r in range(32) for cc in range(8)}
+
+
+@pytest.mark.parametrize("cfg", [n for n, c in CFGS.items() if c.out == "bf16" and c.joint])
+def test_epilogue_joint_line(cfg):
+    """The line two wave halves share: the left half writes its block bn - 1 into chunks 0-3 of the
+    common region's rows, the right half its block 0 into chunks 4-7 (the pass's write addresses of
+    jj = 0 / 1); after the barrier the left half reads rows 0-15 and the right half rows 16-31 with
+    the pair read-back, so every row of the line -- columns 32 (bn - 1) .. 32 bn + 31 of the left
+    half's frame, i.e. tile columns 32 bn - 32 .. 32 bn + 31 -- is stored whole, once, by one wave,
+    at the column the store offset names (block bn - 1 for the left half, block -1 for the right)."""
+    c = CFGS[cfg]
+    region = {}
+    for wn, jj, blk in ((0, 0, c.bn - 1), (1, 1, 0)):
+        for g in range(4):
+            for lane in range(64):
+                rl, hl = lane & 31, lane >> 5
+                addr = rl * 128 + 8 * hl + (((4 * jj + g) ^ ((rl >> 1) & 7)) << 4)
+                col = 32 * c.bn * wn + 32 * blk + 8 * g + 4 * hl        # tile column of 4 values
+                assert addr not in region
+                region[addr] = (rl, col)
+    stored = {}
+    for wn in range(2):
+        j0 = c.bn - 1 if wn == 0 else -1
+        for row, rb, off in GEN.Gen.joint_stores(wn):
+            for lane in range(64):
+                rr, rc, rs = lane >> 3, lane & 7, ((lane >> 3) >> 1) & 7
+                base = (rr * 128 + 16 * (rc ^ rs)) if rb == 0 else ((8 + rr) * 128 + 16 * (rc ^ (rs ^ 4)))
+                r = row + rr
+                gcol = 32 * c.bn * wn + 32 * j0 + 8 * rc          # where the store puts the chunk
+                assert region[base + off] == (r, gcol) and region[base + off + 8] == (r, gcol + 4)
+                assert (r, gcol) not in stored
+                stored[(r, gcol)] = wn
+    assert set(stored) == {(r, 32 * c.bn - 32 + 8 * q) for r in range(32) for q in range(8)}
 
 
 def test_epilogue_f32_staging_and_store_coverage():
@@ -787,8 +819,7 @@ def test_mx_epilogue_lane_values(stride_cm):
         rs = (rr >> 1) & 7
         r1, c1 = lane >> 2, lane & 3
         want = dict(ew_base=rl * 128 + 8 * hl, ew_s=(rl >> 1) & 7, rb_even=rr * 128 + 16 * (rc ^ rs),
-                    rb_odd=(8 + rr) * 128 + 16 * (rc ^ (rs ^ 4)), gb=(rr * stride_cm + 8 * rc) * 2,
-                    rb1=r1 * 128 + 16 * (c1 ^ ((r1 >> 1) & 7)), gb1=(r1 * stride_cm + 8 * c1) * 2)
+                    rb_odd=(8 + rr) * 128 + 16 * (rc ^ (rs ^ 4)), gb=(rr * stride_cm + 8 * rc) * 2)
         assert got[lane] == want, lane
 
 
@@ -805,17 +836,57 @@ def test_mx_lane_value_registers_are_free():
 
 
 @pytest.mark.parametrize("cfg", [n for n, c in CFGS.items() if c.out == "bf16"])
-def test_bf16_two_block_passes_store_whole_lines(cfg):
-    """Every two-block bf16 pass of every wave stores 128-byte row pieces that start on a 128-byte
-    boundary of the tile row (a C row starts on one at the MoE shapes), so only the line shared by
-    the left and right half of an odd block count is written in two pieces."""
+def test_bf16_stores_whole_lines(cfg):
+    """Every bf16 store writes 128-byte row pieces starting on a 128-byte boundary of the tile row
+    (a C row starts on one at the MoE shapes): the pairs of each wave half and the joint pass's
+    shared line; together they cover each wave's blocks once."""
     c = CFGS[cfg]
     for wn in range(2):
-        for blocks in (c.pairs_wn1 if wn else c.pairs):
-            start = 2 * (32 * c.bn * wn + 32 * blocks[0])          # bytes into the tile row
-            if len(blocks) == 2:
-                assert start % 128 == 0, (wn, blocks)
-            else:
-                assert start % 64 == 0
+        starts = [2 * (32 * c.bn * wn + 32 * blocks[0]) for blocks in (c.pairs_wn1 if wn else c.pairs)]
+        if c.joint:
+            starts.append(2 * (32 * c.bn * wn + 32 * (c.bn - 1 if wn == 0 else -1)))
+        assert all(x % 128 == 0 for x in starts), (wn, starts)
         got = sorted(j for blocks in (c.pairs_wn1 if wn else c.pairs) for j in blocks)
-        assert got == list(range(c.bn))
+        got += [c.joint_block[wn]] if c.joint else []
+        assert sorted(got) == list(range(c.bn))
+
+
+@pytest.mark.parametrize("cfg", [n for n, c in CFGS.items() if c.out == "bf16" and c.joint])
+@pytest.mark.parametrize("wave", range(4))
+def test_epilogue_joint_region_ordering(cfg, wave):
+    """The common region is written by one wave and read by another, so in each wave's program:
+    an m-block's joint writes complete (lgkmcnt(0)) and a barrier follows before its joint reads;
+    a buffer (m-block parity) is written again only after a barrier that follows this wave's reads
+    of it -- the partner passes the same barriers, so its reads are done too."""
+    c = CFGS[cfg]
+    ev, spans, _ = _run_tiles(c, [(0, 0, 0, 0, 100)], wave)
+    a, b = spans[0]
+    v0 = c.vop0
+    xw = {f"v{v0 + 70 + g}" for g in range(4)}
+    xr = {f"v{v0 + 74 + k}" for k in range(2)}
+
+    def off(arg):
+        m = re.search(r"offset:(\d+)", arg)
+        return int(m.group(1)) if m else 0
+    seq = []
+    for i in range(a, b):
+        e = ev[i]
+        if e[0] == "ds_write_b64" and e[1][0].split()[0] in xw:
+            seq.append(("w", off(e[1][-1]) // 4096, i))
+        elif e[0] == "ds_read_b128" and e[1][1].split()[0] in xr:
+            seq.append(("r", (off(e[1][1]) % 8192) // 4096, i))
+        elif e[0] in ("barrier", "lgkmcnt"):
+            seq.append((e[0], e[1] if e[0] == "lgkmcnt" else None, i))
+    writes = [x for x in seq if x[0] == "w"]
+    reads = [x for x in seq if x[0] == "r"]
+    assert len(writes) == 4 * c.bm and len(reads) == 2 * c.bm
+    for blk in range(c.bm):
+        w = writes[4 * blk:4 * blk + 4]
+        r = reads[2 * blk:2 * blk + 2]
+        assert {x[1] for x in w} == {blk % 2} and {x[1] for x in r} == {blk % 2}
+        between = [x for x in seq if w[-1][2] < x[2] < r[0][2]]
+        kinds = [x[0] for x in between]
+        assert "barrier" in kinds and ("lgkmcnt", 0) in [(x[0], x[1]) for x in between[:kinds.index("barrier")]]
+        if blk + 2 < c.bm:
+            nxt = writes[4 * (blk + 2)]
+            assert any(x[0] == "barrier" and r[-1][2] < x[2] < nxt[2] for x in seq)
