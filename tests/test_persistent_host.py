@@ -393,3 +393,61 @@ def test_persistent_code_object_instructions(pkg, co_path):
             assert ins[k + 1].startswith("buffer_load_dwordx4") and ins[k + 1].rstrip().endswith("lds"), ins[k + 1]
             n_dma += 1
     assert n_dma >= 8
+
+
+def test_pair_epilogue_map_at_tn384():
+    """The TN = 384 epilogue (persistent_kernel.h, kPairEpi): waves wn = 2P, 2P + 1 stage their
+    48 x 96 bf16 block of a pass in the region of pair (wm, P), chunk c of 384-byte row r at
+    c ^ pswz(r); after the barrier wave half h reads rows 24 h .. 24 h + 23 and stores them. Every
+    element of the tile's pass is read back from where it was staged and stored exactly once, each
+    group of 8 consecutive lanes stores one whole 128-byte line (64 columns starting at a multiple
+    of 64), the four regions fill the slot, and the LDS accesses are conflict-free: 8 lanes of a
+    16-byte read hit 8 distinct chunks, 16 lanes of an 8-byte write 16 distinct 8-byte units of a
+    256-byte bank window."""
+    row, chunks, region = 384, 24, 48 * 384
+    pswz = lambda r: (r & 7) ^ ((r >> 3) & 1)
+    assert 4 * region == (TILE_M + 384) * 128
+    for p in range(2):
+        staged, stored = {}, {}
+        for wave in range(8):
+            wm, wn = wave & 1, wave >> 1
+            h, base = wn & 1, (2 * wm + (wn >> 1)) * region
+            for ii in range(3):
+                for j in range(6):
+                    addrs = []
+                    for lane in range(64):
+                        s16, q = lane & 15, lane >> 4
+                        r = ii * 16 + s16
+                        c = 12 * h + 2 * j + (q >> 1)
+                        addr = base + r * row + 16 * (c ^ pswz(r)) + 8 * (q & 1)
+                        m = wm * 96 + 48 * p + r
+                        n = wn * 96 + 16 * j + 4 * q            # first of the lane's 4 columns
+                        assert addr not in staged
+                        staged[addr] = (m, n)
+                        addrs.append(addr)
+                    for g in range(4):
+                        units = {(a // 8) % 32 for a in addrs[16 * g:16 * g + 16]}
+                        assert len(units) == 16
+        for wave in range(8):
+            wm, wn = wave & 1, wave >> 1
+            h, base = wn & 1, (2 * wm + (wn >> 1)) * region
+            for k in range(24 * chunks // 64):
+                addrs = []
+                for el in range(64):
+                    f = 64 * k + el
+                    r, c = 24 * h + f // chunks, f % chunks
+                    addr = base + r * row + 16 * (c ^ pswz(r))
+                    m = wm * 96 + 48 * p + r
+                    n = (wn >> 1) * 192 + 8 * c
+                    assert staged[addr] == (m, n) and staged[addr + 8] == (m, n + 4)
+                    assert (m, n) not in stored
+                    stored[(m, n)] = wave
+                    addrs.append((addr, m, n))
+                for g in range(8):
+                    grp = addrs[8 * g:8 * g + 8]
+                    assert len({a // 16 for a, _, _ in grp}) == 8 and len({(a // 16) % 8 for a, _, _ in grp}) == 8
+                    assert len({m for _, m, _ in grp}) == 1
+                    ns = sorted(n for _, _, n in grp)
+                    assert ns[0] % 64 == 0 and ns == [ns[0] + 8 * i for i in range(8)]
+        want = {(wm * 96 + 48 * p + r, n) for wm in range(2) for r in range(48) for n in range(0, 384, 8)}
+        assert set(stored) == want
