@@ -95,16 +95,11 @@ __device__ __forceinline__ int dma_base(int wave, int lane, int stride) {
   return (8 * wave + (lane >> 3)) * stride + 16 * dma_chunk(wave, lane);
 }
 
-// Epilogue at TN = 384: a wave pair's 48 x 192 bf16 per pass (384-byte rows of 24 chunks) in one
-// of four regions that fill the freed 72 KiB slot; chunk c of row r at c ^ pswz(r), a permutation
-// inside each 8-chunk line, distinct for rows r and r + 8 (16 lanes write one chunk column).
+// Epilogue at TN = 384: whole-line stores through wave-pair regions (epilogue_pairs).
 template <int kTN>
 constexpr bool kPairEpi = kTN == 384;
-constexpr int kPairRow = 384, kPairChunks = kPairRow / 16, kPairRegion = 48 * kPairRow;
-constexpr int kPairReads = 24 * kPairChunks / 64;
 static_assert(4 * kPairRegion == Cfg2<384>::kSlot && kPairReads == Cfg<384>::EpiReads,
               "pair staging fills the slot; the same stores per wave as the per-wave epilogue");
-__device__ __forceinline__ int pswz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 // One operand block of 16 rows: the low 16 bytes at lo, the high 16 at hi (= lo ^ 16).
 __device__ __forceinline__ v8i read_nt(const GG_LDS uint8_t* lo, const GG_LDS uint8_t* hi) {
@@ -350,42 +345,8 @@ __device__ __forceinline__ void persistent_body(const Args& a, GG_LDS uint8_t* l
     uint16_t* cbase = a.c + (int64_t)T.row_base * a.stride_cm;
     const int m_end = T.m0 + T.rows;
     if constexpr (kPairEpi<kTN>) {
-      // Wave pairs (wn = 2P, 2P + 1) hold 96 + 96 columns of the same rows: 384 bytes, three whole
-      // 128-byte lines of a C row (a row of the tile starts on a line at N % 384 == 0 with 16-byte
-      // aligned strides), where one wave's 192 bytes would start or end mid-line. Per pass both
-      // waves stage their 48 x 96 block in the pair's region of the freed slot (row r at 384 r,
-      // 16-byte chunk c of the pair row at c ^ pswz(r)); after a barrier each stores half of the
-      // rows (h = wn & 1: rows 24 h .. 24 h + 23), eight lanes per line; a second barrier frees the
-      // region for the next pass.
-      const int h = wn & 1;
-      GG_LDS uint8_t* prg = lds + (cur ^ 1) * C2::kSlot + (2 * wm + (wn >> 1)) * kPairRegion;
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        if (p) lds_barrier();   // the pass-0 reads of the region are done in both waves
-#pragma unroll
-        for (int ii = 0; ii < 3; ++ii) {
-          const int r = ii * 16 + s16;
-#pragma unroll
-          for (int j = 0; j < NB; ++j) {
-            const v4f v = acc[3 * p + ii][j];
-            const v2i pk = v2i{(int)(f32_to_bf16_rne(v[0] * alpha) | (f32_to_bf16_rne(v[1] * alpha) << 16)),
-                               (int)(f32_to_bf16_rne(v[2] * alpha) | (f32_to_bf16_rne(v[3] * alpha) << 16))};
-            const int c = 12 * h + 2 * j + (q >> 1);
-            *(GG_LDS v2i*)(prg + r * kPairRow + 16 * (c ^ pswz(r)) + 8 * (q & 1)) = pk;
-          }
-        }
-        lds_barrier();          // both halves of every pair row are staged
-#pragma unroll
-        for (int k = 0; k < kPairReads; ++k) {
-          const int f = k * 64 + el;
-          const int r = 24 * h + f / kPairChunks;
-          const int c = f - (f / kPairChunks) * kPairChunks;
-          const v4i v = *(const GG_LDS v4i*)(prg + r * kPairRow + 16 * (c ^ pswz(r)));
-          const int m = T.m0 + wm * kWaveM + 48 * p + r;
-          const int n = T.n0 + (wn >> 1) * 2 * C::WaveN + 8 * c;
-          if (m < m_end && n < a.N) store_c16(cbase + (int64_t)m * a.stride_cm + n, v);
-        }
-      }
+      epilogue_pairs<NB>(acc, alpha, lds + (cur ^ 1) * C2::kSlot, cbase, a.stride_cm, T.m0, m_end, T.n0, a.N, wm, wn,
+                         s16, q, el);
       full_prev = T.rows == kTileM && T.n0 + kTN <= a.N;
       t = t_next;
       T = N;

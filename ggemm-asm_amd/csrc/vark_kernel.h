@@ -210,6 +210,57 @@ __device__ __forceinline__ void dma16(v4i rsrc, uint32_t lds_addr, int voff) {
 // trail it by two wait states on gfx950, which the compiler inserts only for stores it emits.
 __device__ __forceinline__ void store_c16(uint16_t* p, v4i v) { __builtin_nontemporal_store(v, (v4i*)p); }
 
+// bf16 epilogue of a 192 x 384 tile with whole-line stores (both 512-thread kernels at TN = 384).
+// Lane (s16, q) of wave (wm, wn) holds C[m][n..n+3] for m = 96 wm + 16 i + s16 and n = 96 wn +
+// 16 j + 4 q (i, j = 0..5) of the tile. A wave's 96 columns are 192 bytes of a C row, starting or
+// ending mid-line; waves wn = 2P, 2P + 1 together hold 384 bytes, three whole 128-byte lines (a
+// tile row starts on a line with N % 384 == 0 and 16-byte aligned strides). Per pass of 48 rows
+// both waves of a pair stage their block in the pair's 18 KiB region of the freed 72 KiB slot
+// (row r at 384 r, 16-byte chunk c of the pair row at c ^ pswz(r), a permutation inside each
+// 8-chunk line that separates rows r and r + 8); after a barrier wave half h = wn & 1 stores rows
+// 24 h .. 24 h + 23, eight lanes per line; a second barrier frees the region for the next pass.
+// Stores per wave: 2 x kPairReads, the same as the per-wave epilogue. Rows from m_end and columns
+// from n_end on are not stored.
+constexpr int kPairRow = 384, kPairChunks = kPairRow / 16, kPairRegion = 48 * kPairRow;
+constexpr int kPairReads = 24 * kPairChunks / 64;
+__device__ __forceinline__ int pswz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+template <int NB>
+__device__ __forceinline__ void epilogue_pairs(const v4f (&acc)[kMB][NB], float alpha, GG_LDS uint8_t* slot,
+                                               uint16_t* c, int stride_cm, int m0, int m_end, int n0, int n_end,
+                                               int wm, int wn, int s16, int q, int el) {
+  static_assert(NB == 6 && 4 * kPairRegion == kLhsBytes + kKStep * 384, "pair staging fills a 384-wide slot");
+  const int h = wn & 1;
+  GG_LDS uint8_t* prg = slot + (2 * wm + (wn >> 1)) * kPairRegion;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    if (p) lds_barrier();   // the pass-0 reads of the region are done in both waves
+#pragma unroll
+    for (int ii = 0; ii < 3; ++ii) {
+      const int r = ii * 16 + s16;
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const v4f v = acc[3 * p + ii][j];
+        const v2i pk = v2i{(int)(f32_to_bf16_rne(v[0] * alpha) | (f32_to_bf16_rne(v[1] * alpha) << 16)),
+                           (int)(f32_to_bf16_rne(v[2] * alpha) | (f32_to_bf16_rne(v[3] * alpha) << 16))};
+        const int ch = 12 * h + 2 * j + (q >> 1);
+        *(GG_LDS v2i*)(prg + r * kPairRow + 16 * (ch ^ pswz(r)) + 8 * (q & 1)) = pk;
+      }
+    }
+    lds_barrier();          // both halves of every pair row are staged
+#pragma unroll
+    for (int k = 0; k < kPairReads; ++k) {
+      const int f = k * 64 + el;
+      const int r = 24 * h + f / kPairChunks;
+      const int ch = f - (f / kPairChunks) * kPairChunks;
+      const v4i v = *(const GG_LDS v4i*)(prg + r * kPairRow + 16 * (ch ^ pswz(r)));
+      const int m = m0 + wm * kWaveM + 48 * p + r;
+      const int n = n0 + (wn >> 1) * 192 + 8 * ch;
+      if (m < m_end && n < n_end) store_c16(c + (int64_t)m * stride_cm + n, v);
+    }
+  }
+}
+
 __device__ __forceinline__ uint32_t lds_u32(const GG_LDS void* p) {
   return (uint32_t)reinterpret_cast<uintptr_t>(p);
 }
@@ -926,6 +977,11 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
       int el = lane;
       asm volatile("" : "+v"(el));
       uint16_t* cg = static_cast<uint16_t*>(a.out) + (int64_t)T.g * a.stride_cg;
+      if constexpr (kTN == 384) {
+        // whole-line stores through wave-pair regions of the freed slot
+        epilogue_pairs<NB>(acc, alpha, cur ? lm.L[0] : lm.L[1], cg, a.stride_cm, T.m0, a.OUT_M, T.n0, a.OUT_N,
+                           wm, wn, s16, q, el);
+      } else {
   #pragma unroll
       for (int p = 0; p < 2; ++p) {
   #pragma unroll
@@ -951,6 +1007,7 @@ __device__ __forceinline__ void vark_body(const VarKArgs& a, GG_LDS uint8_t* lds
           if ((C::EpiReads * 64 == 48 * C::EpiChunks || f < 48 * C::EpiChunks) && m < a.OUT_M && n < a.OUT_N)
             store_c16(cg + (int64_t)m * a.stride_cm + n, v);
         }
+      }
       }
       full_prev = T.m0 + kTileM <= a.OUT_M && T.n0 + kTN <= a.OUT_N;
     }
