@@ -106,6 +106,38 @@ __device__ __forceinline__ void load8(const void* x, int64_t row, int64_t stride
   }
 }
 
+// Row and 16-byte chunk of the kUnroll chunks a thread streams per round: flat chunk index
+// i0 + u T (T = threads in the grid) split as (row, chunk) once, then advanced by kUnroll T per round
+// with adds and one compare, instead of a 64-bit division per chunk.
+struct ChunkWalk {
+  int64_t row[kUnroll];
+  int col[kUnroll];
+  int64_t drow;
+  int dcol, cpr;
+  __device__ __forceinline__ ChunkWalk(int64_t i_first, int64_t T, int cpr_) : cpr(cpr_) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = i_first + u * T;
+      row[u] = i / cpr;
+      col[u] = (int)(i - row[u] * cpr);
+    }
+    const int64_t step = kUnroll * T;
+    drow = step / cpr;
+    dcol = (int)(step - drow * cpr);
+  }
+  __device__ __forceinline__ void advance() {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      col[u] += dcol;
+      row[u] += drow;
+      if (col[u] >= cpr) {
+        col[u] -= cpr;
+        ++row[u];
+      }
+    }
+  }
+};
+
 // ---------------------------------------------------------------------------------- amax
 
 __global__ void __launch_bounds__(64) amax_init(uint32_t* amax_bits) {
@@ -121,14 +153,14 @@ __global__ void __launch_bounds__(kThreads) amax_kernel(const void* x, int64_t r
   const int64_t n = rows * cpr;
   const int64_t T = (int64_t)gridDim.x * kThreads;
   uint32_t m = 0;
+  const int64_t i_first = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  ChunkWalk cw(i_first, T, cpr);
   // kUnroll chunks per thread and round: their loads are all in flight before the first is used
-  for (int64_t i0 = (int64_t)blockIdx.x * kThreads + threadIdx.x; i0 < n; i0 += kUnroll * T) {
+  for (int64_t i0 = i_first; i0 < n; i0 += kUnroll * T, cw.advance()) {
     float v[kUnroll][8];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int64_t i = i0 + u * T;
-      const int64_t row = i / cpr;
-      if (i < n) load8<kF32>(x, row, stride, (int)(i - row * cpr), v[u]);
+      if (i0 + u * T < n) load8<kF32>(x, cw.row[u], stride, cw.col[u], v[u]);
       else for (int k = 0; k < 8; ++k) v[u][k] = 0.0f;
     }
 #pragma unroll
@@ -156,38 +188,72 @@ __device__ __forceinline__ float tensor_scale(uint32_t amax_bits) {
   return amax > 0.0f ? amax / fmax_of<kE5M2>() : (amax == 0.0f ? 1.0f : amax);   // NaN stays NaN
 }
 
+// x / scale, correctly rounded, computed as q = x y (y = fl(1 / scale)) corrected by one FMA
+// residual: by Markstein's theorem fl(q + fl(x - q scale) y) is the correctly rounded quotient when y
+// is the correctly rounded reciprocal and nothing over- or underflows. With amax finite and at least
+// 2^-60 the scale and y are normal and |q| stays near fmax at most (|x| <= amax); an x small enough
+// for the residual to underflow (|x| < 2^-102) has a quotient below 2^-26, which fp8 rounds to zero
+// either way. Zero keeps the sign of x. Other amax (NaN, infinite, zero, below 2^-60) take the
+// division itself, decided once per kernel (fast is uniform).
+struct ScaleDiv {
+  float scale, inv;
+  bool fast;
+};
+template <bool kE5M2>
+__device__ __forceinline__ ScaleDiv scale_div(uint32_t amax_bits) {
+  const float amax = __uint_as_float(amax_bits);
+  const float scale = tensor_scale<kE5M2>(amax_bits);
+  return ScaleDiv{scale, 1.0f / scale, amax >= 0x1p-60f && amax <= 3.4028235e38f};   // false for NaN
+}
+template <bool kFast>
+__device__ __forceinline__ float div_scale(float x, const ScaleDiv& d) {
+  if constexpr (kFast) {
+    const float q = x * d.inv;
+    const float r = __builtin_fmaf(-q, d.scale, x);
+    const float c = __builtin_fmaf(r, d.inv, q);
+    return __uint_as_float((__float_as_uint(c) & 0x7fffffffu) | (__float_as_uint(x) & 0x80000000u));
+  } else {
+    return x / d.scale;
+  }
+}
+
+template <bool kF32, bool kE5M2, bool kFast>
+__device__ __forceinline__ void tensorwise_body(const void* x, int64_t rows, int cols, int64_t stride, uint8_t* out,
+                                                int64_t out_stride, const ScaleDiv& d) {
+  const int cpr = cols / 8;
+  const int64_t n = rows * cpr;
+  const int64_t T = (int64_t)gridDim.x * kThreads;
+  const int64_t i_first = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  ChunkWalk cw(i_first, T, cpr);
+  for (int64_t i0 = i_first; i0 < n; i0 += kUnroll * T, cw.advance()) {
+    float v[kUnroll][8];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      if (i0 + u * T < n) load8<kF32>(x, cw.row[u], stride, cw.col[u], v[u]);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (i0 + u * T >= n) break;
+      float y[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) y[k] = clamp_fmax<kE5M2>(div_scale<kFast>(v[u][k], d));
+      const uint32_t w0 = pack4_fp8<kE5M2>(y[0], y[1], y[2], y[3]);
+      const uint32_t w1 = pack4_fp8<kE5M2>(y[4], y[5], y[6], y[7]);
+      *(v2u*)(out + cw.row[u] * out_stride + 8 * (int64_t)cw.col[u]) = v2u{w0, w1};
+    }
+  }
+}
+
 template <bool kF32, bool kE5M2>
 __global__ void __launch_bounds__(kThreads) quant_tensorwise_kernel(const void* x, int64_t rows, int cols,
                                                                     int64_t stride, uint8_t* out,
                                                                     int64_t out_stride, const uint32_t* amax_bits,
                                                                     float* scale_out) {
-  const float scale = tensor_scale<kE5M2>(*amax_bits);
-  if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
-  const int cpr = cols / 8;
-  const int64_t n = rows * cpr;
-  const int64_t T = (int64_t)gridDim.x * kThreads;
-  for (int64_t i0 = (int64_t)blockIdx.x * kThreads + threadIdx.x; i0 < n; i0 += kUnroll * T) {
-    float v[kUnroll][8];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t i = i0 + u * T;
-      const int64_t row = i / cpr;
-      if (i < n) load8<kF32>(x, row, stride, (int)(i - row * cpr), v[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int64_t i = i0 + u * T;
-      if (i >= n) break;
-      const int64_t row = i / cpr;
-      const int c = (int)(i - row * cpr);
-      float y[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) y[k] = clamp_fmax<kE5M2>(v[u][k] / scale);
-      const uint32_t w0 = pack4_fp8<kE5M2>(y[0], y[1], y[2], y[3]);
-      const uint32_t w1 = pack4_fp8<kE5M2>(y[4], y[5], y[6], y[7]);
-      *(v2u*)(out + row * out_stride + 8 * (int64_t)c) = v2u{w0, w1};
-    }
-  }
+  const ScaleDiv d = scale_div<kE5M2>(*amax_bits);
+  if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = d.scale;
+  if (d.fast)
+    tensorwise_body<kF32, kE5M2, true>(x, rows, cols, stride, out, out_stride, d);
+  else
+    tensorwise_body<kF32, kE5M2, false>(x, rows, cols, stride, out, out_stride, d);
 }
 
 // ---------------------------------------------------------------------------------- tensorwise + transpose
@@ -205,14 +271,10 @@ __global__ void __launch_bounds__(kThreads) quant_tensorwise_kernel(const void* 
 constexpr int kTT = 128;                    // transpose tile edge (elements)
 constexpr int kTTPitch = kTT + 4;           // LDS row pitch in bytes
 
-template <bool kF32, bool kE5M2>
-__global__ void __launch_bounds__(kThreads) quant_transpose_kernel(const void* x, int batch, int rows, int cols,
-                                                                   uint8_t* out, int64_t out_stride, uint8_t* out_t,
-                                                                   int64_t out_t_stride, const uint32_t* amax_bits,
-                                                                   float* scale_out) {
-  __shared__ uint8_t s_t[kTT * kTTPitch];
-  const float scale = tensor_scale<kE5M2>(*amax_bits);
-  if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
+template <bool kF32, bool kE5M2, bool kFast>
+__device__ __forceinline__ void transpose_body(const void* x, int batch, int rows, int cols, uint8_t* out,
+                                               int64_t out_stride, uint8_t* out_t, int64_t out_t_stride,
+                                               const ScaleDiv& d, uint8_t* s_t) {
   const int tid = threadIdx.x;
   const int tr = tid >> 3;                  // first tile row (then + 32, + 64, + 96)
   const int tc = 16 * (tid & 7);            // first tile column of this thread's segments
@@ -241,9 +303,10 @@ __global__ void __launch_bounds__(kThreads) quant_transpose_kernel(const void* x
       uint32_t w[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        w[k] = pack4_fp8<kE5M2>(clamp_fmax<kE5M2>(v[h][4 * k] / scale), clamp_fmax<kE5M2>(v[h][4 * k + 1] / scale),
-                                clamp_fmax<kE5M2>(v[h][4 * k + 2] / scale),
-                                clamp_fmax<kE5M2>(v[h][4 * k + 3] / scale));
+        w[k] = pack4_fp8<kE5M2>(clamp_fmax<kE5M2>(div_scale<kFast>(v[h][4 * k], d)),
+                                clamp_fmax<kE5M2>(div_scale<kFast>(v[h][4 * k + 1], d)),
+                                clamp_fmax<kE5M2>(div_scale<kFast>(v[h][4 * k + 2], d)),
+                                clamp_fmax<kE5M2>(div_scale<kFast>(v[h][4 * k + 3], d)));
       const int64_t row = (int64_t)b * rows + r0 + tr + 32 * h;
       if (out) *(v4u*)(out + row * out_stride + c0 + tc) = v4u{w[0], w[1], w[2], w[3]};
 #pragma unroll
@@ -264,6 +327,20 @@ __global__ void __launch_bounds__(kThreads) quant_transpose_kernel(const void* x
     }
     __syncthreads();
   }
+}
+
+template <bool kF32, bool kE5M2>
+__global__ void __launch_bounds__(kThreads) quant_transpose_kernel(const void* x, int batch, int rows, int cols,
+                                                                   uint8_t* out, int64_t out_stride, uint8_t* out_t,
+                                                                   int64_t out_t_stride, const uint32_t* amax_bits,
+                                                                   float* scale_out) {
+  __shared__ uint8_t s_t[kTT * kTTPitch];
+  const ScaleDiv d = scale_div<kE5M2>(*amax_bits);
+  if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = d.scale;
+  if (d.fast)
+    transpose_body<kF32, kE5M2, true>(x, batch, rows, cols, out, out_stride, out_t, out_t_stride, d, s_t);
+  else
+    transpose_body<kF32, kE5M2, false>(x, batch, rows, cols, out, out_stride, out_t, out_t_stride, d, s_t);
 }
 
 // ---------------------------------------------------------------------------------- MX, grouped

@@ -70,6 +70,60 @@ def test_tensorwise_rounding_ties_and_subnormals(pkg, orq, cuda, fmt):
     np.testing.assert_array_equal(_bytes(q), q_ref)
 
 
+def _near_tie_inputs(fmt, amax, seed):
+    """fp32 inputs whose quotients x / scale lie within 4 fp32 ulps of every fp8 tie and value, for
+    a scale that is not a power of two, plus random values up to amax, values small enough for the
+    division's residual to underflow (|x| < 2^-102), amax itself and signed zeros."""
+    scale = np.float32(np.float32(amax) / orq_fmax(fmt))
+    b = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(TDT[fmt]).float().numpy()
+    vals = np.sort(np.unique(b[np.isfinite(b) & (b >= 0)]))
+    mids = ((vals[:-1].astype(np.float64) + vals[1:]) / 2).astype(np.float32)
+    x0 = np.concatenate([vals[1:], mids]) * scale
+    x = [x0.astype(np.float32)]
+    up, dn = x[0].copy(), x[0].copy()
+    for _ in range(4):
+        up, dn = np.nextafter(up, np.float32(np.inf)), np.nextafter(dn, np.float32(0))
+        x += [up, dn]
+    rng = np.random.default_rng(seed)
+    x.append((rng.uniform(-1, 1, 1 << 16) * np.float64(amax)).astype(np.float32))
+    x.append(np.ldexp(np.float32(1.0), -np.arange(102, 150)).astype(np.float32))
+    v = np.concatenate(x)
+    v = v[np.abs(v) <= np.float32(amax)]
+    v = np.concatenate([v, -v, [np.float32(amax), np.float32(-0.0), np.float32(0.0)]]).astype(np.float32)
+    return np.concatenate([v, np.zeros((-v.size) % 1024, np.float32)]).reshape(-1, 64)   # rows: multiple of 16
+
+
+def orq_fmax(fmt):
+    return np.float32(448.0 if fmt == "e4m3" else 57344.0)
+
+
+# amax values: ordinary non-power-of-two scales, the smallest amax (2^-60) the kernels' FMA-corrected
+# quotient covers and one below it (the plain division), and one near the largest fp32
+NEAR_TIE_AMAX = [613.76, 1.3e-4, 2.0 ** -60, 2.0 ** -61 * 1.7, 3.0e38]
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("amax", NEAR_TIE_AMAX, ids=[f"a{i}" for i in range(len(NEAR_TIE_AMAX))])
+def test_tensorwise_quotients_near_ties(pkg, orq, cuda, fmt, amax):
+    """x / scale must be the correctly rounded fp32 quotient before the fp8 rounding: quotients a
+    few ulps either side of each fp8 tie tell a faithful or double-rounded quotient from the correct
+    one. Both producers (plain and transposing) against the oracle's bytes."""
+    v = _near_tie_inputs(fmt, amax, seed=len(fmt))
+    _say(f"tensorwise near ties {fmt} amax={amax} {v.shape}")
+    q_ref, s_ref, a_ref = orq.quantize_tensorwise(v, fmt)
+    assert float(a_ref) == np.float32(amax)
+    q, scale, am = pkg.quantize_fp8_tensorwise(torch.from_numpy(v).to(cuda), fmt)
+    torch.cuda.synchronize()
+    assert float(am) == float(a_ref) and float(scale) == float(s_ref)
+    np.testing.assert_array_equal(_bytes(q), q_ref)
+    w = torch.from_numpy(v).reshape(1, -1, 64).to(cuda)
+    q, q_t, scale, _ = pkg.quantize_fp8_tensorwise_transpose(w, fmt)
+    torch.cuda.synchronize()
+    assert float(scale) == float(s_ref)
+    np.testing.assert_array_equal(_bytes(q).reshape(-1, 64), q_ref)
+    np.testing.assert_array_equal(_bytes(q_t)[0], q_ref.T)
+
+
 def _assert_bytes_nan_signless(got, ref):
     """Bytes equal, except that a NaN code (0x7F / 0xFF) may carry either sign: the sign of a NaN
     result is unspecified (the GPU's x / NaN and numpy's differ there)."""

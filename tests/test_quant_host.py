@@ -175,3 +175,59 @@ def test_overlapping_rows_are_copied_not_read_past():
     assert quant._row_stride(quant._as_2d(z)) == 256
     one = torch.randn(1, 2, 256)[:, 0]                 # one row, stride(0) = 512
     assert quant._row_stride(quant._as_2d(one)) == 256
+
+
+def _rnd32(fr):
+    """Round a rational to the nearest fp32 (ties to even, subnormals included), exactly."""
+    from fractions import Fraction as F
+    if fr == 0:
+        return np.float32(0.0)
+    a = abs(fr)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    while F(2) ** e > a:
+        e -= 1
+    while F(2) ** (e + 1) <= a:
+        e += 1
+    ulp = F(2) ** (max(e, -126) - 23)
+    k, r = divmod(a / ulp, 1)
+    k = int(k) + (1 if r > F(1, 2) or (r == F(1, 2) and int(k) % 2) else 0)
+    return np.float32((1 if fr > 0 else -1) * float(k * ulp))
+
+
+def test_fma_corrected_quotient_is_correctly_rounded():
+    """The tensorwise kernels divide by the scale as q = fl(x y), y = fl(1 / scale), corrected by
+    c = fl(q + fl(x - q scale) y) (two FMAs), then give c the sign of x, whenever amax lies in
+    [2^-60, FLT_MAX]. In exact rational arithmetic, over random and adversarial x (scale times an
+    fp8 grid value, one ulp off), amax at both ends of that range and x whose residual underflows:
+    c is the correctly rounded quotient, or (|x| < 2^-102 only) both round to fp8 zero (quotient
+    below 2^-26, under half the smallest e5m2 subnormal 2^-16)."""
+    import random
+    from fractions import Fraction as F
+    rng = random.Random(5)
+    fmaxes = [np.float32(448.0), np.float32(57344.0)]
+    amaxes = [np.float32(2.0 ** -60), np.float32(3.4028235e38)]
+    amaxes += [np.float32(abs(rng.gauss(0, 1)) * 2.0 ** rng.randint(-59, 120)) for _ in range(60)]
+    n = 0
+    for amax in amaxes:
+        for fmax in fmaxes:
+            s = _rnd32(F(float(amax)) / F(float(fmax)))
+            y = _rnd32(F(1) / F(float(s)))
+            xs = [amax, -amax, np.float32(2.0 ** -110), np.float32(-(2.0 ** -103) * 1.5), np.float32(1e-45)]
+            for _ in range(20):
+                xs.append(np.float32(rng.uniform(-1, 1) * float(amax)))
+                g = _rnd32(F(float(s)) * rng.randint(1, 2 ** 10) / 2 ** rng.randint(0, 12))
+                xs.append(np.nextafter(g, np.float32(np.inf if rng.random() < 0.5 else -np.inf), dtype=np.float32))
+            for x in xs:
+                if not (abs(x) <= amax):
+                    continue
+                q = np.float32(x * y)
+                r = _rnd32(F(float(x)) - F(float(q)) * F(float(s)))
+                c = _rnd32(F(float(r)) * F(float(y)) + F(float(q)))
+                c = np.float32(np.copysign(c, x))
+                exact = _rnd32(F(float(x)) / F(float(s)))
+                if abs(x) < 2.0 ** -102:
+                    assert abs(float(exact)) < 2.0 ** -26 and abs(float(c)) < 2.0 ** -26
+                else:
+                    assert c == exact and np.signbit(c) == np.signbit(x), (x, s, c, exact)
+                n += 1
+    assert n > 4000
