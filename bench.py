@@ -454,7 +454,10 @@ def main():
                   "out": "bf16", "acc": "fp32",
                   "inputs": "reference recipe: seed-42 exponential group sizes, randn bf16 cast to fp8, "
                             "scales 0.1, in HBM",
-                  "kernel": "hip gfx950 persistent {tile_m}x{tile_n} tiles, 128-K stages, mfma k128".format(**geo),
+                  "kernel": ("hip gfx950 persistent wide 256x320 tiles (256 threads, one wave per SIMD, generated "
+                             "assembly), 128-K stages, mfma 32x32x64"
+                             if pkg.persistent.selected_kernel(p.N, p.K, p.a.stride(0), p.b.stride(1), p.N) == "wide"
+                             else "hip gfx950 persistent {tile_m}x{tile_n} tiles, 128-K stages, mfma k128".format(**geo)),
                   "baseline_number": "none published for this site"}
         vs_baseline = None
     else:

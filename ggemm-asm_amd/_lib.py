@@ -26,6 +26,8 @@ EXPORTS = (
 
 PERSISTENT_EXPORTS = (
     "ggemm_persistent_fp8",
+    "ggemm_persistent_fp8_kernel",
+    "ggemm_persistent_selected_kernel",
     "ggemm_persistent_clear_tail",
     "ggemm_persistent_transpose_u8",
 )
@@ -94,6 +96,10 @@ def load():
     lib.ggemm_vark_launch_geometry.restype = None
     lib.ggemm_persistent_fp8.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 9 + [ctypes.c_int64, vp]
     lib.ggemm_persistent_fp8.restype = ctypes.c_int
+    lib.ggemm_persistent_fp8_kernel.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 9 + [ctypes.c_int64, i32, vp]
+    lib.ggemm_persistent_fp8_kernel.restype = ctypes.c_int
+    lib.ggemm_persistent_selected_kernel.argtypes = [i32] * 5
+    lib.ggemm_persistent_selected_kernel.restype = i32
     lib.ggemm_persistent_clear_tail.argtypes = [vp, i32, i32, vp, i32, ctypes.c_int64, vp]
     lib.ggemm_persistent_clear_tail.restype = ctypes.c_int
     lib.ggemm_persistent_transpose_u8.argtypes = [vp, i32, i32, i32, ctypes.c_int64, ctypes.c_int64, vp,

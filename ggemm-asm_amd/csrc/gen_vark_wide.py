@@ -110,6 +110,9 @@ class Config:
         self.vt = f"v{self.vsc0 - (1 if mx else 2)}"
         self.vt2 = f"v{self.vop0 - 1}"
         self.vgpr_clobber = list(range(self.vsc0 - (1 if mx else 2), 256))
+        # the bf16 epilogue's joint-pass addresses (four writes, two reads) in operand registers
+        self.epi_x = self.vop0 + 70
+        assert self.epi_x + 6 <= self.vacc0
         self.sgpr_clobber = SGPR_CLOBBER_MX if mx else SGPR_CLOBBER
         self.rb = 5 if mx else 4                        # LDS reads per operand block (MX: + its scale)
         # bf16 passes of two blocks (64 columns: one 128-byte C line per row). With an odd block count
@@ -555,7 +558,7 @@ class Gen:
         e(f"v_add_u32 v{rbase}, {s['EPI']}, {c.lane_value('rb_even')}")
         e(f"v_add_u32 v{rbase + 1}, {s['EPI']}, {c.lane_value('rb_odd')}")
         self.c_resource()
-        xw, xr = v0 + 70, v0 + 74        # joint pass: write and read addresses in the shared region
+        xw, xr = c.epi_x, c.epi_x + 4    # joint pass: write and read addresses in the shared region
         if c.joint:
             # IB (free in the epilogue) = the shared region of this wave row: slot + 16 KiB +
             # wm * 8 KiB, two 4 KiB buffers by m-block parity; T2 = its distance from EPI
@@ -869,12 +872,353 @@ class Gen:
         e(f"s_cselect_b32 {OP['nis']}, {s['IDX']}, 0")
 
 
+# ==================================================================== K-major (persistent fwd / dgrad)
+#
+# The persistent grouped GEMM C[r, :] = s_a s_b A[r, :] B[g]^T (persistent_wide.h) on the same
+# one-wave-per-SIMD tile: 256 rows of A (C rows, the "am" side) x 320 rows of B (C columns, "bn"),
+# both K-contiguous. The K axis goes in stages of 128 bytes, so every LDS-DMA row segment is one
+# whole 128-byte line when the row stride is line-aligned (a 64-byte stage would ask the L2 for a
+# line twice); a stage (256 + 320 rows x 128 bytes, 72 KiB) leaves room for two slots and the
+# schedule tables. Per stage and wave two K-halves of 4 x 5 v_mfma_f32_32x32x64_f8f6f4; a half's
+# operands (two ds_read_b128 per 32-row block) are read during the previous half as registers free
+# up. The slot's next stage is requested right after the barrier in the stage's second half (18
+# LDS-DMA instructions per wave, 8 rows x 128 bytes each, two or three per MFMA gap), so a stage's
+# loads have one stage time to land. K % 128 == 64 (K = 2880) makes the tile's last stage a half
+# stage: its second half is neither computed nor read.
+KSLOTS = 2
+KKS = 128                    # K bytes per stage
+WORD3_K = WORD3
+
+
+def kswz(r):
+    """Chunk swizzle of a 128-byte K row (persistent_kernel.h's): logical chunk c of row r at
+    physical chunk c ^ kswz(r); the 8 rows a 128-bit read serves together land on 8 distinct
+    chunks."""
+    return (r & 7) ^ ((r >> 3) & 1)
+
+
+class KConfig(Config):
+    def __init__(self, tm, tn, a_e5m2):
+        self.tm, self.tn = tm, tn
+        self.a_e5m2 = a_e5m2
+        self.out, self.mx, self.kmajor = "bf16", False, True
+        self.name = f"pk{tm}x{tn}_" + ("e5m2" if a_e5m2 else "e4m3")
+        self.bm, self.bn = tm // 64, tn // 64
+        self.rhs_off = KKS * tm
+        self.slot = KKS * (tm + tn)
+        self.nl = KKS * tm // 4096
+        self.nr = KKS * tn // 4096
+        self.loads = self.nl + self.nr
+        nblk = self.bm * self.bn
+        assert 16 < nblk <= 32
+        self.vacc0 = 256 - 16 * (nblk - 16)
+        self.scale_map, self.nsl, self.nsr = {}, 0, 0
+        self.vop0 = self.vacc0 - 8 * (self.bm + self.bn)
+        self.vsc0 = self.vop0
+        self.vt = f"v{self.vop0 - 2}"
+        self.vt2 = f"v{self.vop0 - 1}"
+        # the epilogue's joint-pass addresses below the operands: the 72 operand registers leave
+        # no room above them before the VGPR accumulators
+        self.epi_x = self.vop0 - 8
+        self.vgpr_clobber = list(range(self.epi_x, 256))
+        self.sgpr_clobber = list(range(56, 90))
+        self.rb = 2                                     # two 128-bit reads per 32-row block
+        self.joint = self.bn % 2 == 1
+        self.pairs = [(2 * q, 2 * q + 1) for q in range(self.bn // 2)]
+        self.pairs_wn1 = [(2 * q + 1, 2 * q + 2) for q in range(self.bn // 2)] if self.joint else self.pairs
+        self.joint_block = (self.bn - 1, 0)
+        self.e_stores = self.bm * (4 * len(self.pairs) + (2 if self.joint else 0))
+        self.parity_bases = False
+        ops = [("c0", "+s"), ("nis", "+s"), ("vmt", "+s"), ("q0", "+s"), ("q1", "+s"), ("q2", "+s"), ("np", "+s"),
+               ("lds_base", "s"), ("w1k", "s"),
+               ("bLT_lo", "s"), ("bLT_hi", "s"), ("bRT_lo", "s"), ("bRT_hi", "s"), ("klenT", "s"), ("recAT", "s"),
+               ("recBT", "s"),
+               ("bLN_lo", "s"), ("bLN_hi", "s"), ("bRN_lo", "s"), ("bRN_hi", "s"), ("klenN", "s"), ("recAN", "s"),
+               ("recBN", "s"),
+               ("cT_lo", "s"), ("cT_hi", "s"), ("crecT", "s"), ("cm2", "s"), ("alpha", "s"), ("sw_epi", "s")]
+        ops += [(f"voffL{j}", "v") for j in range(self.nl)] + [(f"voffR{j}", "v") for j in range(self.nr)]
+        ops += [(f"{side}{hl}{kh}", "v") for side in ("am", "bn") for kh in (0, 1) for hl in ("lo", "hi")]
+        ops += [(n, "v") for n in ("ew_base", "ew_s", "rb_even", "rb_odd", "gb")]
+        self.lane_regs = {}
+        self.operands = ops
+        self.op = {name: f"%{i}" for i, (name, _) in enumerate(ops)}
+        self.order = [(0, j) for j in range(self.bn)] + [(i, j) for j in range(self.bn) for i in range(1, self.bm)]
+        pos = {ij: n for n, ij in enumerate(self.order)}
+        self.barrier_after = self.bn - 1
+        reads = {self.bn - 1: [("am", 0)]}
+        for j in range(self.bn):
+            reads.setdefault(pos[(self.bm - 1, j)], []).append(("bn", j))
+        for i in range(1, self.bm):
+            reads.setdefault(pos[(i, self.bn - 1)], []).append(("am", i))
+        self.reads_after = reads
+        # a half's operand reads in issue order; at the next half's start every block up to the
+        # n-block its (0, bn - 2) MFMA needs must be in: lgkmcnt(rb x blocks read after it)
+        seq = [rd for n in range(len(self.order)) for rd in reads.get(n, [])]
+        need = max(seq.index(("am", 0)), max(seq.index(("bn", j)) for j in range(self.bn - 1)))
+        self.lgk_start = min(15, self.rb * (len(seq) - 1 - need))
+        assert seq[-1][0] == "am" and seq[-2] == ("bn", self.bn - 1)   # lgkmcnt(rb) before MFMA bn - 1
+        # LDS-DMA after the barrier (second half): the free MFMA gaps, two or three loads each
+        free = [n for n in range(self.bn, len(self.order) - 1) if n not in reads]
+        per, extra = divmod(self.loads, len(free))
+        plan, k = {}, 0
+        for q, n in enumerate(free):
+            cnt = per + (1 if q < extra else 0)
+            plan[n] = list(range(k, k + cnt))
+            k += cnt
+        assert k == self.loads and max(len(v) for v in plan.values()) <= 3
+        self.dma_plan = plan
+        self.setup_after = (0, 1, 2)
+        assert self.epi_x >= 28 and self.vop0 % 2 == 0 and self.e_stores + self.loads <= 63
+        assert self.vop0 + 56 <= self.vacc0          # the epilogue's other temporaries (up to vop0 + 55)
+        assert self.nl * 4 * 1024 == KKS * tm and self.nr * 4 * 1024 == KKS * tn
+        assert KSLOTS * self.slot + 16384 <= 160 * 1024   # two slots and the schedule tables
+
+    def read_base(self, side, b):
+        raise NotImplementedError
+
+
+KCONFIGS = (KConfig(256, 320, False), KConfig(256, 320, True))
+SGPR_K = dict(SGPR, RECA=SGPR["CM0"], RECB=SGPR["CN0"], HALF="s89")
+
+
+class GenK(Gen):
+    """The K-major pipeline; the bf16 epilogue (and vm model) is the wgrad kernels'."""
+
+    def wait_oldest(self):
+        s, OP, c = SGPR_K, self.OP, self.cfg
+        self.emit(f"s_sub_u32 {s['NEED']}, {OP['vmt']}, {OP['q0']}")
+        self.emit(f"s_mov_b32 {OP['q0']}, {OP['q1']}")
+        self.emit(f"s_mov_b32 {OP['q1']}, {OP['q2']}")
+        self.emit(f"s_sub_u32 {OP['np']}, {OP['np']}, 1")
+        # after the oldest stage: nothing (a stage's barrier), or at a tile's start the previous
+        # epilogue's stores and / or the stage the tile's top-up issued
+        counts = sorted({c.e_stores + c.loads, c.e_stores, c.loads}, reverse=True)
+        done = self.label("wdone")
+        tgt = {n: self.label(f"w{n}_") for n in counts}
+        for n in counts:
+            self.emit(f"s_cmp_ge_u32 {s['NEED']}, {n}")
+            self.emit(f"s_cbranch_scc1 {tgt[n]}")
+        self.emit("s_waitcnt vmcnt(0)")
+        self.emit(f"s_branch {done}")
+        for n in counts:
+            self.emit(f"{tgt[n]}:")
+            self.emit(f"s_waitcnt vmcnt({n})")
+            self.emit(f"s_branch {done}")
+        self.emit(f"{done}:")
+
+    def issue_setup(self):
+        """Buffer resources of the cursor's stage: base at its K offset, num_records ending at the
+        last valid row's K bytes of the stage (rows past the group end / N, and a half stage's
+        second half of the last valid row, read as zero); this wave's LDS-DMA base in slot ISLOT."""
+        s, OP, e = SGPR_K, self.OP, self.emit
+        e(f"s_min_i32 {s['T']}, {s['REM']}, {KKS}")
+        e(f"s_max_i32 {s['T']}, {s['T']}, 0")
+        e(f"s_add_u32 {s['RL2']}, {s['RECA']}, {s['T']}")
+        e(f"s_add_u32 {s['RR2']}, {s['RECB']}, {s['T']}")
+        e(f"s_mov_b32 {s['RL0']}, {s['BL0']}")
+        e(f"s_and_b32 {s['RL1']}, {s['BL1']}, 0xffff")
+        e(f"s_mov_b32 {s['RL3']}, 0x{WORD3_K:x}")
+        e(f"s_mov_b32 {s['RR0']}, {s['BR0']}")
+        e(f"s_and_b32 {s['RR1']}, {s['BR1']}, 0xffff")
+        e(f"s_mov_b32 {s['RR3']}, 0x{WORD3_K:x}")
+        e(f"s_add_u32 {s['IB']}, {OP['lds_base']}, {s['ISLOT']}")
+        e(f"s_add_u32 {s['IB']}, {s['IB']}, {OP['w1k']}")
+
+    def issue_finish(self):
+        s, OP, e, c = SGPR_K, self.OP, self.emit, self.cfg
+        e(f"s_add_u32 {OP['vmt']}, {OP['vmt']}, {c.loads}")
+        for n, q in enumerate(("q0", "q1", "q2")):
+            e(f"s_cmp_eq_u32 {OP['np']}, {n}")
+            e(f"s_cselect_b32 {OP[q]}, {OP['vmt']}, {OP[q]}")
+        e(f"s_add_u32 {OP['np']}, {OP['np']}, 1")
+        e(f"s_add_u32 {s['IDX']}, {s['IDX']}, 1")
+        e(f"s_sub_i32 {s['REM']}, {s['REM']}, {KKS}")
+        e(f"s_add_u32 {s['BL0']}, {s['BL0']}, {KKS}")
+        e(f"s_addc_u32 {s['BL1']}, {s['BL1']}, 0")
+        e(f"s_add_u32 {s['BR0']}, {s['BR0']}, {KKS}")
+        e(f"s_addc_u32 {s['BR1']}, {s['BR1']}, 0")
+        e(f"s_sub_u32 {s['ISLOT']}, {c.slot}, {s['ISLOT']}")
+
+    def cursor_prep(self):
+        """Move the cursor to the next tile once this one is fully issued (the next tile's first
+        stage is its limit there: the other slot stages this tile's epilogue); SCC = a stage to
+        issue."""
+        s, OP, e = SGPR_K, self.OP, self.emit
+        nosw = self.label("nosw")
+        e(f"s_cmp_eq_u32 {s['INT']}, 1")
+        e(f"s_cbranch_scc0 {nosw}")
+        e(f"s_cmp_eq_u32 {s['IDX']}, {s['S']}")
+        e(f"s_cbranch_scc0 {nosw}")
+        e(f"s_mov_b32 {s['INT']}, 0")
+        e(f"s_mov_b32 {s['IDX']}, 0")
+        e(f"s_mov_b32 {s['REM']}, {OP['klenN']}")
+        e(f"s_add_u32 {s['T']}, {OP['klenN']}, {KKS - 1}")
+        e(f"s_lshr_b32 {s['T']}, {s['T']}, 7")
+        e(f"s_min_u32 {s['LIM']}, {s['T']}, 1")
+        e(f"s_mov_b32 {s['BL0']}, {OP['bLN_lo']}")
+        e(f"s_mov_b32 {s['BL1']}, {OP['bLN_hi']}")
+        e(f"s_mov_b32 {s['BR0']}, {OP['bRN_lo']}")
+        e(f"s_mov_b32 {s['BR1']}, {OP['bRN_hi']}")
+        e(f"s_mov_b32 {s['RECA']}, {OP['recAN']}")
+        e(f"s_mov_b32 {s['RECB']}, {OP['recBN']}")
+        e(f"{nosw}:")
+        e(f"s_cmp_lt_u32 {s['IDX']}, {s['LIM']}")
+
+    def read_block(self, side, b, slot, kh=0):
+        """Block b of one side for K-half kh: two 128-bit reads (logical chunks 4 kh + 2 h and
+        4 kh + 2 h + 1 of row l % 32, h = l / 32) from slot `slot`."""
+        c, e = self.cfg, self.emit
+        reg0 = c.am(b) if side == "am" else c.bn_reg(b)
+        off = 4096 * b                  # 32 rows of 128 bytes; the side's offset is in the base
+        for hh, hl in enumerate(("lo", "hi")):
+            e(f"v_add_u32 {c.vt}, {slot}, {self.OP[f'{side}{hl}{kh}']}")
+            e(f"ds_read_b128 v[{reg0 + 4 * hh}:{reg0 + 4 * hh + 3}], {c.vt} offset:{off}")
+
+    def mfma(self, i, j, first):
+        c = self.cfg
+        d = c.acc_range(i, j)
+        src = "0" if first else d
+        a, b = c.bn_reg(j), c.am(i)
+        self.emit(f"v_mfma_f32_32x32x64_f8f6f4 {d}, v[{a}:{a + 7}], v[{b}:{b + 7}], {src}"
+                  + (" blgp:1" if c.a_e5m2 else ""))
+
+    def half(self, kh, first, wait_first, barrier, reads_from, issue):
+        """One K-half: 4 x 5 MFMAs. wait_first: the half's operands were read by the tile's
+        prologue (all in); barrier: wait for the next stage's loads and pass the barrier after the
+        first row; reads_from: (slot register, K-half) of the next half's operands, or None;
+        issue: the cursor's next stage goes out after the barrier."""
+        s, e, c = SGPR_K, self.emit, self.cfg
+        setup = self.capture(self.issue_setup) if issue else []
+        third = (len(setup) + 2) // 3
+        pieces = [setup[:third], setup[third:2 * third], setup[2 * third:]]
+        e("s_waitcnt lgkmcnt(0)" if wait_first else f"s_waitcnt lgkmcnt({c.lgk_start})")
+        for n, (i, j) in enumerate(c.order):
+            if not wait_first and n == c.bn - 1:
+                e(f"s_waitcnt lgkmcnt({c.rb})")
+            self.mfma(i, j, first)
+            if issue and n in c.setup_after:
+                for line in pieces[c.setup_after.index(n)]:
+                    e(line)
+            if n == c.barrier_after:
+                e("s_waitcnt lgkmcnt(0)")
+                if barrier:
+                    self.wait_oldest()
+                    e("s_barrier")
+            if reads_from is not None:
+                for side, b in c.reads_after.get(n, []):
+                    self.read_block(side, b, reads_from[0], reads_from[1])
+            if issue and n in c.dma_plan:
+                for k in c.dma_plan[n]:
+                    self.issue_dma(k)
+                    if k == c.loads - 1:
+                        self.issue_finish()
+
+    def kstage(self, first, last, issue, half_only=False):
+        """Stage k from slot CS: K-half 0 (reading half 1 from CS), then K-half 1 (unless last:
+        barrier after its first row, then reading the next stage's half 0 from NS = the other
+        slot, and with issue the cursor's next stage into CS). half_only: the tile's last stage
+        under K % 128 == 64, half 0 alone."""
+        s, e, c = SGPR_K, self.emit, self.cfg
+        assert not (half_only and not last) and not (issue and last)
+        if not last:
+            e(f"s_sub_u32 {s['NS']}, {c.slot}, {s['CS']}")
+        self.half(0, first, first, False, None if half_only else (s["CS"], 1), False)
+        if half_only:
+            return
+        self.half(1, False, False, not last, None if last else (s["NS"], 0), issue)
+
+    def variant_pair(self, first):
+        e = self.emit
+        noiss, join = self.label("noiss"), self.label("join")
+        self.cursor_prep()
+        e(f"s_cbranch_scc0 {noiss}")
+        self.kstage(first=first, last=False, issue=True)
+        e(f"s_branch {join}")
+        e(f"{noiss}:")
+        self.kstage(first=first, last=False, issue=False)
+        e(f"{join}:")
+
+    def last_stage(self, first):
+        e = self.emit
+        full, join = self.label("full"), self.label("ljoin")
+        e(f"s_cmp_eq_u32 {SGPR_K['HALF']}, 0")
+        e(f"s_cbranch_scc1 {full}")
+        self.kstage(first=first, last=True, issue=False, half_only=True)
+        e(f"s_branch {join}")
+        e(f"{full}:")
+        self.kstage(first=first, last=True, issue=False)
+        e(f"{join}:")
+
+    def tile(self):
+        s, OP, e, c = SGPR_K, self.OP, self.emit, self.cfg
+        e("s_nop 4")   # inputs may come from v_readfirstlane (VALU-written SGPRs) just before
+        e(f"s_add_u32 {s['S']}, {OP['klenT']}, {KKS - 1}")
+        e(f"s_lshr_b32 {s['S']}, {s['S']}, 7")
+        e(f"s_and_b32 {s['HALF']}, {OP['klenT']}, {KKS // 2}")
+        e(f"s_mul_i32 {s['CS']}, {OP['c0']}, {c.slot}")
+        e(f"s_add_u32 {s['T']}, {OP['c0']}, {OP['nis']}")
+        e(f"s_cmp_ge_u32 {s['T']}, {KSLOTS}")
+        e(f"s_cselect_b32 {s['T2']}, {KSLOTS}, 0")
+        e(f"s_sub_u32 {s['T']}, {s['T']}, {s['T2']}")
+        e(f"s_mul_i32 {s['ISLOT']}, {s['T']}, {c.slot}")
+        e(f"s_mov_b32 {s['INT']}, 1")
+        e(f"s_mov_b32 {s['IDX']}, {OP['nis']}")
+        e(f"s_mov_b32 {s['LIM']}, {s['S']}")
+        e(f"s_lshl_b32 {s['T']}, {OP['nis']}, 7")
+        e(f"s_sub_i32 {s['REM']}, {OP['klenT']}, {s['T']}")
+        e(f"s_add_u32 {s['BL0']}, {OP['bLT_lo']}, {s['T']}")
+        e(f"s_addc_u32 {s['BL1']}, {OP['bLT_hi']}, 0")
+        e(f"s_add_u32 {s['BR0']}, {OP['bRT_lo']}, {s['T']}")
+        e(f"s_addc_u32 {s['BR1']}, {OP['bRT_hi']}, 0")
+        e(f"s_mov_b32 {s['RECA']}, {OP['recAT']}")
+        e(f"s_mov_b32 {s['RECB']}, {OP['recBT']}")
+        e("s_barrier")   # the previous tile's epilogue is done with its staging slot
+        e(f"s_min_u32 {s['LIMTOP']}, {s['S']}, {KSLOTS}")
+        top, topdone = self.label("top"), self.label("topdone")
+        e(f"{top}:")
+        e(f"s_cmp_lt_u32 {s['IDX']}, {s['LIMTOP']}")
+        e(f"s_cbranch_scc0 {topdone}")
+        self.issue_core()
+        e(f"s_branch {top}")
+        e(f"{topdone}:")
+        self.wait_oldest()
+        e("s_barrier")
+        for i in range(c.bm):
+            self.read_block("am", i, s["CS"], 0)
+        for j in range(c.bn):
+            self.read_block("bn", j, s["CS"], 0)
+        first_last, loop, steady_last, epi = (self.label(x) for x in ("fl", "loop", "sl", "epi"))
+        e(f"s_cmp_eq_u32 {s['S']}, 1")
+        e(f"s_cbranch_scc1 {first_last}")
+        self.variant_pair(first=True)
+        e(f"s_mov_b32 {s['CS']}, {s['NS']}")
+        e(f"s_mov_b32 {s['K']}, 1")
+        e(f"{loop}:")
+        e(f"s_add_u32 {s['T']}, {s['K']}, 1")
+        e(f"s_cmp_eq_u32 {s['T']}, {s['S']}")
+        e(f"s_cbranch_scc1 {steady_last}")
+        self.variant_pair(first=False)
+        e(f"s_mov_b32 {s['CS']}, {s['NS']}")
+        e(f"s_add_u32 {s['K']}, {s['K']}, 1")
+        e(f"s_branch {loop}")
+        e(f"{first_last}:")
+        self.last_stage(first=True)
+        e(f"s_branch {epi}")
+        e(f"{steady_last}:")
+        self.last_stage(first=False)
+        e(f"{epi}:")
+        self.epilogue()
+        e(f"s_cmp_eq_u32 {s['INT']}, 0")
+        e(f"s_cselect_b32 {OP['nis']}, {s['IDX']}, 0")
+
+
 def render():
     out = ["// Generated by gen_vark_wide.py; do not edit. Per-tile bodies of the wide-tile FP8 grouped",
-           "// wgrad kernels (vark_wide.h): gfx950 assembly, one inline asm statement per tile shape."]
+           "// wgrad kernels (vark_wide.h) and of the wide persistent fwd / dgrad kernel (persistent_wide.h):",
+           "// gfx950 assembly, one inline asm statement per tile shape."]
     total = 0
-    for c in CONFIGS:
-        g = Gen(c)
+    for c in CONFIGS + KCONFIGS:
+        g = GenK(c) if isinstance(c, KConfig) else Gen(c)
         g.tile()
         total += len(g.lines)
         text = "\\n\\t".join(g.lines)

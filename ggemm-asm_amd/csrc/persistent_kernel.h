@@ -108,6 +108,112 @@ __device__ __forceinline__ v8i read_nt(const GG_LDS uint8_t* lo, const GG_LDS ui
   return v8i{l[0], l[1], l[2], l[3], h[0], h[1], h[2], h[3]};
 }
 
+// Group tables in LDS for kT threads and kTM-row tiles: s_offs[g] = offs[g] clamped to [0, m_total]
+// (32-bit rows), s_pre[g] = tiles of groups 0..g-1 (g = 0..G, n_tn column tiles per M-tile). Each
+// thread takes (kMaxGroups + 1) / kT consecutive groups, an inclusive scan over the thread totals
+// (s_scan, kT entries) gives every thread its first group's prefix. Offsets outside [0, kMaxRow] or
+// more than 2^30 tiles in all (inputs of hundreds of GB; the host rejects them from M_total) return
+// false in every thread: the whole grid then returns.
+template <int kT, int kTM>
+__device__ __forceinline__ bool group_tables(const Args& a, int n_tn, GG_LDS int* s_pre, GG_LDS int* s_offs,
+                                             GG_LDS int64_t* s_scan) {
+  const int tid = threadIdx.x;
+  const int G = a.G;
+  constexpr int kPer = (kMaxGroups + 1) / kT;
+  static_assert(kPer * kT == kMaxGroups + 1, "groups split evenly over the threads");
+  // all loads first (indices clamped to G), so they are in flight together
+  int64_t o[kPer + 1];
+#pragma unroll
+  for (int k = 0; k <= kPer; ++k) o[k] = a.group_offs[min(tid * kPer + k, G)];
+  // rows past the tensors are neither read nor written: offsets clamp to m_total (<= kMaxRow)
+#pragma unroll
+  for (int k = 0; k <= kPer; ++k) o[k] = o[k] > a.m_total ? a.m_total : o[k];
+  int64_t mine[kPer];
+  int64_t sum = 0;
+  bool bad = false;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int g = tid * kPer + k;
+    int64_t tiles = 0;
+    if (g <= G) {
+      bad |= o[k] < 0 || o[k] > kMaxRow;
+      s_offs[g] = (int)o[k];
+      const int64_t len = o[k + 1] - o[k];   // 0 for g = G (both clamped to offs[G])
+      tiles = len > 0 ? (len + kTM - 1) / kTM * n_tn : 0;
+    }
+    mine[k] = tiles;
+    sum += tiles;
+  }
+  s_scan[tid] = bad ? kMaxTiles + 1 : sum;   // a bad group pushes the total past the limit
+  __syncthreads();
+  for (int d = 1; d < kT; d <<= 1) {
+    const int64_t v = tid >= d ? s_scan[tid - d] : 0;
+    __syncthreads();
+    s_scan[tid] += v;
+    __syncthreads();
+  }
+  if (s_scan[kT - 1] > kMaxTiles) return false;   // uniform: every thread reads the same total
+  int64_t run = s_scan[tid] - sum;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int g = tid * kPer + k;
+    if (g < G) s_pre[g] = (int)run;
+    run += mine[k];
+  }
+  if (tid == kT - 1) s_pre[G] = (int)s_scan[tid];
+  __syncthreads();
+  return true;
+}
+
+// XCD pairs: slices of equal tile counts, the two XCDs of a slice alternating rounds of their
+// workgroups; workgroup blockIdx.x takes tiles t_begin, t_begin + t_step, ... below t_end.
+struct Slices {
+  int t_begin, t_end, t_step;
+};
+__device__ __forceinline__ Slices xcd_slices(int total, int num_wg) {
+  const bool spread = num_wg % kXcds == 0;
+  const int xcds = spread ? kXcds : 1;
+  const int n_slices = spread ? kXcdPairs : 1;
+  const int per_slice = xcds / n_slices;
+  const int xcd = (int)blockIdx.x % xcds;
+  const int slice = xcd % n_slices, part = xcd / n_slices;
+  const int wgs_per_xcd = num_wg / xcds;
+  Slices r;
+  r.t_begin = (int)((int64_t)total * slice / n_slices) + part * wgs_per_xcd + (int)blockIdx.x / xcds;
+  r.t_end = (int)((int64_t)total * (slice + 1) / n_slices);
+  r.t_step = per_slice * wgs_per_xcd;
+  return r;
+}
+
+// Tile t of the launch: its group is the last g with s_pre[g] <= t (groups without tiles share
+// their successor's prefix, so the search lands on the group that owns t); a group's tiles in
+// 4-wide N bands, M-tile fastest. Wave-uniform: scalar registers from here on.
+template <int kTM, int kTN>
+__device__ __forceinline__ Tile tile_of(const GG_LDS int* s_pre, const GG_LDS int* s_offs, int G, int n_tn, int t) {
+  int lo = 0, hi = G - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_pre[mid] <= t) lo = mid; else hi = mid - 1;
+  }
+  lo = __builtin_amdgcn_readfirstlane(lo);
+  Tile T;
+  T.g = lo;
+  T.row_base = __builtin_amdgcn_readfirstlane(s_offs[lo]);
+  const int len = __builtin_amdgcn_readfirstlane(s_offs[lo + 1]) - T.row_base;
+  const int n_tm = (len + kTM - 1) / kTM;
+  const int in_g = t - __builtin_amdgcn_readfirstlane(s_pre[lo]);
+  constexpr int kBandN = 4;
+  const int band = in_g / (n_tm * kBandN);
+  const int r = in_g - band * n_tm * kBandN;
+  const int bw = min(kBandN, n_tn - band * kBandN);
+  const int tm = r / bw;
+  const int tn = band * kBandN + (r - tm * bw);
+  T.m0 = tm * kTM;
+  T.n0 = tn * kTN;
+  T.rows = min(kTM, len - T.m0);
+  return T;
+}
+
 template <bool kAE5M2, int kTN>
 __device__ __forceinline__ void persistent_body(const Args& a, GG_LDS uint8_t* lds) {
   using C = Cfg<kTN>;
@@ -125,97 +231,13 @@ __device__ __forceinline__ void persistent_body(const Args& a, GG_LDS uint8_t* l
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = a.G;
 
-  // ---- group offsets into LDS and tiles per group prefix-summed: each thread takes kPer
-  // consecutive groups, an inclusive scan over the 512 thread totals gives every thread its first
-  // group's offset. Row and tile indices below are 32-bit: offsets outside [0, kMaxRow] or more
-  // than 2^30 tiles in all (inputs of hundreds of GB; the host rejects them from M_total) make the
-  // whole grid return.
+  // ---- group offsets into LDS and tiles per group prefix-summed (group_tables), XCD slices
   const int n_tn = (a.N + kTN - 1) / kTN;
-  {
-    constexpr int kPer = (kMaxGroups + 1) / kThreads;
-    // all loads first (indices clamped to G), so they are in flight together
-    int64_t o[kPer + 1];
-#pragma unroll
-    for (int k = 0; k <= kPer; ++k) o[k] = a.group_offs[min(tid * kPer + k, G)];
-    // rows past the tensors are neither read nor written: offsets clamp to m_total (<= kMaxRow)
-#pragma unroll
-    for (int k = 0; k <= kPer; ++k) o[k] = o[k] > a.m_total ? a.m_total : o[k];
-    int64_t mine[kPer];
-    int64_t sum = 0;
-    bool bad = false;
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int g = tid * kPer + k;
-      int64_t tiles = 0;
-      if (g <= G) {
-        bad |= o[k] < 0 || o[k] > kMaxRow;
-        s_offs[g] = (int)o[k];
-        const int64_t len = o[k + 1] - o[k];   // 0 for g = G (both clamped to offs[G])
-        tiles = len > 0 ? (len + kTileM - 1) / kTileM * n_tn : 0;
-      }
-      mine[k] = tiles;
-      sum += tiles;
-    }
-    s_scan[tid] = bad ? kMaxTiles + 1 : sum;   // a bad group pushes the total past the limit
-    __syncthreads();
-    for (int d = 1; d < kThreads; d <<= 1) {
-      const int64_t v = tid >= d ? s_scan[tid - d] : 0;
-      __syncthreads();
-      s_scan[tid] += v;
-      __syncthreads();
-    }
-    if (s_scan[kThreads - 1] > kMaxTiles) return;   // uniform: every thread reads the same total
-    int64_t run = s_scan[tid] - sum;
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int g = tid * kPer + k;
-      if (g < G) s_pre[g] = (int)run;
-      run += mine[k];
-    }
-    if (tid == kThreads - 1) s_pre[G] = (int)s_scan[tid];
-    __syncthreads();
-  }
+  if (!group_tables<kThreads, kTileM>(a, n_tn, s_pre, s_offs, s_scan)) return;
   const int total = s_pre[G];
-
-  // ---- XCD pairs: slices of equal tile counts, the two XCDs of a slice alternating 32-tile rounds
-  const bool spread = num_wg % kXcds == 0;
-  const int xcds = spread ? kXcds : 1;
-  const int n_slices = spread ? kXcdPairs : 1;
-  const int per_slice = xcds / n_slices;
-  const int xcd = (int)blockIdx.x % xcds;
-  const int slice = xcd % n_slices, part = xcd / n_slices;
-  const int wgs_per_xcd = num_wg / xcds;
-  const int t_begin = (int)((int64_t)total * slice / n_slices) + part * wgs_per_xcd + (int)blockIdx.x / xcds;
-  const int t_end = (int)((int64_t)total * (slice + 1) / n_slices);
-  const int t_step = per_slice * wgs_per_xcd;
-
-  auto tile_at = [&](int t) {
-    // the tile's group: the last g with s_pre[g] <= t (groups without tiles share their
-    // successor's prefix, so the search lands on the group that owns t)
-    int lo = 0, hi = G - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_pre[mid] <= t) lo = mid; else hi = mid - 1;
-    }
-    // wave-uniform by construction: scalar registers and scalar loads from here on
-    lo = __builtin_amdgcn_readfirstlane(lo);
-    Tile T;
-    T.g = lo;
-    T.row_base = __builtin_amdgcn_readfirstlane(s_offs[lo]);
-    const int len = __builtin_amdgcn_readfirstlane(s_offs[lo + 1]) - T.row_base;
-    const int n_tm = (len + kTileM - 1) / kTileM;
-    const int in_g = t - __builtin_amdgcn_readfirstlane(s_pre[lo]);
-    constexpr int kBandN = 4;
-    const int band = in_g / (n_tm * kBandN);
-    const int r = in_g - band * n_tm * kBandN;
-    const int bw = min(kBandN, n_tn - band * kBandN);
-    const int tm = r / bw;
-    const int tn = band * kBandN + (r - tm * bw);
-    T.m0 = tm * kTileM;
-    T.n0 = tn * kTN;
-    T.rows = min(kTileM, len - T.m0);
-    return T;
-  };
+  const Slices sl = xcd_slices(total, num_wg);
+  const int t_begin = sl.t_begin, t_end = sl.t_end, t_step = sl.t_step;
+  auto tile_at = [&](int t) { return tile_of<kTileM, kTN>(s_pre, s_offs, G, n_tn, t); };
 
   const float alpha = *a.a_scale * *a.b_scale;
   const int nsteps = (a.K + kKStep - 1) / kKStep;

@@ -22,6 +22,16 @@ _FORMATS = {torch.float8_e4m3fn: GGEMM_FP8_E4M3, torch.float8_e5m2: GGEMM_FP8_E5
 _FORMAT_NAMES = {"e4m3": GGEMM_FP8_E4M3, "e5m2": GGEMM_FP8_E5M2}
 
 
+# kernel choices of ggemm_persistent_fp8_kernel (include/ggemm_persistent.h)
+KERNELS = {"auto": 0, "512": 1, "wide": 2}
+
+
+def selected_kernel(N: int, K: int, stride_am: int, stride_bn: int, stride_cm: int) -> str:
+    """The kernel the library runs for this shape and these strides ("512" or "wide")."""
+    k = _lib.load().ggemm_persistent_selected_kernel(N, K, stride_am, stride_bn, stride_cm)
+    return {v: n for n, v in KERNELS.items()}[k]
+
+
 def _a_format(a: torch.Tensor, a_format: str | None) -> int:
     if a_format is not None:
         if a_format not in _FORMAT_NAMES:
@@ -59,7 +69,7 @@ def transpose_b(b: torch.Tensor) -> torch.Tensor:
 def grouped_gemm_fp8_tensorwise(a: torch.Tensor, b: torch.Tensor, a_scale: torch.Tensor, b_scale: torch.Tensor,
                                 group_offs: torch.Tensor, trans_b: bool = True, out: torch.Tensor | None = None,
                                 *, a_format: str | None = None, validate: bool = False,
-                                zero_tail: bool = False) -> torch.Tensor:
+                                zero_tail: bool = False, kernel: str = "auto") -> torch.Tensor:
     """``out[r] = a_scale * b_scale * a[r] @ B[g]^T`` for ``offs[g] <= r < offs[g+1]`` (bf16).
 
     a: float8_e4m3fn (forward) or float8_e5m2 (data gradient) [M_total, K]; b: float8_e4m3fn
@@ -70,7 +80,10 @@ def grouped_gemm_fp8_tensorwise(a: torch.Tensor, b: torch.Tensor, a_scale: torch
     fp32 tensors on the device; group_offs: int64 [G+1]. Rows outside ``[0, offs[G])`` of ``out``
     are left unwritten, or set to zero with ``zero_tail=True`` (the library's device-side clear, no
     sync: dropped tokens get exact zeros). ``validate=True`` checks group_offs on the host first (a
-    sync). Offsets past M_total are clamped to it on the device.
+    sync). Offsets past M_total are clamped to it on the device. ``kernel``: "auto" (the library's
+    choice: the wide-tile kernel where N % 320 == 0, K % 64 == 0 and the a and b row strides are
+    multiples of 128, else the 512-thread kernel),
+    "512" or "wide" (GGemmError GGEMM_E_SHAPE where the wide kernel does not apply).
     """
     if a.dim() != 2 or b.dim() != 3:
         raise ValueError("a must be 2-D [M_total, K] and b 3-D [G, N, K] (trans_b) or [G, K, N]")
@@ -106,14 +119,17 @@ def grouped_gemm_fp8_tensorwise(a: torch.Tensor, b: torch.Tensor, a_scale: torch
         raise ValueError(f"out must be bf16 [{M_total}, {N}] on the input device")
     if validate:
         _validate_offsets(group_offs, M_total, mx=False)
+    if kernel not in KERNELS:
+        raise ValueError(f"kernel must be one of {sorted(KERNELS)}, got {kernel!r}")
     if M_total == 0:
         return out
     lib = _lib.load()
     with torch.cuda.device(dev):
-        rc = lib.ggemm_persistent_fp8(
+        rc = lib.ggemm_persistent_fp8_kernel(
             a.data_ptr(), b.data_ptr(), out.data_ptr(), a_scale.data_ptr(), b_scale.data_ptr(), group_offs.data_ptr(),
-            G, N, K, a.stride(0), b.stride(0), b.stride(1), out.stride(0), out.stride(1), fmt, M_total, _stream(dev))
-        _lib.check(rc, "ggemm_persistent_fp8")
+            G, N, K, a.stride(0), b.stride(0), b.stride(1), out.stride(0), out.stride(1), fmt, M_total,
+            KERNELS[kernel], _stream(dev))
+        _lib.check(rc, "ggemm_persistent_fp8_kernel")
         if zero_tail:
             rc = lib.ggemm_persistent_clear_tail(out.data_ptr(), N, out.stride(0), group_offs.data_ptr(), G, M_total,
                                                  _stream(dev))

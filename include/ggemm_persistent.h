@@ -52,6 +52,29 @@ int ggemm_persistent_fp8(const void* a, const void* b, void* out, const float* a
                          int32_t stride_bg, int32_t stride_bn, int32_t stride_cm, int32_t stride_cn,
                          int32_t a_format, int64_t M_total, void* stream);
 
+/* Kernels behind ggemm_persistent_fp8 (same semantics; each deterministic, the two differ in
+ * fp32 summation order): the 512-thread kernel of the reference's launch geometry (192-row tiles,
+ * also the drop-in code objects) and a wide-tile kernel (256 threads, one wave per SIMD, 256 x 320
+ * tiles, 160 KiB of LDS) for N % 320 == 0, K % 64 == 0, 256*stride_am, 320*stride_bn and
+ * 512*stride_cm below 2^31 - 2^16. ggemm_persistent_fp8 runs the wide kernel where it applies and
+ * stride_am and stride_bn are multiples of 128 (row segments on whole 128-byte lines). */
+#define GGEMM_PERSISTENT_KERNEL_AUTO 0
+#define GGEMM_PERSISTENT_KERNEL_512 1
+#define GGEMM_PERSISTENT_KERNEL_WIDE 2
+
+/* ggemm_persistent_fp8 with the kernel chosen by the caller: GGEMM_PERSISTENT_KERNEL_AUTO (as
+ * ggemm_persistent_fp8), _512 or _WIDE (GGEMM_E_SHAPE where the wide kernel does not apply). No
+ * reference counterpart (the reference ships one kernel); for comparisons of the two kernels. */
+int ggemm_persistent_fp8_kernel(const void* a, const void* b, void* out, const float* a_scale, const float* b_scale,
+                                const int64_t* group_offs, int32_t G, int32_t N, int32_t K, int32_t stride_am,
+                                int32_t stride_bg, int32_t stride_bn, int32_t stride_cm, int32_t stride_cn,
+                                int32_t a_format, int64_t M_total, int32_t kernel, void* stream);
+
+/* The kernel ggemm_persistent_fp8 runs for this shape and these strides (_512 or _WIDE). No
+ * reference counterpart. */
+int32_t ggemm_persistent_selected_kernel(int32_t N, int32_t K, int32_t stride_am, int32_t stride_bn,
+                                         int32_t stride_cm);
+
 /* Zeroes rows [min(offs[G], M_total), M_total) of out (bf16 [M_total, N], row stride stride_cm):
  * the rows ggemm_persistent_fp8 leaves unwritten when routing drops tokens (offs[G] < M_total).
  * offs[G] is read on the device, so the call needs no host synchronisation and can be captured in

@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define GGEMM_VARK_ABI_VERSION 7
+#define GGEMM_VARK_ABI_VERSION 8
 
 enum {
   GGEMM_OK = 0,
