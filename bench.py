@@ -66,6 +66,13 @@ def parse_args():
                     help="time the reference's call sites (one, or a group) with its own input recipe and print "
                          "a per-site summary table; replaces --config")
     ap.add_argument("--mfma", default="k128", choices=["k128", "k32"])
+    ap.add_argument("--persistent-kernel", default="auto", choices=["auto", "512", "wide"],
+                    help="fwd / dgrad sites: the library's kernel choice, or the 512-thread or the wide-tile "
+                         "persistent kernel forced")
+    ap.add_argument("--row-align", type=int, default=0,
+                    help="fwd / dgrad sites: copy A and B into buffers whose row strides are multiples of this "
+                         "many bytes (128: row segments on whole lines, the autograd op's layout); 0 keeps the "
+                         "reference's contiguous inputs")
     ap.add_argument("--out", default="bf16", choices=["bf16", "f32", "f32_accum"],
                     help="tensorwise wgrad configs: C bf16, fp32, or fp32 accumulated in place (C += result)")
     ap.add_argument("--lens", default="multinomial", choices=["multinomial", "reference"],
@@ -128,14 +135,28 @@ def print_info(pkg):
         print(json.dumps(harness.kernel_info(path)), flush=True)
 
 
-def make_runner(pkg, p, dev, mfma):
+def fwd_operands(p, row_align):
+    """A and B of a fwd / dgrad site, in buffers with row strides rounded up to row_align bytes
+    (views of the logical shape) when row_align > 0."""
+    import torch
+    a, b = p.a, p.b
+    if row_align and p.K % row_align:
+        kp = -(-p.K // row_align) * row_align
+        a = torch.zeros((p.M, kp), dtype=torch.uint8, device=p.a.device)[:, :p.K]
+        a.copy_(p.a)
+        b = torch.zeros((p.G, p.N, kp), dtype=torch.uint8, device=p.b.device)[:, :, :p.K]
+        b.copy_(p.b)
+    return a.view(p.a_dtype), b.view(torch.float8_e4m3fn)
+
+
+def make_runner(pkg, p, dev, mfma, kernel="auto", row_align=0):
     import torch
     if hasattr(p, "a_format"):   # forward / data-gradient site: the persistent grouped GEMM
         sa = torch.tensor(p.a_scale, dtype=torch.float32, device=dev)
         sb = torch.tensor(p.b_scale, dtype=torch.float32, device=dev)
         out = torch.empty((p.M, p.N), dtype=torch.bfloat16, device=dev)
-        a, b = p.a.view(p.a_dtype), p.b.view(torch.float8_e4m3fn)
-        return lambda: pkg.grouped_gemm_fp8_tensorwise(a, b, sa, sb, p.group_offs, out=out)
+        a, b = fwd_operands(p, row_align)
+        return lambda: pkg.grouped_gemm_fp8_tensorwise(a, b, sa, sb, p.group_offs, out=out, kernel=kernel)
     if p.is_mx:
         out = torch.empty((p.G, p.OUT_M, p.OUT_N), dtype=torch.bfloat16, device=dev)
         return lambda: pkg.grouped_gemm_mxfp8_variable_k(p.lhs, p.rhs, p.lhs_mx, p.rhs_mx, p.group_offs, out=out)
@@ -362,7 +383,7 @@ def main_sites(args, pkg, dev):
         else:
             p = pkg.inputs.make_wgrad_site_problem(name, seed=args.seed, device=dev)
         torch.cuda.synchronize()
-        run = make_runner(pkg, p, dev, args.mfma)
+        run = make_runner(pkg, p, dev, args.mfma, args.persistent_kernel, args.row_align)
         ms = time_steps(run, args.steps, args.warmup)
         rows.append({"site": name, "ms": round(ms, 4), "TFLOPS": round(p.flops / (ms * 1e-3) / 1e12, 2),
                      "TFLOP": round(p.flops / 1e12, 4)})
@@ -422,6 +443,8 @@ def main():
         return
     fwd = args.config in FWD_SITES
     tw_wgrad = args.config in ("gate_up_wgrad", "down_wgrad", "gate_up_zipf")
+    if (args.persistent_kernel != "auto" or args.row_align) and not fwd:
+        raise SystemExit("--persistent-kernel / --row-align apply to the fwd / dgrad sites")
     if (args.out != "bf16" or args.lens != "multinomial") and not tw_wgrad:
         raise SystemExit("--out / --lens apply to the tensorwise wgrad configs (gate_up_wgrad, down_wgrad, "
                          "gate_up_zipf)")
@@ -441,7 +464,7 @@ def main():
                                                                   out_dtype=torch.float32,
                                                                   accumulate=args.out == "f32_accum")
     else:
-        run = make_runner(pkg, p, dev, args.mfma)
+        run = make_runner(pkg, p, dev, args.mfma, args.persistent_kernel, args.row_align)
     ms = time_steps(run, args.steps, args.warmup)
     tflops = p.flops / (ms * 1e-3) / 1e12
     # traffic measured for this exact variant (profiles/traffic_<config>[_<out>][_reference_lens].txt)
@@ -449,14 +472,17 @@ def main():
                                            + ("" if args.lens == "multinomial" else "_reference_lens"))
     if fwd:
         geo = pkg.launch_geometry(p.N)
+        stride = -(-p.K // args.row_align) * args.row_align if args.row_align else p.K
+        kern = args.persistent_kernel
+        if kern == "auto":
+            kern = pkg.persistent.selected_kernel(p.N, p.K, stride, stride, p.N)
         config = {"workload": p.name, "G": p.G, "M_total": p.M, "K": p.K, "N": p.N,
                   "a": {"e4m3": "e4m3fn", "e5m2": "e5m2"}[p.a_format], "b": "e4m3fn [G, N, K] (trans_b)",
                   "out": "bf16", "acc": "fp32",
                   "inputs": "reference recipe: seed-42 exponential group sizes, randn bf16 cast to fp8, "
-                            "scales 0.1, in HBM",
+                            "scales 0.1, in HBM" + (f", A and B row strides {stride} bytes" if stride != p.K else ""),
                   "kernel": ("hip gfx950 persistent wide 256x320 tiles (256 threads, one wave per SIMD, generated "
-                             "assembly), 128-K stages, mfma 32x32x64"
-                             if pkg.persistent.selected_kernel(p.N, p.K, p.a.stride(0), p.b.stride(1), p.N) == "wide"
+                             "assembly), 128-K stages, mfma 32x32x64" if kern == "wide"
                              else "hip gfx950 persistent {tile_m}x{tile_n} tiles, 128-K stages, mfma k128".format(**geo)),
                   "baseline_number": "none published for this site"}
         vs_baseline = None
