@@ -265,11 +265,25 @@ __global__ void __launch_bounds__(kThreads) quant_tensorwise_kernel(const void* 
 // N-major). rows and cols are multiples of 16. Persistent grid over 128 x 128 tiles, so every row
 // segment of q and of q^T a tile writes is one whole 128-byte line: thread t quantizes 16 elements
 // of each of the tile rows t / 8 + 32h (h = 0..3; all four loads issued before any is used), writes
-// its bytes of q and deposits them in an LDS tile (row pitch 132 bytes); after a barrier it gathers
-// 64 bytes of tile column t / 2 for q^T. The 16-element segments of a ragged edge tile are wholly
-// inside the matrix or outside.
+// its bytes of q and deposits them in an LDS tile (tt_off); after a barrier it reads the dwords of
+// tile columns 4 (t / 8) .. +3 in tile rows 16 (t % 8) .. +15 and writes 16 bytes to each of those
+// four q^T rows, so the 8 threads of a column group cover one 128-byte line per store instruction.
+// The 16-element segments of a ragged edge tile are wholly inside the matrix or outside.
 constexpr int kTT = 128;                    // transpose tile edge (elements)
-constexpr int kTTPitch = kTT + 4;           // LDS row pitch in bytes
+
+// LDS tile of the transposing producer: 128 rows of 128 bytes, 16-byte chunk k of row r stored at
+// chunk k ^ ((r >> 4) & 7). A thread's 16-byte write of a row chunk stays whole; the transposed
+// read (the dword of 4 columns from 16 consecutive rows per thread, 8 threads per row group) finds
+// the 8 row groups of a column group on 8 distinct chunk positions, i.e. distinct banks.
+__device__ __forceinline__ int tt_off(int r, int c) {
+  return r * kTT + ((((c >> 4) ^ (r >> 4)) & 7) << 4) + (c & 15);
+}
+
+// Bytes k of four dwords, packed low to high (one column of a 4 x 4 byte block).
+__device__ __forceinline__ uint32_t byte_col(uint32_t a, uint32_t b, uint32_t c, uint32_t d, int k) {
+  return ((a >> (8 * k)) & 0xffu) | (((b >> (8 * k)) & 0xffu) << 8) | (((c >> (8 * k)) & 0xffu) << 16) |
+         (((d >> (8 * k)) & 0xffu) << 24);
+}
 
 template <bool kF32, bool kE5M2, bool kFast>
 __device__ __forceinline__ void transpose_body(const void* x, int batch, int rows, int cols, uint8_t* out,
@@ -278,8 +292,8 @@ __device__ __forceinline__ void transpose_body(const void* x, int batch, int row
   const int tid = threadIdx.x;
   const int tr = tid >> 3;                  // first tile row (then + 32, + 64, + 96)
   const int tc = 16 * (tid & 7);            // first tile column of this thread's segments
-  const int qc = tid >> 1;                  // q^T: tile column (row of q^T)
-  const int qb = 64 * (tid & 1);            // q^T: first tile row of this thread's 64 bytes
+  const int cg = tid >> 3;                  // q^T: tile columns 4 cg .. 4 cg + 3 (rows of q^T)
+  const int rj = tid & 7;                   // q^T: tile rows 16 rj .. 16 rj + 15 (8 threads: one line)
   const int rt = (rows + kTT - 1) / kTT, ct = (cols + kTT - 1) / kTT;
   const int per = rt * ct;
   const int64_t tiles = (int64_t)batch * per;
@@ -309,20 +323,21 @@ __device__ __forceinline__ void transpose_body(const void* x, int batch, int row
                                 clamp_fmax<kE5M2>(div_scale<kFast>(v[h][4 * k + 3], d)));
       const int64_t row = (int64_t)b * rows + r0 + tr + 32 * h;
       if (out) *(v4u*)(out + row * out_stride + c0 + tc) = v4u{w[0], w[1], w[2], w[3]};
-#pragma unroll
-      for (int k = 0; k < 4; ++k) *(uint32_t*)(s_t + (tr + 32 * h) * kTTPitch + tc + 4 * k) = w[k];
+      *(v4u*)(s_t + tt_off(tr + 32 * h, tc)) = v4u{w[0], w[1], w[2], w[3]};
     }
     __syncthreads();
-    if (c0 + qc < cols) {
-      uint8_t* dst = out_t + ((int64_t)b * cols + c0 + qc) * out_t_stride + r0 + qb;
+    // q^T: the dwords of columns 4 cg .. 4 cg + 3 in rows 16 rj + i, transposed in registers into
+    // 16 bytes of each of the four q^T rows; a store instruction's 8 threads of a row group write
+    // one whole 128-byte line
+    if (r0 + 16 * rj < rows && c0 + 4 * cg < cols) {
+      uint32_t dw[16];
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        if (r0 + qb + 16 * h >= rows) continue;
-        uint32_t o[4] = {0u, 0u, 0u, 0u};
+      for (int i = 0; i < 16; ++i) dw[i] = *(const uint32_t*)(s_t + tt_off(16 * rj + i, 4 * cg));
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-          o[i >> 2] |= (uint32_t)s_t[(qb + 16 * h + i) * kTTPitch + qc] << (8 * (i & 3));
-        *(v4u*)(dst + 16 * h) = v4u{o[0], o[1], o[2], o[3]};
+      for (int k = 0; k < 4; ++k) {
+        uint8_t* dst = out_t + ((int64_t)b * cols + c0 + 4 * cg + k) * out_t_stride + r0 + 16 * rj;
+        *(v4u*)dst = v4u{byte_col(dw[0], dw[1], dw[2], dw[3], k), byte_col(dw[4], dw[5], dw[6], dw[7], k),
+                         byte_col(dw[8], dw[9], dw[10], dw[11], k), byte_col(dw[12], dw[13], dw[14], dw[15], k)};
       }
     }
     __syncthreads();
@@ -334,7 +349,7 @@ __global__ void __launch_bounds__(kThreads) quant_transpose_kernel(const void* x
                                                                    uint8_t* out, int64_t out_stride, uint8_t* out_t,
                                                                    int64_t out_t_stride, const uint32_t* amax_bits,
                                                                    float* scale_out) {
-  __shared__ uint8_t s_t[kTT * kTTPitch];
+  __shared__ __attribute__((aligned(16))) uint8_t s_t[kTT * kTT];
   const ScaleDiv d = scale_div<kE5M2>(*amax_bits);
   if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = d.scale;
   if (d.fast)

@@ -102,11 +102,21 @@ def test_grouped_linear_refuses_cpu(pkg):
 
 # ----------------------------------------------------------------------------- transpose index model
 
-def _transpose_model(B, R, C, q_stride, t_stride):
-    """Restatement of the 128 x 128 tile arithmetic of quant_transpose_kernel (and of
-    ggemm_persistent_transpose_u8, which shares it): every byte of q and of q^T written exactly
-    once from the right source element, no access outside the buffers."""
-    T, P = 128, 132
+def _tt_off(r, c):
+    """quant_kernel.h's LDS tile map: 128-byte rows, 16-byte chunk k of row r at k ^ ((r >> 4) & 7)."""
+    return r * 128 + ((((c >> 4) ^ (r >> 4)) & 7) << 4) + (c & 15)
+
+
+def _transpose_model(B, R, C, q_stride, t_stride, gather="lines"):
+    """Restatement of the 128 x 128 tile arithmetic of quant_transpose_kernel (gather="lines": LDS
+    map _tt_off, q^T from the dwords of 4 columns x 16 rows per thread) and of
+    ggemm_persistent_transpose_u8 (gather="columns": row pitch 132, 64 bytes of one column per
+    thread): every byte of q and of q^T written exactly once from the right source element, no
+    access outside the buffers, and (lines) every q^T store instruction of a wave writing whole
+    128-byte segments."""
+    T = 128
+    P = 132 if gather == "columns" else 128
+    loc = (lambda r, c: r * P + c) if gather == "columns" else _tt_off
     rt, ct = -(-R // T), -(-C // T)
     per = rt * ct
     x = np.arange(B * R * C, dtype=np.int64).reshape(B, R, C)
@@ -126,22 +136,46 @@ def _transpose_model(B, R, C, q_stride, t_stride):
                     o = row * q_stride + c0 + tc
                     assert o + 16 <= q.size and (q[o:o + 16] == -1).all()
                     q[o:o + 16] = vals
-                    lo = (tr + 32 * h) * P + tc
-                    assert lo + 16 <= T * P
+                    lo = loc(tr + 32 * h, tc)
+                    assert lo + 16 <= T * P and all(loc(tr + 32 * h, tc + i) == lo + i for i in range(16))
                     lds[lo:lo + 16] = vals
-        for tid in range(256):
-            qc, qb = tid >> 1, 64 * (tid & 1)
-            if c0 + qc >= C:
-                continue
-            base = (b * C + c0 + qc) * t_stride + r0 + qb
-            for h in range(4):
-                if r0 + qb + 16 * h >= R:
+        if gather == "columns":
+            for tid in range(256):
+                qc, qb = tid >> 1, 64 * (tid & 1)
+                if c0 + qc >= C:
                     continue
-                vals = [lds[(qb + 16 * h + i) * P + qc] for i in range(16)]
-                assert min(vals) >= 0 and r0 + qb + 16 * h + 16 <= R
-                o = base + 16 * h
-                assert o + 16 <= qt.size and (qt[o:o + 16] == -1).all()
-                qt[o:o + 16] = vals
+                base = (b * C + c0 + qc) * t_stride + r0 + qb
+                for h in range(4):
+                    if r0 + qb + 16 * h >= R:
+                        continue
+                    vals = [lds[(qb + 16 * h + i) * P + qc] for i in range(16)]
+                    assert min(vals) >= 0 and r0 + qb + 16 * h + 16 <= R
+                    o = base + 16 * h
+                    assert o + 16 <= qt.size and (qt[o:o + 16] == -1).all()
+                    qt[o:o + 16] = vals
+            continue
+        for k in range(4):                       # one store instruction per k
+            for wave in range(4):
+                segs = {}
+                for lane in range(64):
+                    tid = 64 * wave + lane
+                    cg, rj = tid >> 3, tid & 7
+                    if not (r0 + 16 * rj < R and c0 + 4 * cg < C):
+                        continue
+                    assert c0 + 4 * cg + 4 <= C and r0 + 16 * rj + 16 <= R
+                    # dwords of columns 4 cg .. 4 cg + 3 of rows 16 rj + i, byte k of each
+                    vals = []
+                    for i in range(16):
+                        d0 = _tt_off(16 * rj + i, 4 * cg)
+                        assert d0 % 4 == 0 and all(_tt_off(16 * rj + i, 4 * cg + m) == d0 + m for m in range(4))
+                        vals.append(lds[d0 + k])
+                    assert min(vals) >= 0
+                    o = (b * C + c0 + 4 * cg + k) * t_stride + r0 + 16 * rj
+                    assert o + 16 <= qt.size and (qt[o:o + 16] == -1).all()
+                    qt[o:o + 16] = vals
+                    segs.setdefault(o - 16 * rj, []).append(rj)
+                # 8 threads per q^T row: the 128 bytes from r0 (whole lines when t_stride and r0 are)
+                assert all(sorted(v) == list(range(len(v))) for v in segs.values())
     qv = q.reshape(B, R, q_stride)[:, :, :C]
     tv = qt.reshape(B, C, t_stride)[:, :, :R]
     assert np.array_equal(qv, x) and np.array_equal(tv, np.swapaxes(x, 1, 2))
@@ -149,13 +183,31 @@ def _transpose_model(B, R, C, q_stride, t_stride):
     assert (q.reshape(B, R, q_stride)[:, :, C:] == -1).all() and (qt.reshape(B, C, t_stride)[:, :, R:] == -1).all()
 
 
+@pytest.mark.parametrize("gather", ["lines", "columns"])
 @pytest.mark.parametrize("B,R,C,qs,ts", [
     (3, 80, 48, 48, 80), (1, 144, 208, 256, 256), (2, 272, 80, 128, 384), (1, 208, 64, 64, 208),
     (5, 16, 1040, 1040, 16), (1, 256, 384, 384, 256), (2, 16, 16, 128, 128),
 ])
-def test_transpose_tile_index_model(B, R, C, qs, ts):
-    _transpose_model(B, R, C, qs, ts)
+def test_transpose_tile_index_model(B, R, C, qs, ts, gather):
+    _transpose_model(B, R, C, qs, ts, gather)
 
+
+def test_transpose_gather_conflict_free():
+    """quant_transpose_kernel's LDS traffic: a wave's 16-byte row-chunk writes cover each 128-byte
+    row once per 8 lanes, and each dword read instruction of the gather touches 16 distinct
+    dwords in at most 2 passes of 32 banks (256 bytes for 64 lanes at 128 bytes per cycle)."""
+    for wave in range(4):
+        for h in range(4):
+            addrs = [_tt_off((64 * wave + l >> 3) + 32 * h, 16 * (l & 7)) for l in range(64)]
+            for g in range(8):
+                banks = sorted((a // 4 + m) % 32 for a in addrs[8 * g:8 * g + 8] for m in range(4))
+                assert banks == list(range(32))
+        for i in range(16):
+            dws = [_tt_off(16 * ((64 * wave + l) & 7) + i, 4 * ((64 * wave + l) >> 3)) // 4 for l in range(64)]
+            per_bank = {}
+            for dw in set(dws):
+                per_bank.setdefault(dw % 32, set()).add(dw)
+            assert max(len(v) for v in per_bank.values()) <= 2
 
 
 def test_overlapping_rows_are_copied_not_read_past():
