@@ -11,6 +11,7 @@
 #include "capi_common.h"
 #include "persistent_kernel.h"
 #include "persistent_wide.h"
+#include "transpose_tile.h"
 
 GGEMM_DEFINE_PERSISTENT_LIB_KERNEL(_grouped_fp8_persistent_gemm_kernel, false)
 GGEMM_DEFINE_PERSISTENT_LIB_KERNEL(_grouped_fp8_persistent_gemm_kernel_e5m2, true)
@@ -44,20 +45,22 @@ int validate(const void* a, const void* b, const void* out, const void* as, cons
   return GGEMM_OK;
 }
 
-// Byte transpose over 128 x 128 tiles (ggemm_persistent_transpose_u8): thread t loads 16 bytes of
-// each of the tile rows t / 8 + 32h (h = 0..3, all loads issued first) into an LDS tile (row pitch
-// 132 bytes), and after a barrier gathers 64 bytes of tile column t / 2, so four threads write one
-// whole 128-byte line of the destination row. Edge tiles hold whole 16-byte segments.
-constexpr int kXT = 128, kXPitch = kXT + 4, kXThreads = 256;
+// Byte transpose over 128 x 128 tiles (ggemm_persistent_transpose_u8), the tile scheme of the
+// quantize-and-transpose producer (transpose_tile.h: LDS map tt_off, byte_col): thread t loads 16
+// bytes of each of the tile rows t / 8 + 32h (h = 0..3, all loads issued first) into the LDS tile;
+// after a barrier it reads the dwords of tile columns 4 (t / 8) .. +3 in tile rows 16 (t % 8) ..
+// +15 and writes 16 bytes to each of those four destination rows, so a store instruction's 8
+// threads of a column group write one whole 128-byte line. Edge tiles hold whole 16-byte segments.
+constexpr int kXT = 128, kXThreads = 256;
 typedef unsigned int xv4u __attribute__((ext_vector_type(4)));
 
 __global__ void __launch_bounds__(kXThreads) transpose_u8_kernel(const uint8_t* src, int batch, int rows, int cols,
                                                                  int64_t sb, int64_t sr, uint8_t* dst, int64_t db,
                                                                  int64_t dr) {
-  __shared__ uint8_t s_t[kXT * kXPitch];
+  __shared__ __attribute__((aligned(16))) uint8_t s_t[kXT * kXT];
   const int tid = threadIdx.x;
   const int tr = tid >> 3, tc = 16 * (tid & 7);
-  const int qc = tid >> 1, qb = 64 * (tid & 1);
+  const int cg = tid >> 3, rj = tid & 7;
   const int rt = (rows + kXT - 1) / kXT, ct = (cols + kXT - 1) / kXT;
   const int per = rt * ct;
   const int64_t tiles = (int64_t)batch * per;
@@ -72,20 +75,18 @@ __global__ void __launch_bounds__(kXThreads) transpose_u8_kernel(const uint8_t* 
         v[h] = *(const xv4u*)(src + b * sb + (int64_t)(r0 + tr + 32 * h) * sr + c0 + tc);
 #pragma unroll
     for (int h = 0; h < 4; ++h)
-      if (c0 + tc < cols && r0 + tr + 32 * h < rows) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) *(uint32_t*)(s_t + (tr + 32 * h) * kXPitch + tc + 4 * k) = v[h][k];
-      }
+      if (c0 + tc < cols && r0 + tr + 32 * h < rows) *(xv4u*)(s_t + ggemm::qt::tt_off(tr + 32 * h, tc)) = v[h];
     __syncthreads();
-    if (c0 + qc < cols) {
-      uint8_t* out = dst + b * db + (int64_t)(c0 + qc) * dr + r0 + qb;
+    if (r0 + 16 * rj < rows && c0 + 4 * cg < cols) {
+      uint32_t dw[16];
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        if (r0 + qb + 16 * h >= rows) continue;
-        uint32_t o[4] = {0u, 0u, 0u, 0u};
+      for (int i = 0; i < 16; ++i) dw[i] = *(const uint32_t*)(s_t + ggemm::qt::tt_off(16 * rj + i, 4 * cg));
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[i >> 2] |= (uint32_t)s_t[(qb + 16 * h + i) * kXPitch + qc] << (8 * (i & 3));
-        *(xv4u*)(out + 16 * h) = xv4u{o[0], o[1], o[2], o[3]};
+      for (int k = 0; k < 4; ++k) {
+        using ggemm::qt::byte_col;
+        uint8_t* out = dst + b * db + (int64_t)(c0 + 4 * cg + k) * dr + r0 + 16 * rj;
+        *(xv4u*)out = xv4u{byte_col(dw[0], dw[1], dw[2], dw[3], k), byte_col(dw[4], dw[5], dw[6], dw[7], k),
+                           byte_col(dw[8], dw[9], dw[10], dw[11], k), byte_col(dw[12], dw[13], dw[14], dw[15], k)};
       }
     }
     __syncthreads();

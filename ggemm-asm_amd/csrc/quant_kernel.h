@@ -24,6 +24,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "transpose_tile.h"
+
 namespace ggemm {
 namespace qt {
 
@@ -269,21 +271,6 @@ __global__ void __launch_bounds__(kThreads) quant_tensorwise_kernel(const void* 
 // tile columns 4 (t / 8) .. +3 in tile rows 16 (t % 8) .. +15 and writes 16 bytes to each of those
 // four q^T rows, so the 8 threads of a column group cover one 128-byte line per store instruction.
 // The 16-element segments of a ragged edge tile are wholly inside the matrix or outside.
-constexpr int kTT = 128;                    // transpose tile edge (elements)
-
-// LDS tile of the transposing producer: 128 rows of 128 bytes, 16-byte chunk k of row r stored at
-// chunk k ^ ((r >> 4) & 7). A thread's 16-byte write of a row chunk stays whole; the transposed
-// read (the dword of 4 columns from 16 consecutive rows per thread, 8 threads per row group) finds
-// the 8 row groups of a column group on 8 distinct chunk positions, i.e. distinct banks.
-__device__ __forceinline__ int tt_off(int r, int c) {
-  return r * kTT + ((((c >> 4) ^ (r >> 4)) & 7) << 4) + (c & 15);
-}
-
-// Bytes k of four dwords, packed low to high (one column of a 4 x 4 byte block).
-__device__ __forceinline__ uint32_t byte_col(uint32_t a, uint32_t b, uint32_t c, uint32_t d, int k) {
-  return ((a >> (8 * k)) & 0xffu) | (((b >> (8 * k)) & 0xffu) << 8) | (((c >> (8 * k)) & 0xffu) << 16) |
-         (((d >> (8 * k)) & 0xffu) << 24);
-}
 
 template <bool kF32, bool kE5M2, bool kFast>
 __device__ __forceinline__ void transpose_body(const void* x, int batch, int rows, int cols, uint8_t* out,

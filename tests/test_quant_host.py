@@ -107,16 +107,14 @@ def _tt_off(r, c):
     return r * 128 + ((((c >> 4) ^ (r >> 4)) & 7) << 4) + (c & 15)
 
 
-def _transpose_model(B, R, C, q_stride, t_stride, gather="lines"):
-    """Restatement of the 128 x 128 tile arithmetic of quant_transpose_kernel (gather="lines": LDS
-    map _tt_off, q^T from the dwords of 4 columns x 16 rows per thread) and of
-    ggemm_persistent_transpose_u8 (gather="columns": row pitch 132, 64 bytes of one column per
-    thread): every byte of q and of q^T written exactly once from the right source element, no
-    access outside the buffers, and (lines) every q^T store instruction of a wave writing whole
-    128-byte segments."""
-    T = 128
-    P = 132 if gather == "columns" else 128
-    loc = (lambda r, c: r * P + c) if gather == "columns" else _tt_off
+def _transpose_model(B, R, C, q_stride, t_stride):
+    """Restatement of the 128 x 128 tile arithmetic of quant_transpose_kernel and of
+    ggemm_persistent_transpose_u8, which shares it (LDS map _tt_off, the transposed copy from the
+    dwords of 4 columns x 16 rows per thread): every byte of q and of q^T written exactly once from
+    the right source element, no access outside the buffers, and every q^T store instruction of a
+    wave writing whole 128-byte segments."""
+    T = P = 128
+    loc = _tt_off
     rt, ct = -(-R // T), -(-C // T)
     per = rt * ct
     x = np.arange(B * R * C, dtype=np.int64).reshape(B, R, C)
@@ -139,21 +137,6 @@ def _transpose_model(B, R, C, q_stride, t_stride, gather="lines"):
                     lo = loc(tr + 32 * h, tc)
                     assert lo + 16 <= T * P and all(loc(tr + 32 * h, tc + i) == lo + i for i in range(16))
                     lds[lo:lo + 16] = vals
-        if gather == "columns":
-            for tid in range(256):
-                qc, qb = tid >> 1, 64 * (tid & 1)
-                if c0 + qc >= C:
-                    continue
-                base = (b * C + c0 + qc) * t_stride + r0 + qb
-                for h in range(4):
-                    if r0 + qb + 16 * h >= R:
-                        continue
-                    vals = [lds[(qb + 16 * h + i) * P + qc] for i in range(16)]
-                    assert min(vals) >= 0 and r0 + qb + 16 * h + 16 <= R
-                    o = base + 16 * h
-                    assert o + 16 <= qt.size and (qt[o:o + 16] == -1).all()
-                    qt[o:o + 16] = vals
-            continue
         for k in range(4):                       # one store instruction per k
             for wave in range(4):
                 segs = {}
@@ -183,13 +166,12 @@ def _transpose_model(B, R, C, q_stride, t_stride, gather="lines"):
     assert (q.reshape(B, R, q_stride)[:, :, C:] == -1).all() and (qt.reshape(B, C, t_stride)[:, :, R:] == -1).all()
 
 
-@pytest.mark.parametrize("gather", ["lines", "columns"])
 @pytest.mark.parametrize("B,R,C,qs,ts", [
     (3, 80, 48, 48, 80), (1, 144, 208, 256, 256), (2, 272, 80, 128, 384), (1, 208, 64, 64, 208),
     (5, 16, 1040, 1040, 16), (1, 256, 384, 384, 256), (2, 16, 16, 128, 128),
 ])
-def test_transpose_tile_index_model(B, R, C, qs, ts, gather):
-    _transpose_model(B, R, C, qs, ts, gather)
+def test_transpose_tile_index_model(B, R, C, qs, ts):
+    _transpose_model(B, R, C, qs, ts)
 
 
 def test_transpose_gather_conflict_free():
