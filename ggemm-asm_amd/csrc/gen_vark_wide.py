@@ -887,14 +887,6 @@ class Gen:
 # stage: its second half is neither computed nor read.
 KSLOTS = 2
 KKS = 128                    # K bytes per stage
-WORD3_K = WORD3
-
-
-def kswz(r):
-    """Chunk swizzle of a 128-byte K row (persistent_kernel.h's): logical chunk c of row r at
-    physical chunk c ^ kswz(r); the 8 rows a 128-bit read serves together land on 8 distinct
-    chunks."""
-    return (r & 7) ^ ((r >> 3) & 1)
 
 
 class KConfig(Config):
@@ -1017,10 +1009,10 @@ class GenK(Gen):
         e(f"s_add_u32 {s['RR2']}, {s['RECB']}, {s['T']}")
         e(f"s_mov_b32 {s['RL0']}, {s['BL0']}")
         e(f"s_and_b32 {s['RL1']}, {s['BL1']}, 0xffff")
-        e(f"s_mov_b32 {s['RL3']}, 0x{WORD3_K:x}")
+        e(f"s_mov_b32 {s['RL3']}, 0x{WORD3:x}")
         e(f"s_mov_b32 {s['RR0']}, {s['BR0']}")
         e(f"s_and_b32 {s['RR1']}, {s['BR1']}, 0xffff")
-        e(f"s_mov_b32 {s['RR3']}, 0x{WORD3_K:x}")
+        e(f"s_mov_b32 {s['RR3']}, 0x{WORD3:x}")
         e(f"s_add_u32 {s['IB']}, {OP['lds_base']}, {s['ISLOT']}")
         e(f"s_add_u32 {s['IB']}, {s['IB']}, {OP['w1k']}")
 
