@@ -277,6 +277,48 @@ def test_persistent_validation_rejects(pkg, kw, rc):
         assert got == rc
 
 
+def _call_kernel(lib, kernel, **kw):
+    a = dict(a=FAKE, b=FAKE, out=FAKE, as_=FAKE, bs=FAKE, offs=FAKE, G=32, N=5760, K=2880, sam=2944,
+             sbg=5760 * 2944, sbn=2944, scm=5760, scn=1, fmt=0, M=131072)
+    a.update(kw)
+    return lib.ggemm_persistent_fp8_kernel(a["a"], a["b"], a["out"], a["as_"], a["bs"], a["offs"], a["G"], a["N"],
+                                           a["K"], a["sam"], a["sbg"], a["sbn"], a["scm"], a["scn"], a["fmt"], a["M"],
+                                           kernel, None)
+
+
+@pytest.mark.parametrize("kernel,kw,rc", [
+    # the argument checks come first, whatever the kernel
+    (2, dict(a=0), -1), (1, dict(G=0), -2),
+    # a kernel code outside AUTO / 512 / WIDE
+    (3, {}, -2), (-1, {}, -2),
+    # the wide kernel where it does not apply: N not a multiple of 320, K not of 64, and the 32-bit
+    # offsets of its 256-row A and C tiles (its 320 B rows are within the 384 every launch checks)
+    (2, dict(N=5376, sbg=5376 * 2944), -2), (2, dict(K=2896, sam=2896, sbn=2896, sbg=5760 * 2896), -2),
+    (2, dict(sam=8388352), -2), (2, dict(scm=4194240), -2),
+    # applicable shapes pass validation, then M_total = 0 returns before any launch
+    (2, dict(M=0), 0), (1, dict(M=0), 0), (0, dict(M=0), 0),
+    (2, dict(K=64, sam=64, sbn=64, sbg=5760 * 64, M=0), 0),
+])
+def test_persistent_kernel_choice_validation(pkg, kernel, kw, rc):
+    got = _call_kernel(pkg.load_library(), kernel, **kw)
+    if rc == 0:
+        assert got == 0 or got == -6, got   # -6: no device here (the device check precedes M_total = 0)
+    else:
+        assert got == rc, got
+
+
+def test_persistent_selected_kernel(pkg):
+    """The automatic choice: the wide kernel where it applies and A and B rows are line-aligned."""
+    sel = pkg.load_library().ggemm_persistent_selected_kernel
+    assert sel(5760, 2880, 2944, 2944, 5760) == 2          # the autograd op's aligned rows
+    assert sel(2880, 5760, 5760, 5760, 2880) == 2          # K = 5760: aligned when contiguous
+    assert sel(5760, 2880, 2880, 2880, 5760) == 1          # the reference's contiguous K = 2880
+    assert sel(5760, 2880, 2944, 2880, 5760) == 1          # one operand unaligned
+    assert sel(5376, 2944, 2944, 2944, 5376) == 1          # N not a multiple of 320
+    assert sel(640, 2880 + 48, 3072, 3072, 640) == 1       # K not a multiple of 64
+    assert sel(320, 64, 128, 128, 320) == 2
+
+
 def _xt(lib, **kw):
     a = dict(src=FAKE, B=2, R=64, C=48, sb=64 * 48, sr=48, dst=FAKE, db=48 * 64, dr=64)
     a.update(kw)
