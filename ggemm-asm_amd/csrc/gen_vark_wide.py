@@ -678,9 +678,11 @@ class Gen:
         """fp32 C, one 32 x 32 block per pass through a private 4 KiB LDS region: lane (r = l % 32,
         h = l / 32) writes its four 16-byte row pieces (chunk 2 g + h of row r, chunk c stored at
         c ^ (((r >> 1) & 3) << 1)); read-back k (0..3) gives lane l row 8 k + l / 8, chunk l % 8, so
-        each 1 KiB store covers 8 whole 128-byte row segments. Accumulating, the old values of the
-        next two passes are in flight while the current pass waits for its own (counted vmcnt), and
-        the product, rounded to fp32 first, is added to them."""
+        each 1 KiB store covers 8 whole 128-byte row segments. Accumulating, the product, rounded to
+        fp32 first, is added to the old values, whose loads run ahead of the pass that adds them:
+        the passes take the blocks held in VGPRs first, and each such block's 16 registers, free once
+        its pass has scaled them, join the three spare 16-register buffers that the old values load
+        into, so later passes keep up to 12 passes of loads in flight (counted vmcnt)."""
         s, OP, e, c = SGPR, self.OP, self.emit, self.cfg
         acc_mode = c.out == "f32acc"
         v0 = c.vop0                      # the operand registers are free here
@@ -703,18 +705,34 @@ class Gen:
         e(f"v_add_u32 v{rbase}, {s['EPI']}, {OP['frb']}")
         self.c_resource()
         blocks = [(i, j) for i in range(c.bm) for j in range(c.bn)]
+        if acc_mode:
+            # blocks held in VGPRs first: their registers become old-value buffers after their pass
+            blocks.sort(key=lambda ij: c.acc(*ij)[0] != "v")
         P = len(blocks)
+        pool = list(oset)        # free 16-register buffers for old values
+        buf = {}                 # pass -> its old-value buffer
+        vm_log = []              # vector memory operations of this epilogue, in issue order
+        issued = [0]             # passes whose old-value loads are out
 
-        def load_old(n):
+        def load_old(n, o0):
             i, j = blocks[n]
             for k in range(4):
-                o = oset[n % (look + 1)] + 4 * k
+                o = o0 + 4 * k
                 self.f32_store_offset(i, j, k)
                 e(f"buffer_load_dwordx4 v[{o}:{o + 3}], {c.vt2}, {s['RC']}, 0 offen")
+                vm_log.append(("L", n))
+
+        def issue_loads():
+            while issued[0] < P and pool:
+                n = issued[0]
+                buf[n] = pool.pop(0)
+                load_old(n, buf[n])
+                issued[0] += 1
 
         if acc_mode:
-            for n in range(min(look, P)):
-                load_old(n)
+            pool = pool[:look]   # two passes ahead at first, as many as buffers free up later
+            issue_loads()
+            pool = list(oset[look:])
         for n, (i, j) in enumerate(blocks):
             kind, base = c.acc(i, j)
             for g in range(4):
@@ -732,20 +750,24 @@ class Gen:
             for k in range(4):
                 e(f"ds_read_b128 v[{dset + 4 * k}:{dset + 4 * k + 3}], v{rbase} offset:{1024 * k}")
             if acc_mode:
-                if n + look < P:
-                    load_old(n + look)
-                # issued after this pass's old values: the next passes' loads and the stores of the
-                # passes since (vector memory counts complete in issue order)
-                later = 4 * sum(1 for m in range(n + 1, n + look + 1) if m < P) + 4 * min(n, look)
-                e(f"s_waitcnt vmcnt({later})")
+                if kind == "v":
+                    pool.append(base)          # scaled above: the block's registers are free
+                issue_loads()
+                # issued after this pass's old values: later passes' loads and the stores of the
+                # passes since (vector memory counts complete in issue order; vmcnt holds 63)
+                last = max(k for k, op in enumerate(vm_log) if op == ("L", n))
+                e(f"s_waitcnt vmcnt({min(len(vm_log) - 1 - last, 63)})")
             e("s_waitcnt lgkmcnt(0)")
             if acc_mode:
-                o0 = oset[n % (look + 1)]
+                o0 = buf[n]
                 for r in range(16):
                     e(f"v_add_f32 v{dset + r}, v{dset + r}, v{o0 + r}")
             for k in range(4):
                 self.f32_store_offset(i, j, k)
                 e(f"buffer_store_dwordx4 v[{dset + 4 * k}:{dset + 4 * k + 3}], {c.vt2}, {s['RC']}, 0 offen nt")
+                vm_log.append(("S", n))
+            if acc_mode:
+                pool.append(buf[n])            # added: the buffer takes a later pass's loads
         e(f"s_add_u32 {OP['vmt']}, {OP['vmt']}, {c.e_stores}")
 
     def zero_epilogue(self):

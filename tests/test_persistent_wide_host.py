@@ -413,11 +413,15 @@ def test_generated_include_lists_kmajor_configs():
 @pytest.mark.parametrize("cfg", [c.name for c in GEN.CONFIGS + GEN.KCONFIGS])
 def test_only_mfma_writes_accumulators(cfg):
     """Accumulator registers (AGPRs and the VGPRs from vacc0 up) are written by MFMAs alone: no
-    epilogue temporary, LDS load or address computation of any configuration lands on them."""
+    epilogue temporary, LDS load or address computation of any configuration lands on them. The
+    one exception is by design: the fp32-accumulate epilogue loads old C values into the VGPRs of a
+    block whose pass has already scaled them -- every v_mul_f32 reading such a register comes
+    earlier in the (straight-line) epilogue than the load that overwrites it."""
     c = {x.name: x for x in GEN.CONFIGS + GEN.KCONFIGS}[cfg]
     g = GEN.GenK(c) if isinstance(c, GEN.KConfig) else GEN.Gen(c)
     g.tile()
-    for line in g.lines:
+    reused = 0
+    for n, line in enumerate(g.lines):
         if line.endswith(":"):
             continue
         op, _, rest = line.partition(" ")
@@ -428,4 +432,12 @@ def test_only_mfma_writes_accumulators(cfg):
         for m in re.finditer(r"\bv(\d+)\b|v\[(\d+):(\d+)\]", dst):
             lo = int(m.group(1) or m.group(2))
             hi = int(m.group(1) or m.group(3))
-            assert hi < c.vacc0 or lo >= 256, line
+            if hi < c.vacc0 or lo >= 256:
+                continue
+            assert c.out == "f32acc" and op == "buffer_load_dwordx4", line
+            regs = {f"v{r}" for r in range(lo, hi + 1)}
+            reads = [k for k, ln in enumerate(g.lines) if ln.startswith("v_mul_f32 ")
+                     and ln.split(",")[-1].strip() in regs]
+            assert reads and max(reads) < n, line
+            reused += 1
+    assert (reused > 0) == (c.out == "f32acc")

@@ -195,6 +195,8 @@ class Block:
                 self.ev.append(("sread", self.v[reg], int(mod.split(":")[1]), a[0], halves))
             elif op in ("ds_write_b64", "ds_write_b128", "ds_read_b128"):
                 self.ev.append((op, a))
+            elif op == "v_add_f32":          # fp32 accumulation: the old value added to the product
+                self.ev.append(("vadd", a[0], a[1], a[2]))
             elif op.startswith("v_"):
                 pass
             else:
@@ -441,6 +443,33 @@ def _check(cfg, tiles, wave=0, stride_l=2880, stride_r=5760, stride_cm=5760, OUT
             for si, se in st_ev:
                 li = max(i for i, le in ol if le[1] == se[1] and i < si)
                 assert li in done_at and done_at[li] < si, "store before its old values arrived"
+            # register data flow: each stored register was last written by a v_add_f32 whose old-value
+            # operand was last written by the completed load of that store's offset, same position
+            # in the 16-byte chunk; accumulator registers reused as old-value buffers are loaded only
+            # after their block's last read (its v_mul_f32s precede every load into them here)
+            writer = {}
+            for idx in range(a, b):
+                e = ev[idx]
+                if e[0] == "oload":
+                    lo, hi = (int(x) for x in re.fullmatch(r"v\[(\d+):(\d+)\]", e[3]).groups())
+                    for r in range(lo, hi + 1):
+                        writer[r] = ("oload", idx, e[1], r - lo)
+                elif e[0] == "ds_read_b128":
+                    lo, hi = (int(x) for x in re.fullmatch(r"v\[(\d+):(\d+)\]", e[1][0]).groups())
+                    for r in range(lo, hi + 1):
+                        writer[r] = ("lds", idx)
+                elif e[0] == "vadd":
+                    d, s0, s1 = (int(x[1:]) for x in e[1:4])
+                    assert d == s0 and writer.get(d, ("",))[0] == "lds", e
+                    src = writer.get(s1)
+                    assert src and src[0] == "oload", f"old-value operand v{s1} not from a load: {src}"
+                    assert src[1] in done_at and done_at[src[1]] < idx, "add before its old value arrived"
+                    writer[d] = ("vadd", idx, src[2], src[3])
+                elif e[0] == "store":
+                    lo, hi = (int(x) for x in re.fullmatch(r"v\[(\d+):(\d+)\]", e[3]).groups())
+                    for r in range(lo, hi + 1):
+                        w = writer.get(r)
+                        assert w and w[0] == "vadd" and w[2] == e[1] and w[3] == r - lo, (e, w)
     assert state["np"] == 0 and state["nis"] == 0
     return ev
 
