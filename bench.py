@@ -14,7 +14,8 @@ bench.py:153-180, inputs as in bench.py:205-223,238-247; FLOPs = 2 * M_total * K
 ``--config gate_up_layer`` measures one training step of the FP8 grouped linear layer at the
 gate_up shape (x bf16 [131072, 2880], w bf16 [32, 5760, 2880], dy bf16 [131072, 5760]): quantize
 x and w, forward GEMM, quantize dy, dgrad GEMM, wgrad GEMM accumulated into an fp32 main-grad;
-FLOPs = 3 * 2 * M * K * N.
+FLOPs = 3 * 2 * M * K * N. ``--scaling delayed`` quantizes x and dy with delayed scaling (scale
+from an amax history, amax recorded in the quantizing pass: no amax pass over x or dy).
 
 ``--site all | all_fwd | all_wgrad | <site>`` runs the reference's call sites one after the other
 with its own input recipe and prints its summary table (per-site ms, TFLOPS, share of the total)
@@ -78,6 +79,9 @@ def parse_args():
     ap.add_argument("--lens", default="multinomial", choices=["multinomial", "reference"],
                     help="tensorwise wgrad configs: the configuration's group sizes, or the reference's seed-42 "
                          "exponential ones (reference bench.py:205-223)")
+    ap.add_argument("--scaling", default="current", choices=["current", "delayed"],
+                    help="gate_up_layer: x and dy quantized with their own amax (an amax pass each), or with "
+                         "delayed scaling (an amax history of 16; the amax reduced in the quantizing pass)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU work for the cpu_baseline sample (0 disables)")
@@ -321,7 +325,7 @@ def main_quant(args, pkg, dev):
 
 def main_layer(args, pkg, dev):
     import torch
-    from ggemm_asm_amd.autograd import grouped_linear_fp8
+    from ggemm_asm_amd.autograd import FP8DelayedScaling, grouped_linear_fp8
     gen = torch.Generator(device=dev).manual_seed(args.seed)
     M, K, N, G = pkg.inputs.M_TOTAL, pkg.inputs.F_DIM, pkg.inputs.F2_DIM, pkg.inputs.E_EXPERTS
     offs = pkg.inputs.make_group_offs(pkg.inputs.make_group_lens_reference()).to(dev)
@@ -329,10 +333,12 @@ def main_layer(args, pkg, dev):
     w = (torch.randn((G, N, K), generator=gen, device=dev, dtype=torch.bfloat16) * 0.02).requires_grad_(True)
     dy = torch.randn((M, N), generator=gen, device=dev, dtype=torch.bfloat16) * 1e-3
     main_grad = torch.zeros((G, K, N), dtype=torch.float32, device=dev)
+    # delayed: the first (warm-up) step seeds the history with current scaling
+    rec = FP8DelayedScaling(16) if args.scaling == "delayed" else None
 
     def step():
         x.grad = None
-        out = grouped_linear_fp8(x, w, offs, main_grad=main_grad)
+        out = grouped_linear_fp8(x, w, offs, main_grad=main_grad, scaling=rec)
         out.backward(dy)
 
     ms = time_steps(step, args.steps, args.warmup)
@@ -347,7 +353,7 @@ def main_layer(args, pkg, dev):
 
         def step_cached():
             x.grad = None
-            out = grouped_linear_fp8(x, w, offs, main_grad=main_grad, weight_cache=cache)
+            out = grouped_linear_fp8(x, w, offs, main_grad=main_grad, weight_cache=cache, scaling=rec)
             out.backward(dy)
 
         t = time_steps(step_cached, max(args.steps // 2, 10), max(args.warmup // 2, 5))
@@ -360,6 +366,7 @@ def main_layer(args, pkg, dev):
             "config": {"workload": "gate_up_layer", "G": G, "M_total": M, "K": K, "N": N,
                        "step": "quantize x, w (e4m3) + fwd GEMM + quantize dy (e5m2) + dgrad GEMM + wgrad GEMM "
                                "accumulated into an fp32 main-grad",
+                       "scaling": args.scaling + (" (amax history 16)" if rec else " (amax pass per tensor)"),
                        "inputs": "seed-42 exponential group sizes, randn bf16, in HBM"},
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP8_DENSE_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(tflops / FP8_DENSE_PEAK_TFLOPS, 4), "traffic": None},
@@ -438,6 +445,8 @@ def main():
     if args.config in QUANT_CONFIGS:
         main_quant(args, pkg, dev)
         return
+    if args.scaling != "current" and args.config not in LAYER_CONFIGS:
+        raise SystemExit("--scaling applies to gate_up_layer")
     if args.config in LAYER_CONFIGS:
         main_layer(args, pkg, dev)
         return

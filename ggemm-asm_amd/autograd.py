@@ -24,6 +24,9 @@ the autograd wiring left to the framework (Primus-Turbo, not vendored).
   calls and redone only when the weight changes (its storage, shape or version counter: an
   optimizer's in-place update bumps it). With gradient accumulation over several micro-batches
   the weight pass then runs once per update instead of once per step.
+* ``scaling=FP8DelayedScaling()``: x and dy are quantized with delayed scaling (the largest amax
+  of their previous calls, recorded on the device in the quantizing pass itself), which drops the
+  standalone amax passes over x and dy; values beyond the historical range saturate at +-fmax.
 There is no CPU path: the tensors must live on a gfx950 GPU.
 """
 from __future__ import annotations
@@ -33,7 +36,7 @@ import weakref
 import torch
 
 from .persistent import grouped_gemm_fp8_tensorwise
-from .quant import quantize_fp8_tensorwise, quantize_fp8_tensorwise_transpose
+from .quant import quantize_fp8_tensorwise, quantize_fp8_tensorwise_delayed, quantize_fp8_tensorwise_transpose
 from .vark import grouped_gemm_fp8_tensorwise_variable_k
 
 _LINE = 128   # bytes per cache line
@@ -84,16 +87,54 @@ class FP8WeightCache:
         self._ref = self._key = self._val = None
 
 
+class FP8DelayedScaling:
+    """Delayed-scaling recipe for one layer's activations (``"x"``, forward) and output gradients
+    (``"dy"``, backward).
+
+    Each tensor role keeps an fp32 amax history of ``history_len`` entries on the device. The first
+    call for a role quantizes with the tensor's own amax (current scaling) and records it; call n
+    after that takes slot n % history_len: the producer's delayed entry point scales by the largest
+    amax in the other slots, i.e. of up to ``history_len - 1`` previous calls, and writes this
+    tensor's amax into the slot in the same pass. The amax pass over the tensor is gone; a tensor
+    whose values outgrow the history saturates at +-fmax for that call. The slot index is host state,
+    so a graph capture replays one slot. ``calls`` counts the calls per role."""
+
+    def __init__(self, history_len: int = 16):
+        if not 2 <= history_len <= 1024:
+            raise ValueError("history_len must be in [2, 1024]")
+        self.history_len = history_len
+        self.history: dict[str, torch.Tensor] = {}
+        self.calls: dict[str, int] = {}
+
+    def quantize(self, role: str, x: torch.Tensor, fmt: str):
+        """(q, scale) of x for this role, rows on 128-byte lines."""
+        n = self.calls.get(role, 0)
+        hist = self.history.get(role)
+        if n == 0 or hist is None or hist.device != x.device:
+            q, scale, am = quantize_fp8_tensorwise(x, fmt, row_align=_LINE)
+            hist = torch.zeros(self.history_len, dtype=torch.float32, device=x.device)
+            hist[:1].copy_(am.reshape(1))
+            self.history[role] = hist
+            self.calls[role] = 1
+            return q, scale
+        q, scale = quantize_fp8_tensorwise_delayed(x, hist, n % self.history_len, fmt, row_align=_LINE)
+        self.calls[role] = n + 1
+        return q, scale
+
+
 class GroupedLinearFP8(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, w, group_offs, main_grad, weight_cache=None):
+    def forward(ctx, x, w, group_offs, main_grad, weight_cache=None, scaling=None):
         if x.dim() != 2 or w.dim() != 3 or x.shape[1] != w.shape[2]:
             raise ValueError("x must be [M, K] and w [G, N, K]")
         if w.shape[0] != group_offs.numel() - 1:
             raise ValueError("w holds one weight per group")
         # operand rows start on 128-byte lines (padded buffers): K-major rows of K = 2880 bytes
         # would otherwise straddle lines and cost the GEMMs 1.5 line requests per row segment
-        qx, sx, _ = quantize_fp8_tensorwise(x.contiguous(), "e4m3", row_align=_LINE)
+        if scaling is not None:
+            qx, sx = scaling.quantize("x", x.contiguous(), "e4m3")
+        else:
+            qx, sx, _ = quantize_fp8_tensorwise(x.contiguous(), "e4m3", row_align=_LINE)
         if weight_cache is not None:
             qw, qwt, sw = weight_cache.get(w, ctx.needs_input_grad[0])
         else:
@@ -102,13 +143,17 @@ class GroupedLinearFP8(torch.autograd.Function):
         out = grouped_gemm_fp8_tensorwise(qx, qw, sx, sw, group_offs, zero_tail=True)
         ctx.save_for_backward(qx, sx, qwt, sw, group_offs)
         ctx.main_grad = main_grad
+        ctx.scaling = scaling
         ctx.x_dtype, ctx.w_dtype = x.dtype, w.dtype
         return out
 
     @staticmethod
     def backward(ctx, dy):
         qx, sx, qwt, sw, group_offs = ctx.saved_tensors
-        qdy, sdy, _ = quantize_fp8_tensorwise(dy.contiguous(), "e5m2", row_align=_LINE)
+        if ctx.scaling is not None:
+            qdy, sdy = ctx.scaling.quantize("dy", dy.contiguous(), "e5m2")
+        else:
+            qdy, sdy, _ = quantize_fp8_tensorwise(dy.contiguous(), "e5m2", row_align=_LINE)
         dx = dw = None
         if ctx.needs_input_grad[0]:
             # dx[r] = dy[r] @ w[g]: B[g] = w[g]^T, [N_out = K, K_red = N] K-major
@@ -121,19 +166,21 @@ class GroupedLinearFP8(torch.autograd.Function):
             else:
                 dwt = grouped_gemm_fp8_tensorwise_variable_k(qx, qdy, sx, sdy, group_offs)   # [G, K, N]
                 dw = dwt.transpose(1, 2).to(ctx.w_dtype)
-        return dx, dw, None, None, None
+        return dx, dw, None, None, None, None
 
 
 def grouped_linear_fp8(x: torch.Tensor, w: torch.Tensor, group_offs: torch.Tensor,
                        main_grad: torch.Tensor | None = None,
-                       weight_cache: FP8WeightCache | None = None) -> torch.Tensor:
+                       weight_cache: FP8WeightCache | None = None,
+                       scaling: FP8DelayedScaling | None = None) -> torch.Tensor:
     """FP8 grouped linear layer: ``out[r] = x[r] @ w[g]^T`` for the rows of group g, bf16 out.
 
     x: bf16 / fp32 [M, K] (rows grouped by expert); w: bf16 / fp32 [G, N, K]; group_offs: int64
     [G+1] on the device. Backward gives dx [M, K] and dw [G, N, K]; with ``main_grad`` (fp32
     [G, K, N], the wgrad kernel's orientation) the weight gradient is added into it instead. With
-    ``weight_cache`` the weight's fp8 copy is reused while the weight is unchanged."""
+    ``weight_cache`` the weight's fp8 copy is reused while the weight is unchanged. With ``scaling``
+    (one FP8DelayedScaling per layer) x and dy take delayed scaling (module docstring)."""
     if main_grad is not None:
         if main_grad.dtype != torch.float32 or tuple(main_grad.shape) != (w.shape[0], w.shape[2], w.shape[1]):
             raise ValueError(f"main_grad must be fp32 [G, K, N] = {[w.shape[0], w.shape[2], w.shape[1]]}")
-    return GroupedLinearFP8.apply(x, w, group_offs, main_grad, weight_cache)
+    return GroupedLinearFP8.apply(x, w, group_offs, main_grad, weight_cache, scaling)

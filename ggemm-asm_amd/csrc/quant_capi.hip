@@ -85,6 +85,32 @@ int ggemm_quant_fp8_tensorwise(const void* x, int32_t in_dtype, int64_t rows, in
   return (int)hipGetLastError();
 }
 
+int ggemm_quant_fp8_tensorwise_delayed(const void* x, int32_t in_dtype, int64_t rows, int32_t cols, int64_t stride,
+                                       int32_t out_format, void* out, int64_t out_stride, float* amax_history,
+                                       int32_t history_len, int32_t slot, float* scale_out, void* stream) {
+  int rc = check_2d(x, in_dtype, rows, cols, stride);
+  if (rc) return rc;
+  if (!out || !amax_history || !scale_out) return GGEMM_E_NULL;
+  if (out_format != GGEMM_FP8_E4M3 && out_format != GGEMM_FP8_E5M2) return GGEMM_E_FORMAT;
+  if (history_len < 1 || history_len > GGEMM_QUANT_MAX_HISTORY || slot < 0 || slot >= history_len)
+    return GGEMM_E_SHAPE;
+  if (out_stride < cols || out_stride % 8) return GGEMM_E_STRIDE;
+  if (!aligned(out, 8) || !aligned(scale_out, 4) || !aligned(amax_history, 4)) return GGEMM_E_ALIGN;
+  int cus = 0;
+  rc = device_cus(&cus);
+  if (rc) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(qt::amax_init, dim3(1), dim3(64), 0, s, reinterpret_cast<uint32_t*>(amax_history + slot));
+  const int grid = grid_for(rows * (cols / 8), cus);
+  const bool f32 = in_dtype == GGEMM_IN_F32, e5 = out_format == GGEMM_FP8_E5M2;
+  auto k = f32 ? (e5 ? qt::quant_tensorwise_delayed_kernel<true, true> : qt::quant_tensorwise_delayed_kernel<true, false>)
+               : (e5 ? qt::quant_tensorwise_delayed_kernel<false, true>
+                     : qt::quant_tensorwise_delayed_kernel<false, false>);
+  hipLaunchKernelGGL(k, dim3(grid), dim3(qt::kThreads), 0, s, x, rows, cols, stride, static_cast<uint8_t*>(out),
+                     out_stride, amax_history, history_len, slot, scale_out);
+  return (int)hipGetLastError();
+}
+
 int ggemm_quant_fp8_tensorwise_transpose(const void* x, int32_t in_dtype, int32_t batch, int32_t rows, int32_t cols,
                                          int32_t out_format, void* out, int64_t out_stride, void* out_t,
                                          int64_t out_t_stride, float* scale_out, float* amax_out, void* stream) {

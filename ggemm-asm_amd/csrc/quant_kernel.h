@@ -146,6 +146,20 @@ __global__ void __launch_bounds__(64) amax_init(uint32_t* amax_bits) {
   if (threadIdx.x == 0) *amax_bits = 0u;
 }
 
+// The workgroup's max of its threads' m (|x| as fp32 bits) into *amax_bits, one atomic.
+__device__ __forceinline__ void block_amax(uint32_t m, uint32_t* amax_bits) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
+  __shared__ uint32_t s_m[kThreads / 64];
+  if ((threadIdx.x & 63) == 0) s_m[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) m = max(m, s_m[w]);
+    if (m) atomicMax(amax_bits, m);
+  }
+}
+
 // max of |x| as fp32 bits (ordered like unsigned integers for non-negative values; any NaN is
 // larger than +inf, so NaN propagates), one atomic per workgroup
 template <bool kF32>
@@ -170,16 +184,7 @@ __global__ void __launch_bounds__(kThreads) amax_kernel(const void* x, int64_t r
 #pragma unroll
       for (int k = 0; k < 8; ++k) m = max(m, __float_as_uint(v[u][k]) & 0x7fffffffu);
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
-  __shared__ uint32_t s_m[kThreads / 64];
-  if ((threadIdx.x & 63) == 0) s_m[threadIdx.x >> 6] = m;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-#pragma unroll
-    for (int w = 1; w < kThreads / 64; ++w) m = max(m, s_m[w]);
-    if (m) atomicMax(amax_bits, m);
-  }
+  block_amax(m, amax_bits);
 }
 
 // ---------------------------------------------------------------------------------- tensorwise
@@ -207,6 +212,14 @@ __device__ __forceinline__ ScaleDiv scale_div(uint32_t amax_bits) {
   const float scale = tensor_scale<kE5M2>(amax_bits);
   return ScaleDiv{scale, 1.0f / scale, amax >= 0x1p-60f && amax <= 3.4028235e38f};   // false for NaN
 }
+// A scale that does not come from this tensor's amax (delayed scaling: earlier steps' amax). The
+// FMA-corrected quotient (div_scale_guarded) is used for scales in [2^-80, 2^100]: the scale and
+// its reciprocal are normal, a residual can underflow only for |x| < 2^-102, whose quotient is below
+// 2^-22 and rounds to fp8 zero either way.
+__device__ __forceinline__ ScaleDiv scale_div_given(float scale) {
+  return ScaleDiv{scale, 1.0f / scale, scale >= 0x1p-80f && scale <= 0x1p100f};   // false for NaN
+}
+
 template <bool kFast>
 __device__ __forceinline__ float div_scale(float x, const ScaleDiv& d) {
   if constexpr (kFast) {
@@ -219,9 +232,27 @@ __device__ __forceinline__ float div_scale(float x, const ScaleDiv& d) {
   }
 }
 
-template <bool kF32, bool kE5M2, bool kFast>
-__device__ __forceinline__ void tensorwise_body(const void* x, int64_t rows, int cols, int64_t stride, uint8_t* out,
-                                                int64_t out_stride, const ScaleDiv& d) {
+// x / scale when |x / scale| is not bounded by fmax (a given scale): a product x (1 / scale) beyond
+// 2 fmax is returned as it is -- the exact quotient is then beyond fmax too and the clamp maps both
+// to +-fmax -- so the correction never meets an overflow; below it the corrected quotient is the
+// correctly rounded one (div_scale). NaN passes through.
+template <bool kFast, bool kE5M2>
+__device__ __forceinline__ float div_scale_guarded(float x, const ScaleDiv& d) {
+  if constexpr (kFast) {
+    const float q = x * d.inv;
+    if (!(__builtin_fabsf(q) <= 2.0f * fmax_of<kE5M2>())) return q;
+    return div_scale<true>(x, d);
+  } else {
+    return x / d.scale;
+  }
+}
+
+// kGiven: the scale is a given one (guarded quotients) and the thread's max |x| (fp32 bits) is
+// returned for the tensor's amax; otherwise 0.
+template <bool kF32, bool kE5M2, bool kFast, bool kGiven = false>
+__device__ __forceinline__ uint32_t tensorwise_body(const void* x, int64_t rows, int cols, int64_t stride,
+                                                    uint8_t* out, int64_t out_stride, const ScaleDiv& d) {
+  uint32_t m = 0;
   const int cpr = cols / 8;
   const int64_t n = rows * cpr;
   const int64_t T = (int64_t)gridDim.x * kThreads;
@@ -237,12 +268,20 @@ __device__ __forceinline__ void tensorwise_body(const void* x, int64_t rows, int
       if (i0 + u * T >= n) break;
       float y[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) y[k] = clamp_fmax<kE5M2>(div_scale<kFast>(v[u][k], d));
+      for (int k = 0; k < 8; ++k) {
+        if constexpr (kGiven) {
+          m = max(m, __float_as_uint(v[u][k]) & 0x7fffffffu);
+          y[k] = clamp_fmax<kE5M2>(div_scale_guarded<kFast, kE5M2>(v[u][k], d));
+        } else {
+          y[k] = clamp_fmax<kE5M2>(div_scale<kFast>(v[u][k], d));
+        }
+      }
       const uint32_t w0 = pack4_fp8<kE5M2>(y[0], y[1], y[2], y[3]);
       const uint32_t w1 = pack4_fp8<kE5M2>(y[4], y[5], y[6], y[7]);
       *(v2u*)(out + cw.row[u] * out_stride + 8 * (int64_t)cw.col[u]) = v2u{w0, w1};
     }
   }
+  return m;
 }
 
 template <bool kF32, bool kE5M2>
@@ -256,6 +295,24 @@ __global__ void __launch_bounds__(kThreads) quant_tensorwise_kernel(const void* 
     tensorwise_body<kF32, kE5M2, true>(x, rows, cols, stride, out, out_stride, d);
   else
     tensorwise_body<kF32, kE5M2, false>(x, rows, cols, stride, out, out_stride, d);
+}
+
+// Delayed scaling: scale = amax / fmax from the history's entries other than `slot` (the one this
+// call replaces; 1 when they are all zero, NaN when one is NaN), written to scale_out; x quantized
+// with it; the max |x| of this x reduced into hist[slot], which the host zeroed just before.
+template <bool kF32, bool kE5M2>
+__global__ void __launch_bounds__(kThreads) quant_tensorwise_delayed_kernel(const void* x, int64_t rows, int cols,
+                                                                            int64_t stride, uint8_t* out,
+                                                                            int64_t out_stride, float* hist, int H,
+                                                                            int slot, float* scale_out) {
+  uint32_t hm = 0;
+  for (int i = 0; i < H; ++i)
+    if (i != slot) hm = max(hm, __float_as_uint(hist[i]) & 0x7fffffffu);
+  const ScaleDiv d = scale_div_given(tensor_scale<kE5M2>(hm));
+  if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = d.scale;
+  const uint32_t m = d.fast ? tensorwise_body<kF32, kE5M2, true, true>(x, rows, cols, stride, out, out_stride, d)
+                            : tensorwise_body<kF32, kE5M2, false, true>(x, rows, cols, stride, out, out_stride, d);
+  block_amax(m, reinterpret_cast<uint32_t*>(hist + slot));
 }
 
 // ---------------------------------------------------------------------------------- tensorwise + transpose

@@ -110,6 +110,35 @@ def quantize_fp8_tensorwise(x: torch.Tensor, fmt: str = "e4m3", row_align: int |
     return q, scale, am
 
 
+def quantize_fp8_tensorwise_delayed(x: torch.Tensor, amax_history: torch.Tensor, slot: int, fmt: str = "e4m3",
+                                    row_align: int | None = None):
+    """Per-tensor FP8 quantization with delayed scaling. ``amax_history``: fp32 [H] on x's device;
+    the scale is ``max(amax_history[i] for i != slot) / fmax`` (1 when those are all 0), computed on
+    the device, and ``amax_history[slot]`` becomes this x's amax in the same pass (no separate amax
+    pass). Returns ``(q, scale)`` as ``quantize_fp8_tensorwise`` does; values beyond ``fmax * scale``
+    saturate to +-fmax."""
+    _check(x, fmt)
+    if amax_history.dtype != torch.float32 or amax_history.dim() != 1 or not amax_history.is_contiguous():
+        raise ValueError("amax_history must be a contiguous fp32 [H] tensor")
+    if amax_history.device != x.device:
+        raise ValueError("amax_history must be on x's device")
+    H = amax_history.numel()
+    if not 0 <= slot < H:
+        raise ValueError(f"slot {slot} outside the history of {H}")
+    x2 = _as_2d(x)
+    code, dt = _OUT[fmt]
+    q = _padded_empty(x.shape, row_align, dt, x.device)
+    q2 = q.as_strided((x2.shape[0], x.shape[-1]), (q.stride(-2), 1))
+    scale = torch.empty((), dtype=torch.float32, device=x.device)
+    qp = q2 if q2.shape[0] > 0 else torch.empty((1, x.shape[-1]), dtype=dt, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = _lib.load().ggemm_quant_fp8_tensorwise_delayed(
+            _ptr(x2), _IN[x.dtype], x2.shape[0], x2.shape[1], _row_stride(x2), code, qp.data_ptr(),
+            _row_stride(qp), amax_history.data_ptr(), H, slot, scale.data_ptr(), _stream(x.device))
+    _lib.check(rc, "ggemm_quant_fp8_tensorwise_delayed")
+    return q, scale
+
+
 def quantize_fp8_tensorwise_transpose(x: torch.Tensor, fmt: str = "e4m3", keep: bool = True,
                                       row_align: int | None = None):
     """Per-tensor FP8 quantization of a contiguous [B, R, C] (or [R, C]) tensor with a transposed

@@ -50,6 +50,23 @@ int ggemm_quant_fp8_tensorwise(const void* x, int32_t in_dtype, int64_t rows, in
                                int32_t out_format, void* out, int64_t out_stride, float* scale_out,
                                float* amax_out, void* stream);
 
+/* Longest amax history of ggemm_quant_fp8_tensorwise_delayed. */
+#define GGEMM_QUANT_MAX_HISTORY 1024
+
+/* Per-tensor quantization with delayed scaling: the scale comes from earlier amax values, and this
+ * tensor's amax is recorded in the same pass (no separate amax pass over x). amax_history is a
+ * device fp32 array of history_len entries; scale_out = m / fmax with m the largest entry other
+ * than amax_history[slot] (1 when m == 0, NaN when an entry is NaN); out[r, c] = fp8(clamp(x[r, c]
+ * / scale, -fmax, fmax)) with the same rounding as ggemm_quant_fp8_tensorwise; then
+ * amax_history[slot] = max |x| of this x (NaN propagates). A caller cycling slot through the
+ * history gets "the largest amax of the previous history_len - 1 calls" as its scale. Other
+ * requirements as for ggemm_quant_fp8_tensorwise; 1 <= history_len <= GGEMM_QUANT_MAX_HISTORY,
+ * 0 <= slot < history_len. No reference counterpart (the reference harness quantizes with fixed
+ * scales, bench.py:220-223); the FP8 grouped linear layer's delayed-scaling recipe uses it. */
+int ggemm_quant_fp8_tensorwise_delayed(const void* x, int32_t in_dtype, int64_t rows, int32_t cols, int64_t stride,
+                                       int32_t out_format, void* out, int64_t out_stride, float* amax_history,
+                                       int32_t history_len, int32_t slot, float* scale_out, void* stream);
+
 /* Per-tensor quantization of a batch of matrices with a transposed copy: x is a contiguous
  * [batch, rows, cols] (a weight [G, N, K]); amax_out and scale_out as in
  * ggemm_quant_fp8_tensorwise over all batch*rows*cols elements;

@@ -13,19 +13,26 @@ configurations:
 
 * per-tensor: ``amax = max|x|``, ``scale = fl32(amax / fmax)`` (1 when amax == 0),
   ``q = fp8(clamp(fl32(x / scale), -fmax, fmax))``;
+* per-tensor with delayed scaling (the layer's amax-history recipe; no reference counterpart):
+  the same with amax taken as the largest entry of an amax history other than the slot this call
+  replaces, and amax(x) recorded in that slot;
 * MX along the token axis: per 32-token block and column ``X = floor(log2(fl32(amax / fmax)))``
   (exact floor of the fp32 quotient's log2) clamped to [-127, 127], 0 for an all-zero block,
   e8m0 byte ``X + 127``; ``q = fp8(clamp(x * 2^-X, -fmax, fmax))``; each group padded with zero rows
   to a multiple of 32, padded offsets the prefix sums of ``ceil(len/32) * 32``.
 
 ``fp8()`` rounds to nearest even (subnormals included); NaN maps to a NaN code, ``0x7F | sign``
-here (the sign of a NaN result is unspecified in IEEE arithmetic, so checks compare NaN-ness).
+here (the sign of a NaN result is unspecified in IEEE arithmetic, and e5m2 has three NaN codes,
+0x7D-0x7F, so checks compare NaN-ness).
 
 Pinning (tests/test_oracle_quant.py): the encoder against torch's own float8 casts on every fp8
 value, every midpoint between neighbours (ties), both neighbours of each midpoint and random fp32
 values over the whole range; the per-tensor and MX recipes against their torch restatements in
 ``ggemm_asm_amd.inputs`` on random data; the MX exponent rule against exact rational arithmetic
-at and around powers of two; the padded layout against quantizing zero-padded groups one by one.
+at and around powers of two; the padded layout against quantizing zero-padded groups one by one;
+the delayed recipe against torch (scale from the history by torch's max and division, bytes by
+torch's float8 cast of the clamped quotient), the slot's old entry ignored, saturation codes and
+the special histories (all zero, NaN).
 """
 from __future__ import annotations
 
@@ -67,19 +74,40 @@ def amax(x) -> np.float32:
     return np.float32(np.max(np.abs(x))) if x.size else np.float32(0.0)   # np.max propagates NaN
 
 
+def tensor_scale(am, fmt: str) -> np.float32:
+    """fl32(amax / fmax); 1 for amax == 0; NaN stays NaN."""
+    am = np.float32(am)
+    if am > 0:
+        return np.float32(am / FMAX[fmt])
+    return np.float32(1.0) if am == 0 else am
+
+
+def quantize_with_scale(x, scale, fmt: str) -> np.ndarray:
+    """fp8(clamp(fl32(x / scale), -fmax, fmax)) bytes for a given fp32 scale."""
+    x = np.asarray(x, dtype=np.float32)
+    with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
+        return encode_fp8(_clamp((x / np.float32(scale)).astype(np.float32), fmt), fmt)
+
+
 def quantize_tensorwise(x, fmt: str):
     """(q bytes, scale, amax) of the per-tensor recipe; x float32 (bf16 inputs widened exactly)."""
     x = np.asarray(x, dtype=np.float32)
     am = amax(x)
-    if am > 0:
-        scale = np.float32(am / FMAX[fmt])
-    elif am == 0:
-        scale = np.float32(1.0)
-    else:
-        scale = am                                  # NaN
-    with np.errstate(invalid="ignore", divide="ignore"):
-        q = encode_fp8(_clamp((x / scale).astype(np.float32), fmt), fmt)
-    return q, scale, am
+    scale = tensor_scale(am, fmt)
+    return quantize_with_scale(x, scale, fmt), scale, am
+
+
+def quantize_tensorwise_delayed(x, history, slot: int, fmt: str):
+    """Delayed scaling: (q bytes, scale, new history). The scale is tensor_scale of the largest
+    |entry| of the amax history other than ``slot`` (NaN when one is NaN); x quantizes with it
+    (values beyond fmax * scale saturate); the new history holds amax(x) at ``slot``."""
+    x = np.asarray(x, dtype=np.float32)
+    h = np.asarray(history, dtype=np.float32).copy()
+    others = np.abs(np.delete(h, slot))
+    m = np.float32(np.max(others)) if others.size else np.float32(0.0)   # np.max propagates NaN
+    scale = tensor_scale(m, fmt)
+    h[slot] = amax(x)
+    return quantize_with_scale(x, scale, fmt), scale, h
 
 
 def block_exponent(amax_blk, fmt: str) -> np.ndarray:

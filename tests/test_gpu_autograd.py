@@ -167,3 +167,64 @@ def test_grouped_linear_fp8_weight_cache(pkg, cuda):
     torch.cuda.synchronize()
     assert torch.equal(out3.view(torch.int16), ref3.view(torch.int16))
     assert not torch.equal(out3.view(torch.int16), ref.view(torch.int16))
+
+
+def test_grouped_linear_fp8_delayed_scaling(pkg, orc, orp, cuda):
+    """scaling=FP8DelayedScaling: with the same x and dy every step the history holds their own
+    amax, so every output and gradient equals the current-scaling op's bit for bit; a step whose
+    x and dy shrink quantizes them with the scale of the history (the previous steps' larger
+    amax), which the forward and dgrad against the oracle on those bytes confirm, and records
+    their amax in the slot."""
+    from ggemm_asm_amd.autograd import FP8DelayedScaling, grouped_linear_fp8
+    lens, K, N = [96, 0, 160, 64], 192, 256
+    g = torch.Generator().manual_seed(29)
+    G, M = len(lens), sum(lens)
+    x0 = torch.randn((M, K), generator=g).to(torch.bfloat16).to(cuda)
+    w = (torch.randn((G, N, K), generator=g) * 0.05).to(torch.bfloat16).to(cuda)
+    dy = (torch.randn((M, N), generator=g) * 1e-2).to(torch.bfloat16).to(cuda)
+    offs = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int64, device=cuda)
+    o = offs.cpu().numpy()
+
+    def step(xv, dyv, scaling):
+        xg, wg = xv.clone().requires_grad_(True), w.clone().requires_grad_(True)
+        out = grouped_linear_fp8(xg, wg, offs, scaling=scaling)
+        out.backward(dyv)
+        return out, xg.grad, wg.grad
+
+    rec = FP8DelayedScaling(history_len=4)
+    _say("grouped linear fp8 delayed scaling: constant steps")
+    ref = step(x0, dy, None)
+    for n in range(3):
+        got = step(x0, dy, rec)
+        torch.cuda.synchronize()
+        for a, b in zip(got, ref):
+            assert torch.equal(a.view(torch.int16), b.view(torch.int16)), n
+    assert rec.calls == {"x": 3, "dy": 3}
+    hx, hdy = rec.history["x"].clone(), rec.history["dy"].clone()
+    ax, ady = float(pkg.amax(x0)), float(pkg.amax(dy))
+    assert hx.tolist() == [ax, ax, ax, 0.0] and hdy.tolist() == [ady, ady, ady, 0.0]
+
+    _say("grouped linear fp8 delayed scaling: shrinking step")
+    x1, dy1 = (x0.float() * 0.5).to(torch.bfloat16), (dy.float() * 0.25).to(torch.bfloat16)
+    out, dx, dw = step(x1, dy1, rec)
+    torch.cuda.synchronize()
+    assert rec.calls == {"x": 4, "dy": 4}
+    assert float(rec.history["x"][3]) == float(pkg.amax(x1)) and float(rec.history["dy"][3]) == float(pkg.amax(dy1))
+    qx, sx = pkg.quantize_fp8_tensorwise_delayed(x1, hx, 3, "e4m3")
+    qdy, sdy = pkg.quantize_fp8_tensorwise_delayed(dy1, hdy, 3, "e5m2")
+    qw, sw, _ = pkg.quantize_fp8_tensorwise(w, "e4m3")
+    assert float(sx) == float(np.float32(ax) / np.float32(448.0))
+    assert float(sdy) == float(np.float32(ady) / np.float32(57344.0))
+    m = orc.compare(pkg.as_bf16_bits(out), orp.grouped_fp8(_bytes(qx), _bytes(qw), float(sx), float(sw), o, "e4m3"))
+    _say(f"forward: {m}")
+    assert orc.parity_ok(m)
+    m = orc.compare(pkg.as_bf16_bits(dx), orp.grouped_fp8(_bytes(qdy), _bytes(qw), float(sdy), float(sw), o, "e5m2",
+                                                          trans_b=False))
+    _say(f"dgrad: {m}")
+    assert orc.parity_ok(m)
+    m = orc.compare(pkg.as_bf16_bits(dw.transpose(1, 2)),
+                    orc.vark_wgrad_tensorwise(_bytes(qx), _bytes(qdy), float(sx), float(sdy), o), o)
+    _say(f"wgrad: {m}")
+    assert orc.parity_ok(m)
+    ref64 = torch.cat([x1[o[i]:o[i + 1]].double() @ w[i].double().T for i in range(G)])
+    assert _cos(out, ref64) >= 0.99

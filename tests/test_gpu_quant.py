@@ -124,11 +124,18 @@ def test_tensorwise_quotients_near_ties(pkg, orq, cuda, fmt, amax):
     np.testing.assert_array_equal(_bytes(q_t)[0], q_ref.T)
 
 
-def _assert_bytes_nan_signless(got, ref):
-    """Bytes equal, except that a NaN code (0x7F / 0xFF) may carry either sign: the sign of a NaN
-    result is unspecified (the GPU's x / NaN and numpy's differ there)."""
-    nan = (ref & 0x7F) == 0x7F
-    assert np.all((got[nan] & 0x7F) == 0x7F)
+def _is_nan_code(b, fmt):
+    """e4m3fn has one NaN code per sign (0x7F); in e5m2 every code with the exponent all ones and a
+    nonzero mantissa (0x7D-0x7F) is a NaN."""
+    return (b & 0x7F) == 0x7F if fmt == "e4m3" else (b & 0x7F) > 0x7C
+
+
+def _assert_bytes_nan_signless(got, ref, fmt="e4m3"):
+    """Bytes equal, except where the oracle's byte is a NaN code: there any NaN code of the format,
+    with either sign, passes (the sign of a NaN result is unspecified, the GPU's x / NaN and numpy's
+    differ there, and e5m2 has several NaN codes)."""
+    nan = _is_nan_code(ref, fmt)
+    assert np.all(_is_nan_code(got[nan], fmt))
     np.testing.assert_array_equal(got[~nan], ref[~nan])
 
 
@@ -361,3 +368,118 @@ def test_tensorwise_producer_feeds_persistent_gemm(pkg, orc, orp, cuda):
     m = orc.compare(pkg.as_bf16_bits(out), ref)
     _say(f"tensorwise end to end: {m}")
     assert orc.parity_ok(m)
+
+
+def _delayed(pkg, x, hist, slot, fmt, cuda):
+    h = torch.from_numpy(np.asarray(hist, np.float32).copy()).to(cuda)
+    q, scale = pkg.quantize_fp8_tensorwise_delayed(torch.from_numpy(x).to(cuda) if isinstance(x, np.ndarray)
+                                                   else x.to(cuda), h, slot, fmt)
+    torch.cuda.synchronize()
+    return q, float(scale), h.cpu().numpy()
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", [(4096, 2880), (777, 136), (3, 8)])
+def test_delayed_bit_exact(pkg, orq, cuda, fmt, dtype, shape):
+    """Delayed scaling against the oracle: bytes, the scale from the history's other entries, and
+    the whole new history (max |x| at the slot, the rest untouched), for histories below x's range
+    (saturation), at it and above it; the slot's old entry (the largest) is ignored."""
+    g = torch.Generator().manual_seed(shape[0] + 1)
+    x = (torch.randn(shape, generator=g) * (1e-3 if fmt == "e5m2" else 1.0)).to(dtype)
+    xf = x.float().numpy()
+    am = float(np.abs(xf).max())
+    rng = np.random.default_rng(shape[1])
+    for hs, slot in ((0.5, 0), (1.0, 7), (3.0, 15)):
+        hist = (rng.uniform(0.3, 1.0, 16) * am * hs).astype(np.float32)
+        hist[slot] = 1e30
+        _say(f"delayed {fmt} {dtype} {shape} history x{hs} slot {slot}")
+        q, scale, h2 = _delayed(pkg, x, hist, slot, fmt, cuda)
+        q_ref, s_ref, h_ref = orq.quantize_tensorwise_delayed(xf, hist, slot, fmt)
+        assert q.dtype == TDT[fmt] and q.shape == x.shape
+        assert scale == float(s_ref)
+        np.testing.assert_array_equal(h2, h_ref)
+        np.testing.assert_array_equal(_bytes(q), q_ref)
+
+
+# history amax values: ordinary scales, the ends of the FMA-corrected quotient's scale range
+# [2^-80, 2^100] (as amax = scale * fmax) and one past each end (the plain division)
+DELAYED_AMAX = [613.76, 1.3e-4, "lo", "lo-", "hi", "hi+"]
+
+
+def _delayed_amax(tag, fmt):
+    fmax = float(orq_fmax(fmt))
+    return {"lo": 2.0 ** -80 * fmax, "lo-": 2.0 ** -81 * fmax * 1.3, "hi": 2.0 ** 100 * fmax,
+            "hi+": 2.0 ** 101 * fmax * 1.1}.get(tag, tag)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("tag", DELAYED_AMAX, ids=[f"a{i}" for i in range(len(DELAYED_AMAX))])
+def test_delayed_quotients_near_ties_and_saturation(pkg, orq, cuda, fmt, tag):
+    """The given-scale quotient is the correctly rounded one near every fp8 tie (x up to the
+    history's amax), and x far beyond it saturates, products overflowing fp32 included: the inputs
+    of the near-tie test plus the same scaled by 1.5, 2 +- ulps (the kernel's 2 fmax guard), 2^20
+    and up to FLT_MAX, and infinities."""
+    amax = np.float32(_delayed_amax(tag, fmt))
+    v = _near_tie_inputs(fmt, float(amax), seed=3).reshape(-1)
+    big = [v * np.float32(1.5), v * np.float32(2.0)]
+    big += [np.nextafter(big[1], np.float32(np.inf)), np.nextafter(big[1], np.float32(0))]
+    with np.errstate(over="ignore"):
+        big += [v * np.float32(2.0 ** 20), np.float32(3.4e38) * np.sign(v[:4096])]
+    w = np.concatenate([v] + [b.astype(np.float32) for b in big] + [[np.inf, -np.inf]]).astype(np.float32)
+    w = np.where(np.isfinite(w) | np.isinf(w), w, 0).astype(np.float32)
+    w = np.concatenate([w, np.zeros((-w.size) % 1024, np.float32)]).reshape(-1, 64)
+    hist = np.array([0.0, amax, amax * np.float32(0.25), 0.0], np.float32)
+    _say(f"delayed near ties {fmt} amax={amax} {w.shape}")
+    q, scale, h2 = _delayed(pkg, w, hist, 3, fmt, cuda)
+    q_ref, s_ref, h_ref = orq.quantize_tensorwise_delayed(w, hist, 3, fmt)
+    assert scale == float(s_ref) and np.isinf(h2[3])
+    np.testing.assert_array_equal(h2, h_ref)
+    np.testing.assert_array_equal(_bytes(q), q_ref)
+
+
+def test_delayed_special_histories_and_inputs(pkg, orq, cuda):
+    x = torch.randn((64, 128)).to(torch.bfloat16)
+    xf = x.float().numpy()
+    _say("delayed zero history / NaN history / NaN input / empty input")
+    q, scale, h2 = _delayed(pkg, x, np.zeros(4, np.float32), 2, "e4m3", cuda)     # scale 1
+    q_ref, s_ref, h_ref = orq.quantize_tensorwise_delayed(xf, np.zeros(4, np.float32), 2, "e4m3")
+    assert scale == 1.0 == s_ref
+    np.testing.assert_array_equal(h2, h_ref)
+    np.testing.assert_array_equal(_bytes(q), q_ref)
+    hist = np.array([1.0, np.nan, 2.0], np.float32)                             # NaN entry: NaN scale
+    q, scale, h2 = _delayed(pkg, x, hist, 0, "e5m2", cuda)
+    q_ref, _, h_ref = orq.quantize_tensorwise_delayed(xf, hist, 0, "e5m2")
+    assert np.isnan(scale) and h2[0] == h_ref[0] and np.isnan(h2[1])
+    _assert_bytes_nan_signless(_bytes(q), q_ref, "e5m2")
+    y = x.clone()
+    y[5, 9] = float("nan")                                                       # NaN input: NaN amax
+    q, scale, h2 = _delayed(pkg, y, np.array([3.0, 9.0], np.float32), 1, "e4m3", cuda)
+    q_ref, s_ref, _ = orq.quantize_tensorwise_delayed(y.float().numpy(), np.array([3.0, 9.0], np.float32), 1,
+                                                      "e4m3")
+    assert scale == float(s_ref) and h2[0] == 3.0 and np.isnan(h2[1])
+    _assert_bytes_nan_signless(_bytes(q), q_ref)
+    z = torch.zeros((0, 64), dtype=torch.bfloat16)                               # no rows: amax 0
+    q, scale, h2 = _delayed(pkg, z, np.array([448.0, 5.0], np.float32), 1, "e4m3", cuda)
+    assert q.shape == (0, 64) and scale == 1.0 and h2[1] == 0.0 and h2[0] == 448.0
+
+
+def test_delayed_cycle_matches_oracle(pkg, orq, cuda):
+    """Eight calls cycling the slot through a 4-entry history, the first one seeded by the
+    current-scaling quantizer, with the input's range growing and shrinking: each call's bytes and
+    scale against the oracle run over the same sequence, and the history in step."""
+    rng = np.random.default_rng(4)
+    xs = [(rng.standard_normal((512, 256)) * m).astype(np.float32) for m in (1, 2, 8, 0.5, 1, 4, 0.1, 1)]
+    _say("delayed cycle of 8 calls, history 4")
+    q0, _, am = pkg.quantize_fp8_tensorwise(torch.from_numpy(xs[0]).to(cuda), "e4m3")
+    h = torch.zeros(4, dtype=torch.float32, device=cuda)
+    h[:1].copy_(am.reshape(1))
+    h_ref = np.zeros(4, np.float32)
+    h_ref[0] = orq.amax(xs[0])
+    for n in range(1, len(xs)):
+        q, scale = pkg.quantize_fp8_tensorwise_delayed(torch.from_numpy(xs[n]).to(cuda), h, n % 4, "e4m3")
+        q_ref, s_ref, h_ref = orq.quantize_tensorwise_delayed(xs[n], h_ref, n % 4, "e4m3")
+        torch.cuda.synchronize()
+        assert float(scale) == float(s_ref), n
+        np.testing.assert_array_equal(h.cpu().numpy(), h_ref)
+        np.testing.assert_array_equal(_bytes(q), q_ref)

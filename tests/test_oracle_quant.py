@@ -147,3 +147,54 @@ def test_mx_dequantized_error_bound(orq):
     err = np.abs(deq - x)[~sat]
     assert np.all(err <= np.maximum(np.abs(x[~sat]) * 2.0 ** -4, 2.0 ** -10 * scale[~sat]))
     assert sat.any()          # the recipe puts block maxima in [448, 896): some saturate
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_delayed_matches_torch_recipe(orq, fmt):
+    """The delayed recipe against torch: scale = max(|history| without the slot) / fmax by torch's
+    own max and fp32 division, bytes by torch's float8 cast of clamp(x / scale); the slot's old
+    entry (here the largest) plays no part; the new history differs from the old one at the slot
+    only, where it holds max |x|."""
+    rng = np.random.default_rng(11)
+    fmax = float(orq.FMAX[fmt])
+    x = (rng.standard_normal((300, 64)) * (1e-3 if fmt == "e5m2" else 1.0)).astype(np.float32)
+    am = float(np.abs(x).max())
+    for hist_scale in (0.5, 1.0, 2.0):                       # values past the history's range saturate
+        hist = (rng.uniform(0.2, 1.0, 16) * am * hist_scale).astype(np.float32)
+        slot = 5
+        hist[slot] = 1e9
+        q, scale, h2 = orq.quantize_tensorwise_delayed(x, hist, slot, fmt)
+        ht = torch.from_numpy(hist)
+        m = torch.cat([ht[:slot], ht[slot + 1:]]).abs().max()
+        s_ref = m / torch.tensor(fmax, dtype=torch.float32)
+        assert np.float32(scale) == np.float32(s_ref.item())
+        y = torch.clamp(torch.from_numpy(x) / s_ref, -fmax, fmax)
+        np.testing.assert_array_equal(q, y.to(TDT[fmt]).view(torch.uint8).numpy())
+        assert h2[slot] == np.float32(am)
+        np.testing.assert_array_equal(np.delete(h2, slot), np.delete(hist, slot))
+        n_sat = int(np.sum(np.abs(x) / np.float32(scale) > fmax))
+        sat = 0x7E if fmt == "e4m3" else 0x7B
+        assert int(np.sum((q & 0x7F) == sat)) >= n_sat and (hist_scale >= 1.0 or n_sat > 0)
+
+
+def test_delayed_special_histories(orq):
+    x = np.array([[1.0, -2.0, 0.0, 1e6, -1e6, 0.5, 3.0, -0.0]], np.float32)
+    # all other entries zero: scale 1, x / 1 clamped (1e6 saturates)
+    q, scale, h2 = orq.quantize_tensorwise_delayed(x, np.array([0.0, 7.0, 0.0], np.float32), 1, "e4m3")
+    assert scale == 1.0 and h2[1] == np.float32(1e6)
+    np.testing.assert_array_equal(q, orq.encode_fp8(np.clip(x, -448, 448), "e4m3"))
+    assert q[0, 3] == 0x7E and q[0, 4] == 0xFE
+    # a NaN entry: NaN scale and NaN codes; a NaN in x reaches the new entry
+    q, scale, _ = orq.quantize_tensorwise_delayed(x, np.array([np.nan, 1.0], np.float32), 1, "e5m2")
+    assert np.isnan(scale) and np.all((q & 0x7F) == 0x7F)
+    y = x.copy()
+    y[0, 2] = np.nan
+    _, _, h2 = orq.quantize_tensorwise_delayed(y, np.array([1.0, 1.0], np.float32), 0, "e5m2")
+    assert np.isnan(h2[0]) and h2[1] == 1.0
+    # a one-entry history has no other entries: scale 1
+    _, scale, _ = orq.quantize_tensorwise_delayed(x, np.array([5.0], np.float32), 0, "e4m3")
+    assert scale == 1.0
+    # the largest entry by magnitude, sign ignored (histories hold amax values; a negative entry
+    # is read as its magnitude, as the device reads the bits without the sign)
+    _, scale, _ = orq.quantize_tensorwise_delayed(x, np.array([-896.0, 448.0, 0.0], np.float32), 2, "e4m3")
+    assert scale == 2.0

@@ -41,6 +41,35 @@ def test_tensorwise_validation(pkg, kw, rc):
     assert _tw(pkg.load_library(), **kw) == rc
 
 
+def _dl(lib, **kw):
+    a = dict(x=FAKE, dt=0, rows=100, cols=64, stride=64, fmt=0, out=FAKE, ostride=64, hist=FAKE, H=16, slot=3,
+             scale=FAKE)
+    a.update(kw)
+    return lib.ggemm_quant_fp8_tensorwise_delayed(a["x"], a["dt"], a["rows"], a["cols"], a["stride"], a["fmt"],
+                                                  a["out"], a["ostride"], a["hist"], a["H"], a["slot"], a["scale"],
+                                                  None)
+
+
+@pytest.mark.parametrize("kw,rc", [
+    (dict(x=0), -1), (dict(out=0), -1), (dict(hist=0), -1), (dict(scale=0), -1), (dict(dt=2), -8),
+    (dict(fmt=3), -8), (dict(cols=60, stride=64), -2), (dict(rows=-1), -2), (dict(stride=56), -3),
+    (dict(ostride=60), -3), (dict(H=0, slot=0), -2), (dict(H=1025), -2), (dict(slot=-1), -2),
+    (dict(slot=16), -2), (dict(x=FAKE + 8), -4), (dict(out=FAKE + 4), -4), (dict(hist=FAKE + 2), -4),
+    (dict(scale=FAKE + 1), -4),
+])
+def test_delayed_validation(pkg, kw, rc):
+    assert _dl(pkg.load_library(), **kw) == rc
+
+
+def test_delayed_python_checks_history(pkg):
+    x = torch.zeros((16, 64))
+    with pytest.raises(ValueError, match="GPU only"):
+        pkg.quantize_fp8_tensorwise_delayed(x, torch.zeros(4), 0)
+    from ggemm_asm_amd import autograd
+    with pytest.raises(ValueError, match="history_len"):
+        autograd.FP8DelayedScaling(1)
+
+
 def _mx(lib, **kw):
     a = dict(x=FAKE, dt=0, rows=100, cols=64, stride=64, offs=FAKE, G=4, fmt=1, out=FAKE, ostride=64, orows=100 + 124,
              sc=FAKE, sstride=64, pad=FAKE)
@@ -263,5 +292,60 @@ def test_fma_corrected_quotient_is_correctly_rounded():
                     assert abs(float(exact)) < 2.0 ** -26 and abs(float(c)) < 2.0 ** -26
                 else:
                     assert c == exact and np.signbit(c) == np.signbit(x), (x, s, c, exact)
+                n += 1
+    assert n > 4000
+
+
+def test_guarded_quotient_with_given_scale():
+    """With a given scale (delayed scaling) the kernels compute q = fl(x y), y = fl(1 / scale); a q
+    beyond 2 fmax goes to the clamp as it is, otherwise the FMA-corrected c (as above) does, for
+    scales in [2^-80, 2^100]. In exact rational arithmetic, over scales at both ends and between,
+    and x from far below the scale's range to far above it (overflowing products included),
+    quotients near 2 fmax and fmax, and one-ulp-off grid values: the fp8 byte of clamp(result)
+    equals that of clamp(correctly rounded x / scale)."""
+    import random
+    from fractions import Fraction as F
+    from oracle import quant_oracle as orq
+    rng = random.Random(9)
+    scales = [np.float32(2.0 ** -80), np.float32(2.0 ** 100), np.float32(2.0 ** -80 * 1.9),
+              np.float32(2.0 ** 99 * 1.7)]
+    scales += [np.float32(abs(rng.gauss(0, 1)) * 2.0 ** rng.randint(-79, 99)) for _ in range(40)]
+    n = 0
+    for fmt in ("e4m3", "e5m2"):
+        fmax = orq.FMAX[fmt]
+        for s in scales:
+            y = _rnd32(F(1) / F(float(s)))
+            xs = [np.float32(2.0 ** -110), np.float32(-(2.0 ** -103) * 1.5), np.float32(1e-45),
+                  np.float32(3.4e38), np.float32(-3.4e38)]
+            for k in (2, 1):                                 # around 2 fmax (the guard) and fmax
+                b = _rnd32(F(float(s)) * F(float(fmax)) * k)
+                for d in range(-3, 4):
+                    v = b
+                    for _ in range(abs(d)):
+                        v = np.nextafter(v, np.float32(np.inf if d > 0 else 0), dtype=np.float32)
+                    xs += [v, -v]
+            for _ in range(20):
+                with np.errstate(over="ignore"):
+                    xs.append(np.float32(rng.uniform(-1, 1) * float(s) * float(fmax) * 2.0 ** rng.randint(-30, 30)))
+                g = _rnd32(F(float(s)) * rng.randint(1, 2 ** 10) / 2 ** rng.randint(0, 12))
+                xs.append(np.nextafter(g, np.float32(np.inf if rng.random() < 0.5 else -np.inf), dtype=np.float32))
+            for x in xs:
+                if not np.isfinite(x):
+                    continue
+                with np.errstate(over="ignore"):
+                    q = np.float32(x * y)
+                if not (abs(q) <= 2 * fmax):
+                    got = q
+                else:
+                    r = _rnd32(F(float(x)) - F(float(q)) * F(float(s)))
+                    got = np.float32(np.copysign(_rnd32(F(float(r)) * F(float(y)) + F(float(q))), x))
+                ex = F(float(x)) / F(float(s))
+                exact = _rnd32(ex) if abs(ex) < F(2) ** 128 else np.float32(np.copysign(np.inf, x))
+                b_got = orq.encode_fp8(orq._clamp(np.array([got], np.float32), fmt), fmt)[0]
+                b_ref = orq.encode_fp8(orq._clamp(np.array([exact], np.float32), fmt), fmt)[0]
+                if abs(x) < 2.0 ** -102:
+                    assert b_got & 0x7F == 0 and b_ref & 0x7F == 0
+                else:
+                    assert b_got == b_ref, (fmt, x, s, got, exact)
                 n += 1
     assert n > 4000
