@@ -14,8 +14,8 @@ bench.py:153-180, inputs as in bench.py:205-223,238-247; FLOPs = 2 * M_total * K
 ``--config gate_up_layer`` measures one training step of the FP8 grouped linear layer at the
 gate_up shape (x bf16 [131072, 2880], w bf16 [32, 5760, 2880], dy bf16 [131072, 5760]): quantize
 x and w, forward GEMM, quantize dy, dgrad GEMM, wgrad GEMM accumulated into an fp32 main-grad;
-FLOPs = 3 * 2 * M * K * N. ``--scaling delayed`` quantizes x and dy with delayed scaling (scale
-from an amax history, amax recorded in the quantizing pass: no amax pass over x or dy).
+FLOPs = 3 * 2 * M * K * N. ``--scaling delayed`` quantizes x, w and dy with delayed scaling (scale
+from an amax history, amax recorded in the quantizing pass: no amax pass in the step).
 
 ``--site all | all_fwd | all_wgrad | <site>`` runs the reference's call sites one after the other
 with its own input recipe and prints its summary table (per-site ms, TFLOPS, share of the total)
@@ -80,7 +80,7 @@ def parse_args():
                     help="tensorwise wgrad configs: the configuration's group sizes, or the reference's seed-42 "
                          "exponential ones (reference bench.py:205-223)")
     ap.add_argument("--scaling", default="current", choices=["current", "delayed"],
-                    help="gate_up_layer: x and dy quantized with their own amax (an amax pass each), or with "
+                    help="gate_up_layer: x, w and dy quantized with their own amax (an amax pass each), or with "
                          "delayed scaling (an amax history of 16; the amax reduced in the quantizing pass)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,

@@ -19,7 +19,8 @@ from ._lib import GGemmError, bf16_kernel, launch_geometry, library_path, load a
 from .autograd import FP8DelayedScaling, FP8WeightCache, GroupedLinearFP8, grouped_linear_fp8  # noqa: F401
 from .persistent import grouped_gemm_fp8_tensorwise  # noqa: F401
 from .quant import (amax, padded_rows, quantize_fp8_tensorwise, quantize_fp8_tensorwise_delayed,  # noqa: F401
-                    quantize_fp8_tensorwise_transpose, quantize_mxfp8_grouped)
+                    quantize_fp8_tensorwise_transpose, quantize_fp8_tensorwise_transpose_delayed,
+                    quantize_mxfp8_grouped)
 from .vark import (as_bf16_bits, grouped_gemm_fp8_tensorwise_variable_k,  # noqa: F401
                    grouped_gemm_mxfp8_variable_k)
 

@@ -37,6 +37,7 @@ QUANT_EXPORTS = (
     "ggemm_quant_fp8_tensorwise",
     "ggemm_quant_fp8_tensorwise_delayed",
     "ggemm_quant_fp8_tensorwise_transpose",
+    "ggemm_quant_fp8_tensorwise_transpose_delayed",
     "ggemm_quant_mxfp8_grouped",
 )
 
@@ -115,6 +116,9 @@ def load():
     lib.ggemm_quant_fp8_tensorwise_delayed.restype = ctypes.c_int
     lib.ggemm_quant_fp8_tensorwise_transpose.argtypes = [vp, i32, i32, i32, i32, i32, vp, i64, vp, i64, vp, vp, vp]
     lib.ggemm_quant_fp8_tensorwise_transpose.restype = ctypes.c_int
+    lib.ggemm_quant_fp8_tensorwise_transpose_delayed.argtypes = [vp, i32, i32, i32, i32, i32, vp, i64, vp, i64, vp,
+                                                                 i32, i32, vp, vp]
+    lib.ggemm_quant_fp8_tensorwise_transpose_delayed.restype = ctypes.c_int
     lib.ggemm_quant_mxfp8_grouped.argtypes = [vp, i32, i64, i32, i64, vp, i32, i32, vp, i64, i64, vp, i64, vp, vp]
     lib.ggemm_quant_mxfp8_grouped.restype = ctypes.c_int
     _lib = lib

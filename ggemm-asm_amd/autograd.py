@@ -24,9 +24,9 @@ the autograd wiring left to the framework (Primus-Turbo, not vendored).
   calls and redone only when the weight changes (its storage, shape or version counter: an
   optimizer's in-place update bumps it). With gradient accumulation over several micro-batches
   the weight pass then runs once per update instead of once per step.
-* ``scaling=FP8DelayedScaling()``: x and dy are quantized with delayed scaling (the largest amax
-  of their previous calls, recorded on the device in the quantizing pass itself), which drops the
-  standalone amax passes over x and dy; values beyond the historical range saturate at +-fmax.
+* ``scaling=FP8DelayedScaling()``: x, w and dy are quantized with delayed scaling (the largest
+  amax of their previous calls, recorded on the device in the quantizing pass itself), which drops
+  the standalone amax passes; values beyond the historical range saturate at +-fmax.
 There is no CPU path: the tensors must live on a gfx950 GPU.
 """
 from __future__ import annotations
@@ -36,14 +36,18 @@ import weakref
 import torch
 
 from .persistent import grouped_gemm_fp8_tensorwise
-from .quant import quantize_fp8_tensorwise, quantize_fp8_tensorwise_delayed, quantize_fp8_tensorwise_transpose
+from .quant import (quantize_fp8_tensorwise, quantize_fp8_tensorwise_delayed, quantize_fp8_tensorwise_transpose,
+                    quantize_fp8_tensorwise_transpose_delayed)
 from .vark import grouped_gemm_fp8_tensorwise_variable_k
 
 _LINE = 128   # bytes per cache line
 
 
-def _quantize_weight(w, with_transpose):
-    """(qw, qw^T or None, scale) of a [G, N, K] weight, rows on 128-byte lines."""
+def _quantize_weight(w, with_transpose, scaling=None):
+    """(qw, qw^T or None, scale) of a [G, N, K] weight, rows on 128-byte lines; with ``scaling``
+    (an FP8DelayedScaling) by its delayed recipe for the role "w"."""
+    if scaling is not None:
+        return scaling.quantize_weight(w.contiguous(), with_transpose)
     if with_transpose:
         qw, qwt, sw, _ = quantize_fp8_tensorwise_transpose(w.contiguous(), "e4m3", row_align=_LINE)
         return qw, qwt, sw
@@ -72,14 +76,14 @@ class FP8WeightCache:
     def _key_of(w):
         return (w.data_ptr(), tuple(w.shape), tuple(w.stride()), w.dtype, str(w.device), w._version)
 
-    def get(self, w, with_transpose):
+    def get(self, w, with_transpose, scaling=None):
         key = self._key_of(w)
         same = self._ref is not None and self._ref() is w and self._key == key
         if same and (self._val[1] is not None or not with_transpose):
             self.hits += 1
             return self._val
         self.misses += 1
-        self._val = _quantize_weight(w, with_transpose)
+        self._val = _quantize_weight(w, with_transpose, scaling)
         self._ref, self._key = weakref.ref(w), key
         return self._val
 
@@ -88,8 +92,8 @@ class FP8WeightCache:
 
 
 class FP8DelayedScaling:
-    """Delayed-scaling recipe for one layer's activations (``"x"``, forward) and output gradients
-    (``"dy"``, backward).
+    """Delayed-scaling recipe for one layer's activations (``"x"``, forward), weight (``"w"``,
+    forward; with a weight cache only on its misses) and output gradients (``"dy"``, backward).
 
     Each tensor role keeps an fp32 amax history of ``history_len`` entries on the device. The first
     call for a role quantizes with the tensor's own amax (current scaling) and records it; call n
@@ -106,20 +110,44 @@ class FP8DelayedScaling:
         self.history: dict[str, torch.Tensor] = {}
         self.calls: dict[str, int] = {}
 
-    def quantize(self, role: str, x: torch.Tensor, fmt: str):
-        """(q, scale) of x for this role, rows on 128-byte lines."""
+    def _slot(self, role: str, device):
+        """(history, slot) of this call, or (None, None) for a role's first call on this device."""
         n = self.calls.get(role, 0)
         hist = self.history.get(role)
-        if n == 0 or hist is None or hist.device != x.device:
+        if n == 0 or hist is None or hist.device != device:
+            return None, None
+        return hist, n % self.history_len
+
+    def _seed(self, role: str, am: torch.Tensor):
+        hist = torch.zeros(self.history_len, dtype=torch.float32, device=am.device)
+        hist[:1].copy_(am.reshape(1))
+        self.history[role] = hist
+        self.calls[role] = 1
+
+    def quantize(self, role: str, x: torch.Tensor, fmt: str):
+        """(q, scale) of x for this role, rows on 128-byte lines."""
+        hist, slot = self._slot(role, x.device)
+        if hist is None:
             q, scale, am = quantize_fp8_tensorwise(x, fmt, row_align=_LINE)
-            hist = torch.zeros(self.history_len, dtype=torch.float32, device=x.device)
-            hist[:1].copy_(am.reshape(1))
-            self.history[role] = hist
-            self.calls[role] = 1
+            self._seed(role, am)
             return q, scale
-        q, scale = quantize_fp8_tensorwise_delayed(x, hist, n % self.history_len, fmt, row_align=_LINE)
-        self.calls[role] = n + 1
+        q, scale = quantize_fp8_tensorwise_delayed(x, hist, slot, fmt, row_align=_LINE)
+        self.calls[role] += 1
         return q, scale
+
+    def quantize_weight(self, w: torch.Tensor, with_transpose: bool):
+        """(qw, qw^T or None, scale) of a contiguous [G, N, K] weight (e4m3) for the role "w"."""
+        hist, slot = self._slot("w", w.device)
+        if not with_transpose:
+            q, scale = self.quantize("w", w, "e4m3")
+            return q, None, scale
+        if hist is None:
+            qw, qwt, scale, am = quantize_fp8_tensorwise_transpose(w, "e4m3", row_align=_LINE)
+            self._seed("w", am)
+            return qw, qwt, scale
+        qw, qwt, scale = quantize_fp8_tensorwise_transpose_delayed(w, hist, slot, "e4m3", row_align=_LINE)
+        self.calls["w"] += 1
+        return qw, qwt, scale
 
 
 class GroupedLinearFP8(torch.autograd.Function):
@@ -136,9 +164,9 @@ class GroupedLinearFP8(torch.autograd.Function):
         else:
             qx, sx, _ = quantize_fp8_tensorwise(x.contiguous(), "e4m3", row_align=_LINE)
         if weight_cache is not None:
-            qw, qwt, sw = weight_cache.get(w, ctx.needs_input_grad[0])
+            qw, qwt, sw = weight_cache.get(w, ctx.needs_input_grad[0], scaling)
         else:
-            qw, qwt, sw = _quantize_weight(w, ctx.needs_input_grad[0])
+            qw, qwt, sw = _quantize_weight(w, ctx.needs_input_grad[0], scaling)
         # rows past offs[G] (tokens the routing dropped) come out as exact zeros
         out = grouped_gemm_fp8_tensorwise(qx, qw, sx, sw, group_offs, zero_tail=True)
         ctx.save_for_backward(qx, sx, qwt, sw, group_offs)
@@ -179,7 +207,7 @@ def grouped_linear_fp8(x: torch.Tensor, w: torch.Tensor, group_offs: torch.Tenso
     [G+1] on the device. Backward gives dx [M, K] and dw [G, N, K]; with ``main_grad`` (fp32
     [G, K, N], the wgrad kernel's orientation) the weight gradient is added into it instead. With
     ``weight_cache`` the weight's fp8 copy is reused while the weight is unchanged. With ``scaling``
-    (one FP8DelayedScaling per layer) x and dy take delayed scaling (module docstring)."""
+    (one FP8DelayedScaling per layer) x, w and dy take delayed scaling (module docstring)."""
     if main_grad is not None:
         if main_grad.dtype != torch.float32 or tuple(main_grad.shape) != (w.shape[0], w.shape[2], w.shape[1]):
             raise ValueError(f"main_grad must be fp32 [G, K, N] = {[w.shape[0], w.shape[2], w.shape[1]]}")

@@ -44,6 +44,34 @@ void launch_amax(const void* x, int in_dtype, int64_t rows, int cols, int64_t st
     hipLaunchKernelGGL(qt::amax_kernel<false>, dim3(grid), dim3(qt::kThreads), 0, s, x, rows, cols, stride, bits);
 }
 
+// Arguments of the transposing quantizer (all but the amax / history pointers).
+int check_transpose(const void* x, int in_dtype, int batch, int rows, int cols, int out_format, const void* out,
+                    int64_t out_stride, const void* out_t, int64_t out_t_stride, const float* scale_out) {
+  if (!x || !out_t || !scale_out) return GGEMM_E_NULL;
+  if (in_dtype != GGEMM_IN_BF16 && in_dtype != GGEMM_IN_F32) return GGEMM_E_FORMAT;
+  if (out_format != GGEMM_FP8_E4M3 && out_format != GGEMM_FP8_E5M2) return GGEMM_E_FORMAT;
+  if (batch < 0 || rows <= 0 || cols <= 0 || rows % 16 || cols % 16) return GGEMM_E_SHAPE;
+  if ((out && (out_stride < cols || out_stride % 16)) || out_t_stride < rows || out_t_stride % 16)
+    return GGEMM_E_STRIDE;
+  // tile index (batch * tiles per matrix) and per-matrix offsets fit the kernel's integer widths
+  const int64_t per = (int64_t)((rows + qt::kTT - 1) / qt::kTT) * ((cols + qt::kTT - 1) / qt::kTT);
+  if (per > 0x7fffffffLL) return GGEMM_E_SHAPE;
+  if (!aligned(x, 16) || !aligned(out_t, 16) || (out && !aligned(out, 16)) || !aligned(scale_out, 4))
+    return GGEMM_E_ALIGN;
+  return GGEMM_OK;
+}
+
+// Persistent grid of the transposing quantizer: one workgroup per 128 x 128 tile, at most as many
+// as the CUs hold at once.
+int transpose_grid(const void* kernel, int batch, int rows, int cols, int cus) {
+  const int64_t tiles = (int64_t)batch * ((rows + qt::kTT - 1) / qt::kTT) * ((cols + qt::kTT - 1) / qt::kTT);
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, qt::kThreads, 0) != hipSuccess || per_cu < 1)
+    per_cu = 1;
+  const int64_t cap = (int64_t)cus * per_cu;
+  return (int)(tiles < 1 ? 1 : (tiles < cap ? tiles : cap));
+}
+
 }  // namespace
 
 extern "C" {
@@ -114,38 +142,48 @@ int ggemm_quant_fp8_tensorwise_delayed(const void* x, int32_t in_dtype, int64_t 
 int ggemm_quant_fp8_tensorwise_transpose(const void* x, int32_t in_dtype, int32_t batch, int32_t rows, int32_t cols,
                                          int32_t out_format, void* out, int64_t out_stride, void* out_t,
                                          int64_t out_t_stride, float* scale_out, float* amax_out, void* stream) {
-  if (!x || !out_t || !scale_out || !amax_out) return GGEMM_E_NULL;
-  if (in_dtype != GGEMM_IN_BF16 && in_dtype != GGEMM_IN_F32) return GGEMM_E_FORMAT;
-  if (out_format != GGEMM_FP8_E4M3 && out_format != GGEMM_FP8_E5M2) return GGEMM_E_FORMAT;
-  if (batch < 0 || rows <= 0 || cols <= 0 || rows % 16 || cols % 16) return GGEMM_E_SHAPE;
-  if ((out && (out_stride < cols || out_stride % 16)) || out_t_stride < rows || out_t_stride % 16)
-    return GGEMM_E_STRIDE;
-  // tile index (batch * tiles per matrix) and per-matrix offsets fit the kernel's integer widths
-  const int64_t per = (int64_t)((rows + qt::kTT - 1) / qt::kTT) * ((cols + qt::kTT - 1) / qt::kTT);
-  if (per > 0x7fffffffLL) return GGEMM_E_SHAPE;
-  if (!aligned(x, 16) || !aligned(out_t, 16) || (out && !aligned(out, 16)) || !aligned(scale_out, 4) ||
-      !aligned(amax_out, 4))
-    return GGEMM_E_ALIGN;
+  if (!amax_out) return GGEMM_E_NULL;
+  int rc = check_transpose(x, in_dtype, batch, rows, cols, out_format, out, out_stride, out_t, out_t_stride, scale_out);
+  if (rc) return rc;
+  if (!aligned(amax_out, 4)) return GGEMM_E_ALIGN;
   int cus = 0;
-  int rc = device_cus(&cus);
+  rc = device_cus(&cus);
   if (rc) return rc;
   hipStream_t s = (hipStream_t)stream;
-  const int64_t total_rows = (int64_t)batch * rows;
-  launch_amax(x, in_dtype, total_rows, cols, cols, amax_out, cus, s);
+  launch_amax(x, in_dtype, (int64_t)batch * rows, cols, cols, amax_out, cus, s);
   const bool f32 = in_dtype == GGEMM_IN_F32, e5 = out_format == GGEMM_FP8_E5M2;
   auto k = f32 ? (e5 ? qt::quant_transpose_kernel<true, true> : qt::quant_transpose_kernel<true, false>)
                : (e5 ? qt::quant_transpose_kernel<false, true> : qt::quant_transpose_kernel<false, false>);
-  const int64_t tiles = (int64_t)batch * per;
-  int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(k), qt::kThreads, 0) !=
-          hipSuccess ||
-      per_cu < 1)
-    per_cu = 1;
-  const int64_t cap = (int64_t)cus * per_cu;
-  const int grid = (int)(tiles < 1 ? 1 : (tiles < cap ? tiles : cap));
+  const int grid = transpose_grid(reinterpret_cast<const void*>(k), batch, rows, cols, cus);
   hipLaunchKernelGGL(k, dim3(grid), dim3(qt::kThreads), 0, s, x, batch, rows, cols, static_cast<uint8_t*>(out),
                      out_stride, static_cast<uint8_t*>(out_t), out_t_stride,
                      reinterpret_cast<const uint32_t*>(amax_out), scale_out);
+  return (int)hipGetLastError();
+}
+
+int ggemm_quant_fp8_tensorwise_transpose_delayed(const void* x, int32_t in_dtype, int32_t batch, int32_t rows,
+                                                 int32_t cols, int32_t out_format, void* out, int64_t out_stride,
+                                                 void* out_t, int64_t out_t_stride, float* amax_history,
+                                                 int32_t history_len, int32_t slot, float* scale_out, void* stream) {
+  if (!amax_history) return GGEMM_E_NULL;
+  int rc = check_transpose(x, in_dtype, batch, rows, cols, out_format, out, out_stride, out_t, out_t_stride, scale_out);
+  if (rc) return rc;
+  if (history_len < 1 || history_len > GGEMM_QUANT_MAX_HISTORY || slot < 0 || slot >= history_len)
+    return GGEMM_E_SHAPE;
+  if (!aligned(amax_history, 4)) return GGEMM_E_ALIGN;
+  int cus = 0;
+  rc = device_cus(&cus);
+  if (rc) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(qt::amax_init, dim3(1), dim3(64), 0, s, reinterpret_cast<uint32_t*>(amax_history + slot));
+  const bool f32 = in_dtype == GGEMM_IN_F32, e5 = out_format == GGEMM_FP8_E5M2;
+  auto k = f32 ? (e5 ? qt::quant_transpose_delayed_kernel<true, true> : qt::quant_transpose_delayed_kernel<true, false>)
+               : (e5 ? qt::quant_transpose_delayed_kernel<false, true>
+                     : qt::quant_transpose_delayed_kernel<false, false>);
+  const int grid = transpose_grid(reinterpret_cast<const void*>(k), batch, rows, cols, cus);
+  hipLaunchKernelGGL(k, dim3(grid), dim3(qt::kThreads), 0, s, x, batch, rows, cols, static_cast<uint8_t*>(out),
+                     out_stride, static_cast<uint8_t*>(out_t), out_t_stride, amax_history, history_len, slot,
+                     scale_out);
   return (int)hipGetLastError();
 }
 

@@ -247,6 +247,20 @@ __device__ __forceinline__ float div_scale_guarded(float x, const ScaleDiv& d) {
   }
 }
 
+template <bool kFast, bool kE5M2, bool kGiven>
+__device__ __forceinline__ float quotient(float x, const ScaleDiv& d) {
+  if constexpr (kGiven) return div_scale_guarded<kFast, kE5M2>(x, d);
+  else return div_scale<kFast>(x, d);
+}
+
+// Largest |entry| (fp32 bits) of an amax history other than `slot`; NaN beats every number.
+__device__ __forceinline__ uint32_t history_amax(const float* hist, int H, int slot) {
+  uint32_t hm = 0;
+  for (int i = 0; i < H; ++i)
+    if (i != slot) hm = max(hm, __float_as_uint(hist[i]) & 0x7fffffffu);
+  return hm;
+}
+
 // kGiven: the scale is a given one (guarded quotients) and the thread's max |x| (fp32 bits) is
 // returned for the tensor's amax; otherwise 0.
 template <bool kF32, bool kE5M2, bool kFast, bool kGiven = false>
@@ -305,10 +319,7 @@ __global__ void __launch_bounds__(kThreads) quant_tensorwise_delayed_kernel(cons
                                                                             int64_t stride, uint8_t* out,
                                                                             int64_t out_stride, float* hist, int H,
                                                                             int slot, float* scale_out) {
-  uint32_t hm = 0;
-  for (int i = 0; i < H; ++i)
-    if (i != slot) hm = max(hm, __float_as_uint(hist[i]) & 0x7fffffffu);
-  const ScaleDiv d = scale_div_given(tensor_scale<kE5M2>(hm));
+  const ScaleDiv d = scale_div_given(tensor_scale<kE5M2>(history_amax(hist, H, slot)));
   if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = d.scale;
   const uint32_t m = d.fast ? tensorwise_body<kF32, kE5M2, true, true>(x, rows, cols, stride, out, out_stride, d)
                             : tensorwise_body<kF32, kE5M2, false, true>(x, rows, cols, stride, out, out_stride, d);
@@ -329,10 +340,12 @@ __global__ void __launch_bounds__(kThreads) quant_tensorwise_delayed_kernel(cons
 // four q^T rows, so the 8 threads of a column group cover one 128-byte line per store instruction.
 // The 16-element segments of a ragged edge tile are wholly inside the matrix or outside.
 
-template <bool kF32, bool kE5M2, bool kFast>
-__device__ __forceinline__ void transpose_body(const void* x, int batch, int rows, int cols, uint8_t* out,
-                                               int64_t out_stride, uint8_t* out_t, int64_t out_t_stride,
-                                               const ScaleDiv& d, uint8_t* s_t) {
+// kGiven as in tensorwise_body: guarded quotients, and the thread's max |x| returned.
+template <bool kF32, bool kE5M2, bool kFast, bool kGiven = false>
+__device__ __forceinline__ uint32_t transpose_body(const void* x, int batch, int rows, int cols, uint8_t* out,
+                                                   int64_t out_stride, uint8_t* out_t, int64_t out_t_stride,
+                                                   const ScaleDiv& d, uint8_t* s_t) {
+  uint32_t m = 0;
   const int tid = threadIdx.x;
   const int tr = tid >> 3;                  // first tile row (then + 32, + 64, + 96)
   const int tc = 16 * (tid & 7);            // first tile column of this thread's segments
@@ -358,13 +371,17 @@ __device__ __forceinline__ void transpose_body(const void* x, int batch, int row
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
       if (!(col_in && r0 + tr + 32 * h < rows)) continue;
+      if constexpr (kGiven) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) m = max(m, __float_as_uint(v[h][k]) & 0x7fffffffu);
+      }
       uint32_t w[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        w[k] = pack4_fp8<kE5M2>(clamp_fmax<kE5M2>(div_scale<kFast>(v[h][4 * k], d)),
-                                clamp_fmax<kE5M2>(div_scale<kFast>(v[h][4 * k + 1], d)),
-                                clamp_fmax<kE5M2>(div_scale<kFast>(v[h][4 * k + 2], d)),
-                                clamp_fmax<kE5M2>(div_scale<kFast>(v[h][4 * k + 3], d)));
+        w[k] = pack4_fp8<kE5M2>(clamp_fmax<kE5M2>(quotient<kFast, kE5M2, kGiven>(v[h][4 * k], d)),
+                                clamp_fmax<kE5M2>(quotient<kFast, kE5M2, kGiven>(v[h][4 * k + 1], d)),
+                                clamp_fmax<kE5M2>(quotient<kFast, kE5M2, kGiven>(v[h][4 * k + 2], d)),
+                                clamp_fmax<kE5M2>(quotient<kFast, kE5M2, kGiven>(v[h][4 * k + 3], d)));
       const int64_t row = (int64_t)b * rows + r0 + tr + 32 * h;
       if (out) *(v4u*)(out + row * out_stride + c0 + tc) = v4u{w[0], w[1], w[2], w[3]};
       *(v4u*)(s_t + tt_off(tr + 32 * h, tc)) = v4u{w[0], w[1], w[2], w[3]};
@@ -386,6 +403,7 @@ __device__ __forceinline__ void transpose_body(const void* x, int batch, int row
     }
     __syncthreads();
   }
+  return m;
 }
 
 template <bool kF32, bool kE5M2>
@@ -400,6 +418,25 @@ __global__ void __launch_bounds__(kThreads) quant_transpose_kernel(const void* x
     transpose_body<kF32, kE5M2, true>(x, batch, rows, cols, out, out_stride, out_t, out_t_stride, d, s_t);
   else
     transpose_body<kF32, kE5M2, false>(x, batch, rows, cols, out, out_stride, out_t, out_t_stride, d, s_t);
+}
+
+// Delayed scaling of the transposing pass: the scale from the history's entries other than `slot`
+// (as quant_tensorwise_delayed_kernel), the max |x| of this x reduced into hist[slot], which the
+// host zeroed just before.
+template <bool kF32, bool kE5M2>
+__global__ void __launch_bounds__(kThreads) quant_transpose_delayed_kernel(const void* x, int batch, int rows,
+                                                                           int cols, uint8_t* out, int64_t out_stride,
+                                                                           uint8_t* out_t, int64_t out_t_stride,
+                                                                           float* hist, int H, int slot,
+                                                                           float* scale_out) {
+  __shared__ __attribute__((aligned(16))) uint8_t s_t[kTT * kTT];
+  const ScaleDiv d = scale_div_given(tensor_scale<kE5M2>(history_amax(hist, H, slot)));
+  if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = d.scale;
+  const uint32_t m =
+      d.fast ? transpose_body<kF32, kE5M2, true, true>(x, batch, rows, cols, out, out_stride, out_t, out_t_stride, d, s_t)
+             : transpose_body<kF32, kE5M2, false, true>(x, batch, rows, cols, out, out_stride, out_t, out_t_stride, d,
+                                                        s_t);
+  block_amax(m, reinterpret_cast<uint32_t*>(hist + slot));
 }
 
 // ---------------------------------------------------------------------------------- MX, grouped

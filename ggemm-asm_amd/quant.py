@@ -118,13 +118,8 @@ def quantize_fp8_tensorwise_delayed(x: torch.Tensor, amax_history: torch.Tensor,
     pass). Returns ``(q, scale)`` as ``quantize_fp8_tensorwise`` does; values beyond ``fmax * scale``
     saturate to +-fmax."""
     _check(x, fmt)
-    if amax_history.dtype != torch.float32 or amax_history.dim() != 1 or not amax_history.is_contiguous():
-        raise ValueError("amax_history must be a contiguous fp32 [H] tensor")
-    if amax_history.device != x.device:
-        raise ValueError("amax_history must be on x's device")
+    _check_history(amax_history, slot, x.device)
     H = amax_history.numel()
-    if not 0 <= slot < H:
-        raise ValueError(f"slot {slot} outside the history of {H}")
     x2 = _as_2d(x)
     code, dt = _OUT[fmt]
     q = _padded_empty(x.shape, row_align, dt, x.device)
@@ -147,9 +142,33 @@ def quantize_fp8_tensorwise_transpose(x: torch.Tensor, fmt: str = "e4m3", keep: 
     For a weight [G, N, K], ``q`` is the forward GEMM's B and ``q_t`` the data-gradient GEMM's
     (``dy @ w[g]`` reads ``w[g]^T`` K-major). ``row_align`` as in ``quantize_fp8_tensorwise``, for
     both outputs. R and C must be multiples of 16."""
+    return _transpose(x, fmt, keep, row_align, None, 0)
+
+
+def quantize_fp8_tensorwise_transpose_delayed(x: torch.Tensor, amax_history: torch.Tensor, slot: int,
+                                              fmt: str = "e4m3", keep: bool = True, row_align: int | None = None):
+    """``quantize_fp8_tensorwise_transpose`` with delayed scaling: the scale from ``amax_history``'s
+    entries other than ``slot`` and x's amax recorded at ``slot`` in the same pass, as in
+    ``quantize_fp8_tensorwise_delayed``. Returns ``(q, q_t, scale)``."""
+    q, q_t, scale, _ = _transpose(x, fmt, keep, row_align, amax_history, slot)
+    return q, q_t, scale
+
+
+def _check_history(amax_history: torch.Tensor, slot: int, device):
+    if amax_history.dtype != torch.float32 or amax_history.dim() != 1 or not amax_history.is_contiguous():
+        raise ValueError("amax_history must be a contiguous fp32 [H] tensor")
+    if amax_history.device != device:
+        raise ValueError("amax_history must be on x's device")
+    if not 0 <= slot < amax_history.numel():
+        raise ValueError(f"slot {slot} outside the history of {amax_history.numel()}")
+
+
+def _transpose(x, fmt, keep, row_align, amax_history, slot):
     _check(x, fmt)
     if x.dim() not in (2, 3) or not x.is_contiguous():
         raise ValueError("x must be a contiguous [B, R, C] or [R, C] tensor")
+    if amax_history is not None:
+        _check_history(amax_history, slot, x.device)
     x3 = x if x.dim() == 3 else x.unsqueeze(0)
     B, R, C = x3.shape
     if R % 16 or C % 16:
@@ -158,7 +177,6 @@ def quantize_fp8_tensorwise_transpose(x: torch.Tensor, fmt: str = "e4m3", keep: 
     q = _padded_empty(x.shape, row_align, dt, x.device) if keep else None
     q_t = _padded_empty(x.shape[:-2] + (C, R), row_align, dt, x.device)
     scale = torch.empty((), dtype=torch.float32, device=x.device)
-    am = torch.empty((), dtype=torch.float32, device=x.device)
     q_stride = q.stride(-2) if keep else C
     t_stride = q_t.stride(-2)
     if B == 0:                                   # nothing to read: a one-matrix placeholder pointer
@@ -167,11 +185,21 @@ def quantize_fp8_tensorwise_transpose(x: torch.Tensor, fmt: str = "e4m3", keep: 
         qp = torch.empty((R, q_stride), dtype=dt, device=x.device).data_ptr() if keep else None
     else:
         xp, tp, qp = x.data_ptr(), q_t.data_ptr(), (q.data_ptr() if keep else None)
+    lib = _lib.load()
     with torch.cuda.device(x.device):
-        rc = _lib.load().ggemm_quant_fp8_tensorwise_transpose(
-            xp, _IN[x.dtype], B, R, C, code, qp, q_stride, tp, t_stride, scale.data_ptr(), am.data_ptr(),
-            _stream(x.device))
-    _lib.check(rc, "ggemm_quant_fp8_tensorwise_transpose")
+        if amax_history is None:
+            am = torch.empty((), dtype=torch.float32, device=x.device)
+            name = "ggemm_quant_fp8_tensorwise_transpose"
+            rc = lib.ggemm_quant_fp8_tensorwise_transpose(
+                xp, _IN[x.dtype], B, R, C, code, qp, q_stride, tp, t_stride, scale.data_ptr(), am.data_ptr(),
+                _stream(x.device))
+        else:
+            am = None
+            name = "ggemm_quant_fp8_tensorwise_transpose_delayed"
+            rc = lib.ggemm_quant_fp8_tensorwise_transpose_delayed(
+                xp, _IN[x.dtype], B, R, C, code, qp, q_stride, tp, t_stride, amax_history.data_ptr(),
+                amax_history.numel(), slot, scale.data_ptr(), _stream(x.device))
+    _lib.check(rc, name)
     return q, q_t, scale, am
 
 

@@ -81,6 +81,15 @@ int ggemm_quant_fp8_tensorwise_transpose(const void* x, int32_t in_dtype, int32_
                                          int32_t out_format, void* out, int64_t out_stride, void* out_t,
                                          int64_t out_t_stride, float* scale_out, float* amax_out, void* stream);
 
+/* The transposing pass with delayed scaling: out / out_t as in ggemm_quant_fp8_tensorwise_transpose,
+ * the scale and amax_history as in ggemm_quant_fp8_tensorwise_delayed (the max |x| over all
+ * batch*rows*cols elements recorded at amax_history[slot], no separate amax pass). No reference
+ * counterpart; the FP8 grouped linear layer's delayed-scaling recipe quantizes its weight with it. */
+int ggemm_quant_fp8_tensorwise_transpose_delayed(const void* x, int32_t in_dtype, int32_t batch, int32_t rows,
+                                                 int32_t cols, int32_t out_format, void* out, int64_t out_stride,
+                                                 void* out_t, int64_t out_t_stride, float* amax_history,
+                                                 int32_t history_len, int32_t slot, float* scale_out, void* stream);
+
 /* MX (OCP microscaling) quantization along the token axis with group-aligned padding, the input
  * of ggemm_vark_wgrad_mxfp8. x: [rows, cols] token-major; group_offs: int64 [G+1] (0-based,
  * non-decreasing, <= rows). Group g's rows are written to out rows padded_offs[g] ..

@@ -170,11 +170,11 @@ def test_grouped_linear_fp8_weight_cache(pkg, cuda):
 
 
 def test_grouped_linear_fp8_delayed_scaling(pkg, orc, orp, cuda):
-    """scaling=FP8DelayedScaling: with the same x and dy every step the history holds their own
+    """scaling=FP8DelayedScaling: with the same x, w and dy every step the histories hold their own
     amax, so every output and gradient equals the current-scaling op's bit for bit; a step whose
     x and dy shrink quantizes them with the scale of the history (the previous steps' larger
-    amax), which the forward and dgrad against the oracle on those bytes confirm, and records
-    their amax in the slot."""
+    amax), which the forward, dgrad and wgrad against the oracle on those bytes confirm, and
+    records their amax in the slot. With a weight cache the weight role advances on misses only."""
     from ggemm_asm_amd.autograd import FP8DelayedScaling, grouped_linear_fp8
     lens, K, N = [96, 0, 160, 64], 192, 256
     g = torch.Generator().manual_seed(29)
@@ -199,16 +199,17 @@ def test_grouped_linear_fp8_delayed_scaling(pkg, orc, orp, cuda):
         torch.cuda.synchronize()
         for a, b in zip(got, ref):
             assert torch.equal(a.view(torch.int16), b.view(torch.int16)), n
-    assert rec.calls == {"x": 3, "dy": 3}
+    assert rec.calls == {"x": 3, "w": 3, "dy": 3}
     hx, hdy = rec.history["x"].clone(), rec.history["dy"].clone()
-    ax, ady = float(pkg.amax(x0)), float(pkg.amax(dy))
+    ax, ady, aw = float(pkg.amax(x0)), float(pkg.amax(dy)), float(pkg.amax(w))
     assert hx.tolist() == [ax, ax, ax, 0.0] and hdy.tolist() == [ady, ady, ady, 0.0]
+    assert rec.history["w"].tolist() == [aw, aw, aw, 0.0]
 
     _say("grouped linear fp8 delayed scaling: shrinking step")
     x1, dy1 = (x0.float() * 0.5).to(torch.bfloat16), (dy.float() * 0.25).to(torch.bfloat16)
     out, dx, dw = step(x1, dy1, rec)
     torch.cuda.synchronize()
-    assert rec.calls == {"x": 4, "dy": 4}
+    assert rec.calls == {"x": 4, "w": 4, "dy": 4}
     assert float(rec.history["x"][3]) == float(pkg.amax(x1)) and float(rec.history["dy"][3]) == float(pkg.amax(dy1))
     qx, sx = pkg.quantize_fp8_tensorwise_delayed(x1, hx, 3, "e4m3")
     qdy, sdy = pkg.quantize_fp8_tensorwise_delayed(dy1, hdy, 3, "e5m2")
@@ -228,3 +229,16 @@ def test_grouped_linear_fp8_delayed_scaling(pkg, orc, orp, cuda):
     assert orc.parity_ok(m)
     ref64 = torch.cat([x1[o[i]:o[i + 1]].double() @ w[i].double().T for i in range(G)])
     assert _cos(out, ref64) >= 0.99
+
+    _say("grouped linear fp8 delayed scaling with a weight cache")
+    from ggemm_asm_amd.autograd import FP8WeightCache
+    rec2, cache = FP8DelayedScaling(history_len=4), FP8WeightCache()
+    wg = w.clone().requires_grad_(True)
+    for n in range(3):
+        xg = x0.clone().requires_grad_(True)
+        out = grouped_linear_fp8(xg, wg, offs, weight_cache=cache, scaling=rec2)
+        out.backward(dy)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref[0].view(torch.int16)), n
+        assert torch.equal(xg.grad.view(torch.int16), ref[1].view(torch.int16)), n
+    assert rec2.calls == {"x": 3, "w": 1, "dy": 3} and (cache.hits, cache.misses) == (2, 1)

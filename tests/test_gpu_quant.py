@@ -483,3 +483,64 @@ def test_delayed_cycle_matches_oracle(pkg, orq, cuda):
         assert float(scale) == float(s_ref), n
         np.testing.assert_array_equal(h.cpu().numpy(), h_ref)
         np.testing.assert_array_equal(_bytes(q), q_ref)
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("shape,dtype,align", [((4, 96, 160), torch.bfloat16, None), ((3, 272, 144), torch.float32, 128),
+                                               ((1, 5760 // 4, 2880 // 4), torch.bfloat16, 128)])
+def test_transpose_delayed_bit_exact(pkg, orq, cuda, fmt, shape, dtype, align):
+    """The transposing pass with delayed scaling: q, q^T (the same bytes transposed per matrix),
+    the scale and the new history against the oracle, for histories below (saturation), at and
+    above the tensor's range; keep=False writes only q^T."""
+    g = torch.Generator().manual_seed(shape[1])
+    w = (torch.randn(shape, generator=g) * (1e-3 if fmt == "e5m2" else 0.05)).to(dtype)
+    wf = w.float().numpy()
+    B, R, C = shape
+    am = float(np.abs(wf).max())
+    rng = np.random.default_rng(shape[2])
+    for hs, slot, keep in ((0.5, 1, True), (1.0, 0, False), (2.0, 5, True)):
+        hist = (rng.uniform(0.3, 1.0, 6) * am * hs).astype(np.float32)
+        hist[slot] = 7e20
+        _say(f"transpose delayed {fmt} {shape} {dtype} align={align} history x{hs} slot {slot} keep={keep}")
+        h = torch.from_numpy(hist.copy()).to(cuda)
+        q, q_t, scale = pkg.quantize_fp8_tensorwise_transpose_delayed(w.to(cuda), h, slot, fmt, keep=keep,
+                                                                      row_align=align)
+        torch.cuda.synchronize()
+        q_ref, s_ref, h_ref = orq.quantize_tensorwise_delayed(wf.reshape(-1, C), hist, slot, fmt)
+        q_ref = q_ref.reshape(B, R, C)
+        assert float(scale) == float(s_ref)
+        np.testing.assert_array_equal(h.cpu().numpy(), h_ref)
+        np.testing.assert_array_equal(_bytes(q_t), q_ref.transpose(0, 2, 1))
+        if keep:
+            np.testing.assert_array_equal(_bytes(q), q_ref)
+        else:
+            assert q is None
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("tag", ["lo", "hi+", 613.76])
+def test_transpose_delayed_near_ties_and_saturation(pkg, orq, cuda, fmt, tag):
+    amax = np.float32(_delayed_amax(tag, fmt))
+    v = _near_tie_inputs(fmt, float(amax), seed=5).reshape(-1)
+    with np.errstate(over="ignore"):
+        w = np.concatenate([v, v * np.float32(3.0), v * np.float32(2.0 ** 30), [np.inf, -np.inf]]).astype(np.float32)
+    w = np.concatenate([w, np.zeros((-w.size) % 1024, np.float32)]).reshape(1, -1, 64)
+    hist = np.array([amax, 0.0, amax * np.float32(0.5)], np.float32)
+    _say(f"transpose delayed near ties {fmt} amax={amax} {w.shape}")
+    h = torch.from_numpy(hist.copy()).to(cuda)
+    q, q_t, scale = pkg.quantize_fp8_tensorwise_transpose_delayed(torch.from_numpy(w).to(cuda), h, 1, fmt)
+    torch.cuda.synchronize()
+    q_ref, s_ref, h_ref = orq.quantize_tensorwise_delayed(w.reshape(-1, 64), hist, 1, fmt)
+    assert float(scale) == float(s_ref)
+    np.testing.assert_array_equal(h.cpu().numpy(), h_ref)
+    np.testing.assert_array_equal(_bytes(q).reshape(-1, 64), q_ref)
+    np.testing.assert_array_equal(_bytes(q_t)[0], q_ref.T)
+
+
+def test_transpose_delayed_empty_batch(pkg, cuda):
+    h = torch.tensor([3.0, 448.0], device=cuda)
+    _say("transpose delayed B=0")
+    q, q_t, scale = pkg.quantize_fp8_tensorwise_transpose_delayed(torch.zeros((0, 32, 48), device=cuda), h, 0)
+    torch.cuda.synchronize()
+    assert q.shape == (0, 32, 48) and q_t.shape == (0, 48, 32)
+    assert float(scale) == 1.0 and h.tolist() == [0.0, 448.0]

@@ -61,6 +61,25 @@ def test_delayed_validation(pkg, kw, rc):
     assert _dl(pkg.load_library(), **kw) == rc
 
 
+def _tdl(lib, **kw):
+    a = dict(x=FAKE, dt=0, B=2, R=64, C=48, fmt=0, out=FAKE, os=48, out_t=FAKE, ts=64, hist=FAKE, H=16, slot=3,
+             scale=FAKE)
+    a.update(kw)
+    return lib.ggemm_quant_fp8_tensorwise_transpose_delayed(a["x"], a["dt"], a["B"], a["R"], a["C"], a["fmt"],
+                                                            a["out"], a["os"], a["out_t"], a["ts"], a["hist"], a["H"],
+                                                            a["slot"], a["scale"], None)
+
+
+@pytest.mark.parametrize("kw,rc", [
+    (dict(x=0), -1), (dict(out_t=0), -1), (dict(hist=0), -1), (dict(scale=0), -1), (dict(dt=2), -8),
+    (dict(fmt=2), -8), (dict(B=-1), -2), (dict(R=0), -2), (dict(C=40), -2), (dict(H=0, slot=0), -2),
+    (dict(H=1025), -2), (dict(slot=-1), -2), (dict(slot=16), -2), (dict(x=FAKE + 8), -4),
+    (dict(out_t=FAKE + 8), -4), (dict(hist=FAKE + 2), -4), (dict(os=32), -3), (dict(ts=48), -3),
+])
+def test_transpose_delayed_validation(pkg, kw, rc):
+    assert _tdl(pkg.load_library(), **kw) == rc
+
+
 def test_delayed_python_checks_history(pkg):
     x = torch.zeros((16, 64))
     with pytest.raises(ValueError, match="GPU only"):
