@@ -25,7 +25,9 @@ on stderr; the JSON line carries the sum over the sites (reference bench.py:690-
 x bf16 [131072, 2880] -> per-tensor e4m3 (amax pass + quantize pass: 2 + 2 + 1 bytes per
 element), and dy bf16 [131072, 5760] -> grouped MX e5m2 with 32-token padding (2 + 1 + 1/32
 bytes per element). ``--config quant_weight_transpose``: w bf16 [32, 5760, 2880] -> e4m3 q and its
-per-expert transpose q^T in one pass (2 + 2 + 1 + 1 bytes per element).
+per-expert transpose q^T in one pass (2 + 2 + 1 + 1 bytes per element). The ``_delayed`` variants
+of quant_tensorwise and quant_weight_transpose quantize with delayed scaling (scale from an amax
+history of 16, the amax reduced in the quantizing pass: 2 + 1 and 2 + 1 + 1 bytes per element).
 
 Prints ONE JSON line with ms, TFLOPS, the MFMA roofline fraction and a CPU baseline (the
 build's numpy oracle on a bounded sample of the same workload, timed on this host's cores).
@@ -44,7 +46,8 @@ sys.path.insert(0, ROOT)
 FP8_DENSE_PEAK_TFLOPS = 5000.0    # MI355X dense FP8 MFMA peak
 REF_OPT_ASM_TFLOPS = 1237.0       # reference optimized ASM, gate_up_wgrad, C launcher (README.md:60)
 FWD_SITES = ("gate_up_fwd", "down_fwd", "down_dgrad", "gate_up_dgrad")
-QUANT_CONFIGS = ("quant_tensorwise", "quant_mx", "quant_weight_transpose")
+QUANT_CONFIGS = ("quant_tensorwise", "quant_mx", "quant_weight_transpose", "quant_tensorwise_delayed",
+                 "quant_weight_transpose_delayed")
 LAYER_CONFIGS = ("gate_up_layer",)
 WGRAD_SITES = ("down_wgrad", "gate_up_wgrad")
 SITE_GROUPS = {"all": (*FWD_SITES, *WGRAD_SITES), "all_fwd": FWD_SITES, "all_wgrad": WGRAD_SITES}
@@ -255,22 +258,46 @@ def quant_workload(pkg, name, seed, dev):
     """(runner, bytes per call, config dict, cpu-baseline callable) of a producer workload."""
     import torch
     gen = torch.Generator(device=dev).manual_seed(seed)
-    if name == "quant_tensorwise":
+    H = 16
+    hist, calls = None, [0]
+    if name.endswith("_delayed"):
+        # delayed scaling in steady state: a history of H entries, the slot cycling through it
+        hist = torch.empty(H, dtype=torch.float32, device=dev)
+
+        def slot():
+            calls[0] += 1
+            return calls[0] % H
+    if name in ("quant_tensorwise", "quant_tensorwise_delayed"):
         x = torch.randn((pkg.inputs.M_TOTAL, pkg.inputs.F_DIM), generator=gen, device=dev, dtype=torch.bfloat16)
         n = x.numel()
-        run = lambda: pkg.quantize_fp8_tensorwise(x, "e4m3")
-        cfg = {"workload": name, "x": "bf16 [131072, 2880] (randn)", "out": "e4m3fn, fp32 scale + amax",
-               "bytes_per_element": "2 (amax pass) + 2 (quantize pass) + 1 (fp8 out)"}
-        nbytes = 5 * n
-    elif name == "quant_weight_transpose":
+        if hist is None:
+            run = lambda: pkg.quantize_fp8_tensorwise(x, "e4m3")
+            cfg = {"workload": name, "x": "bf16 [131072, 2880] (randn)", "out": "e4m3fn, fp32 scale + amax",
+                   "bytes_per_element": "2 (amax pass) + 2 (quantize pass) + 1 (fp8 out)"}
+            nbytes = 5 * n
+        else:
+            run = lambda: pkg.quantize_fp8_tensorwise_delayed(x, hist, slot(), "e4m3")
+            cfg = {"workload": name, "x": "bf16 [131072, 2880] (randn)",
+                   "out": f"e4m3fn, fp32 scale from an amax history of {H}, amax recorded in the pass",
+                   "bytes_per_element": "2 (quantize pass, amax reduced in it) + 1 (fp8 out)"}
+            nbytes = 3 * n
+    elif name in ("quant_weight_transpose", "quant_weight_transpose_delayed"):
         E, F, F2 = pkg.inputs.E_EXPERTS, pkg.inputs.F_DIM, pkg.inputs.F2_DIM
         x = (torch.randn((E, F2, F), generator=gen, device=dev, dtype=torch.bfloat16) * 0.02)
         n = x.numel()
-        run = lambda: pkg.quantize_fp8_tensorwise_transpose(x, "e4m3")
-        cfg = {"workload": name, "x": "bf16 weight [32, 5760, 2880] (randn * 0.02)",
-               "out": "e4m3fn q [32, 5760, 2880] + q^T [32, 2880, 5760], fp32 scale + amax",
-               "bytes_per_element": "2 (amax pass) + 2 (quantize pass) + 1 (q) + 1 (q^T)"}
-        nbytes = 6 * n
+        if hist is None:
+            run = lambda: pkg.quantize_fp8_tensorwise_transpose(x, "e4m3")
+            cfg = {"workload": name, "x": "bf16 weight [32, 5760, 2880] (randn * 0.02)",
+                   "out": "e4m3fn q [32, 5760, 2880] + q^T [32, 2880, 5760], fp32 scale + amax",
+                   "bytes_per_element": "2 (amax pass) + 2 (quantize pass) + 1 (q) + 1 (q^T)"}
+            nbytes = 6 * n
+        else:
+            run = lambda: pkg.quantize_fp8_tensorwise_transpose_delayed(x, hist, slot(), "e4m3")
+            cfg = {"workload": name, "x": "bf16 weight [32, 5760, 2880] (randn * 0.02)",
+                   "out": f"e4m3fn q [32, 5760, 2880] + q^T [32, 2880, 5760], fp32 scale from an amax history "
+                          f"of {H}, amax recorded in the pass",
+                   "bytes_per_element": "2 (quantize pass, amax reduced in it) + 1 (q) + 1 (q^T)"}
+            nbytes = 4 * n
     else:
         lens = pkg.inputs.multinomial_lens(pkg.inputs.E_EXPERTS, pkg.inputs.M_TOTAL, torch.Generator().manual_seed(seed))
         offs = pkg.inputs.make_group_offs(lens).to(dev)
@@ -283,6 +310,9 @@ def quant_workload(pkg, name, seed, dev):
                "bytes_per_element": "2 (read) + 1 (fp8 out) + 1/32 (e8m0)"}
         nbytes = n * (3 + 1 / 32)
 
+    if hist is not None:
+        hist.fill_(float(pkg.amax(x)))
+
     def cpu(seconds):
         """numpy oracle on row slices of the same tensor until ~`seconds`; GB/s of the same
         per-element byte count."""
@@ -290,12 +320,17 @@ def quant_workload(pkg, name, seed, dev):
         from oracle import quant_oracle as orq
         rows, t_total, done = 4096, 0.0, 0
         xc = x.reshape(-1, x.shape[-1])[:rows].float().cpu().numpy()
+        h_np = hist.cpu().numpy() if hist is not None else None
         while t_total < seconds:
             t0 = time.perf_counter()
             if name == "quant_tensorwise":
                 orq.quantize_tensorwise(xc, "e4m3")
             elif name == "quant_weight_transpose":
                 np.ascontiguousarray(orq.quantize_tensorwise(xc, "e4m3")[0].T)
+            elif name == "quant_tensorwise_delayed":
+                orq.quantize_tensorwise_delayed(xc, h_np, 1, "e4m3")
+            elif name == "quant_weight_transpose_delayed":
+                np.ascontiguousarray(orq.quantize_tensorwise_delayed(xc, h_np, 1, "e4m3")[0].T)
             else:
                 orq.quantize_mx_grouped(xc, np.array([0, rows], np.int64), "e5m2", out_rows=rows)
             t_total += time.perf_counter() - t0
