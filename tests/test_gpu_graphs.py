@@ -7,7 +7,8 @@ eager work of the same library between replays (as a training loop would interle
 replay is compared with the eager results bit for bit, including a replay after the inputs were
 overwritten in place (the graph reads its inputs, not copies). The launches record no memset: the
 amax result is cleared by a fill kernel. A second test captures the autograd op's forward and
-backward (torch.autograd.grad) in one graph.
+backward (torch.autograd.grad) in one graph; a third the delayed-scaling quantizers with a fixed
+history slot.
 """
 import numpy as np
 import pytest
@@ -139,3 +140,63 @@ def test_graph_captures_autograd_layer(pkg, cuda):
     torch.cuda.synchronize()
     for name, a, b in zip(("out", "dx", "dw"), static, want):
         assert torch.equal(_bits(a), _bits(b)), name
+
+
+def test_graph_replays_delayed_quantizers(pkg, cuda):
+    """The delayed-scaling quantizers (plain and transposing) captured with a fixed history slot:
+    every replay, with eager calls of the same kernels on other data between replays, equals the
+    eager bytes, scale and history; the graph reads the history at replay time (an entry changed in
+    place changes the scale) and records this x's amax in the slot (x overwritten in place)."""
+    g = torch.Generator(device=cuda).manual_seed(3)
+    x = torch.randn((640, 384), generator=g, device=cuda).to(torch.bfloat16)
+    w = (torch.randn((3, 160, 96), generator=g, device=cuda) * 0.05).to(torch.bfloat16)
+    hx = torch.tensor([2.5, 0.0, 3.0, 1.0], device=cuda)
+    hw = torch.tensor([0.1, 0.2, 0.0], device=cuda)
+    other = torch.randn((256, 128), generator=g, device=cuda).to(torch.bfloat16)
+    ho = torch.tensor([1.0, 0.0], device=cuda)
+
+    def run():
+        q, s = pkg.quantize_fp8_tensorwise_delayed(x, hx, 1, "e4m3", row_align=128)
+        qw, qwt, sw = pkg.quantize_fp8_tensorwise_transpose_delayed(w, hw, 2, "e4m3", row_align=128)
+        return q, s, qw, qwt, sw
+
+    def snapshot(outs):
+        return [t.view(torch.uint8).clone() if t.dtype.is_floating_point and t.element_size() == 1 else t.clone()
+                for t in outs] + [hx.clone(), hw.clone()]
+
+    def check(static, ref, tag):
+        got = [t.view(torch.uint8) if t.element_size() == 1 else t for t in static] + [hx, hw]
+        for i, (a, b) in enumerate(zip(got, ref)):
+            assert torch.equal(a, b), (tag, i)
+
+    _say("graph delayed quantizers: eager")
+    ref = snapshot(run())
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    _say("graph delayed quantizers: capturing")
+    with torch.cuda.graph(graph):
+        static = run()
+    for r in range(3):
+        pkg.quantize_fp8_tensorwise_delayed(other, ho, 1, "e5m2")       # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        check(static, ref, f"replay {r}")
+    _say("graph delayed quantizers: history and input changed in place")
+    with torch.no_grad():
+        hx[0] = 40.0
+        hw[1] = 0.05
+        x.mul_(3.0)
+    want = snapshot(run())
+    with torch.no_grad():
+        hx[1] = 0.0
+        hw[2] = 0.0
+    graph.replay()
+    torch.cuda.synchronize()
+    check(static, want, "changed")
+    assert float(static[1]) == float(np.float32(40.0) / np.float32(448.0))
+    assert float(hx[1]) == float(x.float().abs().max())
