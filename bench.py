@@ -21,6 +21,11 @@ from an amax history, amax recorded in the quantizing pass: no amax pass in the 
 with its own input recipe and prints its summary table (per-site ms, TFLOPS, share of the total)
 on stderr; the JSON line carries the sum over the sites (reference bench.py:690-858).
 
+``--config gate_up_ep8 | gate_up_ncol8 | gate_up_ncol6`` measures one GPU's share of gate_up_wgrad
+when the path is sharded without communication: 8-way expert sharding (G = 4, M_total = 65536,
+~16 K tokens per expert, 2880 x 5760) and N-column sharding (G = 32, M_total = 131072, OUT_N = 720
+for 8 GPUs, 960 for 6).
+
 ``--config quant_tensorwise | quant_mx`` measures the FP8 quantization producer (HBM-bound, GB/s):
 x bf16 [131072, 2880] -> per-tensor e4m3 (amax pass + quantize pass: 2 + 2 + 1 bytes per
 element), and dy bf16 [131072, 5760] -> grouped MX e5m2 with 32-token padding (2 + 1 + 1/32
@@ -49,6 +54,11 @@ FWD_SITES = ("gate_up_fwd", "down_fwd", "down_dgrad", "gate_up_dgrad")
 QUANT_CONFIGS = ("quant_tensorwise", "quant_mx", "quant_weight_transpose", "quant_tensorwise_delayed",
                  "quant_weight_transpose_delayed")
 LAYER_CONFIGS = ("gate_up_layer",)
+# one GPU's share of the gate_up wgrad when the path is sharded without communication: expert
+# sharding over 8 GPUs (4 of the 32 experts, ~16 K routed tokens each) and N-column sharding (a
+# slice of RHS and C, LHS replicated) over 8 GPUs (720 columns) or 6 (960 columns: three 320-wide tiles)
+SHARD_CONFIGS = {"gate_up_ep8": dict(G=4, M=65536), "gate_up_ncol8": dict(OUT_N=720),
+                 "gate_up_ncol6": dict(OUT_N=960)}
 WGRAD_SITES = ("down_wgrad", "gate_up_wgrad")
 SITE_GROUPS = {"all": (*FWD_SITES, *WGRAD_SITES), "all_fwd": FWD_SITES, "all_wgrad": WGRAD_SITES}
 HBM_PEAK_GBS = 8000.0             # MI355X HBM3E
@@ -65,7 +75,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="gate_up_wgrad",
                     choices=["gate_up_wgrad", "down_wgrad", "gate_up_zipf", "gate_up_mx", "plumbing", "constant",
-                             *FWD_SITES, *QUANT_CONFIGS, *LAYER_CONFIGS])
+                             *FWD_SITES, *QUANT_CONFIGS, *LAYER_CONFIGS, *SHARD_CONFIGS])
     ap.add_argument("--site", default=None, choices=[*SITE_GROUPS, *FWD_SITES, *WGRAD_SITES],
                     help="time the reference's call sites (one, or a group) with its own input recipe and print "
                          "a per-site summary table; replaces --config")
@@ -496,6 +506,9 @@ def main():
         p = pkg.inputs.constant_problem(device=dev)
     elif fwd:
         p = pkg.inputs.make_fwd_problem(args.config, seed=args.seed, device=dev)
+    elif args.config in SHARD_CONFIGS:
+        p = pkg.inputs.make_problem("gate_up_wgrad", seed=args.seed, device=dev, **SHARD_CONFIGS[args.config])
+        p.name = args.config
     else:
         lens = pkg.inputs.make_group_lens_reference() if args.lens == "reference" else None
         p = pkg.inputs.make_problem(args.config, seed=args.seed, device=dev, lens=lens)

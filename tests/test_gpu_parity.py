@@ -419,16 +419,25 @@ def _oracle_whole(pkg, orc, p, out):
     assert orc.parity_ok(m), (p.name, m)
 
 
-@pytest.mark.parametrize("name", ["down_wgrad", "gate_up_wgrad", "gate_up_zipf", "gate_up_mx", "gate_up_reference_lens"])
+# one GPU's share of gate_up_wgrad sharded 8 ways without communication (bench.py's SHARD_CONFIGS)
+SHARDS = {"gate_up_ep8": dict(G=4, M=65536), "gate_up_ncol8": dict(OUT_N=720), "gate_up_ncol6": dict(OUT_N=960)}
+
+
+@pytest.mark.parametrize("name", ["down_wgrad", "gate_up_wgrad", "gate_up_zipf", "gate_up_mx", "gate_up_reference_lens",
+                                  *SHARDS])
 def test_full_size_config(pkg, orc, cuda, name):
     """Full-size configurations, the whole output against the oracle. gate_up_zipf and
     gate_up_reference_lens (the reference's seed-42 exponential group sizes) are skewed enough that
     the kernel deals its tiles in boustrophedon rounds rather than XCD-pair slices
-    (tests/test_vark_schedule_host.py models the choice)."""
+    (tests/test_vark_schedule_host.py models the choice). gate_up_ep8 / gate_up_ncol8: one GPU's
+    share under 8-way expert / N-column sharding (4 groups of ~16 K tokens; OUT_N = 720), and 6-way
+    N-column sharding (OUT_N = 960)."""
     _say(f"full-size {name}")
     if name == "gate_up_reference_lens":
         p = pkg.inputs.make_problem("gate_up_wgrad", seed=0, device=cuda,
                                     lens=pkg.inputs.make_group_lens_reference())
+    elif name in SHARDS:
+        p = pkg.inputs.make_problem("gate_up_wgrad", seed=0, device=cuda, **SHARDS[name])
     else:
         p = pkg.inputs.make_problem(name, seed=0, device=cuda)
     if p.is_mx:
