@@ -719,7 +719,7 @@ class Gen:
             for k in range(4):
                 o = o0 + 4 * k
                 self.f32_store_offset(i, j, k)
-                e(f"buffer_load_dwordx4 v[{o}:{o + 3}], {c.vt2}, {s['RC']}, 0 offen")
+                e(f"buffer_load_dwordx4 v[{o}:{o + 3}], {c.vt2}, {s['RC']}, 0 offen nt")
                 vm_log.append(("L", n))
 
         def issue_loads():
