@@ -72,7 +72,7 @@ __global__ void __launch_bounds__(kXThreads) transpose_u8_kernel(const uint8_t* 
 #pragma unroll
     for (int h = 0; h < 4; ++h)
       if (c0 + tc < cols && r0 + tr + 32 * h < rows)
-        v[h] = *(const xv4u*)(src + b * sb + (int64_t)(r0 + tr + 32 * h) * sr + c0 + tc);
+        v[h] = __builtin_nontemporal_load((const xv4u*)(src + b * sb + (int64_t)(r0 + tr + 32 * h) * sr + c0 + tc));
 #pragma unroll
     for (int h = 0; h < 4; ++h)
       if (c0 + tc < cols && r0 + tr + 32 * h < rows) *(xv4u*)(s_t + ggemm::qt::tt_off(tr + 32 * h, tc)) = v[h];
@@ -85,8 +85,10 @@ __global__ void __launch_bounds__(kXThreads) transpose_u8_kernel(const uint8_t* 
       for (int k = 0; k < 4; ++k) {
         using ggemm::qt::byte_col;
         uint8_t* out = dst + b * db + (int64_t)(c0 + 4 * cg + k) * dr + r0 + 16 * rj;
-        *(xv4u*)out = xv4u{byte_col(dw[0], dw[1], dw[2], dw[3], k), byte_col(dw[4], dw[5], dw[6], dw[7], k),
-                           byte_col(dw[8], dw[9], dw[10], dw[11], k), byte_col(dw[12], dw[13], dw[14], dw[15], k)};
+        __builtin_nontemporal_store(xv4u{byte_col(dw[0], dw[1], dw[2], dw[3], k), byte_col(dw[4], dw[5], dw[6], dw[7], k),
+                                          byte_col(dw[8], dw[9], dw[10], dw[11], k),
+                                          byte_col(dw[12], dw[13], dw[14], dw[15], k)},
+                                    (xv4u*)out);
       }
     }
     __syncthreads();
@@ -221,6 +223,7 @@ int ggemm_persistent_transpose_u8(const void* src, int32_t batch, int32_t rows, 
                                                    kXThreads, 0) != hipSuccess ||
       per_cu < 1)
     per_cu = 1;
+  if (per_cu > 3) per_cu = 3;   // as the transposing quantizer: 3 per CU beats the 4 or more that fit
   const int64_t tiles = (int64_t)batch * per, cap = (int64_t)cus * per_cu;
   const int grid = (int)(tiles < cap ? tiles : cap);
   hipLaunchKernelGGL(transpose_u8_kernel, dim3(grid), dim3(kXThreads), 0, (hipStream_t)stream,
