@@ -29,7 +29,8 @@ Pinning (tests/test_oracle.py): fp8/e8m0/bf16 codecs against torch's
 independent implementations and textbook values; the GEMM against exact
 rational brute force on tiny ragged shapes; the launcher.cpp constant-fill
 closed form (C == 20.5); permutation / split / scale-linearity invariants;
-the reference input generator against the survey's recorded seed-42 lengths.
+the reference input generator against seed-42 lengths recorded from a CPU run of
+the reference's recipe.
 """
 from __future__ import annotations
 

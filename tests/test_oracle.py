@@ -223,7 +223,7 @@ def test_c_oracle_agrees_with_numpy_oracle(orc):
 
 # ----------------------------------------------------------------------------- reference generator
 
-SURVEY_SEED42_LENS = [350, 380, 772, 316, 4372, 3791, 18183, 15463, 510, 832, 1000, 2754, 10820, 11965,
+RECORDED_SEED42_LENS = [350, 380, 772, 316, 4372, 3791, 18183, 15463, 510, 832, 1000, 2754, 10820, 11965,
                       2775, 5548, 539, 7070, 5716, 3365, 454, 6733, 2191, 2164, 186, 241, 15728, 966, 1802,
                       818, 1698, 1570]
 
@@ -231,7 +231,7 @@ SURVEY_SEED42_LENS = [350, 380, 772, 316, 4372, 3791, 18183, 15463, 510, 832, 10
 def test_reference_group_lens_seed42(pkg):
     """reference bench.py:205-212 restated: the recorded seed-42 CPU lengths."""
     lens = pkg.inputs.make_group_lens_reference(32, 131072, 42)
-    assert lens.tolist() == SURVEY_SEED42_LENS
+    assert lens.tolist() == RECORDED_SEED42_LENS
     offs = pkg.inputs.make_group_offs(lens)
     assert offs[0] == 0 and offs[-1] == 131072 and offs.dtype == torch.int64
 
