@@ -21,6 +21,12 @@ import torch
 from conftest import ROOT
 
 TILE_M, K_STEP, XCDS = 192, 128, 8
+BAND_N = 3          # N tiles per band of a group's tile order (persistent_kernel.h kBandN)
+
+
+def test_band_width_matches_kernel():
+    text = open(os.path.join(ROOT, "ggemm-asm_amd", "csrc", "persistent_kernel.h")).read()
+    assert re.findall(r"constexpr int kBandN = (\d+);", text) == [str(BAND_N)]
 
 
 def _tn(N):
@@ -59,11 +65,11 @@ def _tile_at(t, pre, offs, n_tn, N):
     ln = offs[g + 1] - offs[g]
     n_tm = -(-ln // TILE_M)
     in_g = t - pre[g]
-    band = in_g // (n_tm * 4)
-    r = in_g - band * n_tm * 4
-    bw = min(4, n_tn - band * 4)
+    band = in_g // (n_tm * BAND_N)
+    r = in_g - band * n_tm * BAND_N
+    bw = min(BAND_N, n_tn - band * BAND_N)
     tm = r // bw
-    tn = band * 4 + (r - tm * bw)
+    tn = band * BAND_N + (r - tm * bw)
     m0 = tm * TILE_M
     return g, m0, tn * _tn(N), min(TILE_M, ln - m0)
 
