@@ -98,6 +98,11 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU work for the cpu_baseline sample (0 disables)")
+    ap.add_argument("--no-parity", dest="parity", action="store_false",
+                    help="skip the check of the last timed launch's output against the oracle over every group "
+                         "(on by default; a failed bar exits with status 1)")
+    ap.add_argument("--no-drop-in", dest="drop_in", action="store_false",
+                    help="tensorwise wgrad configs: do not time the drop-in code object beside the library")
     ap.add_argument("--extra", action="store_true", help="also time the other configs (not part of the line)")
     ap.add_argument("--info", action="store_true",
                     help="print the registers, spills, LDS and MFMA counts of this build's code objects and exit "
@@ -167,20 +172,26 @@ def fwd_operands(p, row_align):
 
 
 def make_runner(pkg, p, dev, mfma, kernel="auto", row_align=0):
+    """Closure launching one step of the workload; ``run.out`` is the output tensor it writes, so the
+    last timed launch's result can be checked after timing."""
     import torch
     if hasattr(p, "a_format"):   # forward / data-gradient site: the persistent grouped GEMM
         sa = torch.tensor(p.a_scale, dtype=torch.float32, device=dev)
         sb = torch.tensor(p.b_scale, dtype=torch.float32, device=dev)
         out = torch.empty((p.M, p.N), dtype=torch.bfloat16, device=dev)
         a, b = fwd_operands(p, row_align)
-        return lambda: pkg.grouped_gemm_fp8_tensorwise(a, b, sa, sb, p.group_offs, out=out, kernel=kernel)
-    if p.is_mx:
+        run = lambda: pkg.grouped_gemm_fp8_tensorwise(a, b, sa, sb, p.group_offs, out=out, kernel=kernel)
+    elif p.is_mx:
         out = torch.empty((p.G, p.OUT_M, p.OUT_N), dtype=torch.bfloat16, device=dev)
-        return lambda: pkg.grouped_gemm_mxfp8_variable_k(p.lhs, p.rhs, p.lhs_mx, p.rhs_mx, p.group_offs, out=out)
-    sl = torch.tensor(p.lhs_scale, dtype=torch.float32, device=dev)
-    sr = torch.tensor(p.rhs_scale, dtype=torch.float32, device=dev)
-    out = torch.empty((p.G, p.OUT_M, p.OUT_N), dtype=torch.bfloat16, device=dev)
-    return lambda: pkg.grouped_gemm_fp8_tensorwise_variable_k(p.lhs, p.rhs, sl, sr, p.group_offs, out=out, mfma=mfma)
+        run = lambda: pkg.grouped_gemm_mxfp8_variable_k(p.lhs, p.rhs, p.lhs_mx, p.rhs_mx, p.group_offs, out=out)
+    else:
+        sl = torch.tensor(p.lhs_scale, dtype=torch.float32, device=dev)
+        sr = torch.tensor(p.rhs_scale, dtype=torch.float32, device=dev)
+        out = torch.empty((p.G, p.OUT_M, p.OUT_N), dtype=torch.bfloat16, device=dev)
+        run = lambda: pkg.grouped_gemm_fp8_tensorwise_variable_k(p.lhs, p.rhs, sl, sr, p.group_offs, out=out,
+                                                                  mfma=mfma)
+    run.out = out
+    return run
 
 
 def time_steps(run, steps, warmup):
@@ -207,14 +218,95 @@ def _blas_threads():
         return os.cpu_count() or 1
 
 
-def cpu_baseline_fwd(p, seconds):
-    """Numpy oracle of the persistent GEMM (fp32 dequantize + BLAS sgemm + bf16 RNE) on whole
-    groups until ~`seconds` of CPU time; throughput in TFLOPS over the groups processed."""
+PARITY_BAR = ("cos >= 0.99999 and max_rel <= 2e-2 over |ref| > 1e-3 * max|ref| of the whole output, no "
+              "non-finite value, empty groups exactly zero")
+
+
+def _bf16_bits(t):
+    """Bit patterns (numpy uint16) of a bf16 tensor, or of an fp32 one rounded to bf16 (RNE)."""
     import numpy as np
-    from oracle import persistent_oracle as orp
+    import torch
+    if t.dtype != torch.bfloat16:
+        t = t.to(torch.bfloat16)
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _parity_record(orc, got_parts, refs, empty, groups):
+    """The whole-output metrics of ``got_parts`` (one bf16-bit array per group, aligned with
+    ``refs``) against the oracle, and whether they meet the bar."""
+    import numpy as np
+    amax = max((float(np.abs(orc.bf16_bits_to_f32(r)).max()) for r in refs if r.size), default=0.0)
+    m = orc.compare_parts(zip(got_parts, refs), amax)
+    m["empty_groups"] = len(empty)
+    m["empty_zero"] = bool(all(np.all((got_parts[g] & 0x7FFF) == 0) for g in empty))
+    m["groups"] = groups
+    m["ok"] = bool(orc.parity_ok(m))
+    m["bar"] = PARITY_BAR
+    return {k: (round(v, 7) if isinstance(v, float) else v) for k, v in m.items()}
+
+
+def oracle_leg(p, outs, seconds):
+    """The numpy oracle over every group of the timed workload, run after the timed region.
+
+    Parity: each group's oracle C (fp32 dequantize + per-group sgemm + bf16 RNE) against the C
+    that the last timed launch left in each tensor of ``outs`` (name -> [G, OUT_M, OUT_N], bf16 or
+    fp32 rounded to bf16), the whole tensor, every group: the reference checks the kernel it
+    benchmarks in the same harness (reference bench.py:594-648; cosine over the whole output at
+    :641-646). CPU baseline: the same oracle calls timed, over the groups computed until ~`seconds`
+    of CPU time (the parity pass continues past it untimed); None when ``seconds`` <= 0.
+    Returns ({name: parity record}, cpu_baseline)."""
+    import numpy as np
+    from oracle import vark_oracle as orc
     threads = _blas_threads()
     offs = p.group_offs.cpu().numpy()
-    done_flops, t_total, groups, rows = 0.0, 0.0, 0, 0
+    refs, empty = [], []
+    done_flops, t_total, timed_groups, tokens = 0.0, 0.0, 0, 0
+    for g in range(p.G):
+        lo, hi = int(offs[g]), int(offs[g + 1])
+        if hi == lo:
+            refs.append(np.zeros((p.OUT_M, p.OUT_N), dtype=np.uint16))
+            empty.append(g)
+            continue
+        L = p.lhs[lo:hi].cpu().numpy()
+        R = p.rhs[lo:hi].cpu().numpy()
+        sub = np.array([0, hi - lo], dtype=np.int64)
+        t0 = time.perf_counter()
+        if p.is_mx:   # MX groups start on 32-token blocks (groups padded to multiples of 32)
+            ref = orc.vark_wgrad_mxfp8(L, R, p.lhs_mx[lo // 32:(hi + 31) // 32].cpu().numpy(),
+                                       p.rhs_mx[lo // 32:(hi + 31) // 32].cpu().numpy(), sub)
+        else:
+            ref = orc.vark_wgrad_tensorwise(L, R, p.lhs_scale, p.rhs_scale, sub)
+        dt = time.perf_counter() - t0
+        refs.append(ref[0])
+        if seconds > 0 and t_total < seconds:
+            t_total += dt
+            done_flops += 2.0 * (hi - lo) * p.OUT_M * p.OUT_N
+            timed_groups += 1
+            tokens += hi - lo
+    parity = {name: _parity_record(orc, [_bf16_bits(out[g]) for g in range(p.G)], refs, empty,
+                                   f"{p.G} of {p.G}")
+              for name, out in outs.items()}
+    base = None
+    if timed_groups:
+        base = {"value": round(done_flops / t_total / 1e12, 4), "unit": "TFLOPS", "cores": int(threads),
+                "host_cores": host_cores(), "kind": "port",
+                "sample": f"{timed_groups} of {p.G} groups ({tokens} tokens, {done_flops / 1e12:.2f} TFLOP) of "
+                          f"{p.name}: numpy fp32 dequantize + OpenBLAS sgemm + bf16 RNE, {t_total:.1f} s"}
+    return parity, base
+
+
+def oracle_leg_fwd(p, out, seconds):
+    """``oracle_leg`` for a forward / data-gradient site: every row of every group of the last
+    timed launch's ``out`` [M_total, N] against the persistent GEMM's oracle, and the CPU
+    baseline from the same calls. Returns (parity record, cpu_baseline)."""
+    import numpy as np
+    from oracle import persistent_oracle as orp
+    from oracle import vark_oracle as orc
+    threads = _blas_threads()
+    offs = p.group_offs.cpu().numpy()
+    got = _bf16_bits(out)
+    refs, parts, empty = [], [], []
+    done_flops, t_total, timed_groups, rows = 0.0, 0.0, 0, 0
     for g in range(p.G):
         lo, hi = int(offs[g]), int(offs[g + 1])
         if hi == lo:
@@ -222,46 +314,52 @@ def cpu_baseline_fwd(p, seconds):
         A = p.a[lo:hi].cpu().numpy()
         B = p.b[g:g + 1].cpu().numpy()
         t0 = time.perf_counter()
-        orp.grouped_fp8(A, B, p.a_scale, p.b_scale, np.array([0, hi - lo], dtype=np.int64), p.a_format)
-        t_total += time.perf_counter() - t0
-        done_flops += 2.0 * (hi - lo) * p.K * p.N
-        groups += 1
-        rows += hi - lo
-        if t_total >= seconds:
-            break
-    return {"value": round(done_flops / t_total / 1e12, 4), "unit": "TFLOPS", "cores": int(threads),
-            "host_cores": host_cores(), "kind": "port",
-            "sample": f"{groups} of {p.G} groups ({rows} rows, {done_flops / 1e12:.2f} TFLOP) of {p.name}: "
-                      f"numpy fp32 dequantize + OpenBLAS sgemm + bf16 RNE, {t_total:.1f} s"}
+        refs.append(orp.grouped_fp8(A, B, p.a_scale, p.b_scale, np.array([0, hi - lo], dtype=np.int64),
+                                    p.a_format))
+        dt = time.perf_counter() - t0
+        parts.append(got[lo:hi])
+        if seconds > 0 and t_total < seconds:
+            t_total += dt
+            done_flops += 2.0 * (hi - lo) * p.K * p.N
+            timed_groups += 1
+            rows += hi - lo
+    parity = _parity_record(orc, parts, refs, empty, f"{p.G} of {p.G} ({int(offs[-1] - offs[0])} rows)")
+    base = None
+    if timed_groups:
+        base = {"value": round(done_flops / t_total / 1e12, 4), "unit": "TFLOPS", "cores": int(threads),
+                "host_cores": host_cores(), "kind": "port",
+                "sample": f"{timed_groups} of {p.G} groups ({rows} rows, {done_flops / 1e12:.2f} TFLOP) of "
+                          f"{p.name}: numpy fp32 dequantize + OpenBLAS sgemm + bf16 RNE, {t_total:.1f} s"}
+    return parity, base
 
 
-def cpu_baseline(p, seconds):
-    """Numpy oracle (fp32 dequantize + BLAS sgemm + bf16 RNE) on whole groups of the workload
-    until ~`seconds` of CPU time; throughput in TFLOPS over the groups processed."""
-    import numpy as np
-    from oracle import vark_oracle as orc
-    threads = _blas_threads()
-    offs = p.group_offs.cpu().numpy()
-    done_flops, t_total, groups, tokens = 0.0, 0.0, 0, 0
-    for g in range(p.G):
-        lo, hi = int(offs[g]), int(offs[g + 1])
-        if hi == lo:
-            continue
-        L = p.lhs[lo:hi].cpu().numpy()
-        R = p.rhs[lo:hi].cpu().numpy()
-        sub = np.array([0, hi - lo], dtype=np.int64)
-        t0 = time.perf_counter()
-        orc.vark_wgrad_tensorwise(L, R, p.lhs_scale, p.rhs_scale, sub)
-        t_total += time.perf_counter() - t0
-        done_flops += 2.0 * (hi - lo) * p.OUT_M * p.OUT_N
-        groups += 1
-        tokens += hi - lo
-        if t_total >= seconds:
-            break
-    return {"value": round(done_flops / t_total / 1e12, 4), "unit": "TFLOPS", "cores": int(threads),
-            "host_cores": host_cores(), "kind": "port",
-            "sample": f"{groups} of {p.G} groups ({tokens} tokens, {done_flops / 1e12:.2f} TFLOP) of {p.name}: "
-                      f"numpy fp32 dequantize + OpenBLAS sgemm + bf16 RNE, {t_total:.1f} s"}
+def time_drop_in_co(pkg, p, dev, steps, warmup):
+    """The drop-in code object (``variable_k_wgrad.co``) timed on the same inputs the way the
+    reference times its own: loaded through the hipModule path, launched with the 16-entry
+    kernelParams array on the null stream, grid num_cus x 512 threads, 64 KiB dynamic LDS
+    (reference bench.py:364-413,768-801), HIP events on the null stream around ``steps``
+    back-to-back launches. No C re-zeroing between launches: the kernel overwrites all of C.
+    Returns (record, output tensor of the last launch)."""
+    import torch
+    from ggemm_asm_amd import harness
+    module, func, name = harness.load_kernel(pkg.CODE_OBJECT_PATH)
+    try:
+        sl = torch.tensor(p.lhs_scale, dtype=torch.float32, device=dev)
+        sr = torch.tensor(p.rhs_scale, dtype=torch.float32, device=dev)
+        out = torch.empty((p.G, p.OUT_M, p.OUT_N), dtype=torch.bfloat16, device=dev)
+        ncu = harness.get_num_cus(dev.index or 0)
+        launch, _keep = harness.prepare_variable_k_args(func, p.lhs, p.rhs, out, sl, sr, p.group_offs, p.G, p.OUT_M,
+                                                        p.OUT_N, ncu)
+        torch.cuda.synchronize()
+        ms = harness.time_null_stream(launch, steps, warmup)
+    finally:
+        harness.unload_kernel(module)
+    geo = pkg.launch_geometry(p.OUT_N)
+    rec = {"ms": round(ms, 4), "TFLOPS": round(p.flops / (ms * 1e-3) / 1e12, 2),
+           "kernel": f"{os.path.basename(pkg.CODE_OBJECT_PATH)}: {name}, {geo['tile_m']}x{geo['tile_n']} tiles, "
+                     f"grid {ncu} x {harness.BLOCK} threads, {harness.SHARED_MEM} B dynamic LDS, kernelParams launch "
+                     f"on the null stream (what reference launcher.cpp / bench.py --kernel callers run)"}
+    return rec, out
 
 
 def quant_workload(pkg, name, seed, dev):
@@ -520,10 +618,13 @@ def main():
         run = lambda: pkg.grouped_gemm_fp8_tensorwise_variable_k(p.lhs, p.rhs, sl, sr, p.group_offs, out=c32,
                                                                   out_dtype=torch.float32,
                                                                   accumulate=args.out == "f32_accum")
+        run.out = c32
     else:
         run = make_runner(pkg, p, dev, args.mfma, args.persistent_kernel, args.row_align)
     ms = time_steps(run, args.steps, args.warmup)
     tflops = p.flops / (ms * 1e-3) / 1e12
+    drop_in_co = (args.drop_in and not fwd and not p.is_mx and args.out == "bf16" and args.mfma == "k128"
+                  and args.config not in SHARD_CONFIGS)
     # traffic measured for this exact variant (profiles/traffic_<config>[_<out>][_reference_lens].txt)
     traffic, traffic_source = read_traffic(args.config + ("" if args.out == "bf16" else "_" + args.out)
                                            + ("" if args.lens == "multinomial" else "_reference_lens"))
@@ -630,13 +731,38 @@ def main():
                                                          "TFLOPS": round(q.flops / (t * 1e-3) / 1e12, 2)}
             del c32, q
         line["extra"] = extra
-    if args.cpu_seconds > 0 and fwd:
-        line["cpu_baseline"] = cpu_baseline_fwd(p, args.cpu_seconds)
-    elif args.cpu_seconds > 0 and not p.is_mx:
-        line["cpu_baseline"] = cpu_baseline(p, args.cpu_seconds)
+    # the drop-in code object on the same inputs: what reference-side callers (launcher.cpp,
+    # bench.py --kernel) get; its C is checked against the oracle beside the library's
+    outs = {} if args.out == "f32_accum" else {"library": run.out}
+    if drop_in_co:
+        line["drop_in_co"], outs["drop_in_co"] = time_drop_in_co(pkg, p, dev, args.steps, args.warmup)
+    # outside the timed region: the oracle over every group of the timed inputs, checked against
+    # the last timed launch's output, and timed as the CPU baseline
+    failed = []
+    if fwd:
+        par, base = (oracle_leg_fwd(p, run.out, args.cpu_seconds) if args.parity or args.cpu_seconds > 0
+                     else (None, None))
+        line["parity"] = par if args.parity else None
+        failed += ["library"] if line["parity"] and not par["ok"] else []
+    elif args.parity and outs:
+        par, base = oracle_leg(p, outs, args.cpu_seconds)
+        line["parity"] = par.pop("library", None)
+        if "drop_in_co" in par:
+            line["drop_in_co"]["parity"] = par["drop_in_co"]
+        failed += [n for n, m in [("library", line["parity"]), ("drop_in_co", par.get("drop_in_co"))]
+                   if m and not m["ok"]]
     else:
-        line["cpu_baseline"] = None
+        line["parity"] = None
+        base = oracle_leg(p, {}, args.cpu_seconds)[1] if args.cpu_seconds > 0 else None
+    if args.parity and args.out == "f32_accum":
+        line["parity_note"] = "not checked here: C accumulates over the timed launches (fp32 accumulate); " \
+                              "tests/test_gpu_wide.py checks C0 + result bit for bit"
+    line["cpu_baseline"] = base
     print(json.dumps(line), flush=True)
+    if failed:
+        print(f"bench.py: the output of {', '.join(failed)} fails the parity bar against the oracle "
+              f"({PARITY_BAR})", file=sys.stderr, flush=True)
+        sys.exit(1)
 
 
 if __name__ == "__main__":

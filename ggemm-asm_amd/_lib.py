@@ -36,10 +36,17 @@ QUANT_EXPORTS = (
     "ggemm_quant_amax",
     "ggemm_quant_fp8_tensorwise",
     "ggemm_quant_fp8_tensorwise_delayed",
+    "ggemm_quant_fp8_tensorwise_delayed_dev",
     "ggemm_quant_fp8_tensorwise_transpose",
     "ggemm_quant_fp8_tensorwise_transpose_delayed",
+    "ggemm_quant_fp8_tensorwise_transpose_delayed_dev",
     "ggemm_quant_mxfp8_grouped",
 )
+
+# GGEMM_VARK_ABI_VERSION of include/ggemm_vark.h that these bindings are written for. Some exports
+# changed signature between versions (ggemm_vark_wgrad_fp8_out and ggemm_vark_wgrad_mxfp8 took
+# M_total from version 3 on), so a library of another version is refused at load.
+ABI_VERSION = 9
 
 ERRORS = {
     0: "GGEMM_OK", -1: "GGEMM_E_NULL", -2: "GGEMM_E_SHAPE", -3: "GGEMM_E_STRIDE",
@@ -70,6 +77,11 @@ def load():
         raise RuntimeError(f"{path} is missing: run `python __graft_entry__.py build` first "
                            "(this package has no CPU or Python fallback for the kernel)")
     lib = ctypes.CDLL(path)
+    lib.ggemm_vark_abi_version.argtypes = []
+    lib.ggemm_vark_abi_version.restype = ctypes.c_int32
+    if lib.ggemm_vark_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{path} has ABI version {lib.ggemm_vark_abi_version()}, these bindings need "
+                           f"{ABI_VERSION}: rebuild with `python __graft_entry__.py build`")
     vp, i32, i64p = ctypes.c_void_p, ctypes.c_int32, ctypes.POINTER(ctypes.c_int64)
     tw = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp]
     for name in ("ggemm_vark_wgrad_fp8", "ggemm_vark_wgrad_fp8_k32"):
@@ -114,11 +126,17 @@ def load():
     lib.ggemm_quant_fp8_tensorwise.restype = ctypes.c_int
     lib.ggemm_quant_fp8_tensorwise_delayed.argtypes = [vp, i32, i64, i32, i64, i32, vp, i64, vp, i32, i32, vp, vp]
     lib.ggemm_quant_fp8_tensorwise_delayed.restype = ctypes.c_int
+    lib.ggemm_quant_fp8_tensorwise_delayed_dev.argtypes = [vp, i32, i64, i32, i64, i32, vp, i64, vp, i32, vp, vp,
+                                                           vp]
+    lib.ggemm_quant_fp8_tensorwise_delayed_dev.restype = ctypes.c_int
     lib.ggemm_quant_fp8_tensorwise_transpose.argtypes = [vp, i32, i32, i32, i32, i32, vp, i64, vp, i64, vp, vp, vp]
     lib.ggemm_quant_fp8_tensorwise_transpose.restype = ctypes.c_int
     lib.ggemm_quant_fp8_tensorwise_transpose_delayed.argtypes = [vp, i32, i32, i32, i32, i32, vp, i64, vp, i64, vp,
                                                                  i32, i32, vp, vp]
     lib.ggemm_quant_fp8_tensorwise_transpose_delayed.restype = ctypes.c_int
+    lib.ggemm_quant_fp8_tensorwise_transpose_delayed_dev.argtypes = [vp, i32, i32, i32, i32, i32, vp, i64, vp, i64,
+                                                                     vp, i32, vp, vp, vp]
+    lib.ggemm_quant_fp8_tensorwise_transpose_delayed_dev.restype = ctypes.c_int
     lib.ggemm_quant_mxfp8_grouped.argtypes = [vp, i32, i64, i32, i64, vp, i32, i32, vp, i64, i64, vp, i64, vp, vp]
     lib.ggemm_quant_mxfp8_grouped.restype = ctypes.c_int
     _lib = lib

@@ -21,9 +21,11 @@ the autograd wiring left to the framework (Primus-Turbo, not vendored).
   ``main_grad=`` an fp32 [G, K, N] tensor, dW is accumulated into it instead (the fp32 epilogue,
   beta = 1) and the returned weight gradient is None.
 * ``weight_cache=FP8WeightCache()``: the weight's quantization (qw, qw^T, scale) is kept between
-  calls and redone only when the weight changes (its storage, shape or version counter: an
-  optimizer's in-place update bumps it). With gradient accumulation over several micro-batches
-  the weight pass then runs once per update instead of once per step.
+  calls and redone only when the weight changes (its storage, shape or version counter, which an
+  in-place write through the weight tensor bumps; writes through ``.data`` or raw pointers do not,
+  so ``cache.attach(optimizer)`` or ``cache.invalidate()`` covers those). With gradient
+  accumulation over several micro-batches the weight pass then runs once per update instead of
+  once per step.
 * ``scaling=FP8DelayedScaling()``: x, w and dy are quantized with delayed scaling (the largest
   amax of their previous calls, recorded on the device in the quantizing pass itself), which drops
   the standalone amax passes; values beyond the historical range saturate at +-fmax.
@@ -60,10 +62,14 @@ class FP8WeightCache:
 
     An entry is reused only for the same tensor object (held by a weak reference, so a new tensor
     that happens to reuse the old one's memory never hits) with the same storage address, shape,
-    strides, dtype and version counter; any in-place write to the weight (an optimizer step,
-    ``copy_``, ``add_``) bumps the version and the next call quantizes again. A cached entry
-    without q^T is upgraded when a call needs the data gradient. ``hits`` / ``misses`` count
-    lookups."""
+    strides, dtype and version counter. An in-place write through the weight itself (``copy_``,
+    ``add_``, an optimizer that updates the parameter tensor in place) bumps the version and the
+    next call quantizes again. Writes that bypass the version counter are NOT seen: through
+    ``w.data`` (a separate tensor with its own counter), through a raw pointer (fused multi-tensor
+    optimizer kernels, C extensions), or from another process. For those, call ``invalidate()``
+    after the update, or ``attach(optimizer)`` once, which invalidates after every
+    ``optimizer.step()``. A cached entry without q^T is upgraded when a call needs the data
+    gradient. ``hits`` / ``misses`` count lookups."""
 
     def __init__(self):
         self._ref = None
@@ -87,47 +93,66 @@ class FP8WeightCache:
         self._ref, self._key = weakref.ref(w), key
         return self._val
 
-    def clear(self):
+    def invalidate(self):
+        """Drop the entry: the next call quantizes the weight again."""
         self._ref = self._key = self._val = None
+
+    clear = invalidate
+
+    def attach(self, optimizer):
+        """Invalidate after every ``optimizer.step()`` (a torch.optim post-step hook), whatever
+        path the optimizer writes the weight through. Returns the hook's handle."""
+        return optimizer.register_step_post_hook(lambda *_: self.invalidate())
 
 
 class FP8DelayedScaling:
     """Delayed-scaling recipe for one layer's activations (``"x"``, forward), weight (``"w"``,
     forward; with a weight cache only on its misses) and output gradients (``"dy"``, backward).
 
-    Each tensor role keeps an fp32 amax history of ``history_len`` entries on the device. The first
-    call for a role quantizes with the tensor's own amax (current scaling) and records it; call n
-    after that takes slot n % history_len: the producer's delayed entry point scales by the largest
-    amax in the other slots, i.e. of up to ``history_len - 1`` previous calls, and writes this
-    tensor's amax into the slot in the same pass. The amax pass over the tensor is gone; a tensor
-    whose values outgrow the history saturates at +-fmax for that call. The slot index is host state,
-    so a graph capture replays one slot. ``calls`` counts the calls per role."""
+    Each tensor role keeps an fp32 amax history of ``history_len`` entries and the slot of its last
+    call (an int32), both on the device. The first call for a role quantizes with the tensor's own
+    amax (current scaling) and records it in slot 0; every later call advances the slot on the
+    device to (slot + 1) % history_len, scales by the largest amax in the other slots, i.e. of up
+    to ``history_len - 1`` previous calls, and writes this tensor's amax into the slot in the same
+    pass. The amax pass over the tensor is gone; a tensor whose values outgrow the history
+    saturates at +-fmax for that call. Because the slot advances on the device, a HIP graph that
+    captures the layer rolls through the history on every replay; the first call of each role
+    (the seeding one) must run eagerly, before any capture. ``calls`` counts the calls per role
+    made from Python (a graph replay does not pass through here)."""
 
     def __init__(self, history_len: int = 16):
         if not 2 <= history_len <= 1024:
             raise ValueError("history_len must be in [2, 1024]")
         self.history_len = history_len
         self.history: dict[str, torch.Tensor] = {}
+        self.slot: dict[str, torch.Tensor] = {}
         self.calls: dict[str, int] = {}
 
-    def _slot(self, role: str, device):
-        """(history, slot) of this call, or (None, None) for a role's first call on this device."""
-        n = self.calls.get(role, 0)
+    def _state(self, role: str, device):
+        """(history, device slot) of this role, or (None, None) before its first call on ``device``."""
         hist = self.history.get(role)
-        if n == 0 or hist is None or hist.device != device:
+        if hist is None or hist.device != device:
             return None, None
-        return hist, n % self.history_len
+        return hist, self.slot[role]
 
     def _seed(self, role: str, am: torch.Tensor):
         hist = torch.zeros(self.history_len, dtype=torch.float32, device=am.device)
         hist[:1].copy_(am.reshape(1))
         self.history[role] = hist
+        self.slot[role] = torch.zeros(1, dtype=torch.int32, device=am.device)
         self.calls[role] = 1
+
+    @staticmethod
+    def _no_seed_in_capture(role: str):
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(f"FP8DelayedScaling: the first call for {role!r} seeds its amax history with current "
+                               "scaling and must run eagerly; run one step before capturing a graph")
 
     def quantize(self, role: str, x: torch.Tensor, fmt: str):
         """(q, scale) of x for this role, rows on 128-byte lines."""
-        hist, slot = self._slot(role, x.device)
+        hist, slot = self._state(role, x.device)
         if hist is None:
+            self._no_seed_in_capture(role)
             q, scale, am = quantize_fp8_tensorwise(x, fmt, row_align=_LINE)
             self._seed(role, am)
             return q, scale
@@ -137,11 +162,12 @@ class FP8DelayedScaling:
 
     def quantize_weight(self, w: torch.Tensor, with_transpose: bool):
         """(qw, qw^T or None, scale) of a contiguous [G, N, K] weight (e4m3) for the role "w"."""
-        hist, slot = self._slot("w", w.device)
         if not with_transpose:
             q, scale = self.quantize("w", w, "e4m3")
             return q, None, scale
+        hist, slot = self._state("w", w.device)
         if hist is None:
+            self._no_seed_in_capture("w")
             qw, qwt, scale, am = quantize_fp8_tensorwise_transpose(w, "e4m3", row_align=_LINE)
             self._seed("w", am)
             return qw, qwt, scale

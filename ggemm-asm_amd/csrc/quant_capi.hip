@@ -123,30 +123,88 @@ int ggemm_quant_fp8_tensorwise(const void* x, int32_t in_dtype, int64_t rows, in
   return (int)hipGetLastError();
 }
 
-int ggemm_quant_fp8_tensorwise_delayed(const void* x, int32_t in_dtype, int64_t rows, int32_t cols, int64_t stride,
-                                       int32_t out_format, void* out, int64_t out_stride, float* amax_history,
-                                       int32_t history_len, int32_t slot, float* scale_out, void* stream) {
+// The delayed quantizers' history argument: a host slot in [0, H), or (slot_dev != nullptr) a device
+// slot that history_advance moves on before the pass.
+static int check_history(const float* amax_history, int32_t history_len, int32_t slot, const int32_t* slot_dev) {
+  if (!amax_history) return GGEMM_E_NULL;
+  if (history_len < 1 || history_len > GGEMM_QUANT_MAX_HISTORY) return GGEMM_E_SHAPE;
+  if (!slot_dev && (slot < 0 || slot >= history_len)) return GGEMM_E_SHAPE;
+  if (!aligned(amax_history, 4) || (slot_dev && !aligned(slot_dev, 4))) return GGEMM_E_ALIGN;
+  return GGEMM_OK;
+}
+
+// Clears the history entry this call records into: hist[slot], or the device slot's next entry.
+static void history_start(float* hist, int32_t H, int32_t slot, int32_t* slot_dev, hipStream_t s) {
+  if (slot_dev)
+    hipLaunchKernelGGL(qt::history_advance, dim3(1), dim3(64), 0, s, hist, H, slot_dev);
+  else
+    hipLaunchKernelGGL(qt::amax_init, dim3(1), dim3(64), 0, s, reinterpret_cast<uint32_t*>(hist + slot));
+}
+
+static int tensorwise_delayed(const void* x, int32_t in_dtype, int64_t rows, int32_t cols, int64_t stride,
+                              int32_t out_format, void* out, int64_t out_stride, float* amax_history,
+                              int32_t history_len, int32_t slot, int32_t* slot_dev, float* scale_out, void* stream) {
   int rc = check_2d(x, in_dtype, rows, cols, stride);
   if (rc) return rc;
-  if (!out || !amax_history || !scale_out) return GGEMM_E_NULL;
+  if (!out || !scale_out) return GGEMM_E_NULL;
   if (out_format != GGEMM_FP8_E4M3 && out_format != GGEMM_FP8_E5M2) return GGEMM_E_FORMAT;
-  if (history_len < 1 || history_len > GGEMM_QUANT_MAX_HISTORY || slot < 0 || slot >= history_len)
-    return GGEMM_E_SHAPE;
+  rc = check_history(amax_history, history_len, slot, slot_dev);
+  if (rc) return rc;
   if (out_stride < cols || out_stride % 8) return GGEMM_E_STRIDE;
-  if (!aligned(out, 8) || !aligned(scale_out, 4) || !aligned(amax_history, 4)) return GGEMM_E_ALIGN;
+  if (!aligned(out, 8) || !aligned(scale_out, 4)) return GGEMM_E_ALIGN;
   int cus = 0;
   rc = device_cus(&cus);
   if (rc) return rc;
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(qt::amax_init, dim3(1), dim3(64), 0, s, reinterpret_cast<uint32_t*>(amax_history + slot));
+  history_start(amax_history, history_len, slot, slot_dev, s);
   const int grid = grid_for(rows * (cols / 8), cus, kQuantPerCu);
   const bool f32 = in_dtype == GGEMM_IN_F32, e5 = out_format == GGEMM_FP8_E5M2;
   auto k = f32 ? (e5 ? qt::quant_tensorwise_delayed_kernel<true, true> : qt::quant_tensorwise_delayed_kernel<true, false>)
                : (e5 ? qt::quant_tensorwise_delayed_kernel<false, true>
                      : qt::quant_tensorwise_delayed_kernel<false, false>);
   hipLaunchKernelGGL(k, dim3(grid), dim3(qt::kThreads), 0, s, x, rows, cols, stride, static_cast<uint8_t*>(out),
-                     out_stride, amax_history, history_len, slot, scale_out);
+                     out_stride, amax_history, history_len, slot, (const int32_t*)slot_dev, scale_out);
   return (int)hipGetLastError();
+}
+
+static int transpose_delayed(const void* x, int32_t in_dtype, int32_t batch, int32_t rows, int32_t cols,
+                             int32_t out_format, void* out, int64_t out_stride, void* out_t, int64_t out_t_stride,
+                             float* amax_history, int32_t history_len, int32_t slot, int32_t* slot_dev,
+                             float* scale_out, void* stream) {
+  int rc = check_history(amax_history, history_len, slot, slot_dev);
+  if (rc) return rc;
+  rc = check_transpose(x, in_dtype, batch, rows, cols, out_format, out, out_stride, out_t, out_t_stride, scale_out);
+  if (rc) return rc;
+  int cus = 0;
+  rc = device_cus(&cus);
+  if (rc) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  history_start(amax_history, history_len, slot, slot_dev, s);
+  const bool f32 = in_dtype == GGEMM_IN_F32, e5 = out_format == GGEMM_FP8_E5M2;
+  auto k = f32 ? (e5 ? qt::quant_transpose_delayed_kernel<true, true> : qt::quant_transpose_delayed_kernel<true, false>)
+               : (e5 ? qt::quant_transpose_delayed_kernel<false, true>
+                     : qt::quant_transpose_delayed_kernel<false, false>);
+  const int grid = transpose_grid(reinterpret_cast<const void*>(k), batch, rows, cols, cus);
+  hipLaunchKernelGGL(k, dim3(grid), dim3(qt::kThreads), 0, s, x, batch, rows, cols, static_cast<uint8_t*>(out),
+                     out_stride, static_cast<uint8_t*>(out_t), out_t_stride, amax_history, history_len, slot,
+                     (const int32_t*)slot_dev, scale_out);
+  return (int)hipGetLastError();
+}
+
+int ggemm_quant_fp8_tensorwise_delayed(const void* x, int32_t in_dtype, int64_t rows, int32_t cols, int64_t stride,
+                                       int32_t out_format, void* out, int64_t out_stride, float* amax_history,
+                                       int32_t history_len, int32_t slot, float* scale_out, void* stream) {
+  return tensorwise_delayed(x, in_dtype, rows, cols, stride, out_format, out, out_stride, amax_history, history_len,
+                            slot, nullptr, scale_out, stream);
+}
+
+int ggemm_quant_fp8_tensorwise_delayed_dev(const void* x, int32_t in_dtype, int64_t rows, int32_t cols,
+                                           int64_t stride, int32_t out_format, void* out, int64_t out_stride,
+                                           float* amax_history, int32_t history_len, int32_t* slot,
+                                           float* scale_out, void* stream) {
+  if (!slot) return GGEMM_E_NULL;
+  return tensorwise_delayed(x, in_dtype, rows, cols, stride, out_format, out, out_stride, amax_history, history_len,
+                            0, slot, scale_out, stream);
 }
 
 int ggemm_quant_fp8_tensorwise_transpose(const void* x, int32_t in_dtype, int32_t batch, int32_t rows, int32_t cols,
@@ -175,26 +233,18 @@ int ggemm_quant_fp8_tensorwise_transpose_delayed(const void* x, int32_t in_dtype
                                                  int32_t cols, int32_t out_format, void* out, int64_t out_stride,
                                                  void* out_t, int64_t out_t_stride, float* amax_history,
                                                  int32_t history_len, int32_t slot, float* scale_out, void* stream) {
-  if (!amax_history) return GGEMM_E_NULL;
-  int rc = check_transpose(x, in_dtype, batch, rows, cols, out_format, out, out_stride, out_t, out_t_stride, scale_out);
-  if (rc) return rc;
-  if (history_len < 1 || history_len > GGEMM_QUANT_MAX_HISTORY || slot < 0 || slot >= history_len)
-    return GGEMM_E_SHAPE;
-  if (!aligned(amax_history, 4)) return GGEMM_E_ALIGN;
-  int cus = 0;
-  rc = device_cus(&cus);
-  if (rc) return rc;
-  hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(qt::amax_init, dim3(1), dim3(64), 0, s, reinterpret_cast<uint32_t*>(amax_history + slot));
-  const bool f32 = in_dtype == GGEMM_IN_F32, e5 = out_format == GGEMM_FP8_E5M2;
-  auto k = f32 ? (e5 ? qt::quant_transpose_delayed_kernel<true, true> : qt::quant_transpose_delayed_kernel<true, false>)
-               : (e5 ? qt::quant_transpose_delayed_kernel<false, true>
-                     : qt::quant_transpose_delayed_kernel<false, false>);
-  const int grid = transpose_grid(reinterpret_cast<const void*>(k), batch, rows, cols, cus);
-  hipLaunchKernelGGL(k, dim3(grid), dim3(qt::kThreads), 0, s, x, batch, rows, cols, static_cast<uint8_t*>(out),
-                     out_stride, static_cast<uint8_t*>(out_t), out_t_stride, amax_history, history_len, slot,
-                     scale_out);
-  return (int)hipGetLastError();
+  return transpose_delayed(x, in_dtype, batch, rows, cols, out_format, out, out_stride, out_t, out_t_stride,
+                           amax_history, history_len, slot, nullptr, scale_out, stream);
+}
+
+int ggemm_quant_fp8_tensorwise_transpose_delayed_dev(const void* x, int32_t in_dtype, int32_t batch, int32_t rows,
+                                                     int32_t cols, int32_t out_format, void* out, int64_t out_stride,
+                                                     void* out_t, int64_t out_t_stride, float* amax_history,
+                                                     int32_t history_len, int32_t* slot, float* scale_out,
+                                                     void* stream) {
+  if (!slot) return GGEMM_E_NULL;
+  return transpose_delayed(x, in_dtype, batch, rows, cols, out_format, out, out_stride, out_t, out_t_stride,
+                           amax_history, history_len, 0, slot, scale_out, stream);
 }
 
 int ggemm_quant_mxfp8_grouped(const void* x, int32_t in_dtype, int64_t rows, int32_t cols, int64_t stride,

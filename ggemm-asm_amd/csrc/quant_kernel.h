@@ -148,6 +148,19 @@ __global__ void __launch_bounds__(64) amax_init(uint32_t* amax_bits) {
   if (threadIdx.x == 0) *amax_bits = 0u;
 }
 
+// Delayed scaling with the slot kept on the device: *slot (the previous call's slot) moves on to
+// the next one, (slot + 1) mod H (a value outside [0, H) restarts at 0), and that entry is zeroed
+// for this call's amax. Launched before the quantizing pass, which reads the slot back, so every
+// launch -- a HIP graph replay included -- advances through the history.
+__global__ void __launch_bounds__(64) history_advance(float* hist, int H, int32_t* slot) {
+  if (threadIdx.x == 0) {
+    const int32_t prev = *slot;
+    const int32_t s = (prev >= 0 && prev < H - 1) ? prev + 1 : 0;
+    *slot = s;
+    reinterpret_cast<uint32_t*>(hist)[s] = 0u;
+  }
+}
+
 // The workgroup's max of its threads' m (|x| as fp32 bits) into *amax_bits, one atomic.
 __device__ __forceinline__ void block_amax(uint32_t m, uint32_t* amax_bits) {
 #pragma unroll
@@ -316,11 +329,14 @@ __global__ void __launch_bounds__(kThreads) quant_tensorwise_kernel(const void* 
 // Delayed scaling: scale = amax / fmax from the history's entries other than `slot` (the one this
 // call replaces; 1 when they are all zero, NaN when one is NaN), written to scale_out; x quantized
 // with it; the max |x| of this x reduced into hist[slot], which the host zeroed just before.
+// slot_dev != nullptr: the slot is *slot_dev (set by history_advance just before) instead.
 template <bool kF32, bool kE5M2>
 __global__ void __launch_bounds__(kThreads) quant_tensorwise_delayed_kernel(const void* x, int64_t rows, int cols,
                                                                             int64_t stride, uint8_t* out,
                                                                             int64_t out_stride, float* hist, int H,
-                                                                            int slot, float* scale_out) {
+                                                                            int slot, const int32_t* slot_dev,
+                                                                            float* scale_out) {
+  if (slot_dev) slot = *slot_dev;
   const ScaleDiv d = scale_div_given(tensor_scale<kE5M2>(history_amax(hist, H, slot)));
   if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = d.scale;
   const uint32_t m = d.fast ? tensorwise_body<kF32, kE5M2, true, true>(x, rows, cols, stride, out, out_stride, d)
@@ -426,14 +442,15 @@ __global__ void __launch_bounds__(kThreads) quant_transpose_kernel(const void* x
 
 // Delayed scaling of the transposing pass: the scale from the history's entries other than `slot`
 // (as quant_tensorwise_delayed_kernel), the max |x| of this x reduced into hist[slot], which the
-// host zeroed just before.
+// host zeroed just before; slot_dev as in quant_tensorwise_delayed_kernel.
 template <bool kF32, bool kE5M2>
 __global__ void __launch_bounds__(kThreads) quant_transpose_delayed_kernel(const void* x, int batch, int rows,
                                                                            int cols, uint8_t* out, int64_t out_stride,
                                                                            uint8_t* out_t, int64_t out_t_stride,
                                                                            float* hist, int H, int slot,
-                                                                           float* scale_out) {
+                                                                           const int32_t* slot_dev, float* scale_out) {
   __shared__ __attribute__((aligned(16))) uint8_t s_t[kTT * kTT];
+  if (slot_dev) slot = *slot_dev;
   const ScaleDiv d = scale_div_given(tensor_scale<kE5M2>(history_amax(hist, H, slot)));
   if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = d.scale;
   const uint32_t m =

@@ -57,10 +57,17 @@ int wide_tile_for(int OUT_M, int OUT_N, int scm) {
   return 0;
 }
 
-// The bf16 entry points run a wide-tile kernel where one takes the shape and the problem is large
-// enough to fill its tiles (OUT_M >= 1024); otherwise the 192 x 384 / 192 x 320 kernel.
-int wide_selected(int OUT_M, int OUT_N, int scm, const void* out) {
-  return OUT_M >= 1024 && aligned(out, 16) ? wide_tile_for(OUT_M, OUT_N, scm) : 0;
+// The wide kernels' epilogues store 16-byte chunks of C rows: every row and group must start on 16
+// bytes. scm / scg in bf16 elements (twice the fp32 strides for an fp32 C).
+bool wide_rows_aligned(const void* out, int64_t scm, int64_t scg) {
+  return aligned(out, 16) && scm % 8 == 0 && scg % 8 == 0;
+}
+
+// The bf16 entry points run a wide-tile kernel where one takes the shape, C rows start on 16 bytes
+// and the problem is large enough to fill its tiles (OUT_M >= 1024); otherwise the 192 x 384 /
+// 192 x 320 kernel.
+int wide_selected(int OUT_M, int OUT_N, int64_t scm, int64_t scg, const void* out) {
+  return OUT_M >= 1024 && wide_rows_aligned(out, scm, scg) ? wide_tile_for(OUT_M, OUT_N, (int)scm) : 0;
 }
 
 int launch_wide(int tile, int out_mode, const void* lhs, const void* rhs, void* out, const float* lhs_scale,
@@ -101,7 +108,7 @@ static int launch_tensorwise(bool legacy, const void* lhs, const void* rhs, void
                            scn);
   if (rc) return rc;
   if (m_total < 0) return GGEMM_E_SHAPE;
-  if (const int tile = legacy ? 0 : wide_selected(OUT_M, OUT_N, scm, out))
+  if (const int tile = legacy ? 0 : wide_selected(OUT_M, OUT_N, scm, scg, out))
     return launch_wide(tile, GGEMM_OUT_BF16, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, slm,
                        srm, scg, scm, scn, m_total, stream);
   int cus = 0;
@@ -131,7 +138,8 @@ int ggemm_vark_wgrad_fp8_wide(const void* lhs, const void* rhs, void* out, const
   if (tile == 320 && (OUT_M % 320 || OUT_N % 320)) tile = 0;
   if (tile == 256 && (OUT_N % 384 || out_mode != GGEMM_OUT_BF16)) tile = 0;   // fp32 epilogues: 320 x 320
   if ((tile != 256 && tile != 320) || fit == 0) return GGEMM_E_SHAPE;
-  if (!aligned(out, 16)) return GGEMM_E_ALIGN;    // 16-byte stores of whole row chunks
+  const int64_t w = out_mode == GGEMM_OUT_BF16 ? 1 : 2;   // strides in bf16 elements
+  if (!wide_rows_aligned(out, w * stride_cm, w * stride_cg)) return GGEMM_E_ALIGN;   // 16-byte row chunks
   return launch_wide(tile, out_mode, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N, stride_lhs_m,
                      stride_rhs_m, stride_cg, stride_cm, stride_cn, M_total, stream);
 }
@@ -167,7 +175,7 @@ int ggemm_vark_wgrad_fp8_out(const void* lhs, const void* rhs, void* out, const 
   if (M_total < 0) return GGEMM_E_SHAPE;
   if (!aligned(out, 16)) return GGEMM_E_ALIGN;    // 16-byte fp32 row segments
   // fp32 C takes the 320 x 320 wide-tile kernel where the bf16 C of the same shape would
-  if (wide_selected(OUT_M, OUT_N, 2 * stride_cm, out) == 320)
+  if (wide_selected(OUT_M, OUT_N, 2 * (int64_t)stride_cm, 2 * (int64_t)stride_cg, out) == 320)
     return launch_wide(320, out_mode, lhs, rhs, out, lhs_scale, rhs_scale, group_offs, G, OUT_M, OUT_N,
                        stride_lhs_m, stride_rhs_m, stride_cg, stride_cm, stride_cn, M_total, stream);
   int cus = 0;
@@ -196,10 +204,10 @@ static int launch_mx(int32_t tile_m, const void* lhs, const void* rhs, void* out
     return GGEMM_E_STRIDE;
   if (!aligned(lhs_scale, 16) || !aligned(rhs_scale, 16)) return GGEMM_E_ALIGN;
   if (tile_m != 0 && tile_m != 320 && tile_m != 192) return GGEMM_E_SHAPE;
-  bool wide = tile_m == 0 ? wide_selected(OUT_M, OUT_N, stride_cm, out) == 320 : tile_m == 320;
+  bool wide = tile_m == 0 ? wide_selected(OUT_M, OUT_N, stride_cm, stride_cg, out) == 320 : tile_m == 320;
   if (tile_m == 320) {
     if (wide_tile_for(OUT_M, OUT_N, stride_cm) != 320) return GGEMM_E_SHAPE;
-    if (!aligned(out, 16)) return GGEMM_E_ALIGN;    // 16-byte stores of whole row chunks
+    if (!wide_rows_aligned(out, stride_cm, stride_cg)) return GGEMM_E_ALIGN;    // 16-byte row chunks
   }
   int cus = 0;
   rc = device_cus(&cus);
@@ -280,7 +288,7 @@ const char* ggemm_vark_strerror(int32_t code) {
 int32_t ggemm_vark_abi_version(void) { return GGEMM_VARK_ABI_VERSION; }
 
 int32_t ggemm_vark_bf16_kernel(int32_t OUT_M, int32_t OUT_N, int32_t stride_cm, const void* out) {
-  return wide_selected(OUT_M, OUT_N, stride_cm, out);
+  return wide_selected(OUT_M, OUT_N, stride_cm, (int64_t)OUT_M * stride_cm, out);
 }
 
 void ggemm_vark_launch_geometry(int32_t out_n, int32_t* block_threads, int32_t* dynamic_lds, int32_t* tile_m,

@@ -51,8 +51,45 @@ def load_hip():
     lib.hipModuleUnload.restype = ctypes.c_int
     lib.hipGetErrorString.argtypes = [ctypes.c_int]
     lib.hipGetErrorString.restype = ctypes.c_char_p
+    lib.hipEventCreate.argtypes = [ctypes.POINTER(vp)]
+    lib.hipEventCreate.restype = ctypes.c_int
+    lib.hipEventRecord.argtypes = [vp, vp]
+    lib.hipEventRecord.restype = ctypes.c_int
+    lib.hipEventSynchronize.argtypes = [vp]
+    lib.hipEventSynchronize.restype = ctypes.c_int
+    lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
+    lib.hipEventElapsedTime.restype = ctypes.c_int
+    lib.hipEventDestroy.argtypes = [vp]
+    lib.hipEventDestroy.restype = ctypes.c_int
+    lib.hipDeviceSynchronize.argtypes = []
+    lib.hipDeviceSynchronize.restype = ctypes.c_int
     _hip = lib
     return lib
+
+
+def time_null_stream(launch, iters: int, warmup: int) -> float:
+    """Average ms per launch of ``launch`` (which enqueues on the null stream, as the reference's
+    launches do) from two HIP events recorded on the null stream around ``iters`` back-to-back
+    launches after ``warmup`` untimed ones (reference bench.py:768-801, launcher.cpp:149-176)."""
+    hip = load_hip()
+    for _ in range(warmup):
+        launch()
+    check_hip(hip.hipDeviceSynchronize(), "synchronizing before timing")
+    ev = [ctypes.c_void_p(), ctypes.c_void_p()]
+    for e in ev:
+        check_hip(hip.hipEventCreate(ctypes.byref(e)), "creating a timing event")
+    try:
+        check_hip(hip.hipEventRecord(ev[0], None), "recording the start event")
+        for _ in range(iters):
+            launch()
+        check_hip(hip.hipEventRecord(ev[1], None), "recording the stop event")
+        check_hip(hip.hipEventSynchronize(ev[1]), "waiting for the stop event")
+        ms = ctypes.c_float()
+        check_hip(hip.hipEventElapsedTime(ctypes.byref(ms), ev[0], ev[1]), "reading the elapsed time")
+    finally:
+        for e in ev:
+            hip.hipEventDestroy(e)
+    return ms.value / max(iters, 1)
 
 
 def check_hip(err: int, msg: str = "") -> None:

@@ -110,27 +110,34 @@ def quantize_fp8_tensorwise(x: torch.Tensor, fmt: str = "e4m3", row_align: int |
     return q, scale, am
 
 
-def quantize_fp8_tensorwise_delayed(x: torch.Tensor, amax_history: torch.Tensor, slot: int, fmt: str = "e4m3",
+def quantize_fp8_tensorwise_delayed(x: torch.Tensor, amax_history: torch.Tensor, slot, fmt: str = "e4m3",
                                     row_align: int | None = None):
     """Per-tensor FP8 quantization with delayed scaling. ``amax_history``: fp32 [H] on x's device;
     the scale is ``max(amax_history[i] for i != slot) / fmax`` (1 when those are all 0), computed on
     the device, and ``amax_history[slot]`` becomes this x's amax in the same pass (no separate amax
     pass). Returns ``(q, scale)`` as ``quantize_fp8_tensorwise`` does; values beyond ``fmax * scale``
-    saturate to +-fmax."""
+    saturate to +-fmax.
+
+    ``slot``: an int in [0, H), or a one-element int32 tensor on x's device holding the previous
+    call's slot, which the call advances to ``(slot + 1) % H`` on the device before using it -- the
+    form a HIP graph capture replays correctly (each replay moves on through the history)."""
     _check(x, fmt)
     _check_history(amax_history, slot, x.device)
     H = amax_history.numel()
+    dev_slot = isinstance(slot, torch.Tensor)
     x2 = _as_2d(x)
     code, dt = _OUT[fmt]
     q = _padded_empty(x.shape, row_align, dt, x.device)
     q2 = q.as_strided((x2.shape[0], x.shape[-1]), (q.stride(-2), 1))
     scale = torch.empty((), dtype=torch.float32, device=x.device)
     qp = q2 if q2.shape[0] > 0 else torch.empty((1, x.shape[-1]), dtype=dt, device=x.device)
+    name = "ggemm_quant_fp8_tensorwise_delayed" + ("_dev" if dev_slot else "")
     with torch.cuda.device(x.device):
-        rc = _lib.load().ggemm_quant_fp8_tensorwise_delayed(
+        rc = getattr(_lib.load(), name)(
             _ptr(x2), _IN[x.dtype], x2.shape[0], x2.shape[1], _row_stride(x2), code, qp.data_ptr(),
-            _row_stride(qp), amax_history.data_ptr(), H, slot, scale.data_ptr(), _stream(x.device))
-    _lib.check(rc, "ggemm_quant_fp8_tensorwise_delayed")
+            _row_stride(qp), amax_history.data_ptr(), H, slot.data_ptr() if dev_slot else slot, scale.data_ptr(),
+            _stream(x.device))
+    _lib.check(rc, name)
     return q, scale
 
 
@@ -145,21 +152,25 @@ def quantize_fp8_tensorwise_transpose(x: torch.Tensor, fmt: str = "e4m3", keep: 
     return _transpose(x, fmt, keep, row_align, None, 0)
 
 
-def quantize_fp8_tensorwise_transpose_delayed(x: torch.Tensor, amax_history: torch.Tensor, slot: int,
+def quantize_fp8_tensorwise_transpose_delayed(x: torch.Tensor, amax_history: torch.Tensor, slot,
                                               fmt: str = "e4m3", keep: bool = True, row_align: int | None = None):
     """``quantize_fp8_tensorwise_transpose`` with delayed scaling: the scale from ``amax_history``'s
     entries other than ``slot`` and x's amax recorded at ``slot`` in the same pass, as in
-    ``quantize_fp8_tensorwise_delayed``. Returns ``(q, q_t, scale)``."""
+    ``quantize_fp8_tensorwise_delayed`` (``slot`` an int, or a device int32 tensor the call
+    advances). Returns ``(q, q_t, scale)``."""
     q, q_t, scale, _ = _transpose(x, fmt, keep, row_align, amax_history, slot)
     return q, q_t, scale
 
 
-def _check_history(amax_history: torch.Tensor, slot: int, device):
+def _check_history(amax_history: torch.Tensor, slot, device):
     if amax_history.dtype != torch.float32 or amax_history.dim() != 1 or not amax_history.is_contiguous():
         raise ValueError("amax_history must be a contiguous fp32 [H] tensor")
     if amax_history.device != device:
         raise ValueError("amax_history must be on x's device")
-    if not 0 <= slot < amax_history.numel():
+    if isinstance(slot, torch.Tensor):
+        if slot.dtype != torch.int32 or slot.numel() != 1 or slot.device != device:
+            raise ValueError("a device slot must be a one-element int32 tensor on x's device")
+    elif not 0 <= slot < amax_history.numel():
         raise ValueError(f"slot {slot} outside the history of {amax_history.numel()}")
 
 
@@ -195,10 +206,11 @@ def _transpose(x, fmt, keep, row_align, amax_history, slot):
                 _stream(x.device))
         else:
             am = None
-            name = "ggemm_quant_fp8_tensorwise_transpose_delayed"
-            rc = lib.ggemm_quant_fp8_tensorwise_transpose_delayed(
+            dev_slot = isinstance(slot, torch.Tensor)
+            name = "ggemm_quant_fp8_tensorwise_transpose_delayed" + ("_dev" if dev_slot else "")
+            rc = getattr(lib, name)(
                 xp, _IN[x.dtype], B, R, C, code, qp, q_stride, tp, t_stride, amax_history.data_ptr(),
-                amax_history.numel(), slot, scale.data_ptr(), _stream(x.device))
+                amax_history.numel(), slot.data_ptr() if dev_slot else slot, scale.data_ptr(), _stream(x.device))
     _lib.check(rc, name)
     return q, q_t, scale, am
 

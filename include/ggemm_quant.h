@@ -67,6 +67,19 @@ int ggemm_quant_fp8_tensorwise_delayed(const void* x, int32_t in_dtype, int64_t 
                                        int32_t out_format, void* out, int64_t out_stride, float* amax_history,
                                        int32_t history_len, int32_t slot, float* scale_out, void* stream);
 
+/* ggemm_quant_fp8_tensorwise_delayed with the slot kept on the device (ABI version 9): `slot` is a
+ * device int32 holding the previous call's slot; the call first moves it to (slot + 1) mod
+ * history_len (a value outside [0, history_len) restarts at 0) and clears that history entry, then
+ * quantizes as ggemm_quant_fp8_tensorwise_delayed with it. The slot is read and advanced by the
+ * launched kernels, so a HIP graph that captures the call rolls through the history on every
+ * replay (with a host slot a replay would record into one fixed entry and scale by a frozen
+ * history). A caller cycling slot 0, 1, ... through the host entry point gets the same results
+ * from this one with *slot starting at history_len - 1. No reference counterpart. */
+int ggemm_quant_fp8_tensorwise_delayed_dev(const void* x, int32_t in_dtype, int64_t rows, int32_t cols,
+                                           int64_t stride, int32_t out_format, void* out, int64_t out_stride,
+                                           float* amax_history, int32_t history_len, int32_t* slot,
+                                           float* scale_out, void* stream);
+
 /* Per-tensor quantization of a batch of matrices with a transposed copy: x is a contiguous
  * [batch, rows, cols] (a weight [G, N, K]); amax_out and scale_out as in
  * ggemm_quant_fp8_tensorwise over all batch*rows*cols elements;
@@ -89,6 +102,14 @@ int ggemm_quant_fp8_tensorwise_transpose_delayed(const void* x, int32_t in_dtype
                                                  int32_t cols, int32_t out_format, void* out, int64_t out_stride,
                                                  void* out_t, int64_t out_t_stride, float* amax_history,
                                                  int32_t history_len, int32_t slot, float* scale_out, void* stream);
+
+/* ggemm_quant_fp8_tensorwise_transpose_delayed with the slot kept on the device, advanced by the
+ * call as in ggemm_quant_fp8_tensorwise_delayed_dev (ABI version 9). No reference counterpart. */
+int ggemm_quant_fp8_tensorwise_transpose_delayed_dev(const void* x, int32_t in_dtype, int32_t batch, int32_t rows,
+                                                     int32_t cols, int32_t out_format, void* out, int64_t out_stride,
+                                                     void* out_t, int64_t out_t_stride, float* amax_history,
+                                                     int32_t history_len, int32_t* slot, float* scale_out,
+                                                     void* stream);
 
 /* MX (OCP microscaling) quantization along the token axis with group-aligned padding, the input
  * of ggemm_vark_wgrad_mxfp8. x: [rows, cols] token-major; group_offs: int64 [G+1] (0-based,

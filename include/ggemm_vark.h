@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-#define GGEMM_VARK_ABI_VERSION 8
+#define GGEMM_VARK_ABI_VERSION 9
 
 enum {
   GGEMM_OK = 0,
@@ -86,8 +86,9 @@ int ggemm_vark_wgrad_fp8_out(const void* lhs, const void* rhs, void* out, const 
  * and result as ggemm_vark_wgrad_fp8_out with the same out_mode, group offsets clamped to
  * [0, min(M_total, 2^31 - 1)]. tile_m: 320 (OUT_M and OUT_N multiples of 320), 256 (OUT_N a
  * multiple of 384; bf16 C only) or 0 (320 where it fits, else 256). Also a group of C within 2^31
- * bytes and out 16-byte aligned; otherwise GGEMM_E_SHAPE / GGEMM_E_ALIGN / GGEMM_E_FORMAT and
- * nothing is launched. */
+ * bytes, and every C row and group starting on 16 bytes (out 16-byte aligned, stride_cm and
+ * stride_cg multiples of 8 for bf16 C, of 4 for fp32 C: the epilogue stores 16-byte row chunks);
+ * otherwise GGEMM_E_SHAPE / GGEMM_E_ALIGN / GGEMM_E_FORMAT and nothing is launched. */
 int ggemm_vark_wgrad_fp8_wide(const void* lhs, const void* rhs, void* out, const float* lhs_scale,
                               const float* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
                               int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,
@@ -110,7 +111,8 @@ int ggemm_vark_wgrad_mxfp8(const void* lhs, const void* rhs, void* out, const ui
 
 /* ggemm_vark_wgrad_mxfp8 on a chosen kernel (no reference counterpart): tile_m 320 = the 320 x 320
  * wide-tile kernel (OUT_M and OUT_N multiples of 320, a group of C within 2^31 bytes, out 16-byte
- * aligned, group offsets clamped to [0, min(M_total, 2^31 - 1)]; otherwise GGEMM_E_SHAPE /
+ * aligned, stride_cm and stride_cg multiples of 8, group offsets clamped to
+ * [0, min(M_total, 2^31 - 1)]; otherwise GGEMM_E_SHAPE /
  * GGEMM_E_ALIGN and nothing is launched), 192 = the 192-row-tile kernel, 0 = the choice of
  * ggemm_vark_wgrad_mxfp8. Same arguments and result otherwise. */
 int ggemm_vark_wgrad_mxfp8_tile(const void* lhs, const void* rhs, void* out, const uint8_t* lhs_scale,
@@ -137,11 +139,12 @@ int32_t ggemm_vark_abi_version(void);
 
 /* Which kernel the bf16 entry points (ggemm_vark_wgrad_fp8, ggemm_vark_wgrad_fp8_out with
  * GGEMM_OUT_BF16) run for a shape: 320 or 256 = the wide-tile kernel with that tile height
- * (OUT_M >= 1024, a shape ggemm_vark_wgrad_fp8_wide takes with tile_m = 0, out 16-byte aligned),
- * 0 = the 192-row-tile kernel of the reference launch geometry. The fp32 modes of
- * ggemm_vark_wgrad_fp8_out run the 320 x 320 kernel where this returns 320 for stride_cm twice
- * the fp32 row stride, ggemm_vark_wgrad_mxfp8 its MX variant where this returns 320. No reference
- * counterpart. Touches no device. */
+ * (OUT_M >= 1024, a shape ggemm_vark_wgrad_fp8_wide takes with tile_m = 0, out 16-byte aligned,
+ * stride_cm a multiple of 8; groups contiguous, stride_cg = OUT_M * stride_cm, which the entry
+ * points also require to be a multiple of 8 for a wide kernel), 0 = the 192-row-tile kernel of the
+ * reference launch geometry. The fp32 modes of ggemm_vark_wgrad_fp8_out run the 320 x 320 kernel
+ * where this returns 320 for stride_cm twice the fp32 row stride, ggemm_vark_wgrad_mxfp8 its MX
+ * variant where this returns 320. No reference counterpart. Touches no device. */
 int32_t ggemm_vark_bf16_kernel(int32_t OUT_M, int32_t OUT_N, int32_t stride_cm, const void* out);
 
 /* Launch geometry the library uses (and the drop-in code object expects) for a problem of width

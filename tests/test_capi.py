@@ -34,6 +34,8 @@ def test_bf16_kernel_selection(pkg):
     assert lib.ggemm_vark_bf16_kernel(2048, 2000, 2000, 4096) == 0      # neither tile divides OUT_N
     assert lib.ggemm_vark_bf16_kernel(1008, 5760, 5760, 4096) == 0      # small OUT_M
     assert lib.ggemm_vark_bf16_kernel(2880, 5760, 5760, 4104) == 0      # C only 8-byte aligned
+    assert lib.ggemm_vark_bf16_kernel(2880, 5760, 5768, 4096) == 320    # padded rows on 16 bytes
+    assert lib.ggemm_vark_bf16_kernel(2880, 5760, 5764, 4096) == 0      # rows on 8 bytes: 192-row kernel
     assert lib.ggemm_vark_bf16_kernel(65536, 384, 65536, 4096) == 0     # group past 32-bit offsets
     assert pkg.bf16_kernel(2880, 5760) == "wide320" and pkg.bf16_kernel(1024, 768) == "wide256"
     assert pkg.bf16_kernel(1000, 2880) == "192-row"
@@ -264,3 +266,19 @@ def test_code_object_resources(pkg):
     assert info["group_segment_fixed_size"] == 98304 and info["kernarg_segment_size"] == 96, info
     assert info["max_flat_workgroup_size"] == 512 and info["wavefront_size"] == 64, info
     assert info["mfma"] >= 36 and info["lds_dma"] >= 9, info
+
+
+@pytest.mark.parametrize("mode,scm,scg,rc", [
+    (0, 5764, 2880 * 5764, -4), (0, 5768, 2880 * 5768 + 4, -4), (1, 5762, 2880 * 5762, -3),
+    (2, 5766, 2880 * 5766, -3),
+])
+def test_wide_entry_requires_16_byte_rows(pkg, mode, scm, scg, rc):
+    """The forced wide-tile entry refuses C rows or groups that do not start on 16 bytes (its
+    epilogue stores 16-byte row chunks): bf16 strides must be multiples of 8 elements, fp32 of 4.
+    Only rejected calls here: nothing is launched."""
+    lib = pkg.load_library()
+    assert lib.ggemm_vark_wgrad_fp8_wide(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 32, 2880, 5760, 2880, 5760, scg, scm, 1,
+                                         131072, 320, mode, None) == rc
+    if mode == 0:   # the MX kernel on request applies the same rule
+        assert lib.ggemm_vark_wgrad_mxfp8_tile(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 32, 2880, 5760, 2880, 5760, scg,
+                                               scm, 1, 2880, 5760, 131072, 320, None) == rc

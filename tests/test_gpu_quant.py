@@ -485,6 +485,39 @@ def test_delayed_cycle_matches_oracle(pkg, orq, cuda):
         np.testing.assert_array_equal(_bytes(q), q_ref)
 
 
+def test_device_slot_cycle_matches_oracle(pkg, orq, cuda):
+    """The device-slot entries (the slot advanced by the call on the device) over nine calls through
+    a 3-entry history, three wraps, with the input's range growing and shrinking: each call's bytes
+    and scale against the oracle at slot n % 3, the history in step and the device slot equal to
+    n % 3 after call n. Plain and transposing quantizers; the transposing one starts from an
+    out-of-range slot value (57), which restarts at 0."""
+    rng = np.random.default_rng(9)
+    mags = (1, 3, 0.25, 8, 1, 0.5, 2, 16, 0.1)
+    xs = [(rng.standard_normal((384, 160)) * m).astype(np.float32) for m in mags]
+    ws = [(rng.standard_normal((2, 96, 64)) * m * 0.05).astype(np.float32) for m in mags]
+    _say("device-slot delayed cycle of 9 calls, history 3")
+    h = torch.tensor([orq.amax(xs[0]) * 2, 0.0, 0.0], dtype=torch.float32, device=cuda)
+    hw = torch.tensor([0.0, 0.0, orq.amax(ws[0])], dtype=torch.float32, device=cuda)
+    h_ref, hw_ref = h.cpu().numpy(), hw.cpu().numpy()
+    slot = torch.tensor([2], dtype=torch.int32, device=cuda)       # the previous call's slot
+    slot_w = torch.tensor([57], dtype=torch.int32, device=cuda)
+    for n in range(len(xs)):
+        q, scale = pkg.quantize_fp8_tensorwise_delayed(torch.from_numpy(xs[n]).to(cuda), h, slot, "e5m2",
+                                                       row_align=128)
+        qw, qwt, sw = pkg.quantize_fp8_tensorwise_transpose_delayed(torch.from_numpy(ws[n]).to(cuda), hw, slot_w,
+                                                                   "e4m3")
+        q_ref, s_ref, h_ref = orq.quantize_tensorwise_delayed(xs[n], h_ref, n % 3, "e5m2")
+        w_ref, sw_ref, hw_ref = orq.quantize_tensorwise_delayed(ws[n].reshape(-1, 64), hw_ref, n % 3, "e4m3")
+        torch.cuda.synchronize()
+        assert int(slot) == n % 3 and int(slot_w) == n % 3, n
+        assert float(scale) == float(s_ref) and float(sw) == float(sw_ref), n
+        np.testing.assert_array_equal(h.cpu().numpy(), h_ref)
+        np.testing.assert_array_equal(hw.cpu().numpy(), hw_ref)
+        np.testing.assert_array_equal(_bytes(q), q_ref)
+        np.testing.assert_array_equal(_bytes(qw).reshape(-1, 64), w_ref)
+        np.testing.assert_array_equal(_bytes(qwt), w_ref.reshape(2, 96, 64).transpose(0, 2, 1))
+
+
 @pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
 @pytest.mark.parametrize("shape,dtype,align", [((4, 96, 160), torch.bfloat16, None), ((3, 272, 144), torch.float32, 128),
                                                ((1, 5760 // 4, 2880 // 4), torch.bfloat16, 128)])

@@ -306,3 +306,76 @@ def test_wide_mx_full_size(pkg, orc, cuda):
     _say(f"gate_up_mx: wide vs 192-row kernel {m}")
     assert orc.parity_ok(m)
     _oracle_whole(pkg, orc, p, out)
+
+
+# ----------------------------------------------------------------------------- C row strides
+
+STRIDE_CASES = [
+    # (OUT_M, OUT_N, extra columns per C row, kernel the library picks)
+    (1280, 1920, 8, "wide320"), (1280, 1920, 4, "192-row"), (1024, 768, 8, "wide256"), (1024, 768, 4, "192-row"),
+]
+
+
+@pytest.mark.parametrize("om,on,pad,kernel", STRIDE_CASES, ids=[f"{k}_pad{p}_{m}x{n}" for m, n, p, k in STRIDE_CASES])
+def test_strided_c_rows_bf16(pkg, orc, cuda, om, on, pad, kernel):
+    """bf16 C rows padded by `pad` columns (stride_cm = OUT_N + pad) at shapes a wide kernel takes:
+    rows on 16 bytes (pad 8) keep the wide kernel, rows on 8 bytes (pad 4) go to the 192-row kernel
+    (the wide epilogue stores 16-byte row chunks). Either way the result meets the bar against the
+    oracle and the padding columns keep their sentinel."""
+    lens = [300, 0, 517, 64]
+    _say(f"strided bf16 C {om}x{on} pad {pad}: {kernel}")
+    assert pkg.bf16_kernel(om, on, on + pad) == kernel
+    lhs, rhs, offs, _, (sl, sr) = _rand_bytes_problem(lens, om, on, seed=om + pad)
+    big = torch.full((len(lens), om, on + pad), 7.0, dtype=torch.bfloat16, device=cuda)
+    out = pkg.grouped_gemm_fp8_tensorwise_variable_k(lhs.to(cuda), rhs.to(cuda), torch.tensor(sl, device=cuda),
+                                                     torch.tensor(sr, device=cuda), offs.to(cuda),
+                                                     out=big[:, :, :on])
+    torch.cuda.synchronize()
+    assert bool((big[:, :, on:] == 7.0).all())
+    ref = orc.vark_wgrad_tensorwise(lhs.numpy(), rhs.numpy(), sl, sr, offs.numpy())
+    _assert_parity(orc, pkg.as_bf16_bits(out), ref, offs.numpy(), f"strided bf16 pad {pad}")
+
+
+@pytest.mark.parametrize("pad", [4, 8])
+def test_strided_c_rows_fp32_accumulate(pkg, cuda, pad):
+    """fp32 accumulate into C rows padded by `pad` floats (16-byte rows: the 320 x 320 kernel): C
+    equals C0 + the contiguous fp32 result bit for bit, padding columns untouched."""
+    lens, om, on = [300, 0, 517, 64], 1280, 1920
+    _say(f"strided fp32-accumulate C pad {pad}")
+    lhs, rhs, offs, _, (sl, sr) = _rand_bytes_problem(lens, om, on, seed=pad + 1)
+    dl, dr, do = lhs.to(cuda), rhs.to(cuda), offs.to(cuda)
+    s1, s2 = torch.tensor(sl, device=cuda), torch.tensor(sr, device=cuda)
+    res = pkg.grouped_gemm_fp8_tensorwise_variable_k(dl, dr, s1, s2, do, out_dtype=torch.float32)
+    c0 = torch.randn((len(lens), om, on), generator=torch.Generator().manual_seed(pad), dtype=torch.float32).to(cuda)
+    big = torch.full((len(lens), om, on + pad), 7.0, dtype=torch.float32, device=cuda)
+    big[:, :, :on] = c0
+    pkg.grouped_gemm_fp8_tensorwise_variable_k(dl, dr, s1, s2, do, out=big[:, :, :on], accumulate=True)
+    torch.cuda.synchronize()
+    assert bool((big[:, :, on:] == 7.0).all())
+    assert torch.equal(big[:, :, :on], c0 + res)
+
+
+@pytest.mark.parametrize("pad,kernel", [(8, "wide320"), (4, "192-row")])
+def test_strided_c_rows_mx(pkg, orc, cuda, pad, kernel):
+    """The MX wgrad with bf16 C rows padded by `pad` columns: the library's choice (wide kernel for
+    16-byte rows), the bar against the oracle, padding untouched."""
+    lens, om, on = [64, 0, 96, 45], 1280, 1920
+    _say(f"strided mx C pad {pad}: {kernel}")
+    assert pkg.bf16_kernel(om, on, on + pad) == kernel
+    lhs, rhs, offs, sc, _ = _rand_bytes_problem(lens, om, on, seed=pad + 17, mx=True)
+    big = torch.full((len(lens), om, on + pad), 7.0, dtype=torch.bfloat16, device=cuda)
+    out = _run_mx(pkg, lhs, rhs, sc, offs, cuda, out=big[:, :, :on], tile_m=0)
+    torch.cuda.synchronize()
+    assert bool((big[:, :, on:] == 7.0).all())
+    ref = orc.vark_wgrad_mxfp8(lhs.numpy(), rhs.numpy(), sc[0].numpy(), sc[1].numpy(), offs.numpy())
+    _assert_parity(orc, pkg.as_bf16_bits(out), ref, offs.numpy(), f"strided mx pad {pad}")
+
+
+def test_forced_wide_rejects_8_byte_rows(pkg, cuda):
+    lhs = torch.zeros((64, 1280), dtype=torch.uint8, device=cuda)
+    rhs = torch.zeros((64, 1920), dtype=torch.uint8, device=cuda)
+    one = torch.tensor(1.0, device=cuda)
+    offs = torch.tensor([0, 64], dtype=torch.int64, device=cuda)
+    big = torch.zeros((1, 1280, 1924), dtype=torch.bfloat16, device=cuda)
+    with pytest.raises(Exception, match="GGEMM_E_ALIGN"):
+        pkg.grouped_gemm_fp8_tensorwise_variable_k(lhs, rhs, one, one, offs, out=big[:, :, :1920], wide=320)

@@ -80,13 +80,50 @@ def test_transpose_delayed_validation(pkg, kw, rc):
     assert _tdl(pkg.load_library(), **kw) == rc
 
 
+def _dl_dev(lib, **kw):
+    a = dict(x=FAKE, dt=0, rows=100, cols=64, stride=64, fmt=0, out=FAKE, ostride=64, hist=FAKE, H=16, slot=FAKE,
+             scale=FAKE)
+    a.update(kw)
+    return lib.ggemm_quant_fp8_tensorwise_delayed_dev(a["x"], a["dt"], a["rows"], a["cols"], a["stride"], a["fmt"],
+                                                      a["out"], a["ostride"], a["hist"], a["H"], a["slot"],
+                                                      a["scale"], None)
+
+
+def _tdl_dev(lib, **kw):
+    a = dict(x=FAKE, dt=0, B=2, R=64, C=48, fmt=0, out=FAKE, os=48, out_t=FAKE, ts=64, hist=FAKE, H=16, slot=FAKE,
+             scale=FAKE)
+    a.update(kw)
+    return lib.ggemm_quant_fp8_tensorwise_transpose_delayed_dev(a["x"], a["dt"], a["B"], a["R"], a["C"], a["fmt"],
+                                                                a["out"], a["os"], a["out_t"], a["ts"], a["hist"],
+                                                                a["H"], a["slot"], a["scale"], None)
+
+
+@pytest.mark.parametrize("kw,rc", [
+    (dict(slot=0), -1), (dict(hist=0), -1), (dict(x=0), -1), (dict(H=0), -2), (dict(H=1025), -2),
+    (dict(slot=FAKE + 2), -4), (dict(hist=FAKE + 2), -4), (dict(fmt=3), -8), (dict(stride=56), -3),
+])
+def test_device_slot_delayed_validation(pkg, kw, rc):
+    """The device-slot entries take any slot value (the kernel wraps it into [0, H)), but a null or
+    misaligned slot pointer and the host-slot entries' other checks fail before any launch."""
+    lib = pkg.load_library()
+    assert _dl_dev(lib, **kw) == rc
+    tkw = {k: v for k, v in kw.items() if k != "stride"}
+    if tkw:
+        assert _tdl_dev(lib, **tkw) == (-8 if tkw.get("fmt") == 3 else rc)
+
+
 def test_delayed_python_checks_history(pkg):
     x = torch.zeros((16, 64))
     with pytest.raises(ValueError, match="GPU only"):
         pkg.quantize_fp8_tensorwise_delayed(x, torch.zeros(4), 0)
-    from ggemm_asm_amd import autograd
+    from ggemm_asm_amd import autograd, quant
     with pytest.raises(ValueError, match="history_len"):
         autograd.FP8DelayedScaling(1)
+    with pytest.raises(ValueError, match="one-element int32"):
+        quant._check_history(torch.zeros(4), torch.zeros(1, dtype=torch.int64), torch.device("cpu"))
+    with pytest.raises(ValueError, match="one-element int32"):
+        quant._check_history(torch.zeros(4), torch.zeros(2, dtype=torch.int32), torch.device("cpu"))
+    quant._check_history(torch.zeros(4), torch.zeros(1, dtype=torch.int32), torch.device("cpu"))
 
 
 def _mx(lib, **kw):
