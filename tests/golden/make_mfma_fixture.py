@@ -18,6 +18,19 @@ Cases (finite fp8 codes only; scales 1.0, so the fp32-output mode returns the ra
     bf16 output.
   * persistent fwd/dgrad GEMM, both A formats, rows [100, 200], K = 128 + 64 (a K tail), N = 48,
     random codes: bf16 output.
+The same cases on the wide-tile kernels (the unscaled and scaled v_mfma_f32_32x32x64_f8f6f4), each
+recording a sample of output rows and columns that covers every wave's quadrant of a tile (an
+element depends only on its own operand row and column, so the inputs are zero outside the sampled
+columns and the file stays small):
+  * wgrad on the 320 x 320 kernel (OUT 320 x 320; rows/columns 0-31 and 160-191, columns 288-319
+    too; the wgrad group sizes and value kinds above, the known answer at (0, 0, 0)): bf16, fp32,
+    and fp32 accumulate into a recorded C0;
+  * wgrad on the 256 x 384 kernel (OUT 256 x 384; rows 0-31 and 128-159, columns 0-31, 192-223 and
+    352-383): bf16;
+  * MX wgrad on the 320 x 320 MX kernel (OUT 320 x 320, group sizes [64, 96], random codes and
+    e8m0 scales 120..134): bf16;
+  * persistent GEMM on the wide kernel (256 x 320 tiles; rows [100, 200], K = 256, N = 320, both A
+    formats, random codes; all rows, columns 0-31, 160-191, 288-319): bf16.
 """
 import os
 import sys
@@ -48,6 +61,100 @@ def _recipe(rng, rows, cols, fmt):
     scale = float(x.abs().max()) / fmax
     dt = torch.float8_e4m3fn if fmt == "e4m3" else torch.float8_e5m2
     return (x / scale).clamp(-fmax, fmax).to(dt).view(torch.uint8).numpy()
+
+
+# sampled output rows / columns of the wide kernels: both waves of a tile in each dimension, and the
+# last block column of the 320-wide tile
+W320_ROWS = np.r_[0:32, 160:192]
+W320_COLS = np.r_[0:32, 160:192, 288:320]
+W256_ROWS = np.r_[0:32, 128:160]
+W384_COLS = np.r_[0:32, 192:224, 352:384]
+
+
+def _only(cols, arr):
+    """arr with every column outside ``cols`` zeroed (last axis)."""
+    out = np.zeros_like(arr)
+    out[..., cols] = arr[..., cols]
+    return out
+
+
+def _wgrad_inputs(rng, lens, om, on, rows, cols):
+    """The wgrad fixture's inputs (known answer in group 0 at (0, 0), random codes in groups 1 and
+    3, the value recipe in group 4), zero outside the sampled columns."""
+    M = sum(lens)
+    offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    lhs = _codes(rng, (M, om), "e4m3")
+    rhs = _codes(rng, (M, on), "e5m2")
+    lhs[0:128, 0] = 0x18
+    rhs[0:128, 0] = 0x2C
+    lhs[0, 0] = 0x50
+    rhs[0, 0] = 0x48
+    o4, o5 = offs[4], offs[5]
+    lhs[o4:o5] = _recipe(rng, o5 - o4, om, "e4m3")
+    rhs[o4:o5] = _recipe(rng, o5 - o4, on, "e5m2")
+    return _only(rows, lhs), _only(cols, rhs), offs
+
+
+def wide_cases(pkg, dev, z):
+    rng = np.random.default_rng(20261203)
+    one = torch.tensor(1.0, dtype=torch.float32, device=dev)
+    lens = [128, 37, 0, 300, 160]
+    T = lambda a: torch.from_numpy(a).to(dev)
+    run = pkg.grouped_gemm_fp8_tensorwise_variable_k
+    sample = lambda t, r, c: t.cpu()[:, r][:, :, c].numpy()
+
+    # ---- 320 x 320 kernel: bf16, fp32, fp32 accumulate
+    lhs, rhs, offs = _wgrad_inputs(rng, lens, 320, 320, W320_ROWS, W320_COLS)
+    dl, dr, do = T(lhs), T(rhs), T(offs)
+    b = run(dl, dr, one, one, do, wide=320)
+    f = run(dl, dr, one, one, do, out_dtype=torch.float32, wide=320)
+    c0 = np.zeros((len(lens), 320, 320), np.float32)
+    c0[:, W320_ROWS[:, None], W320_COLS[None, :]] = rng.standard_normal((len(lens), 64, 96)).astype(np.float32)
+    acc = T(c0)
+    run(dl, dr, one, one, do, out=acc, accumulate=True, wide=320)
+    torch.cuda.synchronize()
+    z.update(w320_lhs=lhs, w320_rhs=rhs, w320_offs=offs, w320_c0=c0[:, W320_ROWS][:, :, W320_COLS],
+             w320_out_bf16=pkg.as_bf16_bits(b)[:, W320_ROWS][:, :, W320_COLS],
+             w320_out_f32=sample(f, W320_ROWS, W320_COLS), w320_out_f32_acc=sample(acc, W320_ROWS, W320_COLS))
+    print(f"wide320 known answer (0, 0, 0): {float(f[0, 0, 0])!r}", flush=True)
+
+    # ---- 256 x 384 kernel: bf16
+    lhs, rhs, offs = _wgrad_inputs(rng, lens, 256, 384, W256_ROWS, W384_COLS)
+    b = run(T(lhs), T(rhs), one, one, T(offs), wide=256)
+    torch.cuda.synchronize()
+    z.update(w256_lhs=lhs, w256_rhs=rhs, w256_offs=offs,
+             w256_out_bf16=pkg.as_bf16_bits(b)[:, W256_ROWS][:, :, W384_COLS])
+
+    # ---- MX on the 320 x 320 kernel
+    mlens = [64, 96]
+    mM = sum(mlens)
+    moffs = np.concatenate([[0], np.cumsum(mlens)]).astype(np.int64)
+    mlhs = _only(W320_ROWS, _codes(rng, (mM, 320), "e4m3"))
+    mrhs = _only(W320_COLS, _codes(rng, (mM, 320), "e5m2"))
+    lsc = rng.integers(120, 135, (mM // 32, 320), dtype=np.uint8)
+    rsc = rng.integers(120, 135, (mM // 32, 320), dtype=np.uint8)
+    mx = pkg.grouped_gemm_mxfp8_variable_k(T(mlhs), T(mrhs), T(lsc), T(rsc), T(moffs), tile_m=320)
+    torch.cuda.synchronize()
+    z.update(w320mx_lhs=mlhs, w320mx_rhs=mrhs, w320mx_lsc=lsc, w320mx_rsc=rsc, w320mx_offs=moffs,
+             w320mx_out_bf16=pkg.as_bf16_bits(mx)[:, W320_ROWS][:, :, W320_COLS])
+
+    # ---- persistent GEMM on the wide kernel, both A formats
+    plens = [100, 200]
+    pM, K, N = sum(plens), 256, 320
+    poffs = np.concatenate([[0], np.cumsum(plens)]).astype(np.int64)
+    pb = _codes(rng, (len(plens), N, K), "e4m3")
+    keep = np.zeros(N, bool)
+    keep[W320_COLS] = True
+    pb[:, ~keep, :] = 0
+    z.update(wp_offs=poffs, wp_b=pb)
+    for fmt in ("e4m3", "e5m2"):
+        a = _codes(rng, (pM, K), fmt)
+        adt = torch.float8_e4m3fn if fmt == "e4m3" else torch.float8_e5m2
+        out = pkg.grouped_gemm_fp8_tensorwise(T(a).view(adt), T(pb).view(torch.float8_e4m3fn), one, one, T(poffs),
+                                              kernel="wide")
+        torch.cuda.synchronize()
+        z[f"wp_a_{fmt}"] = a
+        z[f"wp_out_bf16_{fmt}"] = pkg.as_bf16_bits(out)[:, W320_COLS]
 
 
 def main(path):
@@ -110,6 +217,7 @@ def main(path):
         z[f"p_a_{fmt}"] = a
         z[f"p_out_bf16_{fmt}"] = pkg.as_bf16_bits(out)
 
+    wide_cases(pkg, dev, z)
     np.savez_compressed(path, **z)
     print(f"wrote {path}: {os.path.getsize(path)} bytes", flush=True)
 

@@ -6,12 +6,15 @@ Bar: cosine >= 0.99999, max relative error <= 2e-2 over |C| > 1e-3 * max|C|, no 
 rows outside the groups untouched. Cases: ragged groups around the 256-row tile (0, 1, 17, 255,
 256, 257, 511, 513, 1000 rows), both K parities of its 128-byte stages (K % 128 == 0 and == 64,
 one-stage K = 64 and 128), N of one to nine 320-wide tiles, both A formats, strided views, G = 300
-and G = 2047, and the four full-size call sites (against the 512-thread kernel; test_gpu_persistent
-compares the library's choice there, this kernel, with the oracle on every row).
+and G = 2047, and the four full-size call sites with line-aligned rows (the autograd layer's
+layout), every row against the oracle. Where a heavy cancellation at small K passes the 2e-2
+relative threshold, every element must lie within the rigorous fp8-MFMA error bound instead.
 """
 import numpy as np
 import pytest
 import torch
+
+from test_gpu_persistent import _parity_small_k
 
 pytestmark = pytest.mark.gpu
 
@@ -98,7 +101,9 @@ def test_wide_random_shapes_vs_oracle(pkg, orc, orp, cuda, seed):
     m = orc.compare(pkg.as_bf16_bits(out)[:M], ref[:M])
     _say(f"wide random {seed}: {m}")
     if not orc.parity_ok(m):
-        assert K <= 256 and m["cos"] >= 0.99999 and m["nonfinite"] == 0, m
+        # at small K a heavy cancellation can pass 2e-2 relative; the rigorous bound cannot
+        assert K <= 256, m
+        _parity_small_k(pkg, orc, orp, out, p, f"wide random {seed}")
 
 
 def test_wide_rejects_shapes_it_does_not_take(pkg, cuda):
@@ -155,40 +160,46 @@ def test_wide_most_groups(pkg, orc, orp, cuda):
     m = orc.compare(pkg.as_bf16_bits(out), ref)
     _say(f"wide G=2047: {m}")
     if not orc.parity_ok(m):
-        # K = 64: a heavy cancellation can pass 2e-2 relative; cosine and finiteness must hold
-        assert m["cos"] >= 0.99999 and m["nonfinite"] == 0, m
+        # K = 64: a heavy cancellation can pass 2e-2 relative; every element within the rigorous bound
+        _parity_small_k(pkg, orc, orp, out, p, "wide G=2047")
 
 
 @pytest.mark.parametrize("name", ["gate_up_fwd", "down_fwd", "down_dgrad", "gate_up_dgrad"])
 def test_wide_full_size_site(pkg, orc, orp, cuda, name):
-    """The call sites at full size on the wide kernel: deterministic, finite, in agreement with the
-    512-thread kernel (cosine >= 0.99999 over the whole output); both kernels meet the bar on the
-    first and last 300 rows of the smallest, median and largest groups. (test_gpu_persistent checks
-    the library's choice -- the wide kernel at the line-aligned K = 5760 site -- on every row.)"""
+    """The call sites at full size with A and B rows on 128-byte lines -- the autograd layer's
+    layout, where the library picks this kernel: deterministic, finite, and every row of every
+    group against the oracle with the bar over the whole output (the cosine over all of it, the
+    1e-3 * max|C| threshold from the whole reference, as reference bench.py:641-646 takes it); the
+    512-thread kernel on the same inputs meets the same bar."""
     p = pkg.inputs.make_fwd_problem(name, seed=0, device=cuda)
     M, K, N = p.a.shape[0], p.a.shape[1], p.b.shape[1]
-    _say(f"persistent wide full size {name} M={M} K={K} N={N}")
-    out = _run(pkg, p, cuda, "wide")
-    out2 = _run(pkg, p, cuda, "wide")
-    o512 = _run(pkg, p, cuda, "512")
+    Kp = -(-K // 128) * 128
+    _say(f"persistent wide full size {name} M={M} K={K} N={N}, rows padded to {Kp} bytes")
+    a = torch.zeros((M, Kp), dtype=torch.uint8, device=cuda)[:, :K]
+    a.copy_(p.a)
+    b = torch.zeros((p.G, N, Kp), dtype=torch.uint8, device=cuda)[:, :, :K]
+    b.copy_(p.b)
+    assert pkg.persistent.selected_kernel(N, K, Kp, Kp, N) == "wide"
+    sa = torch.tensor(p.a_scale, dtype=torch.float32, device=cuda)
+    sb = torch.tensor(p.b_scale, dtype=torch.float32, device=cuda)
+    run = lambda kern: pkg.grouped_gemm_fp8_tensorwise(a.view(p.a_dtype), b.view(torch.float8_e4m3fn), sa, sb,
+                                                       p.group_offs, kernel=kern)
+    out = run("auto")
+    out2 = run("wide")
+    o512 = run("512")
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
     assert bool(torch.isfinite(out.float()).all())
-    of, of5 = out.float().double(), o512.float().double()
-    cos = float((of * of5).sum() / (of.norm() * of5.norm()))
-    _say(f"{name}: wide vs 512 cosine {cos:.8f}")
-    assert cos >= 0.99999
     offs = p.group_offs.cpu().numpy()
-    order = np.argsort(np.diff(offs))
-    for g in sorted({int(order[0]), int(order[len(order) // 2]), int(order[-1])}):
-        r0, r1 = int(offs[g]), int(offs[g + 1])
-        rows = sorted(set(range(r0, min(r0 + 300, r1))) | set(range(max(r1 - 300, r0), r1)))
-        if not rows:
-            continue
-        idx = torch.tensor(rows, device=cuda)
-        ref = orp.grouped_fp8(p.a[idx].cpu().numpy(), p.b[g:g + 1].cpu().numpy(), p.a_scale, p.b_scale,
-                              np.array([0, len(rows)], np.int64), p.a_format)
-        for label, o in (("wide", out), ("512-thread", o512)):
-            m = orc.compare(pkg.as_bf16_bits(o[idx]), ref)
-            _say(f"{name} {label} kernel, group {g} ({r1 - r0} rows): {m}")
-            assert orc.parity_ok(m), (label, g, m)
+    a_all, b_all = p.a.cpu().numpy(), p.b.cpu().numpy()
+    refs = []
+    for g in range(p.G):
+        lo, hi = int(offs[g]), int(offs[g + 1])
+        refs.append(orp.grouped_fp8(a_all[lo:hi], b_all[g:g + 1], p.a_scale, p.b_scale,
+                                    np.array([0, hi - lo], np.int64), p.a_format))
+    amax = max(float(np.abs(orc.bf16_bits_to_f32(r)).max()) if r.size else 0.0 for r in refs)
+    for label, o in (("wide", out), ("512-thread", o512)):
+        got = pkg.as_bf16_bits(o)
+        m = orc.compare_parts(((got[offs[g]:offs[g + 1]], refs[g]) for g in range(p.G)), amax)
+        _say(f"{name} {label} kernel, all {int(offs[-1])} rows vs oracle: {m}")
+        assert orc.parity_ok(m), (label, m)

@@ -13,7 +13,10 @@ fp32. This file shows
       shifted column, a scale off by 2x;
   (c) the GPU's own measured outputs (tests/golden/mfma_probe.npz, written on an MI355X by
       tests/golden/make_mfma_fixture.py) lie inside the bound, reproduce the recorded known answer
-      2^6 + 127 * 2^-8 -> 64.46875, and show the truncation the bound models is real.
+      2^6 + 127 * 2^-8 -> 64.46875, and show the truncation the bound models is real -- for the
+      192-row kernels (16x16x128, 16x16x32 and the scaled 32x32x64 of the MX kernel) and, from
+      sampled outputs, the wide-tile kernels (unscaled and scaled 32x32x64, fp32 and bf16
+      epilogues, the accumulate epilogue, the wide persistent kernel).
 """
 import os
 
@@ -264,3 +267,75 @@ def test_fixture_numerics_facts(orc):
     codes = np.zeros(got.shape, bool)
     codes[[1, 3]] = True                                 # the all-codes groups
     assert np.mean((np.abs(got - exact) > fp32_only)[codes]) > 0.5
+
+
+# ----------------------------------------------------------------------------- (c) wide-tile kernels
+
+def _wide_samples():
+    z = _fixture()
+    if "w320_out_bf16" not in z:
+        pytest.skip("fixture has no wide-kernel entries")
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("make_mfma_fixture", os.path.join(GOLDEN, "make_mfma_fixture.py"))
+    fx = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(fx)
+    return z, fx
+
+
+def test_fixture_wide_known_answer(orc):
+    """The 320 x 320 kernel (v_mfma_f32_32x32x64_f8f6f4) gives the known answer 64.46875 for
+    2^6 + 127 * 2^-8 too: the 2^-8 terms are cut below the 11 bits kept under the 2^6 product."""
+    z, _ = _wide_samples()
+    assert z["w320_out_f32"][0, 0, 0] == 64.46875
+    assert z["w320_out_f32"][0, 0, 0] != 64 + 127 * 2.0 ** -8
+
+
+def test_fixture_wide_within_bound(orc, orp):
+    """Every sampled output of the wide-tile kernels lies inside the acceptance bound the wide GPU
+    tests fall back on: 320 x 320 fp32 (no output rounding) and bf16, 256 x 384 bf16, the MX
+    320 x 320 kernel (e8m0 scales in the products), the wide persistent kernel in both A formats.
+    The sampled inputs are the operand columns of the sampled rows / columns of C."""
+    z, fx = _wide_samples()
+    R, C = fx.W320_ROWS, fx.W320_COLS
+    L, Rr, o = z["w320_lhs"][:, R], z["w320_rhs"][:, C], z["w320_offs"]
+    viol, w = orc.mfma_bound_violations(z["w320_out_f32"].astype(np.float64), L, Rr, o, 1.0, 1.0, out_rounding=0.0)
+    assert not viol.any(), w
+    viol, w = orc.mfma_bound_violations(orc.bf16_bits_to_f32(z["w320_out_bf16"]), L, Rr, o, 1.0, 1.0)
+    assert not viol.any(), w
+    viol, w = orc.mfma_bound_violations(orc.bf16_bits_to_f32(z["w256_out_bf16"]), z["w256_lhs"][:, fx.W256_ROWS],
+                                        z["w256_rhs"][:, fx.W384_COLS], z["w256_offs"], 1.0, 1.0)
+    assert not viol.any(), w
+    viol, w = orc.mfma_bound_violations(orc.bf16_bits_to_f32(z["w320mx_out_bf16"]), z["w320mx_lhs"][:, R],
+                                        z["w320mx_rhs"][:, C], z["w320mx_offs"], 1.0, 1.0,
+                                        z["w320mx_lsc"][:, R], z["w320mx_rsc"][:, C])
+    assert not viol.any(), w
+    for fmt in ("e4m3", "e5m2"):
+        a, b, po = z[f"wp_a_{fmt}"], z["wp_b"][:, C, :], z["wp_offs"]
+        dec = orc.decode_e4m3 if fmt == "e4m3" else orc.decode_e5m2
+        av, bv = dec(a).astype(np.float64), orc.decode_e4m3(b).astype(np.float64)
+        exact = orp.grouped_fp8_f32(a, b, 1.0, 1.0, po, fmt, acc_dtype=np.float64)
+        bound = orp.fp8_mfma_error_bound_rows(av, bv, po, 1.0)
+        mag = np.zeros_like(exact)
+        for g in range(po.size - 1):
+            mag[po[g]:po[g + 1]] = np.abs(av[po[g]:po[g + 1]]) @ np.abs(bv[g]).T
+        got = orc.bf16_bits_to_f32(z[f"wp_out_bf16_{fmt}"]).astype(np.float64)
+        assert np.all(np.abs(got - exact) <= 2.0 ** -8 * np.abs(exact) + 1.01 * bound + 4 * 2.0 ** -24 * mag + 1e-38)
+
+
+def test_fixture_wide_numerics_facts(orc):
+    """What the wide kernels' measured samples establish: the bf16 epilogue rounds the same fp32
+    accumulator the fp32 epilogue writes (RNE); the accumulate epilogue is one fp32 addition of that
+    value to C0; and the 32x32x64 instruction also truncates inside its blocks (most all-codes
+    elements are further from the exact sum than fp32 accumulation alone allows), so the wide
+    kernels need the block-truncation term of the bound as much as the 192-row ones."""
+    z, fx = _wide_samples()
+    np.testing.assert_array_equal(orc.bf16_bits_rne(z["w320_out_f32"]), z["w320_out_bf16"])
+    np.testing.assert_array_equal(z["w320_out_f32_acc"], (z["w320_c0"] + z["w320_out_f32"]).astype(np.float32))
+    R, C = fx.W320_ROWS, fx.W320_COLS
+    L, Rr, o = z["w320_lhs"][:, R], z["w320_rhs"][:, C], z["w320_offs"]
+    got = z["w320_out_f32"].astype(np.float64)
+    exact = orc.vark_wgrad_tensorwise_f32(L, Rr, 1.0, 1.0, o, acc_dtype=np.float64)
+    lv, rv = np.abs(orc.decode_e4m3(L).astype(np.float64)), np.abs(orc.decode_e5m2(Rr).astype(np.float64))
+    absum = np.stack([lv[o[g]:o[g + 1]].T @ rv[o[g]:o[g + 1]] for g in range(o.size - 1)])
+    fp32_only = (np.diff(o)[:, None, None] / 32 + 1) * 2.0 ** -24 * absum
+    assert np.mean((np.abs(got - exact) > fp32_only)[[1, 3]]) > 0.5
