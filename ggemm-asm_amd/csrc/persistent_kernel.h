@@ -188,7 +188,9 @@ __device__ __forceinline__ Slices xcd_slices(int total, int num_wg) {
 // Tile t of the launch: its group is the last g with s_pre[g] <= t (groups without tiles share
 // their successor's prefix, so the search lands on the group that owns t); a group's tiles in
 // 3-wide N bands, M-tile fastest (measured against 2, 4 and 6: 1-2 % faster than 4 at every
-// reference site, both kernels). Wave-uniform: scalar registers from here on.
+// reference site, both kernels), down the M-tiles in even bands and back up in odd ones, so the
+// tiles in flight where one band meets the next share A rows (0-1.3 % faster at the four sites,
+// same box). Wave-uniform: scalar registers from here on.
 template <int kTM, int kTN>
 __device__ __forceinline__ Tile tile_of(const GG_LDS int* s_pre, const GG_LDS int* s_offs, int G, int n_tn, int t) {
   int lo = 0, hi = G - 1;
@@ -207,8 +209,9 @@ __device__ __forceinline__ Tile tile_of(const GG_LDS int* s_pre, const GG_LDS in
   const int band = in_g / (n_tm * kBandN);
   const int r = in_g - band * n_tm * kBandN;
   const int bw = min(kBandN, n_tn - band * kBandN);
-  const int tm = r / bw;
-  const int tn = band * kBandN + (r - tm * bw);
+  const int tr = r / bw;
+  const int tm = (band & 1) ? n_tm - 1 - tr : tr;      // serpentine: odd bands walk M back up
+  const int tn = band * kBandN + (r - tr * bw);
   T.m0 = tm * kTM;
   T.n0 = tn * kTN;
   T.rows = min(kTM, len - T.m0);

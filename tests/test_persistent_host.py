@@ -27,6 +27,8 @@ BAND_N = 3          # N tiles per band of a group's tile order (persistent_kerne
 def test_band_width_matches_kernel():
     text = open(os.path.join(ROOT, "ggemm-asm_amd", "csrc", "persistent_kernel.h")).read()
     assert re.findall(r"constexpr int kBandN = (\d+);", text) == [str(BAND_N)]
+    # the serpentine walk the model below restates
+    assert text.count("const int tm = (band & 1) ? n_tm - 1 - tr : tr;") == 1
 
 
 def _tn(N):
@@ -68,8 +70,9 @@ def _tile_at(t, pre, offs, n_tn, N):
     band = in_g // (n_tm * BAND_N)
     r = in_g - band * n_tm * BAND_N
     bw = min(BAND_N, n_tn - band * BAND_N)
-    tm = r // bw
-    tn = band * BAND_N + (r - tm * bw)
+    tr = r // bw
+    tm = n_tm - 1 - tr if band & 1 else tr          # serpentine: odd bands walk M back up
+    tn = band * BAND_N + (r - tr * bw)
     m0 = tm * TILE_M
     return g, m0, tn * _tn(N), min(TILE_M, ln - m0)
 

@@ -128,3 +128,48 @@ def test_unspread_grid_keeps_slices():
     """A grid that is not a multiple of the XCD count has one slice and no choice."""
     _, _, _, _, chosen, _ = _schedule([18000, 10, 10, 10], 2880, 5760, 20)
     assert chosen == "slices"
+
+
+def _tile_in_group(in_g, n_tm, n_tn, band_n=4):
+    """tile_at's walk inside a group (vark_kernel.h): bands of band_n N-tiles, M-tile by M-tile
+    inside a band, down the M-tiles in even bands and back up in odd ones."""
+    band = in_g // (n_tm * band_n)
+    r = in_g - band * n_tm * band_n
+    bw = min(band_n, n_tn - band * band_n)
+    tr = r // bw
+    tm = n_tm - 1 - tr if band & 1 else tr
+    return tm, band * band_n + (r - tr * bw)
+
+
+def test_tile_walk_matches_kernel_and_covers_each_tile_once():
+    import os
+    import re
+    from conftest import ROOT
+    text = open(os.path.join(ROOT, "ggemm-asm_amd", "csrc", "vark_kernel.h")).read()
+    assert re.findall(r"constexpr int kBandN = (\d+);", text) == ["4"]
+    assert text.count("const int tm = (band & 1) ? S.n_tm - 1 - tr : tr;") == 1
+    for n_tm, n_tn in [(9, 18), (15, 15), (9, 9), (1, 1), (3, 7), (16, 5), (2, 13)]:
+        seen = [_tile_in_group(i, n_tm, n_tn) for i in range(n_tm * n_tn)]
+        assert sorted(seen) == [(a, b) for a in range(n_tm) for b in range(n_tn)], (n_tm, n_tn)
+
+
+def test_serpentine_rounds_share_panels():
+    """Where 32 consecutive tiles of a group cross from one band into the next, the serpentine
+    walk keeps them on the M-tiles the band just ended on: at gate_up's 9 x 18 grid of 320 x 320
+    tiles, the distinct LHS + RHS panels summed over every 32-tile window are fewer than with every
+    band walked downward (the panel count is what an XCD's L2 fetches per token of the group)."""
+    n_tm, n_tn = 9, 18
+
+    def panels(walk):
+        tot = 0
+        for s in range(0, n_tm * n_tn - 31):
+            w = [walk(i) for i in range(s, s + 32)]
+            tot += len({a for a, _ in w}) + len({b for _, b in w})
+        return tot
+
+    def one_way(i):
+        band, r = divmod(i, n_tm * 4)
+        bw = min(4, n_tn - band * 4)
+        return r // bw, band * 4 + r % bw
+
+    assert panels(lambda i: _tile_in_group(i, n_tm, n_tn)) < 0.95 * panels(one_way)
