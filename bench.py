@@ -295,17 +295,18 @@ def oracle_leg(p, outs, seconds):
     return parity, base
 
 
-def oracle_leg_fwd(p, out, seconds):
-    """``oracle_leg`` for a forward / data-gradient site: every row of every group of the last
-    timed launch's ``out`` [M_total, N] against the persistent GEMM's oracle, and the CPU
-    baseline from the same calls. Returns (parity record, cpu_baseline)."""
+def oracle_leg_fwd(p, outs, seconds):
+    """``oracle_leg`` for a forward / data-gradient site: every row of every group of the output
+    [M_total, N] each tensor of ``outs`` (name -> tensor) holds after the last timed launch against
+    the persistent GEMM's oracle, and the CPU baseline from the same calls. Returns
+    ({name: parity record}, cpu_baseline)."""
     import numpy as np
     from oracle import persistent_oracle as orp
     from oracle import vark_oracle as orc
     threads = _blas_threads()
     offs = p.group_offs.cpu().numpy()
-    got = _bf16_bits(out)
-    refs, parts, empty = [], [], []
+    got = {name: _bf16_bits(out) for name, out in outs.items()}
+    refs, parts, empty = [], {name: [] for name in outs}, []
     done_flops, t_total, timed_groups, rows = 0.0, 0.0, 0, 0
     for g in range(p.G):
         lo, hi = int(offs[g]), int(offs[g + 1])
@@ -317,13 +318,15 @@ def oracle_leg_fwd(p, out, seconds):
         refs.append(orp.grouped_fp8(A, B, p.a_scale, p.b_scale, np.array([0, hi - lo], dtype=np.int64),
                                     p.a_format))
         dt = time.perf_counter() - t0
-        parts.append(got[lo:hi])
+        for name in outs:
+            parts[name].append(got[name][lo:hi])
         if seconds > 0 and t_total < seconds:
             t_total += dt
             done_flops += 2.0 * (hi - lo) * p.K * p.N
             timed_groups += 1
             rows += hi - lo
-    parity = _parity_record(orc, parts, refs, empty, f"{p.G} of {p.G} ({int(offs[-1] - offs[0])} rows)")
+    parity = {name: _parity_record(orc, parts[name], refs, empty, f"{p.G} of {p.G} ({int(offs[-1] - offs[0])} rows)")
+              for name in outs}
     base = None
     if timed_groups:
         base = {"value": round(done_flops / t_total / 1e12, 4), "unit": "TFLOPS", "cores": int(threads),
@@ -359,6 +362,35 @@ def time_drop_in_co(pkg, p, dev, steps, warmup):
            "kernel": f"{os.path.basename(pkg.CODE_OBJECT_PATH)}: {name}, {geo['tile_m']}x{geo['tile_n']} tiles, "
                      f"grid {ncu} x {harness.BLOCK} threads, {harness.SHARED_MEM} B dynamic LDS, kernelParams launch "
                      f"on the null stream (what reference launcher.cpp / bench.py --kernel callers run)"}
+    return rec, out
+
+
+def time_drop_in_co_fwd(pkg, p, dev, steps, warmup, row_align):
+    """The persistent GEMM's drop-in code object for the site's A format
+    (``persistent_e4m3.co`` / ``persistent_e5m2.co``, the 512-thread kernel) timed as
+    ``time_drop_in_co`` times the wgrad's: the reference's hipModule path with the 16-entry
+    kernelParams array on the null stream (reference bench.py:312-361), on the same operands (with
+    ``row_align``, the same padded views). Returns (record, output tensor of the last launch)."""
+    import torch
+    from ggemm_asm_amd import harness
+    path = pkg.PERSISTENT_CODE_OBJECT_PATHS[p.a_format]
+    module, func, name = harness.load_kernel(path)
+    try:
+        sa = torch.tensor(p.a_scale, dtype=torch.float32, device=dev)
+        sb = torch.tensor(p.b_scale, dtype=torch.float32, device=dev)
+        a, b = fwd_operands(p, row_align)
+        out = torch.empty((p.M, p.N), dtype=torch.bfloat16, device=dev)
+        ncu = harness.get_num_cus(dev.index or 0)
+        launch, _keep = harness.prepare_persistent_args(func, a, b, out, sa, sb, p.group_offs, p.G, p.N, p.K, ncu)
+        torch.cuda.synchronize()
+        ms = harness.time_null_stream(launch, steps, warmup)
+    finally:
+        harness.unload_kernel(module)
+    geo = pkg.launch_geometry(p.N)
+    rec = {"ms": round(ms, 4), "TFLOPS": round(p.flops / (ms * 1e-3) / 1e12, 2),
+           "kernel": f"{os.path.basename(path)}: {name}, {geo['tile_m']}x{geo['tile_n']} tiles, grid {ncu} x "
+                     f"{harness.BLOCK} threads, {harness.SHARED_MEM} B dynamic LDS, kernelParams launch on the null "
+                     f"stream (what the reference's bench.py --kernel callers of this site run)"}
     return rec, out
 
 
@@ -623,8 +655,8 @@ def main():
         run = make_runner(pkg, p, dev, args.mfma, args.persistent_kernel, args.row_align)
     ms = time_steps(run, args.steps, args.warmup)
     tflops = p.flops / (ms * 1e-3) / 1e12
-    drop_in_co = (args.drop_in and not fwd and not p.is_mx and args.out == "bf16" and args.mfma == "k128"
-                  and args.config not in SHARD_CONFIGS)
+    drop_in_co = (args.drop_in and not p.is_mx if not fwd else args.drop_in) and args.out == "bf16" \
+        and args.mfma == "k128" and args.config not in SHARD_CONFIGS
     # traffic measured for this exact variant (profiles/traffic_<config>[_<out>][_reference_lens].txt)
     traffic, traffic_source = read_traffic(args.config + ("" if args.out == "bf16" else "_" + args.out)
                                            + ("" if args.lens == "multinomial" else "_reference_lens"))
@@ -734,18 +766,19 @@ def main():
     # the drop-in code object on the same inputs: what reference-side callers (launcher.cpp,
     # bench.py --kernel) get; its C is checked against the oracle beside the library's
     outs = {} if args.out == "f32_accum" else {"library": run.out}
-    if drop_in_co:
+    if drop_in_co and fwd:
+        line["drop_in_co"], outs["drop_in_co"] = time_drop_in_co_fwd(pkg, p, dev, args.steps, args.warmup,
+                                                                     args.row_align)
+    elif drop_in_co:
         line["drop_in_co"], outs["drop_in_co"] = time_drop_in_co(pkg, p, dev, args.steps, args.warmup)
     # outside the timed region: the oracle over every group of the timed inputs, checked against
     # the last timed launch's output, and timed as the CPU baseline
     failed = []
-    if fwd:
-        par, base = (oracle_leg_fwd(p, run.out, args.cpu_seconds) if args.parity or args.cpu_seconds > 0
-                     else (None, None))
-        line["parity"] = par if args.parity else None
-        failed += ["library"] if line["parity"] and not par["ok"] else []
-    elif args.parity and outs:
-        par, base = oracle_leg(p, outs, args.cpu_seconds)
+    if fwd or (args.parity and outs):
+        if args.parity:
+            par, base = (oracle_leg_fwd if fwd else oracle_leg)(p, outs, args.cpu_seconds)
+        else:
+            par, base = {}, (oracle_leg_fwd(p, {}, args.cpu_seconds)[1] if args.cpu_seconds > 0 else None)
         line["parity"] = par.pop("library", None)
         if "drop_in_co" in par:
             line["drop_in_co"]["parity"] = par["drop_in_co"]

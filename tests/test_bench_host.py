@@ -84,9 +84,9 @@ def test_fwd_leg(pkg, orp, orc):
     p = pkg.inputs.make_fwd_problem("down_fwd", seed=0, device="cpu", lens=torch.tensor([40, 0, 88]), K=64, N=48)
     ref = orp.grouped_fp8(p.a.numpy(), p.b.numpy(), p.a_scale, p.b_scale, p.group_offs.numpy(), p.a_format)
     out = torch.from_numpy(ref.view(np.int16)).view(torch.bfloat16)
-    m, base = bench.oracle_leg_fwd(p, out.clone(), 5.0)
-    assert m["ok"] and m["exact_frac"] == 1.0 and m["groups"] == "3 of 3 (128 rows)" and base is not None
     bad = out.clone()
     bad[100, 3] = -bad[100, 3] if float(bad[100, 3]) != 0 else 1.0
-    m, _ = bench.oracle_leg_fwd(p, bad, 0.0)
-    assert not m["ok"]
+    par, base = bench.oracle_leg_fwd(p, {"library": out.clone(), "drop_in_co": bad}, 5.0)
+    m = par["library"]
+    assert m["ok"] and m["exact_frac"] == 1.0 and m["groups"] == "3 of 3 (128 rows)" and base is not None
+    assert not par["drop_in_co"]["ok"]
