@@ -555,7 +555,8 @@ def main_sites(args, pkg, dev):
     """The reference's multi-site run (bench.py:690-858): each call site in turn with the
     reference's input recipe (seed-42 exponential group lengths, randn bf16 cast to fp8, scales
     0.1), then its summary table (ms, TFLOPS, TFLOP and share of the total per site, and the total)
-    on stderr. The JSON line carries the sum over the sites."""
+    on stderr. The JSON line carries the sum over the sites; each site's row also carries the parity of
+    its last timed output against the oracle over every group (unless --no-parity)."""
     import torch
     names = SITE_GROUPS.get(args.site, (args.site,))
     rows = []
@@ -567,9 +568,16 @@ def main_sites(args, pkg, dev):
         torch.cuda.synchronize()
         run = make_runner(pkg, p, dev, args.mfma, args.persistent_kernel, args.row_align)
         ms = time_steps(run, args.steps, args.warmup)
-        rows.append({"site": name, "ms": round(ms, 4), "TFLOPS": round(p.flops / (ms * 1e-3) / 1e12, 2),
-                     "TFLOP": round(p.flops / 1e12, 4)})
-        print(f"  {name}: {ms:.4f} ms", file=sys.stderr, flush=True)
+        row = {"site": name, "ms": round(ms, 4), "TFLOPS": round(p.flops / (ms * 1e-3) / 1e12, 2),
+               "TFLOP": round(p.flops / 1e12, 4)}
+        if args.parity:   # the site's last timed output against the oracle, every group
+            leg = oracle_leg_fwd if name in FWD_SITES else oracle_leg
+            m = leg(p, {"library": run.out}, 0.0)[0]["library"]
+            row["parity"] = {k: m[k] for k in ("ok", "cos", "max_rel", "nonfinite", "empty_zero", "groups")}
+        rows.append(row)
+        print(f"  {name}: {ms:.4f} ms" + (f", parity {'ok' if row['parity']['ok'] else 'FAILED'} (max_rel "
+                                          f"{row['parity']['max_rel']:.4f})" if args.parity else ""),
+              file=sys.stderr, flush=True)
         del p, run
     total_ms = sum(r["ms"] for r in rows)
     total_tflop = sum(r["TFLOP"] for r in rows)
@@ -596,6 +604,11 @@ def main_sites(args, pkg, dev):
                          "unit": "TFLOP/s", "frac": round(tflops / FP8_DENSE_PEAK_TFLOPS, 4), "traffic": None},
             "cpu_baseline": None}
     print(json.dumps(line), flush=True)
+    bad = [r["site"] for r in rows if r.get("parity") and not r["parity"]["ok"]]
+    if bad:
+        print(f"bench.py: the output of {', '.join(bad)} fails the parity bar against the oracle ({PARITY_BAR})",
+              file=sys.stderr, flush=True)
+        sys.exit(1)
 
 
 def main():
