@@ -64,3 +64,34 @@ int vo_vark_tensorwise(const uint8_t* lhs, const uint8_t* rhs, float sl, float s
   free(acc); free(a); free(b);
   return 0;
 }
+
+/* Persistent fwd / dgrad grouped GEMM (reference bench.py:153-181,238-247): out_bits[r, n] =
+ * bf16(sum_k (sa * A[r, k]) (sb * B[g, n, k])) for the rows r of group g, accumulated in fp32 in
+ * k order; A is e4m3 (a_e5m2 = 0) or e5m2 (a_e5m2 = 1), B e4m3 [G, N, K] (trans_b); rows outside
+ * every group are left as they are. Returns 0, or -1 on bad offsets, -2 on allocation failure. */
+int vo_persistent_fp8(const uint8_t* a, const uint8_t* b, float sa, float sb, const int64_t* offs, int G,
+                      int64_t M, int N, int K, int64_t sam, int64_t sbg, int64_t sbn, int a_e5m2,
+                      uint16_t* out_bits, int64_t som) {
+  if (offs[0] < 0) return -1;
+  for (int g = 0; g < G; ++g)
+    if (offs[g + 1] < offs[g] || offs[g + 1] > M) return -1;
+  float* x = (float*)malloc(sizeof(float) * (size_t)K);
+  float* w = (float*)malloc(sizeof(float) * (size_t)N * K);
+  if (!x || !w) { free(x); free(w); return -2; }
+  for (int g = 0; g < G; ++g) {
+    for (int n = 0; n < N; ++n)
+      for (int k = 0; k < K; ++k) w[(size_t)n * K + k] = vo_e4m3_to_f32(b[g * sbg + n * sbn + k]) * sb;
+    for (int64_t r = offs[g]; r < offs[g + 1]; ++r) {
+      for (int k = 0; k < K; ++k)
+        x[k] = (a_e5m2 ? vo_e5m2_to_f32(a[r * sam + k]) : vo_e4m3_to_f32(a[r * sam + k])) * sa;
+      for (int n = 0; n < N; ++n) {
+        float acc = 0.0f;
+        const float* wn = w + (size_t)n * K;
+        for (int k = 0; k < K; ++k) acc += x[k] * wn[k];
+        out_bits[r * som + n] = vo_f32_to_bf16(acc);
+      }
+    }
+  }
+  free(x); free(w);
+  return 0;
+}

@@ -196,6 +196,10 @@ def _c_oracle():
     lib.vo_vark_tensorwise.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, ctypes.c_float,
                                        ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
                                        ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
+    lib.vo_persistent_fp8.restype = ctypes.c_int
+    lib.vo_persistent_fp8.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, ctypes.c_float, ctypes.c_void_p,
+                                      ctypes.c_int, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
+                                      ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64]
     return lib
 
 
@@ -219,6 +223,37 @@ def test_c_oracle_agrees_with_numpy_oracle(orc):
     ref = orc.vark_wgrad_tensorwise(lhs, rhs, 0.02, 1e-4, offs)
     m = orc.compare(out, ref, offs)
     assert m["cos"] > 0.9999999 and m["max_rel"] <= 2 ** -7 and m["empty_zero"], m
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_c_persistent_oracle_agrees_with_numpy_oracle(orp, orc, fmt):
+    """The C restatement of the persistent GEMM (vo_persistent_fp8) against the numpy one: ragged
+    and empty groups, K not a multiple of 128, B rows strided past K, untouched rows outside every
+    group (the sentinel 0x1234 stays)."""
+    lib = _c_oracle()
+    rng = np.random.default_rng(7 if fmt == "e4m3" else 8)
+    lens, K, N = [37, 0, 130, 5], 208, 48
+    M = sum(lens) + 3
+    offs = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    dt = torch.float8_e4m3fn if fmt == "e4m3" else torch.float8_e5m2
+    a = torch.randn((M, K), generator=torch.Generator().manual_seed(1)).to(dt).view(torch.uint8).numpy()
+    b_full = torch.randn((len(lens), N, K + 32), generator=torch.Generator().manual_seed(2)).to(
+        torch.float8_e4m3fn).view(torch.uint8).numpy()
+    out = np.full((M, N), 0x1234, np.uint16)
+    rc = lib.vo_persistent_fp8(a.ctypes.data, b_full.ctypes.data, ctypes.c_float(0.1), ctypes.c_float(0.05),
+                               offs.ctypes.data, len(lens), M, N, K, K, N * (K + 32), K + 32, int(fmt == "e5m2"),
+                               out.ctypes.data, N)
+    assert rc == 0
+    ref = orp.grouped_fp8(a, np.ascontiguousarray(b_full[:, :, :K]), 0.1, 0.05, offs, fmt)
+    rows = int(offs[-1])
+    m = orc.compare(out[:rows], ref[:rows])
+    assert m["cos"] > 0.9999999 and m["max_rel"] <= 2 ** -7, m
+    assert np.all(out[rows:] == 0x1234)
+    bad = offs.copy()
+    bad[2] = bad[1] - 1
+    assert lib.vo_persistent_fp8(a.ctypes.data, b_full.ctypes.data, ctypes.c_float(1), ctypes.c_float(1),
+                                 bad.ctypes.data, len(lens), M, N, K, K, N * (K + 32), K + 32, 0, out.ctypes.data,
+                                 N) == -1
 
 
 # ----------------------------------------------------------------------------- reference generator
