@@ -121,14 +121,11 @@ bool wide_fits(int N, int K, int sam, int sbn, int scm) {
          (int64_t)sbn * ggemm::pw::kTN < ggemm::nt::kOob && (int64_t)scm * 2 * ggemm::pw::kTM < ggemm::nt::kOob;
 }
 
-// The automatic choice: the wide kernel where it fits and the A and B rows start on 128-byte lines
-// (then each stage's row segment is one line). With a stride of 64 mod 128 (K = 2880 contiguous)
-// half the segments straddle two lines; the wide kernel's 18 loads per wave and stage then measured
-// 2 % slower than the 512-thread kernel at gate_up_fwd (same box), 1 % faster at the N = 2880 sites;
-// with line-aligned rows 2.5-5.5 % faster at all four sites.
-bool wide_preferred(int N, int K, int sam, int sbn, int scm) {
-  return wide_fits(N, K, sam, sbn, scm) && sam % 128 == 0 && sbn % 128 == 0;
-}
+// The automatic choice: the wide kernel wherever it fits. With line-aligned rows it measured 2.5-5.5 %
+// faster than the 512-thread kernel at all four sites; on the reference's contiguous K = 2880 rows
+// (half the 128-byte row segments straddle two lines) 2.0-2.5 % faster at the N = 2880 sites and
+// level (within 0.7 %, either way) at gate_up_fwd, same-box A/Bs on three boxes.
+bool wide_preferred(int N, int K, int sam, int sbn, int scm) { return wide_fits(N, K, sam, sbn, scm); }
 
 int launch(const void* a, const void* b, void* out, const float* a_scale, const float* b_scale,
            const int64_t* group_offs, int G, int N, int K, int sam, int sbg, int sbn, int scm, int scn, int fmt,

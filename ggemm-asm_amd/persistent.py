@@ -81,8 +81,7 @@ def grouped_gemm_fp8_tensorwise(a: torch.Tensor, b: torch.Tensor, a_scale: torch
     are left unwritten, or set to zero with ``zero_tail=True`` (the library's device-side clear, no
     sync: dropped tokens get exact zeros). ``validate=True`` checks group_offs on the host first (a
     sync). Offsets past M_total are clamped to it on the device. ``kernel``: "auto" (the library's
-    choice: the wide-tile kernel where N % 320 == 0, K % 64 == 0 and the a and b row strides are
-    multiples of 128, else the 512-thread kernel),
+    choice: the wide-tile kernel where N % 320 == 0 and K % 64 == 0, else the 512-thread kernel),
     "512" or "wide" (GGemmError GGEMM_E_SHAPE where the wide kernel does not apply).
     """
     if a.dim() != 2 or b.dim() != 3:

@@ -56,8 +56,9 @@ int ggemm_persistent_fp8(const void* a, const void* b, void* out, const float* a
  * fp32 summation order): the 512-thread kernel of the reference's launch geometry (192-row tiles,
  * also the drop-in code objects) and a wide-tile kernel (256 threads, one wave per SIMD, 256 x 320
  * tiles, 160 KiB of LDS) for N % 320 == 0, K % 64 == 0, 256*stride_am, 320*stride_bn and
- * 512*stride_cm below 2^31 - 2^16. ggemm_persistent_fp8 runs the wide kernel where it applies and
- * stride_am and stride_bn are multiples of 128 (row segments on whole 128-byte lines). */
+ * 512*stride_cm below 2^31 - 2^16. ggemm_persistent_fp8 runs the wide kernel wherever it applies
+ * (faster on line-aligned rows, 128-byte multiples, and on the reference's contiguous K = 2880 rows
+ * faster or level). */
 #define GGEMM_PERSISTENT_KERNEL_AUTO 0
 #define GGEMM_PERSISTENT_KERNEL_512 1
 #define GGEMM_PERSISTENT_KERNEL_WIDE 2

@@ -50,7 +50,7 @@ def test_wide_vs_oracle(pkg, orc, orp, cuda, fmt, lens, K, N):
     site = "down_fwd" if fmt == "e4m3" else "down_dgrad"
     _say(f"persistent wide {fmt} lens={lens} K={K} N={N}")
     p = pkg.inputs.make_fwd_problem(site, seed=len(lens) + K, lens=lens, K=K, N=N)
-    assert pkg.persistent.selected_kernel(N, K, K, K, N) == ("wide" if K % 128 == 0 else "512")
+    assert pkg.persistent.selected_kernel(N, K, K, K, N) == "wide"
     M = int(sum(lens))
     out = _run(pkg, p, cuda, "wide")
     torch.cuda.synchronize()
@@ -115,8 +115,8 @@ def test_wide_rejects_shapes_it_does_not_take(pkg, cuda):
         _run(pkg, p, cuda, "wide")
     assert pkg.persistent.selected_kernel(336, 2880, 2880, 2880, 336) == "512"
     assert pkg.persistent.selected_kernel(320, 208, 208, 208, 320) == "512"
-    # the automatic choice: the wide kernel on line-aligned rows only
-    assert pkg.persistent.selected_kernel(5760, 2880, 2880, 2880, 5760) == "512"
+    # the automatic choice: the wide kernel wherever it applies, line-aligned rows or not
+    assert pkg.persistent.selected_kernel(5760, 2880, 2880, 2880, 5760) == "wide"
     assert pkg.persistent.selected_kernel(5760, 2880, 2944, 2944, 5760) == "wide"
     assert pkg.persistent.selected_kernel(2880, 5760, 5760, 5760, 2880) == "wide"
 

@@ -319,12 +319,14 @@ def test_persistent_kernel_choice_validation(pkg, kernel, kw, rc):
 
 
 def test_persistent_selected_kernel(pkg):
-    """The automatic choice: the wide kernel where it applies and A and B rows are line-aligned."""
+    """The automatic choice: the wide kernel wherever it applies (N % 320 == 0, K % 64 == 0, the
+    32-bit offsets of its tiles), line-aligned rows or not."""
     sel = pkg.load_library().ggemm_persistent_selected_kernel
     assert sel(5760, 2880, 2944, 2944, 5760) == 2          # the autograd op's aligned rows
     assert sel(2880, 5760, 5760, 5760, 2880) == 2          # K = 5760: aligned when contiguous
-    assert sel(5760, 2880, 2880, 2880, 5760) == 1          # the reference's contiguous K = 2880
-    assert sel(5760, 2880, 2944, 2880, 5760) == 1          # one operand unaligned
+    assert sel(5760, 2880, 2880, 2880, 5760) == 2          # the reference's contiguous K = 2880
+    assert sel(5760, 2880, 2944, 2880, 5760) == 2          # one operand unaligned
+    assert sel(320, 64, 9_000_000, 64, 320) == 1           # 256 A rows past the 32-bit offsets
     assert sel(5376, 2944, 2944, 2944, 5376) == 1          # N not a multiple of 320
     assert sel(640, 2880 + 48, 3072, 3072, 640) == 1       # K not a multiple of 64
     assert sel(320, 64, 128, 128, 320) == 2
