@@ -962,7 +962,12 @@ class KConfig(Config):
         self.op = {name: f"%{i}" for i, (name, _) in enumerate(ops)}
         self.order = [(0, j) for j in range(self.bn)] + [(i, j) for j in range(self.bn) for i in range(1, self.bm)]
         pos = {ij: n for n, ij in enumerate(self.order)}
-        self.barrier_after = self.bn - 1
+        # the barrier that publishes the next stage and frees this one's slot: after MFMA 2 of the
+        # second half, once the issue set-up (emitted after MFMAs 0-2) is complete; two MFMAs before the
+        # end of the first row (where the wgrad kernels put it) measured 1.1-2.0 % faster at the fwd
+        # sites, the stage's loads starting two gaps earlier; one or none before it would issue loads
+        # from a half-built buffer resource
+        self.barrier_after = 2
         reads = {self.bn - 1: [("am", 0)]}
         for j in range(self.bn):
             reads.setdefault(pos[(self.bm - 1, j)], []).append(("bn", j))
@@ -987,6 +992,7 @@ class KConfig(Config):
         assert k == self.loads and max(len(v) for v in plan.values()) <= 2
         self.dma_plan = plan
         self.setup_after = (0, 1, 2)
+        assert max(self.setup_after) <= self.barrier_after < self.bn - 1
         assert self.epi_x >= 28 and self.vop0 % 2 == 0 and self.e_stores + self.loads <= 63
         assert self.vop0 + 56 <= self.vacc0          # the epilogue's other temporaries (up to vop0 + 55)
         assert self.nl * 4 * 1024 == KKS * tm and self.nr * 4 * 1024 == KKS * tn
@@ -1103,8 +1109,8 @@ class GenK(Gen):
 
     def half(self, kh, first, wait_first, barrier, reads_from, issue):
         """One K-half: 4 x 5 MFMAs. wait_first: the half's operands were read by the tile's
-        prologue (all in); barrier: wait for the next stage's loads and pass the barrier after the
-        first row; reads_from: (slot register, K-half) of the next half's operands, or None;
+        prologue (all in); barrier: wait for the next stage's loads and pass the barrier after
+        MFMA barrier_after; reads_from: (slot register, K-half) of the next half's operands, or None;
         issue: the cursor's next stage goes out after the barrier."""
         s, e, c = SGPR_K, self.emit, self.cfg
         setup = self.capture(self.issue_setup) if issue else []
@@ -1134,7 +1140,7 @@ class GenK(Gen):
 
     def kstage(self, first, last, issue, half_only=False):
         """Stage k from slot CS: K-half 0 (reading half 1 from CS), then K-half 1 (unless last:
-        barrier after its first row, then reading the next stage's half 0 from NS = the other
+        barrier after its third MFMA, then reading the next stage's half 0 from NS = the other
         slot, and with issue the cursor's next stage into CS). half_only: the tile's last stage
         under K % 128 == 64, half 0 alone."""
         s, e, c = SGPR_K, self.emit, self.cfg
