@@ -121,10 +121,10 @@ bool wide_fits(int N, int K, int sam, int sbn, int scm) {
          (int64_t)sbn * ggemm::pw::kTN < ggemm::nt::kOob && (int64_t)scm * 2 * ggemm::pw::kTM < ggemm::nt::kOob;
 }
 
-// The automatic choice: the wide kernel wherever it fits. With line-aligned rows it measured 2.5-5.5 %
-// faster than the 512-thread kernel at all four sites; on the reference's contiguous K = 2880 rows
-// (half the 128-byte row segments straddle two lines) 2.0-2.5 % faster at the N = 2880 sites and
-// level (within 0.7 %, either way) at gate_up_fwd, same-box A/Bs on three boxes.
+// The automatic choice: the wide kernel wherever it fits. Against the 512-thread kernel it measured
+// faster at all four fwd / dgrad sites on both row layouts: on the reference's contiguous K = 2880
+// rows (half the 128-byte row segments straddle two lines) 2-6 % (5.690 against 5.999 ms over the
+// four sites, same box), on line-aligned rows more.
 bool wide_preferred(int N, int K, int sam, int sbn, int scm) { return wide_fits(N, K, sam, sbn, scm); }
 
 int launch(const void* a, const void* b, void* out, const float* a_scale, const float* b_scale,

@@ -57,8 +57,7 @@ int ggemm_persistent_fp8(const void* a, const void* b, void* out, const float* a
  * also the drop-in code objects) and a wide-tile kernel (256 threads, one wave per SIMD, 256 x 320
  * tiles, 160 KiB of LDS) for N % 320 == 0, K % 64 == 0, 256*stride_am, 320*stride_bn and
  * 512*stride_cm below 2^31 - 2^16. ggemm_persistent_fp8 runs the wide kernel wherever it applies
- * (faster on line-aligned rows, 128-byte multiples, and on the reference's contiguous K = 2880 rows
- * faster or level). */
+ * (faster at every measured shape, most on line-aligned rows of 128-byte multiples). */
 #define GGEMM_PERSISTENT_KERNEL_AUTO 0
 #define GGEMM_PERSISTENT_KERNEL_512 1
 #define GGEMM_PERSISTENT_KERNEL_WIDE 2
