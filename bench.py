@@ -42,6 +42,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -139,6 +140,48 @@ def read_traffic(name):
         return None, None
     src = f"profiles/traffic_{name}.txt (rocprofv3 --pmc, kernel revision {rev or 'unrecorded'})"
     return value, (src if value is not None else None)
+
+
+POWER_FILE = os.path.join(ROOT, "profiles", "power_sites.txt")
+POWER_CAP_W = 1400
+
+
+def read_power(label):
+    """The board power and gfx clock measured under this workload (profiles/power_sites.txt: amd-smi
+    sampled beside a long run of it), or None. Every large kernel here runs at the board's power
+    cap, which is what holds the clock and with it roofline.frac. Not measured by this run."""
+    rev = None
+    try:
+        for line in open(POWER_FILE):
+            if line.startswith("kernel_revision:"):
+                rev = line.split(":", 1)[1].strip()
+            m = re.match(r"^  (\S.*?)\s{2,}([\d.]+)\s+(\d+)\s+([\d.]+)\s+([\d.]+)\s*$", line)
+            if m and m.group(1) == label:
+                return {"watts": float(m.group(2)), "cap_watts": POWER_CAP_W, "gfx_clock_mhz": int(m.group(3)),
+                        "energy_per_launch_j": float(m.group(5)),
+                        "source": f"profiles/power_sites.txt (amd-smi, kernel revision {rev or 'unrecorded'})"}
+    except OSError:
+        return None
+    return None
+
+
+def power_label(args):
+    """The power_sites.txt row measured on this exact variant, or None."""
+    if args.config == "gate_up_wgrad" and args.mfma == "k128":
+        if args.out == "bf16" and args.lens == "multinomial":
+            return "gate_up_wgrad, bf16 C"
+        if args.out == "f32" and args.lens == "multinomial":
+            return "gate_up_wgrad, fp32 C"
+        if args.out == "f32_accum" and args.lens == "reference":
+            return "gate_up_wgrad, fp32 accumulate (ref)"
+    if args.config == "gate_up_fwd":
+        if args.persistent_kernel in ("auto", "wide") and not args.row_align:
+            return "gate_up_fwd, contiguous rows"
+        if args.persistent_kernel in ("auto", "wide") and args.row_align == 128:
+            return "gate_up_fwd, 128-byte rows"
+        if args.persistent_kernel == "512" and not args.row_align:
+            return "gate_up_fwd, 512-thread kernel"
+    return None
 
 
 def host_cores():
@@ -731,6 +774,10 @@ def main():
                      "unit": "TFLOP/s", "frac": round(tflops / FP8_DENSE_PEAK_TFLOPS, 4), "traffic": traffic,
                      "traffic_source": traffic_source},
     }
+    label = power_label(args)
+    power = read_power(label) if label else None
+    if power:
+        line["roofline"]["power"] = power
     if args.extra:
         extra = {}
         for name in ("down_wgrad", "gate_up_zipf", "gate_up_mx", "constant", *FWD_SITES):

@@ -3,6 +3,8 @@ with the oracle over every group (the reference checks the kernel it times in th
 reference bench.py:594-648, cosine at :641-646). The checker must accept an exact result, accept a
 result within the bar, and reject each kind of mistake the bar names: one element off by more than
 2e-2 relative, a non-finite value, a non-zero empty group, a wrong group (the cosine)."""
+import sys
+
 import numpy as np
 import pytest
 import torch
@@ -90,3 +92,26 @@ def test_fwd_leg(pkg, orp, orc):
     m = par["library"]
     assert m["ok"] and m["exact_frac"] == 1.0 and m["groups"] == "3 of 3 (128 rows)" and base is not None
     assert not par["drop_in_co"]["ok"]
+
+
+def test_power_record_for_measured_variants_only(monkeypatch):
+    """The roofline object's power record: the default line (gate_up_wgrad, bf16 C, multinomial
+    lengths) and the other measured variants map to their rows of profiles/power_sites.txt, whose
+    figures parse; unmeasured variants get none."""
+    monkeypatch.setattr(sys, "argv", ["bench.py"])
+    args = bench.parse_args()
+    assert bench.power_label(args) == "gate_up_wgrad, bf16 C"
+    rec = bench.read_power(bench.power_label(args))
+    assert rec is not None and rec["cap_watts"] == 1400
+    assert 1000 < rec["watts"] <= 1400 and 1000 < rec["gfx_clock_mhz"] <= 2400 and rec["energy_per_launch_j"] > 0
+    for argv, want in ((["--out", "f32_accum", "--lens", "reference"], "gate_up_wgrad, fp32 accumulate (ref)"),
+                       (["--config", "gate_up_fwd"], "gate_up_fwd, contiguous rows"),
+                       (["--config", "gate_up_fwd", "--row-align", "128"], "gate_up_fwd, 128-byte rows"),
+                       (["--config", "gate_up_fwd", "--persistent-kernel", "512"], "gate_up_fwd, 512-thread kernel"),
+                       (["--out", "f32_accum"], None), (["--mfma", "k32"], None), (["--config", "down_fwd"], None)):
+        monkeypatch.setattr(sys, "argv", ["bench.py", *argv])
+        a = bench.parse_args()
+        assert bench.power_label(a) == want, argv
+        if want:
+            assert bench.read_power(want) is not None, want
+    assert bench.read_power("no such row") is None
