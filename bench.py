@@ -104,6 +104,9 @@ def parse_args():
                          "(on by default; a failed bar exits with status 1)")
     ap.add_argument("--no-drop-in", dest="drop_in", action="store_false",
                     help="tensorwise wgrad configs: do not time the drop-in code object beside the library")
+    ap.add_argument("--drop-in-steps", type=int, default=None,
+                    help="timed launches of the drop-in code object (default: --steps), e.g. a long run of it "
+                         "alone for power sampling after a short library leg")
     ap.add_argument("--extra", action="store_true", help="also time the other configs (not part of the line)")
     ap.add_argument("--info", action="store_true",
                     help="print the registers, spills, LDS and MFMA counts of this build's code objects and exit "
@@ -826,11 +829,12 @@ def main():
     # the drop-in code object on the same inputs: what reference-side callers (launcher.cpp,
     # bench.py --kernel) get; its C is checked against the oracle beside the library's
     outs = {} if args.out == "f32_accum" else {"library": run.out}
+    co_steps = args.drop_in_steps or args.steps
     if drop_in_co and fwd:
-        line["drop_in_co"], outs["drop_in_co"] = time_drop_in_co_fwd(pkg, p, dev, args.steps, args.warmup,
+        line["drop_in_co"], outs["drop_in_co"] = time_drop_in_co_fwd(pkg, p, dev, co_steps, args.warmup,
                                                                      args.row_align)
     elif drop_in_co:
-        line["drop_in_co"], outs["drop_in_co"] = time_drop_in_co(pkg, p, dev, args.steps, args.warmup)
+        line["drop_in_co"], outs["drop_in_co"] = time_drop_in_co(pkg, p, dev, co_steps, args.warmup)
     # outside the timed region: the oracle over every group of the timed inputs, checked against
     # the last timed launch's output, and timed as the CPU baseline
     failed = []
