@@ -3,11 +3,38 @@ include/ggemm_persistent.h and include/ggemm_quant.h)."""
 from __future__ import annotations
 
 import ctypes
+import operator
 import os
 
 from . import build as _build
 
 _lib = None
+
+
+class _CheckedInt:
+    """Argument type of an integer parameter: ctypes' own ``c_int32`` / ``c_int64`` keep only the
+    low bits of a Python int that does not fit (2**32 + 5 arrives as 5), which would hand the
+    library's validation -- and the kernel -- a different size or stride from the tensor's. This
+    one raises OverflowError instead, and TypeError for a non-integer (a float)."""
+    bits = 32
+    ctype = ctypes.c_int32
+
+    @classmethod
+    def from_param(cls, v):
+        v = operator.index(v)
+        if not -(1 << (cls.bits - 1)) <= v < (1 << (cls.bits - 1)):
+            raise OverflowError(f"{v} does not fit the library's {cls.bits}-bit integer parameter")
+        return cls.ctype(v)
+
+
+class _I32(_CheckedInt):
+    pass
+
+
+class _I64(_CheckedInt):
+    bits = 64
+    ctype = ctypes.c_int64
+
 
 EXPORTS = (
     "ggemm_vark_wgrad_fp8",
@@ -82,44 +109,42 @@ def load():
     if lib.ggemm_vark_abi_version() != ABI_VERSION:
         raise RuntimeError(f"{path} has ABI version {lib.ggemm_vark_abi_version()}, these bindings need "
                            f"{ABI_VERSION}: rebuild with `python __graft_entry__.py build`")
-    vp, i32, i64p = ctypes.c_void_p, ctypes.c_int32, ctypes.POINTER(ctypes.c_int64)
+    vp, i32, i64, i64p = ctypes.c_void_p, _I32, _I64, ctypes.POINTER(ctypes.c_int64)
     tw = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, vp]
     for name in ("ggemm_vark_wgrad_fp8", "ggemm_vark_wgrad_fp8_k32"):
         f = getattr(lib, name)
         f.argtypes = tw
         f.restype = ctypes.c_int
-    lib.ggemm_vark_wgrad_fp8_out.argtypes = tw[:-1] + [i32, ctypes.c_int64, vp]
+    lib.ggemm_vark_wgrad_fp8_out.argtypes = tw[:-1] + [i32, i64, vp]
     lib.ggemm_vark_wgrad_fp8_out.restype = ctypes.c_int
-    lib.ggemm_vark_wgrad_fp8_wide.argtypes = tw[:-1] + [ctypes.c_int64, i32, i32, vp]
+    lib.ggemm_vark_wgrad_fp8_wide.argtypes = tw[:-1] + [i64, i32, i32, vp]
     lib.ggemm_vark_wgrad_fp8_wide.restype = ctypes.c_int
-    lib.ggemm_vark_wgrad_mxfp8.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 10 + [ctypes.c_int64, vp]
+    lib.ggemm_vark_wgrad_mxfp8.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 10 + [i64, vp]
     lib.ggemm_vark_wgrad_mxfp8.restype = ctypes.c_int
-    lib.ggemm_vark_wgrad_mxfp8_tile.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 10 + [ctypes.c_int64, i32, vp]
+    lib.ggemm_vark_wgrad_mxfp8_tile.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 10 + [i64, i32, vp]
     lib.ggemm_vark_wgrad_mxfp8_tile.restype = ctypes.c_int
-    lib.ggemm_vark_check_offsets.argtypes = [i64p, i32, ctypes.c_int64, i32]
+    lib.ggemm_vark_check_offsets.argtypes = [i64p, i32, i64, i32]
     lib.ggemm_vark_check_offsets.restype = ctypes.c_int
-    lib.ggemm_vark_num_cus.argtypes = [i32, ctypes.POINTER(i32)]
+    lib.ggemm_vark_num_cus.argtypes = [i32, ctypes.POINTER(ctypes.c_int32)]
     lib.ggemm_vark_num_cus.restype = ctypes.c_int
     lib.ggemm_vark_strerror.argtypes = [i32]
     lib.ggemm_vark_strerror.restype = ctypes.c_char_p
     lib.ggemm_vark_abi_version.argtypes = []
-    lib.ggemm_vark_abi_version.restype = i32
+    lib.ggemm_vark_abi_version.restype = ctypes.c_int32
     lib.ggemm_vark_bf16_kernel.argtypes = [i32, i32, i32, vp]
     lib.ggemm_vark_bf16_kernel.restype = ctypes.c_int32
-    lib.ggemm_vark_launch_geometry.argtypes = [i32] + [ctypes.POINTER(i32)] * 5
+    lib.ggemm_vark_launch_geometry.argtypes = [i32] + [ctypes.POINTER(ctypes.c_int32)] * 5
     lib.ggemm_vark_launch_geometry.restype = None
-    lib.ggemm_persistent_fp8.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 9 + [ctypes.c_int64, vp]
+    lib.ggemm_persistent_fp8.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 9 + [i64, vp]
     lib.ggemm_persistent_fp8.restype = ctypes.c_int
-    lib.ggemm_persistent_fp8_kernel.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 9 + [ctypes.c_int64, i32, vp]
+    lib.ggemm_persistent_fp8_kernel.argtypes = [vp, vp, vp, vp, vp, vp] + [i32] * 9 + [i64, i32, vp]
     lib.ggemm_persistent_fp8_kernel.restype = ctypes.c_int
     lib.ggemm_persistent_selected_kernel.argtypes = [i32] * 5
-    lib.ggemm_persistent_selected_kernel.restype = i32
-    lib.ggemm_persistent_clear_tail.argtypes = [vp, i32, i32, vp, i32, ctypes.c_int64, vp]
+    lib.ggemm_persistent_selected_kernel.restype = ctypes.c_int32
+    lib.ggemm_persistent_clear_tail.argtypes = [vp, i32, i32, vp, i32, i64, vp]
     lib.ggemm_persistent_clear_tail.restype = ctypes.c_int
-    lib.ggemm_persistent_transpose_u8.argtypes = [vp, i32, i32, i32, ctypes.c_int64, ctypes.c_int64, vp,
-                                                  ctypes.c_int64, ctypes.c_int64, vp]
+    lib.ggemm_persistent_transpose_u8.argtypes = [vp, i32, i32, i32, i64, i64, vp, i64, i64, vp]
     lib.ggemm_persistent_transpose_u8.restype = ctypes.c_int
-    i64 = ctypes.c_int64
     lib.ggemm_quant_amax.argtypes = [vp, i32, i64, i32, i64, vp, vp]
     lib.ggemm_quant_amax.restype = ctypes.c_int
     lib.ggemm_quant_fp8_tensorwise.argtypes = [vp, i32, i64, i32, i64, i32, vp, i64, vp, vp, vp]

@@ -133,6 +133,25 @@ def test_mx_validation_rejects(pkg):
     assert lib.ggemm_vark_wgrad_mxfp8(*args, 64, 128, -1, None) == -2       # negative token count
 
 
+def test_integer_arguments_out_of_range_raise(pkg):
+    """A size or stride beyond a parameter's width raises in the binding. Plain ctypes integer
+    types keep the low bits: N = 2**32 + 320 would reach the library as N = 320 (the wide kernel's
+    shape), and a row stride of 2**32 + 5762 as 5762."""
+    import numpy as np
+
+    lib = pkg.load_library()
+    assert lib.ggemm_persistent_selected_kernel(320, 2880, 2880, 2880, 320) == 2
+    with pytest.raises(ctypes.ArgumentError, match="does not fit"):
+        lib.ggemm_persistent_selected_kernel((1 << 32) + 320, 2880, 2880, 2880, 320)
+    with pytest.raises(ctypes.ArgumentError, match="does not fit"):
+        _call(lib, scm=(1 << 32) + 5762)
+    with pytest.raises(ctypes.ArgumentError, match="does not fit"):
+        lib.ggemm_vark_check_offsets(None, 1, 1 << 63, 0)
+    with pytest.raises(ctypes.ArgumentError):   # a float is not a size
+        _call(lib, G=32.0)
+    assert _call(lib, scm=np.int64(5762), G=np.int32(32)) == -3   # numpy integers pass as ints
+
+
 def test_python_op_refuses_cpu_tensors(pkg):
     lhs = torch.zeros(64, 64, dtype=torch.uint8)
     rhs = torch.zeros(64, 128, dtype=torch.uint8)
