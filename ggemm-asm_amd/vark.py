@@ -31,6 +31,12 @@ def _check_inputs(lhs, rhs, group_offs, lhs_dt=_FP8_LHS, rhs_dt=_FP8_RHS):
                         f"got {lhs.dtype}, {rhs.dtype}")
     if lhs.stride(1) != 1 or rhs.stride(1) != 1:
         raise ValueError("lhs/rhs must be contiguous along the feature dimension")
+    for name, t in (("lhs", lhs), ("rhs", rhs)):
+        # the kernels may read a token row up to its stride: the last row's padding must exist
+        end = (t.storage_offset() + t.shape[0] * t.stride(0)) * t.element_size()
+        if t.shape[0] > 0 and end > t.untyped_storage().nbytes():
+            raise ValueError(f"{name}'s last row does not extend to its row stride ({t.stride(0)}) within its "
+                             "storage: the kernels may read a row's padding; use a view into a tensor of full rows")
     if group_offs.dtype != torch.int64 or group_offs.dim() != 1 or group_offs.numel() < 2:
         raise ValueError("group_offs must be int64 [G+1]")
     dev = lhs.device

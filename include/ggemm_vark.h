@@ -43,7 +43,10 @@ enum {
  * argument list carries no token count; ggemm_vark_wgrad_fp8_out with GGEMM_OUT_BF16 is the same
  * launch bounded by M_total). Every element of out[0:G] is written, empty groups with zeros.
  * Requirements: OUT_M, OUT_N, stride_lhs_m, stride_rhs_m multiples of 16; stride_cm,
- * stride_cg multiples of 4; lhs/rhs 16-byte aligned, out 8-byte aligned. */
+ * stride_cg multiples of 4; lhs/rhs 16-byte aligned, out 8-byte aligned. A token row of lhs / rhs
+ * may be read up to its stride, padding included, so with a padded row stride the last row must
+ * be allocated in full (M_total * stride bytes from the base), as a view into a wider tensor is.
+ * The same holds for every wgrad entry below. */
 int ggemm_vark_wgrad_fp8(const void* lhs, const void* rhs, void* out, const float* lhs_scale,
                          const float* rhs_scale, const int64_t* group_offs, int32_t G, int32_t OUT_M,
                          int32_t OUT_N, int32_t stride_lhs_m, int32_t stride_rhs_m, int32_t stride_cg,

@@ -152,6 +152,24 @@ def test_integer_arguments_out_of_range_raise(pkg):
     assert _call(lib, scm=np.int64(5762), G=np.int32(32)) == -3   # numpy integers pass as ints
 
 
+def test_python_op_refuses_rows_short_of_their_stride(pkg):
+    """An operand whose last row ends before its row stride (an as_strided view over a buffer one
+    padding short) is refused: the kernels may read a row's padding. A view into a tensor of full
+    rows passes that check (and, on the CPU, stops at the device check)."""
+    buf = torch.zeros(63 * 96 + 64, dtype=torch.uint8)
+    short = torch.as_strided(buf, (64, 64), (96, 1))
+    full = torch.zeros(64, 96, dtype=torch.uint8)[:, :64]
+    rhs = torch.zeros(64, 128, dtype=torch.uint8)
+    s = torch.tensor(1.0)
+    offs = torch.tensor([0, 64], dtype=torch.int64)
+    with pytest.raises(ValueError, match="row stride"):
+        pkg.grouped_gemm_fp8_tensorwise_variable_k(short, rhs, s, s, offs)
+    with pytest.raises(ValueError, match="row stride"):
+        pkg.grouped_gemm_fp8_tensorwise_variable_k(rhs, short, s, s, offs)
+    with pytest.raises(ValueError, match="gfx950 GPU only"):
+        pkg.grouped_gemm_fp8_tensorwise_variable_k(full, rhs, s, s, offs)
+
+
 def test_python_op_refuses_cpu_tensors(pkg):
     lhs = torch.zeros(64, 64, dtype=torch.uint8)
     rhs = torch.zeros(64, 128, dtype=torch.uint8)

@@ -379,3 +379,92 @@ def test_forced_wide_rejects_8_byte_rows(pkg, cuda):
     big = torch.zeros((1, 1280, 1924), dtype=torch.bfloat16, device=cuda)
     with pytest.raises(Exception, match="GGEMM_E_ALIGN"):
         pkg.grouped_gemm_fp8_tensorwise_variable_k(lhs, rhs, one, one, offs, out=big[:, :, :1920], wide=320)
+
+
+# ----------------------------------------------------------------------------- seeded random shapes
+
+WIDE_RANDOM_MODES = ("wide256 bf16", "wide320 bf16", "wide320 fp32", "wide320 fp32 accumulate")
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_wide_random_shapes_vs_oracle(pkg, orc, cuda, seed):
+    """Seeded random configurations on each wide-tile kernel, forced: 256 x 384 (bf16 C) and
+    320 x 320 (bf16, fp32 and fp32-accumulate C) in turn. G in 1..24 with empty, tiny (1-63 token)
+    and longer groups, now and then one of 1500-3000 tokens; OUT_M and OUT_N 1-4 and 1-6 tiles of
+    320, or OUT_M any multiple of 16 up to 1024 (a partial last M-tile) and 1-4 tiles of 384; LHS
+    and RHS row strides padded by 0, 16 or 64 bytes; C a view into a buffer with 0 or 16 bytes of
+    padding per row and 0 or 16 spare rows per group, which keep their sentinel. bf16 C: the bar
+    against the oracle, or, when a group is shorter than 40 tokens, the bar's cosine, finiteness
+    and exact-zero empty groups plus every element within the rigorous fp8-MFMA error bound. fp32
+    C: the bar on fp32 values, or the cosine plus the bound without output rounding.
+    Accumulation: C0 + the fp32 result, bit for bit."""
+    rng = np.random.default_rng(7000 + seed)
+    mode = WIDE_RANDOM_MODES[seed % 4]
+    tile = 256 if mode.startswith("wide256") else 320
+    fp32 = "fp32" in mode
+    G = int(rng.integers(1, 25))
+    kind = rng.integers(0, 4, G)
+    lens = np.where(kind == 0, 0, np.where(kind == 1, rng.integers(1, 64, G), rng.integers(64, 700, G)))
+    if seed % 3 == 0:
+        lens[rng.integers(0, G)] = int(rng.integers(1500, 3001))
+    lens = [int(v) for v in lens]
+    if tile == 320:
+        om, on = 320 * int(rng.integers(1, 5)), 320 * int(rng.integers(1, 7))
+    else:
+        om, on = 16 * int(rng.integers(1, 65)), 384 * int(rng.integers(1, 5))
+    lpad, rpad = int(rng.choice([0, 16, 64])), int(rng.choice([0, 16, 64]))
+    esize = 4 if fp32 else 2
+    cpad = int(rng.choice([0, 16])) // esize
+    rows_extra = int(rng.choice([0, 16]))
+    M = sum(lens)
+    _say(f"wide random seed={seed} {mode} G={G} M={M} OUT={om}x{on} lhs/rhs pad {lpad}/{rpad} B, "
+         f"C pad {cpad} cols {rows_extra} rows")
+    lhs, rhs, offs, _, (sl, sr) = _rand_bytes_problem(lens, om, on, seed=seed + 91)
+    dl = torch.zeros((max(M, 1), om + lpad), dtype=torch.uint8, device=cuda)[:M, :om]
+    dl.copy_(lhs)
+    dr = torch.zeros((max(M, 1), on + rpad), dtype=torch.uint8, device=cuda)[:M, :on]
+    dr.copy_(rhs)
+    do = offs.to(cuda)
+    s1 = torch.tensor(sl, dtype=torch.float32, device=cuda)
+    s2 = torch.tensor(sr, dtype=torch.float32, device=cuda)
+    dt = torch.float32 if fp32 else torch.bfloat16
+    big = torch.full((G, om + rows_extra, on + cpad), 7.0, dtype=dt, device=cuda)
+    view = big[:, :om, :on]
+    view.fill_(float("nan"))
+    run = pkg.grouped_gemm_fp8_tensorwise_variable_k
+    run(dl, dr, s1, s2, do, out=view, out_dtype=dt, wide=tile)
+    torch.cuda.synchronize()
+    assert bool((big[:, om:, :] == 7.0).all()) and bool((big[:, :, on:] == 7.0).all())
+    tiny = any(0 < v < 40 for v in lens)
+    if not fp32:
+        ref = orc.vark_wgrad_tensorwise(lhs.numpy(), rhs.numpy(), sl, sr, offs.numpy())
+        bits = pkg.as_bf16_bits(view)
+        if tiny:
+            _assert_parity_small_k(orc, bits, ref, lhs, rhs, offs, sl, sr, f"wide random {seed}")
+        else:
+            _assert_parity(orc, bits, ref, offs.numpy(), f"wide random {seed}")
+        return
+    got = view.cpu().numpy()
+    for g, v in enumerate(lens):
+        if v == 0:
+            assert np.all(got[g] == 0), g
+    ref = orc.vark_wgrad_tensorwise_f32(lhs.numpy(), rhs.numpy(), sl, sr, offs.numpy(), acc_dtype=np.float64)
+    a, b = got.astype(np.float64).ravel(), ref.astype(np.float64).ravel()
+    assert np.isfinite(a).all()
+    cos = float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b) + 1e-300)) if M else 1.0
+    mask = np.abs(b) > 1e-3 * np.abs(b).max() if M else np.zeros(b.shape, bool)
+    rel = float(np.max(np.abs(a[mask] - b[mask]) / np.abs(b[mask]))) if mask.any() else 0.0
+    _say(f"wide random {seed} fp32: cos {cos:.9f} max_rel {rel:.3e}")
+    assert cos >= 0.99999, (seed, cos)
+    if rel > 2e-2:
+        viol, worst = orc.mfma_bound_violations(got, lhs.numpy(), rhs.numpy(), offs.numpy(), sl, sr,
+                                                out_rounding=0.0)
+        _say(f"wide random {seed} fp32: error-bound violations {int(viol.sum())}, worst ratio {worst:.3f}")
+        assert not viol.any()
+    if mode.endswith("accumulate"):
+        c0 = torch.randn((G, om, on), generator=torch.Generator().manual_seed(seed), dtype=torch.float32)
+        view.copy_(c0.to(cuda))
+        run(dl, dr, s1, s2, do, out=view, accumulate=True, wide=tile)
+        torch.cuda.synchronize()
+        assert bool((big[:, om:, :] == 7.0).all()) and bool((big[:, :, on:] == 7.0).all())
+        np.testing.assert_array_equal(view.cpu().numpy(), (c0.numpy() + got).astype(np.float32))
