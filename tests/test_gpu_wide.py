@@ -468,3 +468,46 @@ def test_wide_random_shapes_vs_oracle(pkg, orc, cuda, seed):
         torch.cuda.synchronize()
         assert bool((big[:, om:, :] == 7.0).all()) and bool((big[:, :, on:] == 7.0).all())
         np.testing.assert_array_equal(view.cpu().numpy(), (c0.numpy() + got).astype(np.float32))
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_wide_mx_random_shapes_vs_oracle(pkg, orc, cuda, seed):
+    """Seeded random configurations on the wide MX kernel (forced, tile_m=320): G in 1..16 with
+    empty groups and groups of 32-640 tokens in whole 32-token blocks, the last group of any
+    length; OUT_M and OUT_N 1-4 and 1-6 tiles of 320; LHS / RHS row strides padded by 0, 16 or 64
+    bytes and the e8m0 scale rows by 16 on odd seeds; C a view with 8 columns of padding per row,
+    which keep their sentinel. The bar against the oracle, or its cosine, finiteness and
+    exact-zero empty groups plus every element within the rigorous error bound of the
+    block-scaled product."""
+    rng = np.random.default_rng(8000 + seed)
+    G = int(rng.integers(1, 17))
+    blocks = np.where(rng.integers(0, 4, G) == 0, 0, rng.integers(1, 21, G))
+    lens = [32 * int(v) for v in blocks]
+    lens[-1] = int(rng.integers(1, 700))
+    om, on = 320 * int(rng.integers(1, 5)), 320 * int(rng.integers(1, 7))
+    lpad, rpad = int(rng.choice([0, 16, 64])), int(rng.choice([0, 16, 64]))
+    spad = 16 * (seed % 2)
+    _say(f"wide mx random seed={seed} G={G} M={sum(lens)} OUT={om}x{on} lhs/rhs pad {lpad}/{rpad} B, "
+         f"scale pad {spad} B")
+    lhs, rhs, offs, (sl, sr), _ = _rand_bytes_problem(lens, om, on, seed=seed + 37, mx=True)
+
+    def padded(t, pad):
+        v = torch.zeros((max(t.shape[0], 1), t.shape[1] + pad), dtype=torch.uint8, device=cuda)
+        v = v[:t.shape[0], :t.shape[1]]
+        v.copy_(t)
+        return v
+
+    big = torch.full((G, om, on + 8), 7.0, dtype=torch.bfloat16, device=cuda)
+    view = big[:, :, :on]
+    view.fill_(float("nan"))
+    pkg.grouped_gemm_mxfp8_variable_k(padded(lhs, lpad), padded(rhs, rpad), padded(sl, spad), padded(sr, spad),
+                                      offs.to(cuda), out=view, validate=True, tile_m=320)
+    torch.cuda.synchronize()
+    assert bool((big[:, :, on:] == 7.0).all())
+    ref = orc.vark_wgrad_mxfp8(lhs.numpy(), rhs.numpy(), sl.numpy(), sr.numpy(), offs.numpy())
+    bits = pkg.as_bf16_bits(view)
+    m = orc.compare(bits, ref, offs.numpy())
+    _say(f"wide mx random {seed}: {m}")
+    if not orc.parity_ok(m):
+        assert m["cos"] >= 0.99999 and m["nonfinite"] == 0 and m["empty_zero"], (seed, m)
+        _error_bound_ok(orc, bits, lhs, rhs, offs, 1.0, 1.0, f"wide mx random {seed}", lsc=sl, rsc=sr)
