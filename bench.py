@@ -105,8 +105,16 @@ def parse_args():
     ap.add_argument("--no-drop-in", dest="drop_in", action="store_false",
                     help="tensorwise wgrad configs: do not time the drop-in code object beside the library")
     ap.add_argument("--drop-in-steps", type=int, default=None,
-                    help="timed launches of the drop-in code object (default: --steps), e.g. a long run of it "
-                         "alone for power sampling after a short library leg")
+                    help="timed launches of the drop-in code object (default: --steps)")
+    ap.add_argument("--power-seconds", type=float, default=0.0,
+                    help="after timing, launch the step back to back for this long while amd-smi samples the "
+                         "board's power and gfx clock (every 0.25 s, from a child process started before the GPU "
+                         "is touched); the medians of the window's middle half go into roofline.power (or "
+                         "drop_in_co.power with --power-of drop_in) in place of the recorded figures")
+    ap.add_argument("--power-of", default="library", choices=["library", "drop_in"],
+                    help="what the power window launches: the library step or the drop-in code object")
+    ap.add_argument("--power-sampler", default=None, help=argparse.SUPPRESS)   # child-process mode
+    ap.add_argument("--power-interval", type=float, default=POWER_INTERVAL_S, help=argparse.SUPPRESS)
     ap.add_argument("--extra", action="store_true", help="also time the other configs (not part of the line)")
     ap.add_argument("--info", action="store_true",
                     help="print the registers, spills, LDS and MFMA counts of this build's code objects and exit "
@@ -146,7 +154,132 @@ def read_traffic(name):
 
 
 POWER_FILE = os.path.join(ROOT, "profiles", "power_sites.txt")
-POWER_CAP_W = 1400
+POWER_CAP_W = 1400                # MI355X rated board power; amd-smi metric reports no limit
+POWER_INTERVAL_S = 0.25
+
+
+def parse_amd_smi(text):
+    """(socket power in W, mean gfx clock over the XCDs in MHz) from one ``amd-smi metric -p -c
+    --json`` document of a single GPU."""
+    d = json.loads(text)
+    gpus = d["gpu_data"] if isinstance(d, dict) else d
+    if len(gpus) != 1:
+        raise ValueError(f"amd-smi lists {len(gpus)} GPUs; this reading needs exactly the one in use")
+    g = gpus[0]
+    clks = [float(v["clk"]["value"]) for k, v in g["clock"].items()
+            if k.startswith("gfx_") and isinstance(v, dict) and isinstance(v.get("clk"), dict)]
+    if not clks:
+        raise ValueError("no gfx clock in the amd-smi reading")
+    return float(g["power"]["socket_power"]["value"]), sum(clks) / len(clks)
+
+
+def power_sampler(path, interval):
+    """Body of ``bench.py --power-sampler PATH``: a child process that the parent starts before it
+    touches the GPU and that never touches it itself. Once PATH + ".go" exists it appends one line
+    per ``amd-smi metric -p -c --json`` reading to PATH, ``{"t": unix time, "watts", "mhz"}`` or
+    ``{"t", "error"}``, every ``interval`` s, until the parent terminates it or exits."""
+    import subprocess
+    parent = os.getppid()
+    while os.getppid() == parent and not os.path.exists(path + ".go"):
+        time.sleep(0.05)
+    with open(path, "a") as f:
+        while os.getppid() == parent:
+            t = time.time()
+            try:
+                r = subprocess.run(["amd-smi", "metric", "-p", "-c", "--json"], capture_output=True, text=True,
+                                   timeout=10)
+                watts, mhz = parse_amd_smi(r.stdout)
+                rec = {"t": round(t, 3), "watts": watts, "mhz": round(mhz, 1)}
+            except Exception as e:   # a missing tool or an unexpected document: recorded, not fatal
+                rec = {"t": round(t, 3), "error": f"{type(e).__name__}: {e}"[:200]}
+            f.write(json.dumps(rec) + "\n")
+            f.flush()
+            time.sleep(interval)
+
+
+class PowerSampler:
+    """Parent side of ``power_sampler``: started before the GPU is touched (a process that has
+    initialised the GPU starts no other program), switched on for the power window only."""
+
+    def __init__(self, interval=POWER_INTERVAL_S):
+        import subprocess
+        import tempfile
+        fd, self.path = tempfile.mkstemp(prefix="ggemm_power_", suffix=".jsonl")
+        os.close(fd)
+        self.proc = subprocess.Popen([sys.executable, os.path.abspath(__file__), "--power-sampler", self.path,
+                                      "--power-interval", str(interval)],
+                                     stdin=subprocess.DEVNULL, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL)
+
+    def start(self):
+        open(self.path + ".go", "w").close()
+
+    def stop(self):
+        """End the child; its readings as dicts."""
+        self.proc.terminate()
+        try:
+            self.proc.wait(timeout=15)
+        except Exception:
+            self.proc.kill()
+            self.proc.wait()
+        samples = []
+        for line in open(self.path):
+            try:
+                samples.append(json.loads(line))
+            except ValueError:   # a line cut short by the termination
+                pass
+        for p in (self.path, self.path + ".go"):
+            try:
+                os.unlink(p)
+            except OSError:
+                pass
+        return samples
+
+
+def summarize_power(samples, t0, t1, launches):
+    """The power record of a window [t0, t1] of ``launches`` back-to-back launches: medians of the
+    readings taken in its middle half (the controller settles in the first quarter), the window's
+    wall time per launch, and their product, the energy per launch."""
+    import statistics
+    lo, hi = t0 + (t1 - t0) / 4, t1 - (t1 - t0) / 4
+    mid = [s for s in samples if "watts" in s and lo <= s["t"] <= hi]
+    if not mid:
+        errs = [s["error"] for s in samples if "error" in s]
+        return {"error": errs[-1] if errs else "no amd-smi reading inside the window's middle half"}
+    watts = statistics.median(s["watts"] for s in mid)
+    mhz = statistics.median(s["mhz"] for s in mid)
+    ms = (t1 - t0) * 1e3 / launches
+    return {"watts": round(watts, 1), "cap_watts": POWER_CAP_W, "gfx_clock_mhz": int(round(mhz)),
+            "ms_per_launch": round(ms, 4), "energy_per_launch_j": round(watts * ms * 1e-3, 3), "samples": len(mid),
+            "seconds": round(t1 - t0, 2),
+            "source": "live: amd-smi metric -p -c every 0.25 s beside launches back to back, medians over the "
+                      "window's middle half"}
+
+
+def power_window(launch, seconds, sampler):
+    """Board power under ``launch`` (one step on torch's current stream, which is the null stream
+    here, where the drop-in code object launches too), launched back to back for ``seconds`` with at
+    most two chunks of 16 launches queued (an event per chunk), the sampler on meanwhile."""
+    import torch
+    from collections import deque
+    for _ in range(4):
+        launch()
+    torch.cuda.synchronize()
+    sampler.start()
+    pending, n, t0 = deque(), 0, time.time()
+    while True:
+        for _ in range(16):
+            launch()
+        n += 16
+        ev = torch.cuda.Event()
+        ev.record()
+        pending.append(ev)
+        if len(pending) > 2:
+            pending.popleft().synchronize()
+        if time.time() - t0 >= seconds:
+            break
+    torch.cuda.synchronize()
+    t1 = time.time()
+    return summarize_power(sampler.stop(), t0, t1, n)
 
 
 def read_power(label):
@@ -382,13 +515,15 @@ def oracle_leg_fwd(p, outs, seconds):
     return parity, base
 
 
-def time_drop_in_co(pkg, p, dev, steps, warmup):
+def time_drop_in_co(pkg, p, dev, steps, warmup, power=None):
     """The drop-in code object (``variable_k_wgrad.co``) timed on the same inputs the way the
     reference times its own: loaded through the hipModule path, launched with the 16-entry
     kernelParams array on the null stream, grid num_cus x 512 threads, 64 KiB dynamic LDS
     (reference bench.py:364-413,768-801), HIP events on the null stream around ``steps``
     back-to-back launches. No C re-zeroing between launches: the kernel overwrites all of C.
-    Returns (record, output tensor of the last launch)."""
+    ``power``: a power window (``power_window`` bound to its duration and sampler) to run over the
+    same launch afterwards, its record kept as ``power``. Returns (record, output tensor of the last
+    launch)."""
     import torch
     from ggemm_asm_amd import harness
     module, func, name = harness.load_kernel(pkg.CODE_OBJECT_PATH)
@@ -401,6 +536,7 @@ def time_drop_in_co(pkg, p, dev, steps, warmup):
                                                         p.OUT_N, ncu)
         torch.cuda.synchronize()
         ms = harness.time_null_stream(launch, steps, warmup)
+        pw = power(launch) if power else None
     finally:
         harness.unload_kernel(module)
     geo = pkg.launch_geometry(p.OUT_N)
@@ -408,15 +544,18 @@ def time_drop_in_co(pkg, p, dev, steps, warmup):
            "kernel": f"{os.path.basename(pkg.CODE_OBJECT_PATH)}: {name}, {geo['tile_m']}x{geo['tile_n']} tiles, "
                      f"grid {ncu} x {harness.BLOCK} threads, {harness.SHARED_MEM} B dynamic LDS, kernelParams launch "
                      f"on the null stream (what reference launcher.cpp / bench.py --kernel callers run)"}
+    if pw:
+        rec["power"] = pw
     return rec, out
 
 
-def time_drop_in_co_fwd(pkg, p, dev, steps, warmup, row_align):
+def time_drop_in_co_fwd(pkg, p, dev, steps, warmup, row_align, power=None):
     """The persistent GEMM's drop-in code object for the site's A format
     (``persistent_e4m3.co`` / ``persistent_e5m2.co``, the 512-thread kernel) timed as
     ``time_drop_in_co`` times the wgrad's: the reference's hipModule path with the 16-entry
     kernelParams array on the null stream (reference bench.py:312-361), on the same operands (with
-    ``row_align``, the same padded views). Returns (record, output tensor of the last launch)."""
+    ``row_align``, the same padded views); ``power`` as there. Returns (record, output tensor of the
+    last launch)."""
     import torch
     from ggemm_asm_amd import harness
     path = pkg.PERSISTENT_CODE_OBJECT_PATHS[p.a_format]
@@ -430,6 +569,7 @@ def time_drop_in_co_fwd(pkg, p, dev, steps, warmup, row_align):
         launch, _keep = harness.prepare_persistent_args(func, a, b, out, sa, sb, p.group_offs, p.G, p.N, p.K, ncu)
         torch.cuda.synchronize()
         ms = harness.time_null_stream(launch, steps, warmup)
+        pw = power(launch) if power else None
     finally:
         harness.unload_kernel(module)
     geo = pkg.launch_geometry(p.N)
@@ -437,6 +577,8 @@ def time_drop_in_co_fwd(pkg, p, dev, steps, warmup, row_align):
            "kernel": f"{os.path.basename(path)}: {name}, {geo['tile_m']}x{geo['tile_n']} tiles, grid {ncu} x "
                      f"{harness.BLOCK} threads, {harness.SHARED_MEM} B dynamic LDS, kernelParams launch on the null "
                      f"stream (what the reference's bench.py --kernel callers of this site run)"}
+    if pw:
+        rec["power"] = pw
     return rec, out
 
 
@@ -659,13 +801,29 @@ def main_sites(args, pkg, dev):
 
 def main():
     args = parse_args()
+    if args.power_sampler:
+        power_sampler(args.power_sampler, args.power_interval)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: the grouped wgrad needs no collective and this build runs "
               f"on a single MI355X (asked for --gpus {args.gpus}).", file=sys.stderr)
         sys.exit(2)
+    if args.power_seconds > 0 and (args.site or args.config in QUANT_CONFIGS + LAYER_CONFIGS or args.info
+                                   or args.copy_calibration_mb):
+        raise SystemExit("--power-seconds applies to the single-kernel configs")
     if args.copy_calibration_mb:
         copy_calibration(args.copy_calibration_mb, args.steps)
         return
+    # the power sampler's child process starts here, before anything touches the GPU
+    sampler = PowerSampler() if args.power_seconds > 0 else None
+    try:
+        run_bench(args, sampler)
+    finally:
+        if sampler is not None and sampler.proc.poll() is None:
+            sampler.stop()
+
+
+def run_bench(args, sampler):
     from __graft_entry__ import load_package
     pkg = load_package()
     if args.info:
@@ -716,6 +874,11 @@ def main():
     tflops = p.flops / (ms * 1e-3) / 1e12
     drop_in_co = (args.drop_in and not p.is_mx if not fwd else args.drop_in) and args.out == "bf16" \
         and args.mfma == "k128" and args.config not in SHARD_CONFIGS
+    if sampler is not None and args.power_of == "drop_in" and not drop_in_co:
+        raise SystemExit("--power-of drop_in needs the drop-in code object leg (bf16 C, k128, not --no-drop-in)")
+    power_live = power_window(run, args.power_seconds, sampler) if sampler and args.power_of == "library" else None
+    co_power = ((lambda launch: power_window(launch, args.power_seconds, sampler))
+                if sampler and args.power_of == "drop_in" else None)
     # traffic measured for this exact variant (profiles/traffic_<config>[_<out>][_reference_lens].txt)
     traffic, traffic_source = read_traffic(args.config + ("" if args.out == "bf16" else "_" + args.out)
                                            + ("" if args.lens == "multinomial" else "_reference_lens"))
@@ -778,7 +941,7 @@ def main():
                      "traffic_source": traffic_source},
     }
     label = power_label(args)
-    power = read_power(label) if label else None
+    power = power_live or (read_power(label) if label else None)
     if power:
         line["roofline"]["power"] = power
     if args.extra:
@@ -832,9 +995,9 @@ def main():
     co_steps = args.drop_in_steps or args.steps
     if drop_in_co and fwd:
         line["drop_in_co"], outs["drop_in_co"] = time_drop_in_co_fwd(pkg, p, dev, co_steps, args.warmup,
-                                                                     args.row_align)
+                                                                     args.row_align, co_power)
     elif drop_in_co:
-        line["drop_in_co"], outs["drop_in_co"] = time_drop_in_co(pkg, p, dev, co_steps, args.warmup)
+        line["drop_in_co"], outs["drop_in_co"] = time_drop_in_co(pkg, p, dev, co_steps, args.warmup, co_power)
     # outside the timed region: the oracle over every group of the timed inputs, checked against
     # the last timed launch's output, and timed as the CPU baseline
     failed = []

@@ -115,3 +115,65 @@ def test_power_record_for_measured_variants_only(monkeypatch):
         if want:
             assert bench.read_power(want) is not None, want
     assert bench.read_power("no such row") is None
+
+
+def _smi_doc(watts, clks, gpus=1):
+    """An amd-smi metric -p -c --json document (the fields bench.py reads, with neighbours)."""
+    import json
+    gpu = {"gpu": 0, "power": {"socket_power": {"value": watts, "unit": "W"}, "gfx_voltage": "N/A"},
+           "clock": {**{f"gfx_{i}": {"clk": {"value": c, "unit": "MHz"}, "max_clk": {"value": 2400, "unit": "MHz"}}
+                        for i, c in enumerate(clks)},
+                     "mem_0": {"clk": {"value": 1900, "unit": "MHz"}}, "fclk_0": {"clk": {"value": 2000, "unit": "MHz"}}}}
+    return json.dumps({"gpu_data": [gpu] * gpus})
+
+
+def test_parse_amd_smi():
+    """Socket power and the mean of the XCDs' gfx clocks (memory and fabric clocks left out); a
+    reading that lists several GPUs is refused, the list form is accepted."""
+    import json
+    w, mhz = bench.parse_amd_smi(_smi_doc(1394, [1860, 1880, 1870, 1870, 1860, 1880, 1870, 1870]))
+    assert w == 1394.0 and mhz == 1870.0
+    with pytest.raises(ValueError, match="2 GPUs"):
+        bench.parse_amd_smi(_smi_doc(1394, [1870], gpus=2))
+    doc = json.loads(_smi_doc(700, [2400, 2398]))["gpu_data"]
+    assert bench.parse_amd_smi(json.dumps(doc)) == (700.0, 2399.0)
+
+
+def test_summarize_power_middle_half():
+    """Medians over the readings in the window's middle half only (the ramp of the first quarter and
+    the tail are left out), error lines ignored; ms per launch from the window's wall time, energy
+    per launch = power x ms; no reading inside -> an error record naming the last failure."""
+    t0, t1 = 100.0, 108.0
+    samples = [{"t": t0 + 0.25 * i, "watts": (900.0 if i < 8 else 1390.0 + (i % 3)), "mhz": 2000.0 if i < 8 else 1870.0}
+               for i in range(32)]
+    samples.insert(12, {"t": 104.0, "error": "TimeoutExpired"})
+    rec = bench.summarize_power(samples, t0, t1, launches=5000)
+    assert rec["watts"] == 1391.0 and rec["gfx_clock_mhz"] == 1870 and rec["cap_watts"] == 1400
+    assert rec["ms_per_launch"] == 1.6 and rec["energy_per_launch_j"] == round(1391.0 * 1.6e-3, 3)
+    assert rec["samples"] == 17 and rec["seconds"] == 8.0
+    bad = bench.summarize_power([{"t": 104.0, "error": "FileNotFoundError: amd-smi"}], t0, t1, 10)
+    assert bad == {"error": "FileNotFoundError: amd-smi"}
+
+
+def test_power_sampler_child(tmp_path, monkeypatch):
+    """The sampler protocol end to end on the CPU, with a stand-in amd-smi on PATH: the child
+    records nothing before start(), readings once it is on, and stop() ends it and returns them."""
+    import time
+    fake = tmp_path / "amd-smi"
+    fake.write_text("#!/bin/sh\ncat <<'EOF'\n" + _smi_doc(1234, [1900, 1910]) + "\nEOF\n")
+    fake.chmod(0o755)
+    monkeypatch.setenv("PATH", f"{tmp_path}:{__import__('os').environ['PATH']}")
+    s = bench.PowerSampler(interval=0.05)
+    try:
+        time.sleep(0.5)
+        import os
+        assert os.path.getsize(s.path) == 0
+        s.start()
+        deadline = time.time() + 20
+        while os.path.getsize(s.path) < 200 and time.time() < deadline:
+            time.sleep(0.1)
+    finally:
+        samples = s.stop()
+    assert s.proc.poll() is not None
+    good = [x for x in samples if "watts" in x]
+    assert len(good) >= 2 and all(x["watts"] == 1234.0 and x["mhz"] == 1905.0 for x in good), samples[:3]
